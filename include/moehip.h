@@ -1,0 +1,161 @@
+/*
+ * moehip — MI355X (gfx950) kernels for moelab's MoE-layer hot path, as a C ABI.
+ *
+ * Every pointer argument is device memory owned by the caller (the PyTorch caching allocator,
+ * or expert records held by the runtime's caches). No entry point allocates, frees or
+ * synchronises: each one enqueues its kernels on `stream` (a hipStream_t; NULL = the null
+ * stream) and returns. That keeps every entry point capturable in a HIP graph.
+ *
+ * Return value: 0 on success, otherwise a MOEHIP_E* code; moehip_last_error() gives the
+ * message (thread-local). The Python wrapper turns a non-zero code into RuntimeError, which
+ * the moelab runtime already treats as "kernel unavailable, use the fallback"
+ * (moelab/runtime.py:346-348, 412-414, 737-741).
+ *
+ * Record format (moelab/store.py:76-115): one record per expert, fields 64-B aligned inside a
+ * 4096-B aligned record. A table row is four int64 device addresses
+ * [gate_up.q, gate_up.s, down.q, down.s]; float records repeat [gate_up, gate_up, down, down]
+ * (moelab/kernels.py:797, 882); fp8 records follow the int layout with fp32 128x128 block
+ * scales. Row weights are fp32 and a weight of 0 means "skip this row" (moelab/kernels.py:322).
+ */
+#ifndef MOEHIP_H
+#define MOEHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOEHIP_ABI_VERSION 1
+
+/* error codes */
+#define MOEHIP_OK 0
+#define MOEHIP_EINVAL 1       /* bad argument (null pointer, size, unsupported combination) */
+#define MOEHIP_ELAUNCH 2      /* the HIP runtime refused the launch */
+#define MOEHIP_ENODEV 3       /* no usable gfx950 device */
+
+/* record precisions: the `precision` of moelab/store.py:39-45, plus block-scaled fp8 */
+#define MOEHIP_PREC_INT4 0
+#define MOEHIP_PREC_INT8 1
+#define MOEHIP_PREC_F16 2
+#define MOEHIP_PREC_BF16 3
+#define MOEHIP_PREC_F32 4
+#define MOEHIP_PREC_FP8 5
+
+/* activation / output dtypes */
+#define MOEHIP_DT_F16 0
+#define MOEHIP_DT_BF16 1
+#define MOEHIP_DT_F32 2
+
+int moehip_abi_version(void);
+const char *moehip_last_error(void);
+/* 0 if device `dev` is a gfx950 (MI355X-class) GPU, MOEHIP_ENODEV otherwise. */
+int moehip_device_check(int dev);
+
+/*
+ * y (O,) = W x for one int4 matrix W = (q (O, I/2) u8, s (O, I/gs) f16), x (I,) in `dtype`,
+ * y in `dtype`, fp32 accumulation.
+ * Replaces moelab/kernels.py:60-67 `gemv_int4` (Triton `_gemv_int4_kernel`, kernels.py:38-57).
+ */
+int moehip_gemv_int4(const void *q, const void *s, const void *x, void *y, int O, int I, int gs, int dtype,
+                     void *stream);
+
+/*
+ * Kernel A of the grouped expert FFN: for every table row e < n with w[e] != 0,
+ *   h[e, r] = silu(gate_e[r] . x) * (up_e[r] . x),  r < I,
+ * where gate_e / up_e are rows r and r+I of the record's gate_up matrix (2I, H), dequantised in
+ * registers (int4/int8: (q - 8 | q) * fp16 group scale; fp8: e4m3fn * fp32 block scale).
+ * x (H,) in `xdtype`; h (n, I) fp32. If acc_zero is non-null, acc_zero[0:H] is set to 0 in the
+ * same launch (the reference's ZERO flag).
+ * Replaces moelab/kernels.py:801-815 `_Plan.up` (Triton `_grp4_up` 312-361, `_grp4_up_v4`
+ * 494-541, `_grp8_up` 667-709, `_grpf_up` 398-428, `_grp_int4_up` 98-124).
+ */
+int moehip_grouped_up(int prec, const int64_t *tab, const float *w, const void *x, int xdtype, float *h,
+                      float *acc_zero, int n, int I, int H, int gs, void *stream);
+
+/*
+ * Kernel B with a deterministic combine:
+ *   acc[j] += sum over e = 0..n-1 (table order) with w[e] != 0 of  w[e] * (down_e[j] . h[e]).
+ * `partial` is caller-owned scratch of moehip_down_workspace_floats(n, H) floats (any content).
+ * Replaces moelab/kernels.py:817-831 `_Plan.down` (Triton `_grp4_down` 363-396 and
+ * `_grp4_down_v4` 543-575, `_grp8_down` 711-740, `_grpf_down` 430-451, which add with fp32
+ * atomics in a run-dependent order; the order here is fixed, like v1 `_grp_int4_down` 126-148).
+ */
+int moehip_grouped_down(int prec, const int64_t *tab, const float *w, const float *h, float *acc, int n, int H,
+                        int I, int gs, float *partial, void *stream);
+size_t moehip_down_workspace_floats(int n, int H);
+
+/*
+ * out[t, j] = (accumulate ? out[t, j] : 0) + acc[t, j] (+ add[t, j] if add != NULL), for T rows
+ * of H, computed in fp32 and rounded once to `dtype` (out and add share `dtype`).
+ * Replaces the graph tail `out.copy_(acc); out.add_(cpu_part)` (moelab/kernels.py:949-950) and
+ * `out.add_(acc)` (kernels.py:769, 862, 872, 891).
+ */
+int moehip_combine(const float *acc, const void *add, void *out, int T, int H, int dtype, int accumulate,
+                   void *stream);
+
+/*
+ * Router: logits = x W^T rounded to `dtype` (fp32 accumulation), p = softmax(logits) in fp32,
+ * top-k with the lowest expert index first among equal logits, optional renormalisation
+ * (norm_topk_prob), weights cast to `dtype`.
+ * x (T, H) and Wr (E, H) in `dtype`; outputs logits (T, E) `dtype`, idx (T, k) int64,
+ * w (T, k) `dtype`, w32 (T, k) fp32 (the weights after the cast, as fp32: what the expert
+ * kernels consume, moelab/kernels.py:237). E <= 1024, k <= min(E, 32).
+ * Replaces transformers OlmoeTopKRouter.forward (models/olmoe/modeling_olmoe.py:337-346),
+ * Qwen3MoeTopKRouter (qwen3_moe:249-267) and Qwen3NextTopKRouter (qwen3_next:757-775), called
+ * by moelab at runtime.py:909 and graphs.py:255.
+ */
+int moehip_router_topk(const void *x, const void *Wr, int T, int H, int E, int k, int renorm, int dtype,
+                       void *logits, int64_t *idx, void *w, float *w32, void *stream);
+
+/* HOBBIT policy parameters (moelab/policy.py:50-58); t_mid/t2 < 0 mean "None". */
+typedef struct moehip_policy {
+    int mode;   /* 0 = hobbit, 1 = hi, 2 = lo */
+    float t1;   /* already resolved for the layer (t1_for(layer)) */
+    float t_mid;
+    float t2;
+    int protect; /* 1 if the layer is protected (level 0) */
+    int upgrade; /* allow_upgrade: a more precise resident copy may serve the request */
+} moehip_policy;
+
+/*
+ * Decode-time decision + residency for ONE token (the whole-token-graph path): HOBBIT levels and
+ * skip of the k routed experts (policy.py:77-123), level -> precision (lv2p[3],
+ * policy.py:188-192), choice of the resident copy (most precise allowed resident precision),
+ * and the kernel tables. Inputs: idx (k) int64, w32 (k) fp32, rtab (P, E) int64 device base
+ * addresses of this layer's resident records (0 = absent), offs (P, 4) int64 field offsets,
+ * planned (P) int32 (1 = a kernel plan exists for that precision).
+ * Outputs: tab (P, k, 4) int64 and wtab (P, k) fp32 (rows not chosen get weight 0),
+ * info (3, k) fp32 = [expert id, chosen precision or -2 if skipped (-1 = missing), level],
+ * miss (1) fp32 += number of non-skipped experts with no usable resident copy.
+ * Replaces moelab/fullgraph.py:101-114 `gpu_levels` + 149-171 `FullMoE.layer`, and the host
+ * table fill of `GroupedGraph.run` (kernels.py:952-969).
+ */
+int moehip_decide_table(const int64_t *idx, const float *w32, int k, const moehip_policy *pol, const int *lv2p,
+                        const int64_t *rtab, int P, int E, const int64_t *offs, const int *planned, int64_t *tab,
+                        float *wtab, float *info, float *miss, void *stream);
+
+/*
+ * Token-to-expert dispatch (moelab/runtime.py:471-482, `_decide_general`): pairs (t, j) with
+ * skip == 0 (skip may be NULL) are sorted by expert id, stably in pair order t*k+j.
+ * Outputs: counts (E) int32, offsets (E+1) int32, sorted_pos (T*k) int32 (pair index t*k+j;
+ * entries past offsets[E] are -1), rank (T*k) int32 (position of each pair in the sorted list,
+ * -1 if skipped). One workgroup; T*k <= 65536, E <= 1024.
+ */
+int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E, int32_t *counts,
+                    int32_t *offsets, int32_t *sorted_pos, int32_t *rank, void *stream);
+
+/*
+ * Symmetric absmax quantisation of w (O, I) fp32 row-major with one fp16 scale per group of gs
+ * columns (moelab/quant.py:104-127 with method="absmax", scales from quant.py:57-61, 74-76),
+ * written in the store's packing (quant.py:96-101): bits = 4 -> q (O, I/2) u8, value + 8,
+ * low nibble = even column; bits = 8 -> q (O, I) i8. s (O, I/gs) f16. gs even, gs <= 64.
+ */
+int moehip_quantize(const float *w, int O, int I, int bits, int gs, void *q, void *s, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEHIP_H */

@@ -1,0 +1,252 @@
+// Router (logits -> softmax -> top-k -> renorm) and the decode-time decision/table kernel.
+//
+// Router numerics follow transformers' *TopKRouter.forward (modeling_olmoe.py:337-346):
+// logits are F.linear in the model dtype (here: fp32 accumulation, one rounding to the dtype),
+// softmax in fp32, top-k, optional renormalisation in fp32, weights cast to the model dtype.
+// Top-k compares the (dtype-exact) logits, lowest expert index first among equal logits, which
+// selects the same set as top-k over the probabilities whenever distinct logits give distinct
+// probabilities.
+
+#include <limits.h>
+
+#include "common.hpp"
+
+namespace moehip {
+
+constexpr int ROUTER_TT = 8;  // tokens per block in the logits kernel
+
+// logits[t, e] = round_dt(sum_c x[t, c] * Wr[e, c]); one wave per expert row, 4 waves per block
+__global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ x, const void *__restrict__ Wr, int T,
+                                                       int H, int E, int dt, void *__restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (e >= E) return;
+    const int t0 = blockIdx.y * ROUTER_TT;
+    const int nt = min(ROUTER_TT, T - t0);
+    float acc[ROUTER_TT];
+#pragma unroll
+    for (int t = 0; t < ROUTER_TT; ++t) acc[t] = 0.f;
+    const size_t wrow = (size_t)e * H;
+    if (dt != MOEHIP_DT_F32 && H % 8 == 0 && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0) {
+        // 16-bit dtypes, 8 values per 16-byte load
+        const uint16_t *W16 = reinterpret_cast<const uint16_t *>(Wr);
+        const uint16_t *X16 = reinterpret_cast<const uint16_t *>(x);
+        for (int c = lane * 8; c < H; c += 512) {
+            const uint4 wv = *reinterpret_cast<const uint4 *>(W16 + wrow + c);
+            const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+            float wf[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (dt == MOEHIP_DT_F16) {
+                    wf[2 * j] = f16_to_f32(wd[j] & 0xffffu);
+                    wf[2 * j + 1] = f16_to_f32(wd[j] >> 16);
+                } else {
+                    wf[2 * j] = __uint_as_float(wd[j] << 16);
+                    wf[2 * j + 1] = __uint_as_float(wd[j] & 0xffff0000u);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < ROUTER_TT; ++t) {
+                if (t < nt) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(X16 + (size_t)(t0 + t) * H + c);
+                    const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float xa, xb;
+                        if (dt == MOEHIP_DT_F16) {
+                            xa = f16_to_f32(xd[j] & 0xffffu);
+                            xb = f16_to_f32(xd[j] >> 16);
+                        } else {
+                            xa = __uint_as_float(xd[j] << 16);
+                            xb = __uint_as_float(xd[j] & 0xffff0000u);
+                        }
+                        acc[t] = fmaf(wf[2 * j], xa, acc[t]);
+                        acc[t] = fmaf(wf[2 * j + 1], xb, acc[t]);
+                    }
+                }
+            }
+        }
+    } else {
+        for (int c = lane; c < H; c += 64) {
+            const float wv = load_act(Wr, wrow + c, dt);
+#pragma unroll
+            for (int t = 0; t < ROUTER_TT; ++t)
+                if (t < nt) acc[t] = fmaf(wv, load_act(x, (size_t)(t0 + t) * H + c, dt), acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < ROUTER_TT; ++t) {
+        const float s = wave_sum(acc[t]);
+        if (lane == 0 && t < nt) store_act(logits, (size_t)(t0 + t) * E + e, dt, s);
+    }
+}
+
+// softmax + top-k + renorm for one token per wave (E <= 1024, k <= 32)
+__global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ logits, int T, int E, int k, int renorm,
+                                                    int dt, int64_t *__restrict__ idx, void *__restrict__ wout,
+                                                    float *__restrict__ w32) {
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x;
+    __shared__ int s_idx[32];
+    __shared__ float s_p[32];
+    float lv[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = lane + 64 * i;
+        lv[i] = c < E ? load_act(logits, (size_t)t * E + c, dt) : -INFINITY;
+        m = fmaxf(m, lv[i]);
+    }
+    m = wave_max(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = lane + 64 * i;
+        if (c < E) sum += expf(lv[i] - m);
+    }
+    sum = wave_sum(sum);
+    uint32_t taken = 0;
+    for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = lane + 64 * i;
+            if (c < E && !((taken >> i) & 1u) && (lv[i] > bv || (lv[i] == bv && c < bi))) {
+                bv = lv[i];
+                bi = c;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == 0) {
+            s_idx[j] = bi;
+            s_p[j] = expf(bv - m) / sum;
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float tot = 0.f;
+        if (renorm)
+            for (int j = 0; j < k; ++j) tot += s_p[j];
+        for (int j = 0; j < k; ++j) {
+            const float p = renorm ? s_p[j] / tot : s_p[j];
+            idx[(size_t)t * k + j] = s_idx[j];
+            const float r = round_act(p, dt);
+            if (wout != nullptr) store_act(wout, (size_t)t * k + j, dt, p);
+            if (w32 != nullptr) w32[(size_t)t * k + j] = r;
+        }
+    }
+}
+
+// HOBBIT levels + resident-copy choice + kernel tables for one token (k <= 64), one wave
+__global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__ idx, const float *__restrict__ w32,
+                                                     int k, moehip_policy pol, int lv0, int lv1, int lv2,
+                                                     const int64_t *__restrict__ rtab, int P, int E,
+                                                     const int64_t *__restrict__ offs, const int *__restrict__ planned,
+                                                     int64_t *__restrict__ tab, float *__restrict__ wtab,
+                                                     float *__restrict__ info, float *__restrict__ miss) {
+    const int j = threadIdx.x;
+    __shared__ float s_w[64];
+    __shared__ float s_sorted[64];
+    __shared__ float s_total;
+    const bool act = j < k;
+    const int e = act ? (int)idx[j] : 0;
+    const float wj = act ? w32[j] : 0.f;
+    s_w[j] = wj;
+    __syncthreads();
+    if (j == 0) {
+        float tot = 0.f;
+        for (int i = 0; i < k; ++i) tot += s_w[i];
+        s_total = fmaxf(tot, 1e-12f);
+    }
+    __syncthreads();
+    int lvl;
+    bool skip = false;
+    if (pol.mode == 1 || pol.protect) {
+        lvl = 0;
+    } else if (pol.mode == 2) {
+        lvl = 2;
+    } else {
+        // unimportance (policy.py:77-87): stable descending rank, s = cumsum(sorted) - own weight
+        const float wn = wj / s_total;
+        s_w[j] = wn;
+        __syncthreads();
+        int rank = 0;
+        for (int i = 0; i < k; ++i) {
+            const float o = s_w[i];
+            rank += (o > wn) || (o == wn && i < j);
+        }
+        if (act) s_sorted[rank] = wn;
+        __syncthreads();
+        float cs = 0.f;
+        for (int r = 0; r <= rank && r < k; ++r) cs += s_sorted[r];
+        const float s = cs - wn;
+        lvl = 2;
+        if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
+        if (s <= pol.t1) lvl = 0;
+        skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
+    }
+    const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
+    int chosen = -1;
+    for (int pi = P - 1; pi >= 0; --pi) {
+        const bool avail = act && e >= 0 && e < E && rtab[(size_t)pi * E + e] != 0;
+        const bool ok = avail && (pol.upgrade ? req >= pi : req == pi);
+        if (ok) chosen = pi;
+    }
+    const bool usable = chosen >= 0 && planned[chosen];
+    const bool is_miss = act && !skip && !usable;
+    if (act) {
+        for (int pi = 0; pi < P; ++pi) {
+            const bool sel = (chosen == pi) && !skip && planned[pi];
+            const int64_t base = sel ? rtab[(size_t)pi * E + e] : 0;
+            for (int f = 0; f < 4; ++f) tab[((size_t)pi * k + j) * 4 + f] = sel ? base + offs[pi * 4 + f] : 0;
+            wtab[(size_t)pi * k + j] = sel ? wj : 0.f;
+        }
+        info[j] = (float)e;
+        info[k + j] = skip ? -2.f : (float)chosen;
+        info[2 * k + j] = (float)lvl;
+    }
+    const unsigned long long bal = __ballot(is_miss);
+    if (j == 0 && miss != nullptr) miss[0] += (float)__popcll(bal);
+}
+
+}  // namespace moehip
+
+using namespace moehip;
+
+extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, int E, int k, int renorm, int dtype,
+                                  void *logits, int64_t *idx, void *w, float *w32, void *stream) {
+    MOEHIP_REQUIRE(x && Wr && logits && idx, "router_topk: null pointer");
+    MOEHIP_REQUIRE(dtype >= MOEHIP_DT_F16 && dtype <= MOEHIP_DT_F32, "router_topk: bad dtype %d", dtype);
+    MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E,
+                   "router_topk: bad sizes T=%d H=%d E=%d k=%d", T, H, E, k);
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(k_router_logits, dim3((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT), dim3(256), 0, st, x, Wr, T,
+                       H, E, dtype, logits);
+    int rc = check_launch("router logits");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_router_topk, dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, dtype, idx, w, w32);
+    return check_launch("router topk");
+}
+
+extern "C" int moehip_decide_table(const int64_t *idx, const float *w32, int k, const moehip_policy *pol,
+                                   const int *lv2p, const int64_t *rtab, int P, int E, const int64_t *offs,
+                                   const int *planned, int64_t *tab, float *wtab, float *info, float *miss,
+                                   void *stream) {
+    MOEHIP_REQUIRE(idx && w32 && pol && lv2p && rtab && offs && planned && tab && wtab && info,
+                   "decide_table: null pointer");
+    MOEHIP_REQUIRE(k > 0 && k <= 64 && P > 0 && P <= 8 && E > 0, "decide_table: bad sizes k=%d P=%d E=%d", k, P, E);
+    for (int i = 0; i < 3; ++i) MOEHIP_REQUIRE(lv2p[i] >= 0 && lv2p[i] < P, "decide_table: lv2p[%d]=%d", i, lv2p[i]);
+    hipLaunchKernelGGL(k_decide_table, dim3(1), dim3(64), 0, as_stream(stream), idx, w32, k, *pol, lv2p[0], lv2p[1],
+                       lv2p[2], rtab, P, E, offs, planned, tab, wtab, info, miss);
+    return check_launch("decide_table");
+}

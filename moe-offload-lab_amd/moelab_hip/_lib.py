@@ -1,0 +1,124 @@
+"""
+ctypes binding of libmoehip.so (declared in include/moehip.h).
+
+The library is loaded lazily on first use and there is no fallback: if it is missing or was
+built for another GPU, every call raises RuntimeError with the reason.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("MOEHIP_LIB", Path(__file__).resolve().parent / "libmoehip.so"))
+
+PREC_CODES = {"int4": 0, "int8": 1, "fp16": 2, "bf16": 3, "fp32": 4, "fp8": 5}
+DT_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+
+
+class Policy(ctypes.Structure):
+    """moehip_policy: HOBBIT parameters for one layer (thresholds include the +1e-6 of policy.py:120-122)."""
+
+    _fields_ = [("mode", _i), ("t1", _f), ("t_mid", _f), ("t2", _f), ("protect", _i), ("upgrade", _i)]
+
+
+_SIGS = {
+    "moehip_abi_version": ([], _i),
+    "moehip_last_error": ([], ctypes.c_char_p),
+    "moehip_device_check": ([_i], _i),
+    "moehip_gemv_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "moehip_grouped_up": ([_i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "moehip_grouped_down": ([_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp], _i),
+    "moehip_down_workspace_floats": ([_i, _i], ctypes.c_size_t),
+    "moehip_combine": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "moehip_router_topk": ([_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _i),
+    "moehip_decide_table": ([_vp, _vp, _i, ctypes.POINTER(Policy), _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
+                             _vp, _vp], _i),
+    "moehip_dispatch": ([_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _i),
+    "moehip_quantize": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
+}
+
+EXPORTED = tuple(_SIGS)
+_lib = None
+_checked_devices: set[int] = set()
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+    """Load libmoehip.so (no device access). Raises RuntimeError if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"libmoehip.so not found at {p}: build it with `python -m moelab_hip.build` "
+                           "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(str(p))
+    for name, (args, res) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if lib.moehip_abi_version() != 1:
+        raise RuntimeError(f"libmoehip ABI {lib.moehip_abi_version()} != 1")
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def check_device(device: torch.device | int | str | None = None) -> None:
+    """Raise unless `device` is a gfx950 GPU the library can run on."""
+    lib = load()
+    if not torch.cuda.is_available():
+        raise RuntimeError("no ROCm GPU visible: the moehip kernels need a gfx950 device")
+    dev = torch.device(device) if device is not None and not isinstance(device, int) else None
+    idx = (device if isinstance(device, int) else (dev.index if dev is not None and dev.index is not None
+                                                     else torch.cuda.current_device()))
+    if idx in _checked_devices:
+        return
+    rc = lib.moehip_device_check(idx)
+    if rc != 0:
+        raise RuntimeError(lib.moehip_last_error().decode())
+    _checked_devices.add(idx)
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point; a non-zero return raises RuntimeError with the library's message."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        raise RuntimeError(f"{name} failed ({rc}): {lib.moehip_last_error().decode()}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def prec_code(prec: str) -> int:
+    try:
+        return PREC_CODES[prec]
+    except KeyError:
+        raise RuntimeError(f"unsupported record precision {prec!r}") from None
+
+
+def dt_code(dtype: torch.dtype) -> int:
+    try:
+        return DT_CODES[dtype]
+    except KeyError:
+        raise RuntimeError(f"unsupported activation dtype {dtype}") from None

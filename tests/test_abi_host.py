@@ -1,0 +1,93 @@
+"""CPU tests: the C-ABI library loads and exports what include/moehip.h declares; argument
+validation works without touching a GPU; host-side layout and policy logic match the oracle."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import ROOT
+from moelab_hip import _lib
+from moelab_hip.policy import PrecisionPolicy, level_to_precision
+from moelab_hip.store import dims, field_offsets, group_size_of, record_layout
+
+HEADER = ROOT / "include" / "moehip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(moehip_\w+)\s*\(", text)) - {"moehip_policy"})
+
+
+def test_header_declares_the_bound_entry_points():
+    assert set(_declared()) == set(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.moehip_abi_version() == 1
+
+
+def test_argument_validation_without_gpu():
+    lib = _lib.load()
+    # null pointers / bad sizes are rejected before any HIP call
+    assert lib.moehip_grouped_up(0, None, None, None, 0, None, None, 8, 1024, 2048, 64, None) == 1
+    assert b"null" in lib.moehip_last_error()
+    assert lib.moehip_grouped_down(9, None, None, None, None, 8, 2048, 1024, 64, None, None) == 1
+    assert lib.moehip_quantize(None, 4, 64, 3, 64, None, None, None) == 1
+    assert lib.moehip_router_topk(None, None, 1, 64, 2048, 8, 0, 0, None, None, None, None, None) == 1
+    assert lib.moehip_dispatch(None, None, 1, 8, 64, None, None, None, None, None) == 1
+    assert lib.moehip_down_workspace_floats(8, 2048) == 8 * 2048
+    with pytest.raises(RuntimeError, match="grouped_up"):
+        _lib.call("moehip_grouped_up", 0, None, None, None, 0, None, None, 8, 1024, 2048, 64, None)
+
+
+def test_policy_struct_layout():
+    assert ctypes.sizeof(_lib.Policy) == 24
+
+
+@pytest.mark.parametrize("prec", ["fp32", "fp16", "bf16", "int8", "int4", "fp8"])
+@pytest.mark.parametrize("H,I", [(2048, 1024), (2048, 768), (2048, 512), (64, 32), (96, 48), (512, 256)])
+def test_record_layout_matches_oracle(prec, H, I):
+    mine = record_layout(prec, H, I, 64)
+    ref = O.record_layout(prec, H, I, 64)
+    assert mine == ref
+    assert dims(mine) == (H, I)
+    offs = field_offsets(mine)
+    assert len(offs) == 4 and all(o % 64 == 0 for o in offs)
+    if prec in ("int4", "int8"):
+        assert group_size_of(mine) == (O.pick_group_size(H), O.pick_group_size(I))
+
+
+def test_policy_levels_match_oracle():
+    g = torch.Generator().manual_seed(1)
+    pols = [dict(mode="hobbit", t1=0.3, t_mid=0.7), dict(mode="hobbit", t1=0.5, t_mid=0.6, t2=0.9),
+            dict(mode="hobbit", t1=0.6, t1_layers={1: 0.2, 3: 0.9}), dict(mode="hi"), dict(mode="lo"),
+            dict(mode="hobbit", protect_layers={2})]
+    for kw in pols:
+        mine, ref = PrecisionPolicy(**kw), O.Policy(**kw)
+        for layer in range(4):
+            w = torch.rand(20, 8, generator=g) ** 2
+            l1, s1 = mine.levels(layer, w)
+            l2, s2 = ref.levels(layer, w.numpy())
+            assert np.array_equal(l1.numpy(), l2) and np.array_equal(s1.numpy(), s2)
+            for t in range(4):
+                lo, so, _ = mine.levels_one(layer, w[t].tolist())
+                assert lo == l1[t].tolist() and so == s1[t].tolist()
+
+
+def test_device_policy_thresholds():
+    p = PrecisionPolicy("hobbit", t1=0.6, t2=0.9, t1_layers={3: 0.2}, protect_layers={5})
+    d = p.device_policy(3)
+    assert d.mode == 0 and d.t1 == float(np.float32(0.2 + 1e-6)) and d.t2 == float(np.float32(0.9 + 1e-6))
+    assert d.t_mid == -1.0 and d.protect == 0 and d.upgrade == 1
+    assert p.device_policy(5).protect == 1
+    assert PrecisionPolicy("lo").device_policy(0).upgrade == 0
+    assert [level_to_precision(v, ["fp16", "int4"]) for v in (0, 1, 2)] == ["fp16", "int4", "int4"]

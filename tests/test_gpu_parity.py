@@ -1,0 +1,399 @@
+"""
+GPU parity: every HIP entry point against the oracle on the same seeded inputs.
+
+Bars (the reference's north-star bar): integer / byte / index work bit-exact; layer outputs in
+fp16/bf16 within max-abs 2e-2 and mean-rel 1e-3, where mean-rel = mean|got - ref| / mean|ref|;
+fp32 activations within the reference's own kernel-test bound (rel-err < 1e-4 of max|ref|,
+moelab tests/test_kernels.py:49-50).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from moelab_hip import _lib
+from moelab_hip import kernels as K
+from moelab_hip.layer import MoEDecoder, ResidentStore
+from moelab_hip.policy import PrecisionPolicy
+from moelab_hip.store import encode_record_, record_layout, views
+
+pytestmark = pytest.mark.gpu
+
+NPDT = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+
+
+def mean_rel(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).mean() / max(np.abs(ref).mean(), 1e-30))
+
+
+def assert_layer_close(got, ref, dtype):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    if dtype == torch.float32:
+        err = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+        assert err < 1e-4, err
+    else:
+        assert np.abs(got - ref).max() <= 2e-2, np.abs(got - ref).max()
+        assert mean_rel(got, ref) <= 1e-3, mean_rel(got, ref)
+
+
+def make_records(prec, H, I, n, seed, std=0.1):
+    g = torch.Generator().manual_seed(seed)
+    lay = O.record_layout(prec, H, I, 64, scale="absmax")
+    blobs, mats = [], []
+    for _ in range(n):
+        gu = (torch.randn(2 * I, H, generator=g) * std).numpy()
+        dn = (torch.randn(H, I, generator=g) * std).numpy()
+        b = O.encode_record(lay, gu, dn, method="absmax")
+        blobs.append(b)
+        mats.append(O.materialize(lay, b, "float32"))
+    return lay, blobs, mats
+
+
+def to_dev(blobs, dev):
+    return [torch.from_numpy(b.copy()).to(dev) for b in blobs]
+
+
+# ---------------------------------------------------------------------------------------
+# store encoding (quantiser) — bit-exact
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("O_,I_,gs", [(256, 512, 64), (64, 96, 48), (33, 128, 32), (2048, 1024, 64)])
+def test_quantize_bit_exact(dev, bits, O_, I_, gs):
+    g = torch.Generator().manual_seed(O_ + I_ + bits)
+    w = torch.randn(O_, I_, generator=g) * 0.02
+    w[0, :gs] = 0.0  # zero group -> fp16(1e-7) scale
+    w[1, :gs] = torch.arange(gs) - gs / 2  # exact halves: ties to even
+    if O_ > 2:
+        w[2, :gs] = torch.linspace(-1e-9, 1e-9, gs)  # tiny group: scale clamped at 1e-7
+    q_ref, s_ref = O.quantize(w.numpy(), bits, gs)
+    wd = w.to(dev)
+    q = torch.empty(q_ref.shape, dtype=torch.uint8 if bits == 4 else torch.int8, device=dev)
+    s = torch.empty(s_ref.shape, dtype=torch.float16, device=dev)
+    _lib.call("moehip_quantize", wd.data_ptr(), O_, I_, bits, gs, q.data_ptr(), s.data_ptr(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
+    assert np.array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
+
+
+@pytest.mark.parametrize("prec", ["int4", "int8", "fp16", "bf16", "fp32", "fp8"])
+def test_encode_record_bit_exact(dev, prec):
+    H, I = 256, 128
+    g = torch.Generator().manual_seed(7)
+    gu, dn = torch.randn(2 * I, H, generator=g) * 0.05, torch.randn(H, I, generator=g) * 0.05
+    lay = record_layout(prec, H, I, 64, scale="absmax")
+    blob = torch.empty(lay["record_bytes"], dtype=torch.uint8, device=dev)
+    encode_record_(lay, blob, gu.to(dev), dn.to(dev))
+    ref = O.encode_record(O.record_layout(prec, H, I, 64, scale="absmax"), gu.numpy(), dn.numpy(), method="absmax")
+    assert np.array_equal(blob.cpu().numpy(), ref)
+
+
+# ---------------------------------------------------------------------------------------
+# single-matrix GEMV
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("O_,I_", [(64, 128), (96, 192), (2048, 2048), (100, 96)])
+def test_gemv_int4(dev, dtype, O_, I_):
+    g = torch.Generator().manual_seed(O_ * I_)
+    gs = O.pick_group_size(I_)
+    w = torch.randn(O_, I_, generator=g)
+    q, s = O.quantize(w.numpy(), 4, gs)
+    x = torch.randn(I_, generator=g).to(dtype)
+    ref = O.dequantize(q, s, 4, "float32").astype(np.float64) @ x.double().numpy()
+    y = K.gemv_int4(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), x.to(dev), gs)
+    assert y.dtype == dtype and y.shape == (O_,)
+    got = y.float().cpu().numpy()
+    tol = 1e-4 if dtype == torch.float32 else (2e-3 if dtype == torch.float16 else 1e-2)
+    assert np.abs(got - ref).max() / np.abs(ref).max() < tol
+
+
+# ---------------------------------------------------------------------------------------
+# grouped kernels through the moelab.kernels API (the reference's kernel test shapes)
+# ---------------------------------------------------------------------------------------
+SHAPES = [(64, 32), (96, 48), (512, 256), (256, 128)]
+
+
+@pytest.mark.parametrize("prec", ["int4", "int8", "fp16", "bf16", "fp32", "fp8"])
+@pytest.mark.parametrize("H,I", SHAPES)
+def test_grouped_ffn_matches_oracle_fp32(dev, prec, H, I):
+    """moelab tests/test_kernels.py:16-51: 3 experts, weights 0.5/0.3/0.2, out pre-filled 0.5
+    (the kernels ADD), fp32 activations, rel-err < 1e-4."""
+    lay, blobs, mats = make_records(prec, H, I, 3, H + I)
+    ws = [0.5, 0.3, 0.2]
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(H + I))
+    ref = O.moe_layer(x.numpy(), np.array([[0, 1, 2]]), np.array([ws]), lambda e: mats[e])
+    recs = to_dev(blobs, dev)
+    ents = [(views(lay, b), w) for b, w in zip(recs, ws)]
+    out = torch.full((1, H), 0.5, device=dev)
+    if prec == "int4":
+        K.grouped_ffn_int4(x.to(dev), ents, lay["group_sizes"], out)
+    elif prec == "int8":
+        K.grouped_ffn_int8(x.to(dev), ents, lay, out)
+    elif prec == "fp8":
+        K.grouped_ffn_fp8(x.to(dev), ents, out)
+    else:
+        K.grouped_ffn_float(x.to(dev), ents, out)
+    got = out.cpu().numpy() - 0.5
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err < 1e-4, (prec, H, I, err)
+
+
+@pytest.mark.parametrize("prec", ["int4", "int8", "fp16", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_grouped_olmoe_shape(dev, prec, dtype):
+    """scripts/check_setup.py:88-126 case: 8 experts at OLMoE dims (H=2048, I=1024),
+    W ~ 0.02 N(0,1), weights 0.125, x ~ N(0,1) in the model dtype."""
+    H, I, n = 2048, 1024, 8
+    lay, blobs, mats = make_records(prec, H, I, n, 11, std=0.02)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(12)).to(dtype)
+    ref = O.moe_layer(x.float().numpy(), np.array([list(range(n))]), np.full((1, n), 0.125), lambda e: mats[e])
+    recs = to_dev(blobs, dev)
+    ents = [(views(lay, b), 0.125) for b in recs]
+    out = torch.zeros(1, H, dtype=dtype, device=dev)
+    if prec == "int4":
+        K.grouped_ffn_int4(x.to(dev), ents, lay["group_sizes"], out)
+    elif prec == "int8":
+        K.grouped_ffn_int8(x.to(dev), ents, lay, out)
+    elif prec == "fp8":
+        K.grouped_ffn_fp8(x.to(dev), ents, out)
+    else:
+        K.grouped_ffn_float(x.to(dev), ents, out)
+    assert_layer_close(out.float().cpu().numpy(), ref, dtype)
+
+
+def test_grouped_weight_zero_rows_skipped_and_deterministic(dev):
+    H, I = 512, 256
+    lay, blobs, mats = make_records("int4", H, I, 4, 3)
+    recs = to_dev(blobs, dev)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(1)).to(dev)
+    ws = [0.4, 0.0, 0.35, 0.25]
+    ents = [(views(lay, b), w) for b, w in zip(recs, ws)]
+    outs = []
+    for _ in range(3):
+        out = torch.zeros(1, H, device=dev)
+        K.grouped_ffn_int4(x, ents, lay["group_sizes"], out)
+        outs.append(out.cpu())
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])  # bitwise: table-order combine
+    ref = O.moe_layer(x.cpu().numpy(), np.array([[0, 2, 3]]), np.array([[0.4, 0.35, 0.25]]), lambda e: mats[e])
+    assert np.abs(outs[0].numpy() - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def test_expert_ffn_int4(dev):
+    H, I = 256, 128
+    lay, blobs, mats = make_records("int4", H, I, 1, 5)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(2))
+    ref = O.expert_ffn(x.numpy(), *mats[0])
+    y = K.expert_ffn_int4(x.to(dev), views(lay, to_dev(blobs, dev)[0]), lay["group_sizes"], torch.nn.functional.silu)
+    assert np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def test_grouped_graph_replays(dev):
+    """GroupedGraph captured once, replayed with different tables: every replay equals the
+    eager result, with eager work and syncs between replays."""
+    H, I, k = 512, 256, 4
+    lay4, b4, m4 = make_records("int4", H, I, 6, 21)
+    lay16, b16, m16 = make_records("fp16", H, I, 6, 22)
+    r4, r16 = to_dev(b4, dev), to_dev(b16, dev)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(3)).to(dev)
+    out = torch.zeros(1, H, device=dev)
+    gg = K.GroupedGraph({"fp16": lay16, "int4": lay4}, x, out, k)
+    rng = np.random.default_rng(0)
+    for step in range(5):
+        e16 = rng.choice(6, 1 + step % 2, replace=False)
+        e4 = rng.choice(6, 2, replace=False)
+        w16 = rng.random(len(e16)).astype(np.float32)
+        w4 = rng.random(2).astype(np.float32)
+        cpu = torch.randn(1, H, generator=torch.Generator().manual_seed(step)).to(dev) if step % 2 else None
+        gg.run({"fp16": [(r16[e], float(w)) for e, w in zip(e16, w16)],
+                "int4": [(r4[e], float(w)) for e, w in zip(e4, w4)]}, cpu)
+        torch.cuda.synchronize()
+        ref = O.moe_layer(x.cpu().numpy(), np.array([list(e16)]), np.array([w16]), lambda e: m16[e])
+        ref += O.moe_layer(x.cpu().numpy(), np.array([list(e4)]), np.array([w4]), lambda e: m4[e])
+        if cpu is not None:
+            ref += cpu.cpu().numpy()
+        err = np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err < 1e-4, (step, err)
+        _ = (x * 2).sum().item()  # eager work + sync between replays
+    assert gg.graph is not None and gg.replays == 4
+
+
+# ---------------------------------------------------------------------------------------
+# router
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("T,E,k,renorm", [(1, 64, 8, False), (33, 64, 8, False), (8, 128, 8, True),
+                                          (32, 512, 10, True), (5, 16, 4, True)])
+def test_router_topk(dev, dtype, T, E, k, renorm):
+    H = 2048
+    g = torch.Generator().manual_seed(T * E + k)
+    x = torch.randn(T, H, generator=g).to(dtype)
+    W = (torch.randn(E, H, generator=g) * 0.02).to(dtype)
+    lo, oi, ow, _ = O.router(x.float().numpy(), W.float().numpy(), k, renorm, NPDT[dtype])
+    xd, Wd = x.to(dev), W.to(dev)
+    logits = torch.empty(T, E, dtype=dtype, device=dev)
+    idx = torch.empty(T, k, dtype=torch.int64, device=dev)
+    w = torch.empty(T, k, dtype=dtype, device=dev)
+    w32 = torch.empty(T, k, dtype=torch.float32, device=dev)
+    _lib.call("moehip_router_topk", xd.data_ptr(), Wd.data_ptr(), T, H, E, k, int(renorm), _lib.dt_code(dtype),
+              logits.data_ptr(), idx.data_ptr(), w.data_ptr(), w32.data_ptr(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    gl = logits.float().cpu().numpy()
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    # logits: one rounding of an fp32 sum vs one rounding of the exact sum -> within 1 ulp
+    assert np.all(np.abs(gl - lo) <= ulp * np.exp2(np.floor(np.log2(np.abs(lo) + 1e-30))) + 1e-7)
+    same_logits = np.array_equal(gl, lo)
+    gi = idx.cpu().numpy()
+    kth = -np.sort(-lo, axis=-1)[:, k - 1]
+    clear = O.topk_margin(lo, k) > 2 * ulp * np.exp2(np.floor(np.log2(np.abs(kth) + 1e-30)))
+    for t in range(T):
+        if same_logits or clear[t]:
+            assert gi[t].tolist() == oi[t].tolist(), t  # bit-exact indices, same order
+    if same_logits:
+        assert np.array_equal(gi, oi)
+    gw = w32.cpu().numpy()
+    assert np.allclose(gw[clear], ow[clear], rtol=2 * ulp, atol=1e-6)
+    assert np.array_equal(w.float().cpu().numpy(), gw)
+
+
+def test_router_planted_ties(dev):
+    """Equal logits: the lowest expert index wins, as in the oracle."""
+    H, E = 64, 16
+    W = torch.zeros(E, H)
+    W[:, 0] = torch.tensor([0.1, 0.9, 0.5, 0.2, 0.3, 0.5, 0.4, 0.4, 0.0, 0.5, 0.1, 0.2, 0.3, 0.4, 0.9, 0.0])
+    x = torch.zeros(1, H)
+    x[0, 0] = 1.0
+    for k in (2, 3, 4, 6):
+        _, oi, _, _ = O.router(x.numpy(), W.numpy(), k, False, "float16")
+        logits = torch.empty(1, E, dtype=torch.float16, device=dev)
+        idx = torch.empty(1, k, dtype=torch.int64, device=dev)
+        w32 = torch.empty(1, k, device=dev)
+        _lib.call("moehip_router_topk", x.half().to(dev).data_ptr(), W.half().to(dev).data_ptr(), 1, H, E, k, 0, 0,
+                  logits.data_ptr(), idx.data_ptr(), None, w32.data_ptr(), _lib.stream_of(dev))
+        torch.cuda.synchronize()
+        assert idx.cpu().numpy()[0].tolist() == oi[0].tolist()
+
+
+# ---------------------------------------------------------------------------------------
+# HOBBIT decision + table, dispatch
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("pol_kw", [dict(mode="hobbit", t1=0.6), dict(mode="hobbit", t1=0.3, t_mid=0.7, t2=0.9),
+                                    dict(mode="hi"), dict(mode="lo"), dict(mode="hobbit", t1=0.5, upgrade=False)])
+def test_decide_table_matches_policy(dev, pol_kw):
+    precs = ["fp16", "int8", "int4"]
+    P, E, k = 3, 32, 8
+    g = np.random.default_rng(5)
+    pol = PrecisionPolicy(**pol_kw)
+    ref = O.Policy(**{kk: v for kk, v in pol_kw.items() if kk != "upgrade"})
+    resident = g.random((P, E)) < 0.7
+    rtab = torch.from_numpy(np.where(resident, (np.arange(P * E).reshape(P, E) + 1) * 4096 * 1024, 0).astype(np.int64))
+    offs = torch.tensor([[0, 8, 16, 24], [0, 64, 128, 192], [0, 32, 64, 96]], dtype=torch.int64)
+    planned = torch.tensor([1, 1, 1], dtype=torch.int32)
+    lv2p = (ctypes.c_int * 3)(0, 1, 2)
+    for trial in range(20):
+        idx = g.choice(E, k, replace=False)
+        w = (g.random(k) ** 2).astype(np.float32)
+        tab = torch.zeros(P, k, 4, dtype=torch.int64, device=dev)
+        wtab = torch.zeros(P, k, device=dev)
+        info = torch.zeros(3, k, device=dev)
+        miss = torch.zeros(1, device=dev)
+        _lib.call("moehip_decide_table", torch.from_numpy(idx).to(dev).data_ptr(),
+                  torch.from_numpy(w).to(dev).data_ptr(), k, ctypes.byref(pol.device_policy(2)), lv2p,
+                  rtab.to(dev).data_ptr(), P, E, offs.to(dev).data_ptr(), planned.to(dev).data_ptr(), tab.data_ptr(),
+                  wtab.data_ptr(), info.data_ptr(), miss.data_ptr(), _lib.stream_of(dev))
+        torch.cuda.synchronize()
+        lvl, skip = ref.levels(2, w[None])
+        lvl, skip = lvl[0], skip[0]
+        exp_ch = []
+        for j in range(k):
+            req = lvl[j]
+            ch = -1
+            for pi in reversed(range(P)):
+                if resident[pi, idx[j]] and ((req >= pi) if pol.allow_upgrade else (req == pi)):
+                    ch = pi
+            exp_ch.append(ch)
+        inf = info.cpu().numpy()
+        assert inf[0].tolist() == idx.astype(np.float32).tolist()
+        assert inf[2].tolist() == lvl.astype(np.float32).tolist()
+        assert inf[1].tolist() == [(-2.0 if skip[j] else float(exp_ch[j])) for j in range(k)]
+        assert miss.item() == sum(1 for j in range(k) if not skip[j] and exp_ch[j] < 0)
+        tb, wt = tab.cpu().numpy(), wtab.cpu().numpy()
+        for j in range(k):
+            for pi in range(P):
+                sel = exp_ch[j] == pi and not skip[j]
+                exp_row = (rtab[pi, idx[j]].item() + offs[pi]).numpy() if sel else np.zeros(4, np.int64)
+                assert np.array_equal(tb[pi, j], exp_row)
+                assert wt[pi, j] == (w[j] if sel else 0.0)
+
+
+@pytest.mark.parametrize("T,k,E,with_skip", [(1, 8, 64, False), (8, 8, 64, True), (32, 10, 512, False),
+                                             (512, 8, 128, True), (1000, 8, 1024, False), (3, 2, 4, True)])
+def test_dispatch_bit_exact(dev, T, k, E, with_skip):
+    g = np.random.default_rng(T + k + E)
+    idx = np.stack([g.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+    skip = (g.random((T, k)) < 0.25) if with_skip else None
+    se, sp, counts, offsets = O.dispatch(idx, E, skip)
+    NP = T * k
+    c = torch.empty(E, dtype=torch.int32, device=dev)
+    o = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    s = torch.empty(NP, dtype=torch.int32, device=dev)
+    r = torch.empty(NP, dtype=torch.int32, device=dev)
+    sk = torch.from_numpy(skip.astype(np.uint8)).to(dev) if skip is not None else None
+    _lib.call("moehip_dispatch", torch.from_numpy(idx).to(dev).data_ptr(), _lib.ptr(sk), T, k, E, c.data_ptr(),
+              o.data_ptr(), s.data_ptr(), r.data_ptr(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(c.cpu().numpy(), counts)
+    assert np.array_equal(o.cpu().numpy(), offsets)
+    got_s = s.cpu().numpy()
+    assert np.array_equal(got_s[:len(sp)], sp) and (got_s[len(sp):] == -1).all()
+    rank = r.cpu().numpy()
+    exp_rank = np.full(NP, -1)
+    exp_rank[sp] = np.arange(len(sp))
+    assert np.array_equal(rank, exp_rank)
+
+
+# ---------------------------------------------------------------------------------------
+# the whole decode layer (router -> HOBBIT -> kernels -> combine) at OLMoE shape
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", ["lo", "hobbit"])
+def test_decoder_layer_olmoe(dev, mode):
+    H, I, E, k, L = 2048, 1024, 64, 8, 2
+    dtype = torch.float16
+    g = torch.Generator().manual_seed(100)
+    precs = ["fp16", "int4"] if mode == "hobbit" else ["int4"]
+    layouts = {p: record_layout(p, H, I, 64, scale="absmax") for p in precs}
+    store = ResidentStore(layouts, L, E, dev)
+    weights = {}
+    for l in range(L):
+        for e in range(E):
+            gu = torch.randn(2 * I, H, generator=g) * 0.02
+            dn = torch.randn(H, I, generator=g) * 0.02
+            weights[(l, e)] = (gu, dn)
+            for p in precs:
+                store.encode(p, l, e, gu.to(dev), dn.to(dev))
+    Wr = [(torch.randn(E, H, generator=g) * 0.02).to(dtype) for _ in range(L)]
+    pol = PrecisionPolicy(mode, t1=0.5, upgrade=False)
+    dec = MoEDecoder(store, k, pol, dtype, router_weights=[w.to(dev) for w in Wr])
+    for l in range(L):
+        x = torch.randn(1, H, generator=g).to(dtype)
+        out = torch.zeros(1, H, dtype=dtype, device=dev)
+        dec.layer(l, x.to(dev), out)
+        torch.cuda.synchronize()
+        lo, idx, w, w32 = O.router(x.float().numpy(), Wr[l].float().numpy(), k, False, "float16")
+        assert dec.idx.cpu().numpy().tolist() == idx.tolist()
+        rpol = O.Policy(mode, t1=0.5)
+        lvl, _ = rpol.levels(l, w)
+        layer_of = {}
+        for j in range(k):
+            p = O.level_to_precision(int(lvl[0, j]), precs)
+            gu, dn = weights[(l, int(idx[0, j]))]
+            lay = O.record_layout(p, H, I, 64, scale="absmax")
+            layer_of[int(idx[0, j])] = O.materialize(lay, O.encode_record(lay, gu.numpy(), dn.numpy(), "absmax"))
+        ref = O.moe_layer(x.float().numpy(), idx, w, lambda e: layer_of[e])
+        assert_layer_close(out.float().cpu().numpy(), ref, dtype)
+    assert dec.miss.item() == 0
