@@ -6,13 +6,16 @@ Workload (the OLMoE-shaped 16-layer MoE stack at batch 1, all experts int4 gs64 
 d_model 2048, 64 experts per layer, softmax router top-8 without renormalisation, SwiGLU d_ff
 1024, router weights and expert weights N(0, 0.02) (experts quantised int4 gs64 absmax on the
 GPU with moelab's packing), fp16 hidden states N(0, 1), one seeded state per (token, layer).
-A step = one decode token through the 16 MoE layers: per layer router -> HOBBIT table ->
-kernel A -> kernel B -> combine, all on the GPU, replayed as one HIP graph per token. 16 x 64 int4
+A step = one decode token through the 16 MoE layers: per layer ONE launch of the fused kernel
+(router -> HOBBIT table -> gate/up rows -> down rows -> ordered combine), replayed as one HIP
+graph per token. 16 x 64 int4
 records = 3.42 GB, far above the 256 MB Infinity Cache, and each token routes differently.
 
-Roofline: the dominant kernel is kernel A (gate/up GEMV over the 8 routed records); its
-algorithmic bytes per launch = 8 x (gate_up.q + gate_up.s) + x + h, its duration is measured live
-with HIP events on the stream it runs on, over launches that rotate through all layers.
+Roofline: the dominant (only) kernel is the fused decode-layer kernel, one launch per layer; its
+algorithmic bytes per launch = 8 routed int4 records (3,342,336 B each: gate_up.q/.s, down.q/.s)
++ router weights (64 x 2048 fp16) + x and out (fp16) = 27,009,024 B; its duration is measured
+live with HIP events on the stream it runs on, over launches that rotate through all tokens and
+layers.
 
 CPU baseline: the oracle's restatement of moelab's CPU expert branch (dequantise to fp32,
 F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workload, host cores.
@@ -64,7 +67,6 @@ def gpu_bench(args):
     import torch
 
     from moelab_hip import _lib
-    from moelab_hip.kernels import _Plan
 
     dev = torch.device("cuda:0")
     _lib.check_device(dev)
@@ -111,49 +113,29 @@ def gpu_bench(args):
     ms_step = ms_total / args.steps
     log(f"[bench] {args.steps} tokens x {L} layers: {ms_step * 1000:.1f} us/token ({wall:.2f} s wall)")
 
-    # --- dominant kernel (A) timed live with HIP events on its stream -------------------
-    # routing tables for every (token, layer) are prepared first, then kernel A alone is
-    # launched back to back, rotating over tokens and layers, between two events.
-    plan: _Plan = dec.plans[0]
-    tabs, wts = [], []
-    for s in range(S):
-        for l in range(L):
-            dec.layer(l, xs[s, l], outs[s, l])
-            tabs.append(dec.tab[0].clone())
-            wts.append(dec.wtab[0].clone())
-    torch.cuda.synchronize()
-    h = torch.empty(K_TOP, I, dtype=torch.float32, device=dev)
-    acc = torch.empty(H, dtype=torch.float32, device=dev)
-    nA = len(tabs)
-    reps = max(1, args.kernel_launches // nA)
+    # --- the layer kernel timed live with HIP events on its stream -----------------------
+    # one fused launch per layer: back-to-back eager launches rotating over every (token,
+    # layer), bracketed by two events on the stream the kernel runs on.
     st = torch.cuda.current_stream(dev)
+    nA = S * L
+    reps = max(1, args.kernel_launches // nA)
     for j in range(nA):
-        plan.up(K_TOP, tabs[j], wts[j], xs[j // L, j % L], h, acc, zero=False)
+        dec.layer(j % L, xs[j // L, j % L], outs[j // L, j % L])
+    torch.cuda.synchronize()
     ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     ea.record(st)
     for _ in range(reps):
         for j in range(nA):
-            plan.up(K_TOP, tabs[j], wts[j], xs[j // L, j % L], h, acc, zero=False)
+            dec.layer(j % L, xs[j // L, j % L], outs[j // L, j % L])
     eb.record(st)
     torch.cuda.synchronize()
-    upA_us = ea.elapsed_time(eb) * 1000 / (reps * nA)
-    # kernel B (+ its ordered reduce) the same way
-    part = plan.partial(K_TOP, dev)
-    ea.record(st)
-    for _ in range(reps):
-        for j in range(nA):
-            plan.down(K_TOP, tabs[j], wts[j], h, acc)
-    eb.record(st)
-    torch.cuda.synchronize()
-    downB_us = ea.elapsed_time(eb) * 1000 / (reps * nA)
+    kern_us = ea.elapsed_time(eb) * 1000 / (reps * nA)
+    dec.check_error()
 
     gu_bytes = 2 * I * (H // 2) + 2 * I * (H // 64) * 2  # gate_up.q + gate_up.s of one record
     dn_bytes = H * (I // 2) + H * (I // 64) * 2
     rec_bytes = gu_bytes + dn_bytes
-    bytes_A = K_TOP * gu_bytes + H * 2 + K_TOP * I * 4
     layer_alg = K_TOP * rec_bytes + E * H * 2 + 2 * H * 2  # experts + router + x/out
-    achieved_A = bytes_A / (upA_us * 1e-6) / 1e9
     tok_s = 1000.0 / ms_step
     layer_us = ms_step * 1000 / L
     return {
@@ -161,10 +143,9 @@ def gpu_bench(args):
         "layer_tok_s": tok_s * L,
         "expert_gbs": K_TOP * rec_bytes / (layer_us * 1e-6) / 1e9,
         "layer_alg_gbs": layer_alg / (layer_us * 1e-6) / 1e9,
-        "kernelA_us": upA_us, "kernelB_us": downB_us,
-        "kernelA_bytes": bytes_A, "kernelA_gbs": achieved_A,
-        "kernelB_gbs": (K_TOP * dn_bytes + K_TOP * I * 4 + K_TOP * H * 4) / (downB_us * 1e-6) / 1e9,
-        "layer_bytes": layer_alg, "record_bytes": rec_bytes,
+        "kernel_us": kern_us, "kernel_bytes": layer_alg,
+        "kernel_gbs": layer_alg / (kern_us * 1e-6) / 1e9,
+        "record_bytes": rec_bytes, "fused": dec.fused,
     }
 
 
@@ -245,11 +226,12 @@ def main():
         "layer_us": round(r["layer_us"], 3),
         "expert_gbs_ref_definition": round(r["expert_gbs"], 1),
         "layer_alg_gbs": round(r["layer_alg_gbs"], 1),
-        "kernels_us": {"A_gate_up": round(r["kernelA_us"], 3), "B_down_plus_reduce": round(r["kernelB_us"], 3)},
+        "kernel_us": round(r["kernel_us"], 3),
         "roofline": {
-            "bound": "hbm", "achieved": round(r["kernelA_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(r["kernelA_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_up<int4> (grouped gate/up GEMV, 8 records)", "bytes_per_launch": r["kernelA_bytes"],
+            "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_decode_layer<f16> (router + HOBBIT table + 8 int4 experts + combine, one launch)",
+            "bytes_per_launch": r["kernel_bytes"],
         },
         "cpu_baseline": cpu,
         "torch": torch.__version__,

@@ -112,9 +112,9 @@ int moehip_router_topk(const void *x, const void *Wr, int T, int H, int E, int k
 /* HOBBIT policy parameters (moelab/policy.py:50-58); t_mid/t2 < 0 mean "None". */
 typedef struct moehip_policy {
     int mode;   /* 0 = hobbit, 1 = hi, 2 = lo */
-    float t1;   /* already resolved for the layer (t1_for(layer)) */
-    float t_mid;
-    float t2;
+    float t1;    /* t1_for(layer) + 1e-6 rounded to fp32 (the slack of policy.py:120-122) */
+    float t_mid; /* t_mid + 1e-6, or < 0 */
+    float t2;    /* t2 + 1e-6, or < 0 */
     int protect; /* 1 if the layer is protected (level 0) */
     int upgrade; /* allow_upgrade: a more precise resident copy may serve the request */
 } moehip_policy;
@@ -153,6 +153,54 @@ int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E
  * low nibble = even column; bits = 8 -> q (O, I) i8. s (O, I/gs) f16. gs even, gs <= 64.
  */
 int moehip_quantize(const float *w, int O, int I, int bits, int gs, void *q, void *s, void *stream);
+
+/* Static description of one MoE layer for the fused decode kernel. Precision index p follows
+ * the store's order (most precise first, moelab/store.py `precisions`). */
+typedef struct moehip_layer_desc {
+    int P;              /* number of record precisions (1..4) */
+    int E, k, H, I;     /* experts, top-k, d_model, d_ff */
+    int dtype;          /* activation dtype (MOEHIP_DT_*) */
+    int renorm;         /* norm_topk_prob */
+    int prec[4];        /* MOEHIP_PREC_* of precision index p */
+    int gs_up[4];       /* group size of gate_up / down for int records */
+    int gs_dn[4];
+    int planned[4];     /* 1 = kernels run for this precision */
+    int lv2p[3];        /* HOBBIT level -> precision index (moelab/policy.py:188-192) */
+    int64_t offs[4][4]; /* byte offsets of [gate_up.q, gate_up.s, down.q, down.s] in a record */
+    moehip_policy pol;
+} moehip_layer_desc;
+
+/*
+ * One MoE layer for ONE decode token in a single launch: router logits (x Wr^T, or the given
+ * idx_in / w32_in when Wr is NULL), softmax / top-k / renorm, HOBBIT levels + choice of the
+ * resident copy + kernel tables (as moehip_decide_table), kernel-A and kernel-B rows of every
+ * chosen record, and out = sum over the table in table order (+ add) (+ out if accumulate), cast
+ * to the activation dtype. Optional readouts: logits_out (E), idx_out/w_out/w32_out (k),
+ * info (3, k) and miss (+= number of missing experts), as in moehip_router_topk /
+ * moehip_decide_table. rtab (P, E) holds the base address of each resident record of this layer.
+ * `ws` is caller-owned scratch of moehip_decode_layer_workspace_bytes() bytes, 256-B aligned and
+ * zeroed once before its first use; every launch leaves it ready for the next. Launches sharing a
+ * workspace must not overlap (one workspace per stream). grid = number of workgroups (0 = one per
+ * work item). H, I multiples of 32, H <= 8192, I <= 4096, E <= 1024, k <= 32.
+ * Replaces, for decode, the whole moelab/runtime.py:523-770 `run_layer` GPU path when every
+ * expert is resident (the A5 whole-token path, moelab/fullgraph.py:149-188 + graphs.py:351-426).
+ */
+int moehip_decode_layer(const moehip_layer_desc *desc, const void *x, const void *Wr, const int64_t *idx_in,
+                        const float *w32_in, const int64_t *rtab, void *out, const void *add, int accumulate,
+                        void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info, float *miss,
+                        void *ws, size_t ws_bytes, int grid, void *stream);
+size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H, int I);
+/* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device). */
+int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
+
+/*
+ * Checkpoint-style FP8 block quantisation of w (O, I) fp32: per 128 x 128 block
+ * scale = amax / 448 (1.0 for an all-zero block), q (O, I) = e4m3fn(w / scale) (round to
+ * nearest even, saturating at 448), s (ceil(O/128), ceil(I/128)) fp32 — the
+ * `weight_scale_inv` that moelab/quant.py:208-219 multiplies back (fixture rule of moelab
+ * tests/conftest.py:52-75). Builds "fp8" records; no counterpart kernel in the reference.
+ */
+int moehip_quantize_fp8_block(const float *w, int O, int I, void *q, float *s, void *stream);
 
 #ifdef __cplusplus
 }

@@ -46,24 +46,27 @@ __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
-// load one activation element of dtype dt as fp32
-__device__ __forceinline__ float load_act(const void *p, size_t i, int dt) {
-    if (dt == MOEHIP_DT_F16) return f16_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
-    if (dt == MOEHIP_DT_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
-    return reinterpret_cast<const float *>(p)[i];
+// typed activation access: DT is a compile-time MOEHIP_DT_* code, so kernels carry no runtime
+// dtype switches (each instantiation is straight-line code for one dtype)
+template <int DT>
+__device__ __forceinline__ float ld_act(const void *p, size_t i) {
+    if constexpr (DT == MOEHIP_DT_F16) return f16_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+    else if constexpr (DT == MOEHIP_DT_BF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(p)[i]);
+    else return reinterpret_cast<const float *>(p)[i];
 }
 
-__device__ __forceinline__ void store_act(void *p, size_t i, int dt, float v) {
-    if (dt == MOEHIP_DT_F16) reinterpret_cast<uint16_t *>(p)[i] = f32_to_f16_rne(v);
-    else if (dt == MOEHIP_DT_BF16) reinterpret_cast<uint16_t *>(p)[i] = f32_to_bf16_rne(v);
+template <int DT>
+__device__ __forceinline__ void st_act(void *p, size_t i, float v) {
+    if constexpr (DT == MOEHIP_DT_F16) reinterpret_cast<uint16_t *>(p)[i] = f32_to_f16_rne(v);
+    else if constexpr (DT == MOEHIP_DT_BF16) reinterpret_cast<uint16_t *>(p)[i] = f32_to_bf16_rne(v);
     else reinterpret_cast<float *>(p)[i] = v;
 }
 
-// value of element dt rounded through dtype dt (fp32 -> dt -> fp32)
-__device__ __forceinline__ float round_act(float v, int dt) {
-    if (dt == MOEHIP_DT_F16) return f16_to_f32(f32_to_f16_rne(v));
-    if (dt == MOEHIP_DT_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
-    return v;
+template <int DT>
+__device__ __forceinline__ float rnd_act(float v) {
+    if constexpr (DT == MOEHIP_DT_F16) return f16_to_f32(f32_to_f16_rne(v));
+    else if constexpr (DT == MOEHIP_DT_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
+    else return v;
 }
 
 // OCP e4m3fn byte -> fp32 (gfx950's fp8 conversion is the OCP format)

@@ -18,161 +18,17 @@
 // Determinism: kernel B writes per-expert partial rows; the reduce kernel adds them in table
 // order (moelab's v1 kernel order, kernels.py:132-146), so results do not depend on scheduling.
 
-#include "common.hpp"
+#include "gemv_core.hpp"
 
 namespace moehip {
-
-template <int PREC> struct Fmt;
-template <> struct Fmt<MOEHIP_PREC_INT4> { static constexpr int VPC = 32; };
-template <> struct Fmt<MOEHIP_PREC_INT8> { static constexpr int VPC = 16; };
-template <> struct Fmt<MOEHIP_PREC_F16> { static constexpr int VPC = 8; };
-template <> struct Fmt<MOEHIP_PREC_BF16> { static constexpr int VPC = 8; };
-template <> struct Fmt<MOEHIP_PREC_F32> { static constexpr int VPC = 4; };
-template <> struct Fmt<MOEHIP_PREC_FP8> { static constexpr int VPC = 16; };
-
-static inline int vpc_of(int prec) {
-    switch (prec) {
-        case MOEHIP_PREC_INT4: return 32;
-        case MOEHIP_PREC_INT8: return 16;
-        case MOEHIP_PREC_F16: return 8;
-        case MOEHIP_PREC_BF16: return 8;
-        case MOEHIP_PREC_F32: return 4;
-        case MOEHIP_PREC_FP8: return 16;
-    }
-    return 0;
-}
-
-// ---------------------------------------------------------------------------------------
-// chunk dot products: sum over the chunk's VPC values of weight * v (int formats unscaled)
-// ---------------------------------------------------------------------------------------
-template <int PREC>
-__device__ __forceinline__ float chunk_dot(const uint4 q, const float *v, float vsum);
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_INT4>(const uint4 q, const float *v, float vsum) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t lo = d[j] & 0x0F0F0F0Fu;         // even columns 0,2,4,6 of this dword
-        const uint32_t hi = (d[j] >> 4) & 0x0F0F0F0Fu;  // odd columns 1,3,5,7
-        a0 = fmaf((float)(lo & 0xffu), v[8 * j + 0], a0);
-        a1 = fmaf((float)(hi & 0xffu), v[8 * j + 1], a1);
-        a0 = fmaf((float)((lo >> 8) & 0xffu), v[8 * j + 2], a0);
-        a1 = fmaf((float)((hi >> 8) & 0xffu), v[8 * j + 3], a1);
-        a0 = fmaf((float)((lo >> 16) & 0xffu), v[8 * j + 4], a0);
-        a1 = fmaf((float)((hi >> 16) & 0xffu), v[8 * j + 5], a1);
-        a0 = fmaf((float)(lo >> 24), v[8 * j + 6], a0);
-        a1 = fmaf((float)(hi >> 24), v[8 * j + 7], a1);
-    }
-    return (a0 + a1) - 8.0f * vsum;
-}
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_INT8>(const uint4 q, const float *v, float vsum) {
-    const uint32_t d[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // byte b holds q + 128 as an unsigned value
-        a0 = fmaf((float)(d[j] & 0xffu), v[4 * j + 0], a0);
-        a1 = fmaf((float)((d[j] >> 8) & 0xffu), v[4 * j + 1], a1);
-        a0 = fmaf((float)((d[j] >> 16) & 0xffu), v[4 * j + 2], a0);
-        a1 = fmaf((float)(d[j] >> 24), v[4 * j + 3], a1);
-    }
-    return (a0 + a1) - 128.0f * vsum;
-}
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_F16>(const uint4 q, const float *v, float) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        a0 = fmaf(f16_to_f32(d[j] & 0xffffu), v[2 * j + 0], a0);
-        a1 = fmaf(f16_to_f32(d[j] >> 16), v[2 * j + 1], a1);
-    }
-    return a0 + a1;
-}
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_BF16>(const uint4 q, const float *v, float) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        a0 = fmaf(__uint_as_float(d[j] << 16), v[2 * j + 0], a0);
-        a1 = fmaf(__uint_as_float(d[j] & 0xffff0000u), v[2 * j + 1], a1);
-    }
-    return a0 + a1;
-}
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_F32>(const uint4 q, const float *v, float) {
-    float a = __uint_as_float(q.x) * v[0];
-    a = fmaf(__uint_as_float(q.y), v[1], a);
-    a = fmaf(__uint_as_float(q.z), v[2], a);
-    return fmaf(__uint_as_float(q.w), v[3], a);
-}
-
-template <>
-__device__ __forceinline__ float chunk_dot<MOEHIP_PREC_FP8>(const uint4 q, const float *v, float) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        a0 = fmaf(__builtin_amdgcn_cvt_f32_fp8((int)d[j], 0), v[4 * j + 0], a0);
-        a1 = fmaf(__builtin_amdgcn_cvt_f32_fp8((int)d[j], 1), v[4 * j + 1], a1);
-        a0 = fmaf(__builtin_amdgcn_cvt_f32_fp8((int)d[j], 2), v[4 * j + 2], a0);
-        a1 = fmaf(__builtin_amdgcn_cvt_f32_fp8((int)d[j], 3), v[4 * j + 3], a1);
-    }
-    return a0 + a1;
-}
-
-// scale of chunk c of row `row` (cols = row length in values)
-template <int PREC>
-__device__ __forceinline__ float chunk_scale(const uint8_t *sb, int row, int c, int cols, int gs) {
-    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) {
-        const int ng = cols / gs;
-        const int g = (c * Fmt<PREC>::VPC) / gs;
-        return f16_to_f32(reinterpret_cast<const uint16_t *>(sb)[(size_t)row * ng + g]);
-    } else if constexpr (PREC == MOEHIP_PREC_FP8) {
-        const int sc = (cols + 127) >> 7;
-        return reinterpret_cast<const float *>(sb)[(size_t)(row >> 7) * sc + ((c * 16) >> 7)];
-    } else {
-        return 1.0f;
-    }
-}
-
-// scalar weight (row, col) for the generic kernels
-template <int PREC>
-__device__ __forceinline__ float weight_at(const uint8_t *qb, const uint8_t *sb, int row, int col, int cols, int gs) {
-    if constexpr (PREC == MOEHIP_PREC_INT4) {
-        const uint32_t b = qb[(size_t)row * (cols >> 1) + (col >> 1)];
-        const int n = (int)((col & 1) ? (b >> 4) : (b & 15u)) - 8;
-        return (float)n * f16_to_f32(reinterpret_cast<const uint16_t *>(sb)[(size_t)row * (cols / gs) + col / gs]);
-    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
-        const int n = (int)(int8_t)qb[(size_t)row * cols + col];
-        return (float)n * f16_to_f32(reinterpret_cast<const uint16_t *>(sb)[(size_t)row * (cols / gs) + col / gs]);
-    } else if constexpr (PREC == MOEHIP_PREC_F16) {
-        return f16_to_f32(reinterpret_cast<const uint16_t *>(qb)[(size_t)row * cols + col]);
-    } else if constexpr (PREC == MOEHIP_PREC_BF16) {
-        return bf16_to_f32(reinterpret_cast<const uint16_t *>(qb)[(size_t)row * cols + col]);
-    } else if constexpr (PREC == MOEHIP_PREC_F32) {
-        return reinterpret_cast<const float *>(qb)[(size_t)row * cols + col];
-    } else {
-        const int sc = (cols + 127) >> 7;
-        return fp8_to_f32(qb[(size_t)row * cols + col]) *
-               reinterpret_cast<const float *>(sb)[(size_t)(row >> 7) * sc + (col >> 7)];
-    }
-}
 
 // ---------------------------------------------------------------------------------------
 // kernel A (fast path): h[e, r] = silu(gate_e[r] . x) * (up_e[r] . x)
 // grid (ceil(I / rows_per_block), n), block 256
 // ---------------------------------------------------------------------------------------
-template <int PREC, int CPL, int P>
+template <int PREC, int XDT, int CPL, int P>
 __global__ __launch_bounds__(256) void k_up(const int64_t *__restrict__ tab, const float *__restrict__ w,
-                                            const void *__restrict__ x, int xdt, float *__restrict__ h,
+                                            const void *__restrict__ x, float *__restrict__ h,
                                             float *__restrict__ acc_zero, int I, int H, int gs, int lg) {
     constexpr int VPC = Fmt<PREC>::VPC;
     const int e = blockIdx.y;
@@ -193,11 +49,12 @@ __global__ __launch_bounds__(256) void k_up(const int64_t *__restrict__ tab, con
     float vs[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const int c = cl + i * G;
+        const int c = min(cl + i * G, C - 1);  // lanes past the row read a valid chunk and drop it below
+        const size_t base = (size_t)c * VPC;
         float acc = 0.f;
 #pragma unroll
         for (int t = 0; t < VPC; ++t) {
-            const float val = (c < C) ? load_act(x, (size_t)c * VPC + t, xdt) : 0.f;
+            const float val = ld_act<XDT>(x, base + t);
             v[i][t] = val;
             acc += val;
         }
@@ -245,11 +102,11 @@ __global__ __launch_bounds__(256) void k_up(const int64_t *__restrict__ tab, con
 // kernel B (fast path): partial[e, j] = w[e] * (down_e[j] . h[e])   or, for a single matrix
 // (tab == nullptr), y[j] = W[j] . vec in dtype ydt.   grid (ceil(rows / rows_per_block), n)
 // ---------------------------------------------------------------------------------------
-template <int PREC, int CPL, int P>
+template <int PREC, int VDT, int CPL, int P>
 __global__ __launch_bounds__(256) void k_down(const int64_t *__restrict__ tab, const float *__restrict__ w,
                                               const uint8_t *__restrict__ q1, const uint8_t *__restrict__ s1,
-                                              const void *__restrict__ vec, int vdt, float *__restrict__ partial,
-                                              void *__restrict__ y, int ydt, int rows, int cols, int gs, int lg) {
+                                              const void *__restrict__ vec, float *__restrict__ partial,
+                                              void *__restrict__ y, int rows, int cols, int gs, int lg) {
     constexpr int VPC = Fmt<PREC>::VPC;
     const int e = blockIdx.y;
     const int tid = threadIdx.x;
@@ -274,11 +131,12 @@ __global__ __launch_bounds__(256) void k_down(const int64_t *__restrict__ tab, c
     float vs[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const int c = cl + i * G;
+        const int c = min(cl + i * G, C - 1);  // lanes past the row read a valid chunk and drop it below
+        const size_t base = voff + (size_t)c * VPC;
         float acc = 0.f;
 #pragma unroll
         for (int t = 0; t < VPC; ++t) {
-            const float val = (c < C) ? load_act(vec, voff + (size_t)c * VPC + t, vdt) : 0.f;
+            const float val = ld_act<VDT>(vec, base + t);
             v[i][t] = val;
             acc += val;
         }
@@ -312,7 +170,7 @@ __global__ __launch_bounds__(256) void k_down(const int64_t *__restrict__ tab, c
         const int r = rbase + p * RPW + slot;
         if (cl == 0 && r < rows) {
             if (tab != nullptr) partial[(size_t)e * rows + r] = we * acc;
-            else store_act(y, r, ydt, acc);
+            else st_act<VDT>(y, r, acc);
         }
     }
 }
@@ -320,9 +178,9 @@ __global__ __launch_bounds__(256) void k_down(const int64_t *__restrict__ tab, c
 // ---------------------------------------------------------------------------------------
 // generic kernels (any shape / group size): one wave per row, lanes stride over columns
 // ---------------------------------------------------------------------------------------
-template <int PREC>
+template <int PREC, int XDT>
 __global__ __launch_bounds__(256) void k_up_generic(const int64_t *__restrict__ tab, const float *__restrict__ w,
-                                                    const void *__restrict__ x, int xdt, float *__restrict__ h,
+                                                    const void *__restrict__ x, float *__restrict__ h,
                                                     float *__restrict__ acc_zero, int I, int H, int gs) {
     const int e = blockIdx.y;
     const int tid = threadIdx.x;
@@ -337,7 +195,7 @@ __global__ __launch_bounds__(256) void k_up_generic(const int64_t *__restrict__ 
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(tab[4 * e + 1]);
     float g = 0.f, u = 0.f;
     for (int c = lane; c < H; c += 64) {
-        const float xv = load_act(x, c, xdt);
+        const float xv = ld_act<XDT>(x, c);
         g = fmaf(weight_at<PREC>(qb, sb, r, c, H, gs), xv, g);
         u = fmaf(weight_at<PREC>(qb, sb, r + I, c, H, gs), xv, u);
     }
@@ -346,12 +204,11 @@ __global__ __launch_bounds__(256) void k_up_generic(const int64_t *__restrict__ 
     if (lane == 0) h[(size_t)e * I + r] = silu_mul(g, u);
 }
 
-template <int PREC>
+template <int PREC, int VDT>
 __global__ __launch_bounds__(256) void k_down_generic(const int64_t *__restrict__ tab, const float *__restrict__ w,
                                                       const uint8_t *__restrict__ q1, const uint8_t *__restrict__ s1,
-                                                      const void *__restrict__ vec, int vdt,
-                                                      float *__restrict__ partial, void *__restrict__ y, int ydt,
-                                                      int rows, int cols, int gs) {
+                                                      const void *__restrict__ vec, float *__restrict__ partial,
+                                                      void *__restrict__ y, int rows, int cols, int gs) {
     const int e = blockIdx.y;
     const int tid = threadIdx.x;
     float we = 1.f;
@@ -369,11 +226,11 @@ __global__ __launch_bounds__(256) void k_down_generic(const int64_t *__restrict_
     const int r = blockIdx.x * 4 + (tid >> 6);
     if (r >= rows) return;
     float acc = 0.f;
-    for (int c = lane; c < cols; c += 64) acc = fmaf(weight_at<PREC>(qb, sb, r, c, cols, gs), load_act(vec, voff + c, vdt), acc);
+    for (int c = lane; c < cols; c += 64) acc = fmaf(weight_at<PREC>(qb, sb, r, c, cols, gs), ld_act<VDT>(vec, voff + c), acc);
     acc = wave_sum(acc);
     if (lane == 0) {
         if (tab != nullptr) partial[(size_t)e * rows + r] = we * acc;
-        else store_act(y, r, ydt, acc);
+        else st_act<VDT>(y, r, acc);
     }
 }
 
@@ -388,14 +245,15 @@ __global__ __launch_bounds__(256) void k_reduce(const float *__restrict__ partia
     acc[j] += s;
 }
 
+template <int DT>
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ acc, const void *__restrict__ add,
-                                                 void *__restrict__ out, size_t N, int dt, int accumulate) {
+                                                 void *__restrict__ out, size_t N, int accumulate) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= N) return;
     float v = acc[i];
-    if (accumulate) v += load_act(out, i, dt);
-    if (add != nullptr) v += load_act(add, i, dt);
-    store_act(out, i, dt, v);
+    if (accumulate) v += ld_act<DT>(out, i);
+    if (add != nullptr) v += ld_act<DT>(add, i);
+    st_act<DT>(out, i, v);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -429,26 +287,12 @@ static RowPlan plan_rows(int prec, int cols, int gs, bool aligned) {
 constexpr int UP_P = 4;
 constexpr int DOWN_P = 4;
 
-template <int PREC>
-static void launch_up(const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
-                      const void *x, int xdt, float *h, float *acc_zero, int I, int H, int gs) {
-    switch (rp.cpl) {
-        case 1: hipLaunchKernelGGL((k_up<PREC, 1, UP_P>), grid, dim3(256), 0, st, tab, w, x, xdt, h, acc_zero, I, H, gs, rp.lg); break;
-        case 2: hipLaunchKernelGGL((k_up<PREC, 2, UP_P>), grid, dim3(256), 0, st, tab, w, x, xdt, h, acc_zero, I, H, gs, rp.lg); break;
-        default: hipLaunchKernelGGL((k_up<PREC, 4, UP_P>), grid, dim3(256), 0, st, tab, w, x, xdt, h, acc_zero, I, H, gs, rp.lg); break;
+#define MOEHIP_DT_SWITCH(dt, FN, ...)                                  \
+    switch (dt) {                                                      \
+        case MOEHIP_DT_F16: FN<MOEHIP_DT_F16>(__VA_ARGS__); break;      \
+        case MOEHIP_DT_BF16: FN<MOEHIP_DT_BF16>(__VA_ARGS__); break;    \
+        default: FN<MOEHIP_DT_F32>(__VA_ARGS__); break;                \
     }
-}
-
-template <int PREC>
-static void launch_down(const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
-                        const uint8_t *q1, const uint8_t *s1, const void *vec, int vdt, float *partial, void *y,
-                        int ydt, int rows, int cols, int gs) {
-    switch (rp.cpl) {
-        case 1: hipLaunchKernelGGL((k_down<PREC, 1, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, vdt, partial, y, ydt, rows, cols, gs, rp.lg); break;
-        case 2: hipLaunchKernelGGL((k_down<PREC, 2, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, vdt, partial, y, ydt, rows, cols, gs, rp.lg); break;
-        default: hipLaunchKernelGGL((k_down<PREC, 4, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, vdt, partial, y, ydt, rows, cols, gs, rp.lg); break;
-    }
-}
 
 #define MOEHIP_PREC_SWITCH(prec, FN, ...)                                  \
     switch (prec) {                                                        \
@@ -460,18 +304,61 @@ static void launch_down(const RowPlan &rp, dim3 grid, hipStream_t st, const int6
         default: FN<MOEHIP_PREC_FP8>(__VA_ARGS__); break;                  \
     }
 
-template <int PREC>
-static void launch_up_generic(dim3 grid, hipStream_t st, const int64_t *tab, const float *w, const void *x, int xdt,
-                              float *h, float *acc_zero, int I, int H, int gs) {
-    hipLaunchKernelGGL((k_up_generic<PREC>), grid, dim3(256), 0, st, tab, w, x, xdt, h, acc_zero, I, H, gs);
+template <int PREC, int XDT>
+static void launch_up_dt(const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
+                         const void *x, float *h, float *acc_zero, int I, int H, int gs) {
+    if (!rp.fast) {
+        hipLaunchKernelGGL((k_up_generic<PREC, XDT>), grid, dim3(256), 0, st, tab, w, x, h, acc_zero, I, H, gs);
+        return;
+    }
+    switch (rp.cpl) {
+        case 1: hipLaunchKernelGGL((k_up<PREC, XDT, 1, UP_P>), grid, dim3(256), 0, st, tab, w, x, h, acc_zero, I, H, gs, rp.lg); break;
+        case 2: hipLaunchKernelGGL((k_up<PREC, XDT, 2, UP_P>), grid, dim3(256), 0, st, tab, w, x, h, acc_zero, I, H, gs, rp.lg); break;
+        default: hipLaunchKernelGGL((k_up<PREC, XDT, 4, UP_P>), grid, dim3(256), 0, st, tab, w, x, h, acc_zero, I, H, gs, rp.lg); break;
+    }
 }
 
 template <int PREC>
-static void launch_down_generic(dim3 grid, hipStream_t st, const int64_t *tab, const float *w, const uint8_t *q1,
-                                const uint8_t *s1, const void *vec, int vdt, float *partial, void *y, int ydt,
-                                int rows, int cols, int gs) {
-    hipLaunchKernelGGL((k_down_generic<PREC>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, vdt, partial, y, ydt,
-                       rows, cols, gs);
+static void launch_up(int xdt, const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
+                      const void *x, float *h, float *acc_zero, int I, int H, int gs) {
+    switch (xdt) {
+        case MOEHIP_DT_F16: launch_up_dt<PREC, MOEHIP_DT_F16>(rp, grid, st, tab, w, x, h, acc_zero, I, H, gs); break;
+        case MOEHIP_DT_BF16: launch_up_dt<PREC, MOEHIP_DT_BF16>(rp, grid, st, tab, w, x, h, acc_zero, I, H, gs); break;
+        default: launch_up_dt<PREC, MOEHIP_DT_F32>(rp, grid, st, tab, w, x, h, acc_zero, I, H, gs); break;
+    }
+}
+
+template <int PREC, int VDT>
+static void launch_down(const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
+                        const uint8_t *q1, const uint8_t *s1, const void *vec, float *partial, void *y, int rows,
+                        int cols, int gs) {
+    if (!rp.fast) {
+        hipLaunchKernelGGL((k_down_generic<PREC, VDT>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, partial, y, rows, cols, gs);
+        return;
+    }
+    switch (rp.cpl) {
+        case 1: hipLaunchKernelGGL((k_down<PREC, VDT, 1, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, partial, y, rows, cols, gs, rp.lg); break;
+        case 2: hipLaunchKernelGGL((k_down<PREC, VDT, 2, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, partial, y, rows, cols, gs, rp.lg); break;
+        default: hipLaunchKernelGGL((k_down<PREC, VDT, 4, DOWN_P>), grid, dim3(256), 0, st, tab, w, q1, s1, vec, partial, y, rows, cols, gs, rp.lg); break;
+    }
+}
+
+template <int PREC>
+static void launch_down_f32(const RowPlan &rp, dim3 grid, hipStream_t st, const int64_t *tab, const float *w,
+                            const float *h, float *partial, int rows, int cols, int gs) {
+    launch_down<PREC, MOEHIP_DT_F32>(rp, grid, st, tab, w, nullptr, nullptr, h, partial, nullptr, rows, cols, gs);
+}
+
+template <int DT>
+static void launch_gemv_int4(const RowPlan &rp, dim3 grid, hipStream_t st, const uint8_t *q, const uint8_t *s,
+                             const void *x, void *y, int rows, int cols, int gs) {
+    launch_down<MOEHIP_PREC_INT4, DT>(rp, grid, st, nullptr, nullptr, q, s, x, nullptr, y, rows, cols, gs);
+}
+
+template <int DT>
+static void launch_combine(dim3 grid, hipStream_t st, const float *acc, const void *add, void *out, size_t N,
+                           int accumulate) {
+    hipLaunchKernelGGL((k_combine<DT>), grid, dim3(256), 0, st, acc, add, out, N, accumulate);
 }
 
 static bool valid_prec(int p) { return p >= MOEHIP_PREC_INT4 && p <= MOEHIP_PREC_FP8; }
@@ -491,14 +378,9 @@ extern "C" int moehip_grouped_up(int prec, const int64_t *tab, const float *w, c
     MOEHIP_REQUIRE(prec != MOEHIP_PREC_INT4 || H % 2 == 0, "grouped_up: int4 needs an even H");
     hipStream_t st = as_stream(stream);
     const RowPlan rp = plan_rows(prec, H, gs, true);
-    if (rp.fast) {
-        const int rows_per_block = 4 * rp.rpw * UP_P;
-        dim3 grid((I + rows_per_block - 1) / rows_per_block, n);
-        MOEHIP_PREC_SWITCH(prec, launch_up, rp, grid, st, tab, w, x, xdtype, h, acc_zero, I, H, gs);
-    } else {
-        dim3 grid((I + 3) / 4, n);
-        MOEHIP_PREC_SWITCH(prec, launch_up_generic, grid, st, tab, w, x, xdtype, h, acc_zero, I, H, gs);
-    }
+    const int rows_per_block = rp.fast ? 4 * rp.rpw * UP_P : 4;
+    dim3 grid((I + rows_per_block - 1) / rows_per_block, n);
+    MOEHIP_PREC_SWITCH(prec, launch_up, xdtype, rp, grid, st, tab, w, x, h, acc_zero, I, H, gs);
     return check_launch("grouped_up");
 }
 
@@ -513,16 +395,9 @@ extern "C" int moehip_grouped_down(int prec, const int64_t *tab, const float *w,
     MOEHIP_REQUIRE(prec != MOEHIP_PREC_INT4 || I % 2 == 0, "grouped_down: int4 needs an even I");
     hipStream_t st = as_stream(stream);
     const RowPlan rp = plan_rows(prec, I, gs, true);
-    if (rp.fast) {
-        const int rows_per_block = 4 * rp.rpw * DOWN_P;
-        dim3 grid((H + rows_per_block - 1) / rows_per_block, n);
-        MOEHIP_PREC_SWITCH(prec, launch_down, rp, grid, st, tab, w, nullptr, nullptr, h, MOEHIP_DT_F32, partial,
-                           nullptr, MOEHIP_DT_F32, H, I, gs);
-    } else {
-        dim3 grid((H + 3) / 4, n);
-        MOEHIP_PREC_SWITCH(prec, launch_down_generic, grid, st, tab, w, nullptr, nullptr, h, MOEHIP_DT_F32, partial,
-                           nullptr, MOEHIP_DT_F32, H, I, gs);
-    }
+    const int rows_per_block = rp.fast ? 4 * rp.rpw * DOWN_P : 4;
+    dim3 grid((H + rows_per_block - 1) / rows_per_block, n);
+    MOEHIP_PREC_SWITCH(prec, launch_down_f32, rp, grid, st, tab, w, h, partial, H, I, gs);
     int rc = check_launch("grouped_down");
     if (rc) return rc;
     hipLaunchKernelGGL(k_reduce, dim3((H + 255) / 256), dim3(256), 0, st, partial, w, n, H, acc);
@@ -540,14 +415,9 @@ extern "C" int moehip_gemv_int4(const void *q, const void *s, const void *x, voi
     const RowPlan rp = plan_rows(MOEHIP_PREC_INT4, I, gs, aligned);
     const uint8_t *qb = reinterpret_cast<const uint8_t *>(q);
     const uint8_t *sb = reinterpret_cast<const uint8_t *>(s);
-    if (rp.fast) {
-        const int rows_per_block = 4 * rp.rpw * DOWN_P;
-        dim3 grid((O + rows_per_block - 1) / rows_per_block, 1);
-        launch_down<MOEHIP_PREC_INT4>(rp, grid, st, nullptr, nullptr, qb, sb, x, dtype, nullptr, y, dtype, O, I, gs);
-    } else {
-        dim3 grid((O + 3) / 4, 1);
-        launch_down_generic<MOEHIP_PREC_INT4>(grid, st, nullptr, nullptr, qb, sb, x, dtype, nullptr, y, dtype, O, I, gs);
-    }
+    const int rows_per_block = rp.fast ? 4 * rp.rpw * DOWN_P : 4;
+    dim3 grid((O + rows_per_block - 1) / rows_per_block, 1);
+    MOEHIP_DT_SWITCH(dtype, launch_gemv_int4, rp, grid, st, qb, sb, x, y, O, I, gs);
     return check_launch("gemv_int4");
 }
 
@@ -556,7 +426,7 @@ extern "C" int moehip_combine(const float *acc, const void *add, void *out, int 
     MOEHIP_REQUIRE(acc && out, "combine: null pointer");
     MOEHIP_REQUIRE(valid_dt(dtype) && T > 0 && H > 0, "combine: bad args");
     const size_t N = (size_t)T * H;
-    hipLaunchKernelGGL(k_combine, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, as_stream(stream), acc, add, out, N,
-                       dtype, accumulate);
+    MOEHIP_DT_SWITCH(dtype, launch_combine, dim3((unsigned)((N + 255) / 256)), as_stream(stream), acc, add, out, N,
+                     accumulate);
     return check_launch("combine");
 }

@@ -16,8 +16,9 @@ namespace moehip {
 constexpr int ROUTER_TT = 8;  // tokens per block in the logits kernel
 
 // logits[t, e] = round_dt(sum_c x[t, c] * Wr[e, c]); one wave per expert row, 4 waves per block
+template <int DT>
 __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ x, const void *__restrict__ Wr, int T,
-                                                       int H, int E, int dt, void *__restrict__ logits) {
+                                                       int H, int E, int vec16, void *__restrict__ logits) {
     const int lane = threadIdx.x & 63;
     const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (e >= E) return;
@@ -27,7 +28,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
 #pragma unroll
     for (int t = 0; t < ROUTER_TT; ++t) acc[t] = 0.f;
     const size_t wrow = (size_t)e * H;
-    if (dt != MOEHIP_DT_F32 && H % 8 == 0 && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0) {
+    if (DT != MOEHIP_DT_F32 && vec16) {
         // 16-bit dtypes, 8 values per 16-byte load
         const uint16_t *W16 = reinterpret_cast<const uint16_t *>(Wr);
         const uint16_t *X16 = reinterpret_cast<const uint16_t *>(x);
@@ -37,7 +38,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
             float wf[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                if (dt == MOEHIP_DT_F16) {
+                if constexpr (DT == MOEHIP_DT_F16) {
                     wf[2 * j] = f16_to_f32(wd[j] & 0xffffu);
                     wf[2 * j + 1] = f16_to_f32(wd[j] >> 16);
                 } else {
@@ -53,7 +54,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         float xa, xb;
-                        if (dt == MOEHIP_DT_F16) {
+                        if constexpr (DT == MOEHIP_DT_F16) {
                             xa = f16_to_f32(xd[j] & 0xffffu);
                             xb = f16_to_f32(xd[j] >> 16);
                         } else {
@@ -68,22 +69,23 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
         }
     } else {
         for (int c = lane; c < H; c += 64) {
-            const float wv = load_act(Wr, wrow + c, dt);
+            const float wv = ld_act<DT>(Wr, wrow + c);
 #pragma unroll
             for (int t = 0; t < ROUTER_TT; ++t)
-                if (t < nt) acc[t] = fmaf(wv, load_act(x, (size_t)(t0 + t) * H + c, dt), acc[t]);
+                if (t < nt) acc[t] = fmaf(wv, ld_act<DT>(x, (size_t)(t0 + t) * H + c), acc[t]);
         }
     }
 #pragma unroll
     for (int t = 0; t < ROUTER_TT; ++t) {
         const float s = wave_sum(acc[t]);
-        if (lane == 0 && t < nt) store_act(logits, (size_t)(t0 + t) * E + e, dt, s);
+        if (lane == 0 && t < nt) st_act<DT>(logits, (size_t)(t0 + t) * E + e, s);
     }
 }
 
 // softmax + top-k + renorm for one token per wave (E <= 1024, k <= 32)
+template <int DT>
 __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ logits, int T, int E, int k, int renorm,
-                                                    int dt, int64_t *__restrict__ idx, void *__restrict__ wout,
+                                                    int64_t *__restrict__ idx, void *__restrict__ wout,
                                                     float *__restrict__ w32) {
     const int t = blockIdx.x;
     const int lane = threadIdx.x;
@@ -94,7 +96,7 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int c = lane + 64 * i;
-        lv[i] = c < E ? load_act(logits, (size_t)t * E + c, dt) : -INFINITY;
+        lv[i] = c < E ? ld_act<DT>(logits, (size_t)t * E + min(c, E - 1)) : -INFINITY;
         m = fmaxf(m, lv[i]);
     }
     m = wave_max(m);
@@ -140,8 +142,8 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
         for (int j = 0; j < k; ++j) {
             const float p = renorm ? s_p[j] / tot : s_p[j];
             idx[(size_t)t * k + j] = s_idx[j];
-            const float r = round_act(p, dt);
-            if (wout != nullptr) store_act(wout, (size_t)t * k + j, dt, p);
+            const float r = rnd_act<DT>(p);
+            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + j, p);
             if (w32 != nullptr) w32[(size_t)t * k + j] = r;
         }
     }
@@ -230,12 +232,23 @@ extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, i
     MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E,
                    "router_topk: bad sizes T=%d H=%d E=%d k=%d", T, H, E, k);
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(k_router_logits, dim3((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT), dim3(256), 0, st, x, Wr, T,
-                       H, E, dtype, logits);
-    int rc = check_launch("router logits");
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_router_topk, dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, dtype, idx, w, w32);
-    return check_launch("router topk");
+    const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
+    switch (dtype) {
+        case MOEHIP_DT_F16:
+            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
+            break;
+        case MOEHIP_DT_BF16:
+            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_BF16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_BF16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
+            break;
+        default:
+            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F32>), g1, dim3(256), 0, st, x, Wr, T, H, E, 0, logits);
+            hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F32>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
+            break;
+    }
+    return check_launch("router");
 }
 
 extern "C" int moehip_decide_table(const int64_t *idx, const float *w32, int k, const moehip_policy *pol,

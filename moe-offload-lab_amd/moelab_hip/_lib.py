@@ -29,6 +29,14 @@ class Policy(ctypes.Structure):
     _fields_ = [("mode", _i), ("t1", _f), ("t_mid", _f), ("t2", _f), ("protect", _i), ("upgrade", _i)]
 
 
+class LayerDesc(ctypes.Structure):
+    """moehip_layer_desc: static description of one MoE layer for the fused decode kernel."""
+
+    _fields_ = [("P", _i), ("E", _i), ("k", _i), ("H", _i), ("I", _i), ("dtype", _i), ("renorm", _i),
+                ("prec", _i * 4), ("gs_up", _i * 4), ("gs_dn", _i * 4), ("planned", _i * 4), ("lv2p", _i * 3),
+                ("offs", (ctypes.c_int64 * 4) * 4), ("pol", Policy)]
+
+
 _SIGS = {
     "moehip_abi_version": ([], _i),
     "moehip_last_error": ([], ctypes.c_char_p),
@@ -43,6 +51,11 @@ _SIGS = {
                              _vp, _vp], _i),
     "moehip_dispatch": ([_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_quantize": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
+    "moehip_quantize_fp8_block": ([_vp, _i, _i, _vp, _vp, _vp], _i),
+    "moehip_decode_layer": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                             _vp, _vp, _vp, ctypes.c_size_t, _i, _vp], _i),
+    "moehip_decode_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
+    "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
 }
 
 EXPORTED = tuple(_SIGS)

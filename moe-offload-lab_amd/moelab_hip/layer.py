@@ -7,7 +7,10 @@ rtab (L, P, E) int64 of record base addresses, 0 = not resident (moelab/fullgrap
 layer-major so that one layer's (P, E) slice is contiguous for the decision kernel).
 
 `MoEDecoder.layer(l, x)` runs one MoE layer for one decode token entirely on the GPU with no
-host round trip, so a whole token can be captured in one HIP graph (moelab/fullgraph.py:117-192):
+host round trip, so a whole token can be captured in one HIP graph (moelab/fullgraph.py:117-192).
+By default it is ONE launch of the fused decode-layer kernel (moehip_decode_layer): router,
+softmax/top-k/renorm, HOBBIT levels + resident copy + tables, kernel-A and kernel-B rows and the
+table-order combine. With fused=False the same steps run as separate launches:
   1. router: logits, softmax, top-k, renorm            (moehip_router_topk)
   2. HOBBIT levels + resident copy + kernel tables      (moehip_decide_table)
   3. kernel A per planned precision (acc zeroed by the first)   (moehip_grouped_up)
@@ -25,7 +28,7 @@ import torch
 from . import _lib
 from .kernels import _Plan, _combine
 from .policy import PrecisionPolicy, level_to_precision
-from .store import encode_record_, record_layout
+from .store import encode_record_, group_size_of, record_layout
 
 
 class ResidentStore:
@@ -83,7 +86,8 @@ class MoEDecoder:
     """One decode token through the MoE layers, all on the GPU (capturable)."""
 
     def __init__(self, store: ResidentStore, k: int, policy: PrecisionPolicy | None = None, dtype=torch.float16,
-                 router_weights: list | None = None, renorm: bool = False, planned: list | None = None):
+                 router_weights: list | None = None, renorm: bool = False, planned: list | None = None,
+                 fused: bool = True, grid: int = 0):
         self.store = store
         self.k = k
         self.policy = policy or PrecisionPolicy("lo")
@@ -115,6 +119,41 @@ class MoEDecoder:
         self.info = torch.zeros(store.L, 3, k, dtype=torch.float32, device=dev)
         self.miss = torch.zeros(1, dtype=torch.float32, device=dev)
         self._pols = [self.policy.device_policy(l) for l in range(store.L)]
+        self.grid = grid
+        self.fused = fused and all(store.layouts[p]["precision"] != "fp32" for p in precs) and H <= 2048 \
+            and _dims(store.layouts[precs[0]])[1] <= 2048
+        if self.fused:
+            self._descs = [self._desc(l) for l in range(store.L)]
+            nbytes = _lib.load().moehip_decode_layer_workspace_bytes(self.P, k, E, H, self._descs[0].I)
+            self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+            self.err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def _desc(self, layer: int) -> _lib.LayerDesc:
+        st = self.store
+        d = _lib.LayerDesc()
+        d.P, d.E, d.k = self.P, st.E, self.k
+        d.H, d.I = _dims(st.layouts[st.precisions[0]])
+        d.dtype = _lib.dt_code(self.dtype)
+        d.renorm = 1 if self.renorm else 0
+        for pi, p in enumerate(st.precisions):
+            lay = st.layouts[p]
+            d.prec[pi] = _lib.prec_code(lay["precision"])
+            gu, gd = group_size_of(lay)
+            d.gs_up[pi], d.gs_dn[pi] = gu, gd
+            d.planned[pi] = 1 if pi in self.plans else 0
+            for f, o in enumerate(_offs(lay)):
+                d.offs[pi][f] = o
+        for v in range(3):
+            d.lv2p[v] = self.lv2p[v]
+        d.pol = self._pols[layer]
+        return d
+
+    def check_error(self) -> None:
+        """Raise if a bounded wait inside the fused kernel expired on this decoder's workspace."""
+        if self.fused:
+            _lib.call("moehip_decode_layer_error", self.ws.data_ptr(), self.err.data_ptr(), _lib.stream_of(self.ws.device))
+            if int(self.err.item()) != 0:
+                raise RuntimeError("fused decode-layer kernel: a bounded wait expired (workspace error flag set)")
 
     def route(self, layer: int, x: torch.Tensor) -> None:
         Wr = self.router_weights[layer]
@@ -142,13 +181,23 @@ class MoEDecoder:
         _combine(self.acc, out, cpu_part, accumulate=False)
 
     def layer(self, layer: int, x: torch.Tensor, out: torch.Tensor, idx: torch.Tensor | None = None,
-              w32: torch.Tensor | None = None) -> torch.Tensor:
+              w32: torch.Tensor | None = None, cpu_part: torch.Tensor | None = None) -> torch.Tensor:
         """out (1, H) = MoE layer `layer` applied to x (1, H). With idx/w32 given, the router is skipped."""
+        if self.fused:
+            st = self.store
+            Wr = None if idx is not None else self.router_weights[layer]
+            _lib.call("moehip_decode_layer", ctypes.byref(self._descs[layer]), x.data_ptr(), _lib.ptr(Wr),
+                      _lib.ptr(idx), _lib.ptr(w32), st.rtab[layer].data_ptr(), out.data_ptr(), _lib.ptr(cpu_part), 0,
+                      self.logits.data_ptr(), self.idx.data_ptr() if idx is None else None,
+                      self.w.data_ptr() if idx is None else None, self.w32.data_ptr() if idx is None else None,
+                      self.info[layer].data_ptr(), self.miss.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
+                      self.grid, _lib.stream_of(x.device))
+            return out
         if idx is None:
             self.route(layer, x)
             idx, w32 = self.idx, self.w32
         self.decide(layer, idx, w32)
-        self.experts(x, out)
+        self.experts(x, out, cpu_part)
         return out
 
 

@@ -11,7 +11,8 @@ weights with fp32 128x128 block scales, the `weight_scale_inv` of moelab/quant.p
 laid out with the same alignment rules.
 
 Encoding runs on the GPU (`encode_record_`): absmax int4/int8 through the moehip quantiser
-(bit-exact with moelab/quant.py's absmax path), float records by casting.
+(bit-exact with moelab/quant.py's absmax path), fp8 through the moehip block quantiser (amax/448 scales,
+round-to-nearest-even e4m3fn codes), float records by casting.
 """
 
 from __future__ import annotations
@@ -133,7 +134,7 @@ def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down
     """Write one record into `blob` (uint8 device tensor of record_bytes) from float weights on
     the same device. int4/int8: absmax scales through the moehip quantiser (identical bytes to
     moelab/store.py:122-150 with scale="absmax"); float: cast; fp8: per-128x128-block
-    amax/448 scales and an e4m3fn cast."""
+    amax/448 scales and round-to-nearest-even e4m3fn codes."""
     prec = layout["precision"]
     spec = PRECISIONS[prec]
     if blob.numel() != layout["record_bytes"] or blob.dtype != torch.uint8:
@@ -145,15 +146,16 @@ def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down
         for name, w in mats.items():
             v[name].copy_(w)
         return blob
-    if spec["kind"] == "fp8":
-        for name, w in mats.items():
-            code, sc = fp8_block_quantize(w.float())
-            v[f"{name}.q"].copy_(code.view(torch.uint8))
-            v[f"{name}.s"].copy_(sc)
-        return blob
     if blob.device.type != "cuda":
         raise RuntimeError("encode_record_ quantises on the GPU; blob must be a device tensor")
     _lib.check_device(blob.device)
+    if spec["kind"] == "fp8":
+        for name, w in mats.items():
+            wf = w.float().contiguous()
+            O, I = wf.shape
+            _lib.call("moehip_quantize_fp8_block", wf.data_ptr(), O, I, v[f"{name}.q"].data_ptr(),
+                      v[f"{name}.s"].data_ptr(), _lib.stream_of(blob.device))
+        return blob
     bits = spec["bits"]
     for name, w in mats.items():
         wf = w.float().contiguous()
@@ -162,16 +164,3 @@ def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down
         _lib.call("moehip_quantize", wf.data_ptr(), O, I, bits, gs, v[f"{name}.q"].data_ptr(),
                   v[f"{name}.s"].data_ptr(), _lib.stream_of(blob.device))
     return blob
-
-
-def fp8_block_quantize(w: torch.Tensor, block: int = FP8_BLOCK) -> tuple[torch.Tensor, torch.Tensor]:
-    """Checkpoint-style FP8: scale = amax/448 per block (1.0 for an all-zero block), code = e4m3fn(w/scale)."""
-    O, I = w.shape
-    so, si = math.ceil(O / block), math.ceil(I / block)
-    pad = torch.zeros(so * block, si * block, dtype=torch.float32, device=w.device)
-    pad[:O, :I] = w
-    blk = pad.view(so, block, si, block)
-    amax = blk.abs().amax(dim=(1, 3))
-    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
-    q = (blk / scale[:, None, :, None]).view(so * block, si * block)[:O, :I]
-    return q.to(torch.float8_e4m3fn), scale.contiguous()
