@@ -459,7 +459,10 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             if (s_flag) {
                 if (wave == 0) route_tail<XDT>(a, s_idx, s_w, s_vec);
                 sync_release();
-                if (tid == 0) st_co32(ws + W_READY, 1u);
+                if (tid == 0) {
+                    st_co32(ws + W_READY, 1u);
+                    s_fmt = -1;  // s_vec held the logits: no staged x any more
+                }
             }
         } else if (t < NR + NU) {
             // ---------------- kernel-A rows ----------------
