@@ -181,14 +181,16 @@ typedef struct moehip_layer_desc {
  * `ws` is caller-owned scratch of moehip_decode_layer_workspace_bytes() bytes, 256-B aligned and
  * zeroed once before its first use; every launch leaves it ready for the next. Launches sharing a
  * workspace must not overlap (one workspace per stream). grid = number of workgroups (0 = one per
- * work item). H, I multiples of 32, H <= 8192, I <= 4096, E <= 1024, k <= 32.
+ * work item). trace (optional, NULL in production): 3 uint64 per work item = (start, end,
+ * workgroup) in the GPU's constant real-time clock, for profiling. H, I multiples of 32 and
+ * <= 2048, E <= 1024, k <= 32; x and Wr 16-byte aligned; fp32 records are not supported here.
  * Replaces, for decode, the whole moelab/runtime.py:523-770 `run_layer` GPU path when every
  * expert is resident (the A5 whole-token path, moelab/fullgraph.py:149-188 + graphs.py:351-426).
  */
 int moehip_decode_layer(const moehip_layer_desc *desc, const void *x, const void *Wr, const int64_t *idx_in,
                         const float *w32_in, const int64_t *rtab, void *out, const void *add, int accumulate,
                         void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info, float *miss,
-                        void *ws, size_t ws_bytes, int grid, void *stream);
+                        void *ws, size_t ws_bytes, int grid, uint64_t *trace, void *stream);
 size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H, int I);
 /* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device). */
 int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);

@@ -75,24 +75,60 @@ __device__ __forceinline__ float fp8_to_f32(uint32_t byte) {
 }
 
 // ---------------------------------------------------------------------------------------
-// wave64 reductions
+// wave64 reductions with DPP: quad_perm [1,0,3,2] and [2,3,0,1] (xor 1, xor 2), row_half_mirror
+// and row_mirror (after the previous steps every lane of an aligned group of 8 / 16 holds the
+// group's sum), then v_readlane of the four row results for groups of 32 / 64. Every lane must
+// be active when these are called.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// sum over aligned groups of G = 2^lg lanes; every lane of a group gets the group total
+__device__ __forceinline__ float group_sum(float v, int lg) {
+    if (lg >= 1) v += dpp_f<0xB1>(v);
+    if (lg >= 2) v += dpp_f<0x4E>(v);
+    if (lg >= 3) v += dpp_f<0x141>(v);
+    if (lg >= 4) v += dpp_f<0x140>(v);
+    if (lg >= 5) {
+        const float r0 = lane_f(v, 0), r1 = lane_f(v, 16), r2 = lane_f(v, 32), r3 = lane_f(v, 48);
+        if (lg == 5) v = (threadIdx.x & 32) ? (r2 + r3) : (r0 + r1);
+        else v = (r0 + r1) + (r2 + r3);
+    }
     return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum(v, 6); }
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+    v += dpp_i<0xB1>(v);
+    v += dpp_i<0x4E>(v);
+    v += dpp_i<0x141>(v);
+    v += dpp_i<0x140>(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
-// sum across aligned groups of G = 2^lg lanes (every lane of the group gets the total)
-__device__ __forceinline__ float group_sum(float v, int lg) {
-    for (int off = (1 << lg) >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// order-preserving 32-bit key of a non-NaN float: a > b <=> key(a) > key(b), key(-0) == key(+0)
+__device__ __forceinline__ uint32_t fkey(float f) {
+    const uint32_t u = f == 0.f ? 0u : __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }

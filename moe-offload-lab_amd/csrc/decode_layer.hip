@@ -29,8 +29,10 @@ constexpr int DL_MAXROW = 2048;  // 64 lanes x 32 vector values per lane
 constexpr int DL_MAXH = DL_MAXROW;
 constexpr int UP_ROWS = 16;  // row pairs per up item (4 per wave)
 constexpr int DN_ROWS = 64;  // output rows per down item (16 per wave)
-constexpr int WAIT_SPINS = 1 << 22;
-enum { W_TICKET = 0, W_ROUTER = 1, W_READY = 2, W_DONE = 3, W_ERR = 4, W_HDR = 64 };
+constexpr int WAIT_SPINS = 1 << 22;  // x ~0.3 us per poll: a wait gives up after ~1 s
+// header words, each counter on its own 128-byte line; per-row counters are 32 words apart
+enum { W_TICKET = 0, W_ROUTER = 32, W_READY = 64, W_DONE = 96, W_ERR = 128, W_HDR = 160 };
+constexpr int CSTRIDE = 32;  // words between consecutive up_done / dn_done counters
 
 struct LayerArgs {
     const void *x;          // (H) activation dtype
@@ -57,6 +59,7 @@ struct LayerArgs {
     uint32_t *ws;           // workspace (zeroed once by the caller)
     int nub, ndb;           // up blocks per table row, down blocks
     uint32_t off_up, off_dn, off_tab, off_wtab, off_logits, off_h, off_part;  // byte offsets in ws
+    uint64_t *trace;        // optional per-item trace: [ticket] = (start, end, workgroup) or null
 };
 
 // ---------------------------------------------------------------------------------------
@@ -95,11 +98,22 @@ __device__ __forceinline__ void sync_release() {
     __syncthreads();
 }
 
-// thread 0 polls until *p >= v (bounded); the caller follows with a barrier
+// thread 0 polls until *p >= v, backing off exponentially (s_sleep 1 .. 8, i.e. up to ~500
+// cycles between polls, so hundreds of waiting workgroups do not congest the flag's memory
+// channel); bounded by WAIT_SPINS polls. The caller follows with a barrier.
 __device__ __forceinline__ void wait_geq(uint32_t *p, uint32_t v, uint32_t *err) {
+    int nap = 1;
     for (int it = 0; it < WAIT_SPINS; ++it) {
         if (ld_co32(p) >= v) return;
-        __builtin_amdgcn_s_sleep(2);
+        switch (nap) {  // s_sleep takes an immediate
+            case 1: __builtin_amdgcn_s_sleep(1); break;
+            case 2: __builtin_amdgcn_s_sleep(2); break;
+            case 4: __builtin_amdgcn_s_sleep(4); break;
+            case 8: __builtin_amdgcn_s_sleep(8); break;
+            case 16: __builtin_amdgcn_s_sleep(16); break;
+            default: __builtin_amdgcn_s_sleep(8); break;
+        }
+        if (nap < 8) nap <<= 1;
     }
     __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -286,9 +300,12 @@ __device__ __forceinline__ int64_t pick_off(const int64_t (&v)[4][4], int p, int
 // route tail: softmax / top-k / renorm / HOBBIT / resident copy / tables (wave 0 of one WG)
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float *s_w, float *s_l) {
-    const int lane = threadIdx.x;  // wave 0 only; s_l: E floats of LDS
+__device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float *s_w, float *s_l, uint64_t *ts) {
+    const int lane = threadIdx.x;  // wave 0 only; s_l: E floats of LDS (+ 2 x 32 candidate slots)
     const int k = a.k, E = a.E;
+    const unsigned long long lt = (1ull << lane) - 1ull;  // lanes below this one
+#define TS(i) do { if (ts != nullptr && lane == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+    TS(0);
     if (a.Wr != nullptr) {
         const float *logits = ws_ptr<float>(a, a.off_logits);
         float m = -INFINITY;
@@ -299,55 +316,72 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
             if (a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, v);
         }
         m = wave_max(m);
+        TS(1);
         float sum = 0.f;
         for (int c = lane; c < E; c += 64) sum += expf(s_l[c] - m);
         sum = wave_sum(sum);
-        __builtin_amdgcn_wave_barrier();
-        for (int j = 0; j < k; ++j) {
-            float bv = -INFINITY;
-            int bi = INT_MAX;
-            for (int c = lane; c < E; c += 64) {
-                const float v = s_l[c];
-                if (v > bv) {  // ascending c: the first maximum of this lane's columns wins
-                    bv = v;
-                    bi = c;
-                }
-            }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();
-            if (lane == 0) {
-                s_idx[j] = bi;
-                s_w[j] = expf(bv - m) / sum;
-                s_l[bi] = -INFINITY;  // taken
-            }
-            __builtin_amdgcn_wave_barrier();
+        // k-th largest logit by radix select over order-preserving keys (MSB first)
+        uint32_t prefix = 0, mask = 0;
+        int need = k;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t bit = 1u << b, cand = prefix | bit, m2 = mask | bit;
+            int cnt = 0;
+            for (int c = lane; c < E; c += 64) cnt += (fkey(s_l[c]) & m2) == cand;
+            cnt = wave_sum_i(cnt);
+            if (cnt >= need) prefix = cand;
+            else need -= cnt;
+            mask = m2;
         }
-        if (lane == 0) {
-            float tot = 0.f;
-            if (a.renorm)
-                for (int j = 0; j < k; ++j) tot += s_w[j];
-            for (int j = 0; j < k; ++j) {
-                const float p = a.renorm ? s_w[j] / tot : s_w[j];
-                const float r = rnd_act<XDT>(p);
-                if (a.idx_out) a.idx_out[j] = s_idx[j];
-                if (a.w_out) st_act<XDT>(a.w_out, j, p);
-                if (a.w32_out) a.w32_out[j] = r;
-                s_w[j] = r;
+        // the k winners: every key above the k-th, then the `need` lowest-index keys equal to it
+        float *cv = s_l + E;                              // candidate values
+        int *ci = reinterpret_cast<int *>(s_l + E + 32);  // candidate indices
+        int nsel = 0, neq = 0;
+        for (int c0 = 0; c0 < E; c0 += 64) {
+            const int c = c0 + lane;
+            const uint32_t key = c < E ? fkey(s_l[c]) : 0u;
+            const bool gt = c < E && key > prefix;
+            const bool eq = c < E && key == prefix;
+            const unsigned long long eqm = __ballot(eq);
+            const bool sel = gt || (eq && neq + __popcll(eqm & lt) < need);
+            const unsigned long long sm = __ballot(sel);
+            if (sel) {
+                const int pos = nsel + __popcll(sm & lt);
+                cv[pos] = s_l[c];
+                ci[pos] = c;
             }
+            nsel += __popcll(sm);
+            neq += __popcll(eqm);
+        }
+        __builtin_amdgcn_wave_barrier();
+        // order the winners by (logit desc, index asc), probabilities, renorm, outputs
+        float p = 0.f;
+        int rank = 0, myidx = 0;
+        if (lane < k) {
+            const float v = cv[lane];
+            myidx = ci[lane];
+            for (int i = 0; i < k; ++i) {
+                const float o = cv[i];
+                rank += (o > v) || (o == v && ci[i] < myidx);
+            }
+            p = expf(v - m) / sum;
+        }
+        const float tot = a.renorm ? wave_sum(lane < k ? p : 0.f) : 1.f;
+        TS(2);
+        if (lane < k) {
+            const float pw = a.renorm ? p / tot : p;
+            const float r = rnd_act<XDT>(pw);
+            s_idx[rank] = myidx;
+            s_w[rank] = r;
+            if (a.idx_out) a.idx_out[rank] = myidx;
+            if (a.w_out) st_act<XDT>(a.w_out, rank, pw);
+            if (a.w32_out) a.w32_out[rank] = r;
         }
     } else if (lane < k) {
         s_idx[lane] = (int)a.idx_in[lane];
         s_w[lane] = a.w32_in[lane];
     }
     __builtin_amdgcn_wave_barrier();
+    TS(3);
     // HOBBIT levels (moelab/policy.py:77-123), resident copy, tables (moelab/fullgraph.py:149-171)
     float *s_sorted = s_l;  // reused: k floats
     const int j = lane;
@@ -382,12 +416,14 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
         if (s <= pol.t1) lvl = 0;
         skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
     }
+    TS(4);
     const int req = lvl == 0 ? a.lv2p[0] : (lvl == 1 ? a.lv2p[1] : a.lv2p[2]);
     int chosen = -1;
     for (int pi = a.P - 1; pi >= 0; --pi) {
         const bool avail = act && e >= 0 && e < E && a.rtab[(size_t)pi * E + e] != 0;
         if (avail && (pol.upgrade ? req >= pi : req == pi)) chosen = pi;
     }
+    TS(5);
     const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
     const bool is_miss = act && !skip && !usable;
     int64_t *tab = ws_ptr<int64_t>(a, a.off_tab);
@@ -406,8 +442,11 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
             a.info[2 * k + j] = (float)lvl;
         }
     }
+    TS(6);
     const unsigned long long bal = __ballot(is_miss);
     if (j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
+    TS(7);
+#undef TS
 }
 
 // ---------------------------------------------------------------------------------------
@@ -416,9 +455,11 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
 template <int XDT>
 __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
     __shared__ __align__(16) float s_vec[DL_MAXH];  // x (up items) or h (down items), piece-major
-    __shared__ int s_item, s_flag, s_fmt;
+    __shared__ int s_item, s_next, s_flag, s_fmt, s_routed;
     __shared__ int s_idx[64];
     __shared__ float s_w[64];
+    __shared__ float s_wt[DL_MAXP * 32];          // route cached per workgroup: table weights
+    __shared__ uint64_t s_tab[DL_MAXP * 32 * 4];  // and addresses
     const int tid = threadIdx.x, wave = tid >> 6;
     uint32_t *ws = a.ws;
     uint32_t *err = ws + W_ERR;
@@ -433,22 +474,61 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
     float *wtab = ws_ptr<float>(a, a.off_wtab);
     float *hbuf = ws_ptr<float>(a, a.off_h);
     float *part = ws_ptr<float>(a, a.off_part);
-    if (tid == 0) s_fmt = -1;  // which layout s_vec holds: VPC of staged x, or -1
+    if (tid == 0) {
+        s_fmt = -1;  // which layout s_vec holds: VPC of staged x, or -1
+        s_routed = 0;
+        s_next = (int)add_co32(ws + W_TICKET, 1u);
+    }
     for (;;) {
         __syncthreads();
-        if (tid == 0) s_item = (int)add_co32(ws + W_TICKET, 1u);
+        if (tid == 0) {
+            // take the reserved ticket and reserve the next one (its round trip overlaps the work)
+            s_item = s_next;
+            s_next = s_item < total ? (int)add_co32(ws + W_TICKET, 1u) : total;
+        }
         __syncthreads();
         const int t = s_item;
         if (t >= total) break;
+        uint64_t t_start = 0;
+        if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
         if (t < NR) {
             // ---------------- router rows ----------------
             if (a.Wr != nullptr) {
                 const int e = t * 4 + wave;
                 const int lane = tid & 63;
                 if (e < a.E) {
+                    // each lane: 32 consecutive values (H <= 2048), all loads issued before use
+                    constexpr int ESZ = XDT == MOEHIP_DT_F32 ? 4 : 2;
+                    constexpr int NV = 32 * ESZ / 16;  // 16-byte vectors per lane
+                    const int c0 = lane * 32;
                     float acc = 0.f;
-                    const size_t wrow = (size_t)e * a.H;
-                    for (int c = lane; c < a.H; c += 64) acc = fmaf(ld_act<XDT>(a.Wr, wrow + c), ld_act<XDT>(a.x, c), acc);
+                    if (c0 < a.H) {
+                        const uint8_t *wp = reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ;
+                        const uint8_t *xp = reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * ESZ;
+                        uint4 wv[NV], xv[NV];
+#pragma unroll
+                        for (int i = 0; i < NV; ++i) {
+                            wv[i] = reinterpret_cast<const uint4 *>(wp)[i];
+                            xv[i] = reinterpret_cast<const uint4 *>(xp)[i];
+                        }
+#pragma unroll
+                        for (int i = 0; i < NV; ++i) {
+                            const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+                            const uint32_t xd[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                if constexpr (XDT == MOEHIP_DT_F32) {
+                                    acc = fmaf(__uint_as_float(wd[q]), __uint_as_float(xd[q]), acc);
+                                } else if constexpr (XDT == MOEHIP_DT_F16) {
+                                    acc = fmaf(f16_to_f32(wd[q] & 0xffffu), f16_to_f32(xd[q] & 0xffffu), acc);
+                                    acc = fmaf(f16_to_f32(wd[q] >> 16), f16_to_f32(xd[q] >> 16), acc);
+                                } else {
+                                    acc = fmaf(__uint_as_float(wd[q] << 16), __uint_as_float(xd[q] << 16), acc);
+                                    acc = fmaf(__uint_as_float(wd[q] & 0xffff0000u), __uint_as_float(xd[q] & 0xffff0000u), acc);
+                                }
+                            }
+                        }
+                    }
                     acc = wave_sum(acc);
                     if (lane == 0) st_co(ws_ptr<float>(a, a.off_logits) + e, rnd_act<XDT>(acc));
                 }
@@ -457,9 +537,10 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             if (tid == 0) s_flag = (add_co32(ws + W_ROUTER, 1u) == (uint32_t)(NR - 1));
             __syncthreads();
             if (s_flag) {
-                if (wave == 0) route_tail<XDT>(a, s_idx, s_w, s_vec);
+                if (wave == 0) route_tail<XDT>(a, s_idx, s_w, s_vec, a.trace ? a.trace + 3 * total : nullptr);
                 sync_release();
                 if (tid == 0) {
+                    if (a.trace) a.trace[3 * total + 8] = __builtin_amdgcn_s_memrealtime();
                     st_co32(ws + W_READY, 1u);
                     s_fmt = -1;  // s_vec held the logits: no staged x any more
                 }
@@ -476,20 +557,36 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
                 const int npc = vpc / 4;
                 for (int i4 = tid; i4 < a.H / 4; i4 += 256) {
                     const int dst = vec_slot(i4, npc, C);
-                    s_vec[dst + 0] = ld_act<XDT>(a.x, 4 * i4 + 0);
-                    s_vec[dst + 1] = ld_act<XDT>(a.x, 4 * i4 + 1);
-                    s_vec[dst + 2] = ld_act<XDT>(a.x, 4 * i4 + 2);
-                    s_vec[dst + 3] = ld_act<XDT>(a.x, 4 * i4 + 3);
+                    float4 p4;
+                    if constexpr (XDT == MOEHIP_DT_F32) {
+                        p4 = reinterpret_cast<const float4 *>(a.x)[i4];
+                    } else {
+                        const uint2 r = reinterpret_cast<const uint2 *>(a.x)[i4];
+                        if constexpr (XDT == MOEHIP_DT_F16) {
+                            p4 = make_float4(f16_to_f32(r.x & 0xffffu), f16_to_f32(r.x >> 16), f16_to_f32(r.y & 0xffffu),
+                                             f16_to_f32(r.y >> 16));
+                        } else {
+                            p4 = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                                             __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+                        }
+                    }
+                    *reinterpret_cast<float4 *>(s_vec + dst) = p4;
                 }
                 __syncthreads();
                 if (tid == 0) s_fmt = vpc;
             }
-            if (tid == 0) wait_geq(ws + W_READY, 1u, err);
-            __syncthreads();
-            const float wt = ld_co(wtab + jj);
+            if (!s_routed) {  // first item after the routing: cache the tables in LDS
+                if (tid == 0) wait_geq(ws + W_READY, 1u, err);
+                __syncthreads();
+                for (int i = tid; i < PK; i += 256) s_wt[i] = ld_co(wtab + i);
+                for (int i = tid; i < PK * 4; i += 256) s_tab[i] = (uint64_t)ld_co64(tab + i);
+                __syncthreads();
+                if (tid == 0) s_routed = 1;
+            }
+            const float wt = s_wt[jj];
             if (wt != 0.f) {
-                const uint8_t *qb = reinterpret_cast<const uint8_t *>(ld_co64(tab + (size_t)jj * 4 + 0));
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(ld_co64(tab + (size_t)jj * 4 + 1));
+                const uint8_t *qb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 0]);
+                const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 1]);
                 const int lg = row_lg(a.H);
                 const int r0 = rb * UP_ROWS + wave * (UP_ROWS / 4);
                 float *hout = hbuf + (size_t)jj * a.I;
@@ -503,7 +600,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
                     default: up_rows<MOEHIP_PREC_FP8>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
                 }
                 sync_release();
-                if (tid == 0) add_co32(up_done + jj, 1u);
+                if (tid == 0) add_co32(up_done + jj * CSTRIDE, 1u);
             }
         } else {
             // ---------------- kernel-B rows + ordered combine ----------------
@@ -511,11 +608,17 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             const int jj = d / a.ndb, rb = d % a.ndb;
             const int pi = jj / a.k;
             const int prec = pick4(a.prec, pi);
-            if (tid == 0) wait_geq(ws + W_READY, 1u, err);
-            __syncthreads();
-            const float wt = ld_co(wtab + jj);
+            if (!s_routed) {
+                if (tid == 0) wait_geq(ws + W_READY, 1u, err);
+                __syncthreads();
+                for (int i = tid; i < PK; i += 256) s_wt[i] = ld_co(wtab + i);
+                for (int i = tid; i < PK * 4; i += 256) s_tab[i] = (uint64_t)ld_co64(tab + i);
+                __syncthreads();
+                if (tid == 0) s_routed = 1;
+            }
+            const float wt = s_wt[jj];
             if (wt != 0.f) {
-                if (tid == 0) wait_geq(up_done + jj, (uint32_t)a.nub, err);
+                if (tid == 0) wait_geq(up_done + jj * CSTRIDE, (uint32_t)a.nub, err);
                 __syncthreads();
                 const int vpc = vpc_dev(prec);
                 const int C = a.I / vpc;
@@ -530,8 +633,8 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
                 }
                 if (tid == 0) s_fmt = -1;
                 __syncthreads();
-                const uint8_t *qb = reinterpret_cast<const uint8_t *>(ld_co64(tab + (size_t)jj * 4 + 2));
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(ld_co64(tab + (size_t)jj * 4 + 3));
+                const uint8_t *qb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 2]);
+                const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 3]);
                 const int lg = row_lg(a.I);
                 const int r0 = rb * DN_ROWS + wave * (DN_ROWS / 4);
                 float *pout = part + (size_t)jj * a.H;
@@ -546,27 +649,32 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
                 }
             }
             sync_release();
-            if (tid == 0) s_flag = (add_co32(dn_done + rb, 1u) == (uint32_t)(PK - 1));
+            if (tid == 0) s_flag = (add_co32(dn_done + rb * CSTRIDE, 1u) == (uint32_t)(PK - 1));
             __syncthreads();
             if (s_flag && tid < DN_ROWS) {
                 const int r = rb * DN_ROWS + tid;
                 if (r < a.H) {
                     float s = 0.f;
                     for (int q = 0; q < PK; ++q)
-                        if (ld_co(wtab + q) != 0.f) s += ld_co(part + (size_t)q * a.H + r);
+                        if (s_wt[q] != 0.f) s += ld_co(part + (size_t)q * a.H + r);
                     if (a.accumulate) s += ld_act<XDT>(a.out, r);
                     if (a.add != nullptr) s += ld_act<XDT>(a.add, r);
                     st_act<XDT>(a.out, r, s);
                 }
             }
         }
+        if (a.trace != nullptr && tid == 0) {
+            a.trace[3 * t + 0] = t_start;
+            a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
+            a.trace[3 * t + 2] = blockIdx.x;
+        }
     }
     // every workgroup has taken its last ticket; the last one resets the counters
     if (tid == 0) s_flag = (add_co32(ws + W_DONE, 1u) == gridDim.x - 1);
     __syncthreads();
     if (s_flag) {
-        for (int i = tid; i < PK; i += 256) st_co32(up_done + i, 0u);
-        for (int i = tid; i < a.ndb; i += 256) st_co32(dn_done + i, 0u);
+        for (int i = tid; i < PK; i += 256) st_co32(up_done + i * CSTRIDE, 0u);
+        for (int i = tid; i < a.ndb; i += 256) st_co32(dn_done + i * CSTRIDE, 0u);
         if (tid == 0) {
             st_co32(ws + W_TICKET, 0u);
             st_co32(ws + W_ROUTER, 0u);
@@ -591,9 +699,9 @@ static DlLayout dl_layout(int P, int k, int E, int H, int I) {
     L.ndb = (H + DN_ROWS - 1) / DN_ROWS;
     size_t off = W_HDR * 4;
     L.up = (uint32_t)off;
-    off += (size_t)PK * 4;
+    off += (size_t)PK * CSTRIDE * 4;
     L.dn = (uint32_t)off;
-    off += (size_t)L.ndb * 4;
+    off += (size_t)L.ndb * CSTRIDE * 4;
     off = al256(off);
     L.tab = (uint32_t)off;
     off += (size_t)PK * 32;
@@ -623,7 +731,8 @@ extern "C" size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H
 extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in,
                                    const float *w32_in, const int64_t *rtab, void *out, const void *add,
                                    int accumulate, void *logits_out, int64_t *idx_out, void *w_out, float *w32_out,
-                                   float *info, float *miss, void *ws, size_t ws_bytes, int grid, void *stream) {
+                                   float *info, float *miss, void *ws, size_t ws_bytes, int grid, uint64_t *trace,
+                                   void *stream) {
     MOEHIP_REQUIRE(d && x && rtab && out && ws, "decode_layer: null pointer");
     MOEHIP_REQUIRE(Wr != nullptr || (idx_in != nullptr && w32_in != nullptr),
                    "decode_layer: need router weights or precomputed idx/w32");
@@ -654,6 +763,7 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     const DlLayout L = dl_layout(d->P, d->k, d->E, d->H, d->I);
     MOEHIP_REQUIRE(ws_bytes >= L.total, "decode_layer: workspace %zu bytes < %u", ws_bytes, L.total);
     MOEHIP_REQUIRE(((uintptr_t)ws % 256) == 0, "decode_layer: workspace must be 256-byte aligned");
+    MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)Wr % 16) == 0, "decode_layer: x and Wr must be 16-byte aligned");
     LayerArgs a;
     a.x = x;
     a.Wr = Wr;
@@ -694,6 +804,7 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.off_logits = L.logits;
     a.off_h = L.h;
     a.off_part = L.part;
+    a.trace = trace;
     const int PK = d->P * d->k;
     const int total = (Wr != nullptr ? (d->E + 3) / 4 : 1) + PK * (L.nub + L.ndb);
     const int g = grid > 0 ? (grid < total ? grid : total) : total;

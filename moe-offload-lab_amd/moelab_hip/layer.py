@@ -120,6 +120,7 @@ class MoEDecoder:
         self.miss = torch.zeros(1, dtype=torch.float32, device=dev)
         self._pols = [self.policy.device_policy(l) for l in range(store.L)]
         self.grid = grid
+        self.trace = None  # optional (items + 3, 3) int64 device tensor: per-item (start, end, workgroup)
         self.fused = fused and all(store.layouts[p]["precision"] != "fp32" for p in precs) and H <= 2048 \
             and _dims(store.layouts[precs[0]])[1] <= 2048
         if self.fused:
@@ -147,6 +148,14 @@ class MoEDecoder:
             d.lv2p[v] = self.lv2p[v]
         d.pol = self._pols[layer]
         return d
+
+    def work_items(self) -> int:
+        """Number of work items of one fused launch (router rows, up blocks, down blocks)."""
+        d = self._descs[0]
+        nub = (d.I + 15) // 16
+        ndb = (d.H + 63) // 64
+        nr = (d.E + 3) // 4 if self.router_weights is not None else 1
+        return nr + d.P * d.k * (nub + ndb)
 
     def check_error(self) -> None:
         """Raise if a bounded wait inside the fused kernel expired on this decoder's workspace."""
@@ -191,7 +200,7 @@ class MoEDecoder:
                       self.logits.data_ptr(), self.idx.data_ptr() if idx is None else None,
                       self.w.data_ptr() if idx is None else None, self.w32.data_ptr() if idx is None else None,
                       self.info[layer].data_ptr(), self.miss.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
-                      self.grid, _lib.stream_of(x.device))
+                      self.grid, _lib.ptr(self.trace), _lib.stream_of(x.device))
             return out
         if idx is None:
             self.route(layer, x)

@@ -504,3 +504,27 @@ def test_fused_qwen3next_shape(dev, prec):
         assert dec.idx.cpu().numpy().tolist() == idx.tolist()
         assert_layer_close(out.float().cpu().numpy(), ref, dtype)
     dec.check_error()
+
+
+@pytest.mark.parametrize("k", [2, 3, 6, 13])
+def test_fused_router_planted_ties(dev, k):
+    """Fused router on tied logits (including -0 against +0): equal logits go to the lowest
+    expert index, in the oracle's order."""
+    H, I, E = 512, 256, 16
+    S = _Stack(dev, H, I, E, 1, ["int4"], 5)
+    col = torch.tensor([0.1, 0.9, 0.5, -0.0, 0.3, 0.5, 0.4, 0.4, 0.0, 0.5, 0.1, -0.2, 0.3, 0.4, 0.9, 0.0])
+    W = torch.zeros(E, H)
+    W[:, 0] = col
+    S.Wr[0] = W.half()
+    x = torch.zeros(1, H, dtype=torch.float16)
+    x[0, 0] = 1.0
+    dec = MoEDecoder(S.store, k, PrecisionPolicy("lo"), torch.float16, router_weights=[S.Wr[0].to(dev)])
+    assert dec.fused
+    out = torch.zeros(1, H, dtype=torch.float16, device=dev)
+    dec.layer(0, x.to(dev), out)
+    torch.cuda.synchronize()
+    lo, idx, w, ref = S.reference(0, x, k, False, O.Policy("lo"))
+    assert dec.idx.cpu().numpy().tolist() == idx.tolist()
+    assert np.allclose(dec.w32.cpu().numpy(), w, rtol=2.0 ** -10, atol=0)
+    assert_layer_close(out.float().cpu().numpy(), ref, torch.float16)
+    dec.check_error()
