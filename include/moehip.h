@@ -181,8 +181,9 @@ typedef struct moehip_layer_desc {
  * `ws` is caller-owned scratch of moehip_decode_layer_workspace_bytes() bytes, 256-B aligned and
  * zeroed once before its first use; every launch leaves it ready for the next. Launches sharing a
  * workspace must not overlap (one workspace per stream). grid = number of workgroups (0 = one per
- * work item). trace (optional, NULL in production): 3 uint64 per work item = (start, end,
- * workgroup) in the GPU's constant real-time clock, for profiling. H, I multiples of 32 and
+ * work item), clamped to the number the device holds at once (occupancy x CUs). trace (optional, NULL in production): 3 uint64 per work item = (start, end,
+ * workgroup) in the GPU's constant real-time clock, 9 route stamps, then 8 stage stamps per item,
+ * for profiling (tracing adds waits inside the items). H, I multiples of 32 and
  * <= 2048, E <= 1024, k <= 32; x and Wr 16-byte aligned; fp32 records are not supported here.
  * Replaces, for decode, the whole moelab/runtime.py:523-770 `run_layer` GPU path when every
  * expert is resident (the A5 whole-token path, moelab/fullgraph.py:149-188 + graphs.py:351-426).
@@ -192,6 +193,10 @@ int moehip_decode_layer(const moehip_layer_desc *desc, const void *x, const void
                         void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info, float *miss,
                         void *ws, size_t ws_bytes, int grid, uint64_t *trace, void *stream);
 size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H, int I);
+/* Number of work items (tickets) of one moehip_decode_layer launch for this description, with
+ * (with_router = 1) or without the router rows; -1 for a bad description. A grid larger than
+ * this is clamped to it; the per-item trace needs 3 * (items + 3) + 8 * items uint64. */
+int moehip_decode_layer_work_items(const moehip_layer_desc *desc, int with_router);
 /* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device). */
 int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
 

@@ -131,6 +131,65 @@ __device__ __forceinline__ uint32_t fkey(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// sum over aligned groups of G = 2^lg lanes (lg <= 6), valid in the LAST lane of each group:
+// within 16-lane rows by quad_perm / mirrors, then DPP row_bcast:15 (rows 1, 3 += lane 15 of
+// rows 0, 2) and row_bcast:31 (rows 2, 3 += lane 31). Six DPP adds for a whole wave.
+__device__ __forceinline__ float grp_total(float v, int lg) {
+    if (lg >= 1) v += dpp_f<0xB1>(v);
+    if (lg >= 2) v += dpp_f<0x4E>(v);
+    if (lg >= 3) v += dpp_f<0x141>(v);
+    if (lg >= 4) v += dpp_f<0x140>(v);
+    if (lg >= 5) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xA, 0xF, false));
+    if (lg >= 6) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
+// grp_total of N independent values, step-interleaved so the DPP chains overlap
+template <int N>
+__device__ __forceinline__ void grp_total_n(float (&v)[N], int lg) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (lg >= 1) v[i] += dpp_f<0xB1>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (lg >= 2) v[i] += dpp_f<0x4E>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (lg >= 3) v[i] += dpp_f<0x141>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) if (lg >= 4) v[i] += dpp_f<0x140>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (lg >= 5) v[i] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x142, 0xA, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        if (lg >= 6) v[i] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v[i]), 0x143, 0xC, 0xF, false));
+}
+
+// maximum of an unsigned value over the wave, uniform result
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x140>((int)v));
+    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return max(a, b);
+}
+
+// ---------------------------------------------------------------------------------------
+// packed half2 arithmetic: v_dot2_f32_f16 (two fp16 products, exact, accumulated in fp32)
+// ---------------------------------------------------------------------------------------
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2h(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a), __builtin_bit_cast(half2_t, b), c, false);
+}
+// half2 bits of (lo, hi), each rounded to nearest even
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+    return (uint32_t)f32_to_f16_rne(lo) | ((uint32_t)f32_to_f16_rne(hi) << 16);
+}
+// low halves / high halves of two dwords: (a.lo, b.lo) and (a.hi, b.hi)
+__device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
+__device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 }  // namespace moehip

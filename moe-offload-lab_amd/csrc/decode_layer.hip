@@ -2,21 +2,38 @@
 //   router logits -> softmax / top-k / renorm -> HOBBIT levels, resident copy, tables ->
 //   kernel-A rows (h = silu(gate x) * up x) -> kernel-B rows (w * down h) -> combine in table order.
 //
-// Work distribution: every workgroup takes work items from an ordered ticket counter:
-//   [router items: 4 expert rows each][up items: (table row, 16 row pairs)][down items: (table row,
-//   64 output rows)]. An item only waits on items with SMALLER tickets (up waits for the routing,
-//   down for all up items of its table row), and a ticket is only taken by a running workgroup,
-//   so every wait is on work that is already resident and itself never waits on a larger ticket:
-//   the launch always drains. Every wait is also bounded (WAIT_SPINS polls); on expiry the
-//   workgroup records an error in the workspace and moves on, so no launch can hang.
+// Work distribution: the work items are ordered [router items: 4 expert rows each][up items]
+//   [down items], and workgroup b runs items b, b + grid, b + 2 grid, ... in that order. An item
+//   only waits on SMALLER items (the routing waits for the router rows, up items for the routing,
+//   down items for the h rows of their table row, the combining down items for the other rows'
+//   partial sums). The grid is at most what the GPU holds at once (occupancy x CUs), so every
+//   workgroup is, or eventually becomes, resident (other kernels' workgroups drain), and the
+//   smallest unfinished item always belongs to a resident workgroup whose earlier items are done:
+//   the launch always drains, with no shared counter to take items from. Every wait is also
+//   bounded (WAIT_SPINS polls); on expiry the workgroup records an error in the workspace,
+//   treats the missing data as absent and moves on, so no launch can hang.
 //
-// Cross-workgroup data (logits, tables, h, partial rows, counters) is exchanged with agent-scope
-// relaxed atomic loads/stores (gfx950: global accesses with the sc1 coherence bit) ordered by the
-// workgroup barrier's store wait before each counter update, so no L2 writeback/invalidate is
-// needed. The last workgroup to finish resets all counters, leaving the workspace ready for the
-// next launch (also under HIP-graph replay).
+// Items are sized so that every lane holds its whole share of the item's weights (8 x 16 bytes)
+// in registers: an up item issues all its loads as soon as its routing record appears, and a
+// down item issues its loads BEFORE waiting for h, so the layer's weight bytes are all requested
+// right after the routing and the dependency waits overlap the HBM transfers.
 //
-// Determinism: each output row block is summed by the last of its down items, in table order.
+// Cross-workgroup data is TAGGED instead of guarded by counters: every exchanged value (logit,
+// routing record word, h element, partial output row) is one 64-bit word (launch tag << 32 |
+// payload) written with one agent-scope (sc1) atomic store, and a consumer polls the words it
+// needs until they carry this launch's tag. A producer never waits for its stores and nothing
+// needs resetting between launches: the tag is the workspace's launch generation + 1, read by
+// every workgroup at start (from one of NGEN copies) and advanced by the last combining item to
+// finish (every other item is complete by then).
+//
+// Arithmetic (16-bit activations): weights are turned into fp16 pairs with the 1024 + n
+// magic-exponent trick (int4: n in the mantissa low bits, or 16 n for the odd nibble; int8:
+// q + 128) and multiplied with fp16 pairs of the vector by v_dot2_f32_f16 (exact products, fp32
+// accumulation); the constant 1024-offsets are removed with one per-chunk correction term.
+// bf16 vectors and h are scaled per 16-byte weight chunk by a power of two into fp16's range.
+// fp8 / bf16 records and fp32 activations use fp32 FMAs.
+//
+// Determinism: output rows are summed by the down items of the last table row, in table order.
 
 #include <limits.h>
 
@@ -25,14 +42,15 @@
 namespace moehip {
 
 constexpr int DL_MAXP = 4;
-constexpr int DL_MAXROW = 2048;  // 64 lanes x 32 vector values per lane
-constexpr int DL_MAXH = DL_MAXROW;
-constexpr int UP_ROWS = 16;  // row pairs per up item (4 per wave)
-constexpr int DN_ROWS = 64;  // output rows per down item (16 per wave)
-constexpr int WAIT_SPINS = 1 << 22;  // x ~0.3 us per poll: a wait gives up after ~1 s
-// header words, each counter on its own 128-byte line; per-row counters are 32 words apart
-enum { W_TICKET = 0, W_ROUTER = 32, W_READY = 64, W_DONE = 96, W_ERR = 128, W_HDR = 160 };
-constexpr int CSTRIDE = 32;  // words between consecutive up_done / dn_done counters
+constexpr int DL_MAXROW = 2048;       // 64 lanes x 32 vector values per lane
+constexpr int WAIT_SPINS = 1 << 22;   // x ~0.3 us per poll: a wait gives up after ~1 s
+// header words, each on its own 128-byte line: ticket counter, finished workgroups, sticky
+// error flag, launch generation
+// header words: finished combining items, sticky error flag, and NGEN copies of the launch
+// generation 1 KB apart (read by every workgroup at start)
+constexpr int NGEN = 16;
+enum { W_DONE = 0, W_ERR = 32, W_GEN = 256, W_HDR = W_GEN + 256 * NGEN };
+constexpr int NREC = 16;  // copies of every routing record (spreads the polling over memory channels)
 
 struct LayerArgs {
     const void *x;          // (H) activation dtype
@@ -45,8 +63,15 @@ struct LayerArgs {
     int gs_up[DL_MAXP];
     int gs_dn[DL_MAXP];
     int planned[DL_MAXP];
+    int lg_up[DL_MAXP];     // log2 lanes per gate/up row and per down row
+    int lg_dn[DL_MAXP];
+    int nub[DL_MAXP];       // up / down items per table row of precision p
+    int ndb[DL_MAXP];
+    int up_base[DL_MAXP];   // first up / down item of precision p (relative)
+    int dn_base[DL_MAXP];
     int lv2p[3];
     int P, E, k, H, I, renorm, accumulate;
+    int NU, ND;             // up / down items
     moehip_policy pol;
     void *out;              // (H) activation dtype
     const void *add;        // (H) activation dtype or null
@@ -57,9 +82,26 @@ struct LayerArgs {
     float *info;            // (3, k) or null
     float *miss;            // (1) or null
     uint32_t *ws;           // workspace (zeroed once by the caller)
-    int nub, ndb;           // up blocks per table row, down blocks
-    uint32_t off_up, off_dn, off_tab, off_wtab, off_logits, off_h, off_part;  // byte offsets in ws
+    uint32_t off_rec, off_logits, off_h, off_part;  // byte offsets in ws of the tagged arrays
     uint64_t *trace;        // optional per-item trace: [ticket] = (start, end, workgroup) or null
+    uint64_t *stage;        // with trace: 8 stage stamps per item after the trace rows
+};
+
+// ---------------------------------------------------------------------------------------
+// formats: values per 16-byte chunk, chunks per lane (32 values per lane), passes per item
+// (so that a lane holds 8 chunks of an item: 2 * NPU * CPL for gate/up rows, NPD * CPL for
+// down rows), vector pairs per chunk, and whether the fp16 dot2 path applies.
+// ---------------------------------------------------------------------------------------
+template <int PREC> struct DlFmt {
+    static constexpr int VPC = Fmt<PREC>::VPC;
+    static constexpr int CPL = 32 / VPC;
+    static constexpr int NPU = 4 / CPL;
+    static constexpr int NPD = 8 / CPL;
+    static constexpr int XPC = VPC / 2;
+};
+template <int PREC, int XDT> struct UseDot2 {
+    static constexpr bool v = XDT != MOEHIP_DT_F32 &&
+                              (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8 || PREC == MOEHIP_PREC_F16);
 };
 
 // ---------------------------------------------------------------------------------------
@@ -89,32 +131,28 @@ __device__ __forceinline__ uint32_t add_co32(uint32_t *p, uint32_t v) {
 __device__ __forceinline__ void st_co32(uint32_t *p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-
-// Wait until this wave's outstanding memory operations (the sc1 stores above all) have
-// completed; then a workgroup barrier publishes them to the counter update that follows it.
-// (__syncthreads alone is a bare s_barrier on gfx950 and does not wait for global stores.)
-__device__ __forceinline__ void sync_release() {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+// tagged words: (tag << 32) | payload, one atomic 64-bit store / load each
+__device__ __forceinline__ void st_tag(uint64_t *p, uint32_t payload, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint64_t ld_tag(const uint64_t *p) {
+    return __hip_atomic_load(const_cast<uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_ok(uint64_t v, uint32_t tag) { return (uint32_t)(v >> 32) == tag; }
 
-// thread 0 polls until *p >= v, backing off exponentially (s_sleep 1 .. 8, i.e. up to ~500
-// cycles between polls, so hundreds of waiting workgroups do not congest the flag's memory
-// channel); bounded by WAIT_SPINS polls. The caller follows with a barrier.
-__device__ __forceinline__ void wait_geq(uint32_t *p, uint32_t v, uint32_t *err) {
-    int nap = 1;
-    for (int it = 0; it < WAIT_SPINS; ++it) {
-        if (ld_co32(p) >= v) return;
-        switch (nap) {  // s_sleep takes an immediate
-            case 1: __builtin_amdgcn_s_sleep(1); break;
-            case 2: __builtin_amdgcn_s_sleep(2); break;
-            case 4: __builtin_amdgcn_s_sleep(4); break;
-            case 8: __builtin_amdgcn_s_sleep(8); break;
-            case 16: __builtin_amdgcn_s_sleep(16); break;
-            default: __builtin_amdgcn_s_sleep(8); break;
-        }
-        if (nap < 8) nap <<= 1;
+// exponential backoff between polls: s_sleep 1 .. 8 (up to ~500 cycles), so hundreds of
+// polling workgroups do not congest a memory channel
+__device__ __forceinline__ void backoff(int &nap, int cap = 8) {
+    switch (nap) {  // s_sleep takes an immediate
+        case 1: __builtin_amdgcn_s_sleep(1); break;
+        case 2: __builtin_amdgcn_s_sleep(2); break;
+        case 4: __builtin_amdgcn_s_sleep(4); break;
+        case 8: __builtin_amdgcn_s_sleep(8); break;
+        default: __builtin_amdgcn_s_sleep(16); break;
     }
+    if (nap < cap) nap <<= 1;
+}
+__device__ __forceinline__ void flag_error(uint32_t *err) {
     __hip_atomic_fetch_or(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -123,271 +161,574 @@ __device__ __forceinline__ T *ws_ptr(const LayerArgs &a, uint32_t off) {
     return reinterpret_cast<T *>(reinterpret_cast<uint8_t *>(a.ws) + off);
 }
 
-// ---------------------------------------------------------------------------------------
-// LDS staging of a vector in chunk-piece-major order: piece m (4 floats) of chunk c at
-// [(m * C + c) * 4], so that a wave reading piece m of consecutive chunks is conflict free.
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ int vec_slot(int idx4, int npc, int C) { return ((idx4 % npc) * C + idx4 / npc) * 4; }
+// profiling stamp i of the current item (thread 0, trace runs only)
+__device__ __forceinline__ void stamp(uint64_t *st, int i) {
+    if (st != nullptr && threadIdx.x == 0) st[i] = __builtin_amdgcn_s_memrealtime();
+}
+
+// Select element i of a small argument array without dynamic indexing. The elements pass
+// through v_readfirstlane (they are uniform) so that the compiler cannot turn the select of
+// loads into a load from a selected address: that would copy the whole kernel-argument
+// struct to private memory.
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int pick4(const int (&v)[4], int i) {
+    const int v0 = uni(v[0]), v1 = uni(v[1]), v2 = uni(v[2]), v3 = uni(v[3]);
+    return i == 0 ? v0 : (i == 1 ? v1 : (i == 2 ? v2 : v3));
+}
+__device__ __forceinline__ int64_t pick_off(const int64_t (&v)[4][4], int p, int f) {
+    int64_t r[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t a0 = uni64(v[q][0]), a1 = uni64(v[q][1]), a2 = uni64(v[q][2]), a3 = uni64(v[q][3]);
+        r[q] = f == 0 ? a0 : (f == 1 ? a1 : (f == 2 ? a2 : a3));
+    }
+    return p == 0 ? r[0] : (p == 1 ? r[1] : (p == 2 ? r[2] : r[3]));
+}
+// the precision block holding relative item u (base[] ascending, base[0] = 0)
+__device__ __forceinline__ int block_of(const int (&base)[4], int P, int u) {
+    int p = 0;
+    if (P > 1 && u >= uni(base[1])) p = 1;
+    if (P > 2 && u >= uni(base[2])) p = 2;
+    if (P > 3 && u >= uni(base[3])) p = 3;
+    return p;
+}
 
 // ---------------------------------------------------------------------------------------
-// row engines (one wave): dot products of `nrows` weight rows (or row pairs) with the staged vector
+// vector preparation: the 32 vector values of a lane (CPL chunks of VPC values) as fp16 pairs
+// in the order the chunk dot consumes them, plus per chunk the correction of the weights'
+// 1024-offsets and the power of two the chunk was scaled by.
+//   int4: per 8 values (v0,v4) (v1,v5) (v2,v6) (v3,v7); corr = -1032 * sum(even) - 72 * sum(odd)
+//   int8: per 4 values (v0,v2) (v1,v3);                 corr = -1152 * sum
+//   fp16: natural pairs;                                corr = 0
 // ---------------------------------------------------------------------------------------
-// chunks per lane in the fused kernel: every lane holds 32 vector values (rows <= 2048 values)
-template <int PREC> struct FusedCpl { static constexpr int v = 32 / Fmt<PREC>::VPC; };
+constexpr uint32_t H2_M1032 = 0xE408E408u;  // (-1032, -1032)
+constexpr uint32_t H2_M72 = 0xD480D480u;    // (-72, -72)
+constexpr uint32_t H2_M1152 = 0xE480E480u;  // (-1152, -1152)
 
+// pairs of one chunk from 32-bit words w[0 .. VPC/2) (each word = 2 consecutive fp16 values)
 template <int PREC>
-__device__ __forceinline__ void up_rows(const uint8_t *qb, const uint8_t *sb, const float *sv, int r0, int nrows, int I, int H, int gs,
-                        int lg, float *hout) {
-    constexpr int VPC = Fmt<PREC>::VPC;
-    constexpr int NPC = VPC / 4;
-    constexpr int CPL = FusedCpl<PREC>::v;
-    constexpr int D = CPL >= 4 ? 1 : 4 / CPL;  // passes in flight
+__device__ __forceinline__ void pair_chunk(const uint32_t *w, uint32_t *xp, float &corr) {
+    float c = 0.f;
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d0 = w[4 * j + 0], d1 = w[4 * j + 1], d2 = w[4 * j + 2], d3 = w[4 * j + 3];
+            xp[4 * j + 0] = lo_lo(d0, d2);
+            xp[4 * j + 1] = hi_hi(d0, d2);
+            xp[4 * j + 2] = lo_lo(d1, d3);
+            xp[4 * j + 3] = hi_hi(d1, d3);
+            c = dot2h(H2_M1032, xp[4 * j + 0], c);
+            c = dot2h(H2_M72, xp[4 * j + 1], c);
+            c = dot2h(H2_M1032, xp[4 * j + 2], c);
+            c = dot2h(H2_M72, xp[4 * j + 3], c);
+        }
+    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d0 = w[2 * j + 0], d1 = w[2 * j + 1];
+            xp[2 * j + 0] = lo_lo(d0, d1);
+            xp[2 * j + 1] = hi_hi(d0, d1);
+            c = dot2h(H2_M1152, xp[2 * j + 0], c);
+            c = dot2h(H2_M1152, xp[2 * j + 1], c);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xp[j] = w[j];
+    }
+    corr = c;
+}
+
+// fp32 values -> fp16 words scaled by 2^-e (e from the chunk's largest magnitude, so that it
+// lands in [2^14, 2^15)); returns 2^e
+template <int VPC>
+__device__ __forceinline__ float scale_to_h(const float *v, uint32_t *w) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPC; ++i) m = fmaxf(m, fabsf(v[i]));
+    int e = 0;
+    if (m > 0.f && m <= 3.0e38f) e = max(ilogbf(m) - 14, -100);
+    const float down = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int i = 0; i < VPC / 2; ++i) w[i] = pack_h2(v[2 * i] * down, v[2 * i + 1] * down);
+    return ldexpf(1.0f, e);
+}
+
+// (d & mask) | magic in one v_and_or_b32 (the compiler otherwise splits it into two
+// instructions: gfx9 VOP3 encodings take no literal constants)
+__device__ __forceinline__ uint32_t and_or(uint32_t d, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(d), "s"(mask), "v"(magic));
+    return r;
+}
+
+// chunk dot products sum(weight * v) for the dot2 formats (before the group scale)
+template <int PREC>
+__device__ __forceinline__ float dot2_chunk(const uint4 q, const uint32_t *xp, float corr) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+        float ae = corr, ao = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = d[j] >> 8;
+            ae = dot2h(and_or(d[j], 0x000F000Fu, 0x64006400u), xp[4 * j + 0], ae);
+            ao = dot2h(and_or(d[j], 0x00F000F0u, 0x64006400u), xp[4 * j + 1], ao);
+            ae = dot2h(and_or(t, 0x000F000Fu, 0x64006400u), xp[4 * j + 2], ae);
+            ao = dot2h(and_or(t, 0x00F000F0u, 0x64006400u), xp[4 * j + 3], ao);
+        }
+        return fmaf(ao, 0.0625f, ae);
+    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
+        float a0 = corr, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = d[j] ^ 0x80808080u, t = b >> 8;
+            a0 = dot2h(and_or(b, 0x00FF00FFu, 0x64006400u), xp[2 * j + 0], a0);
+            a1 = dot2h(and_or(t, 0x00FF00FFu, 0x64006400u), xp[2 * j + 1], a1);
+        }
+        return a0 + a1;
+    } else {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = dot2h(d[j], xp[j], a);
+        return a;
+    }
+}
+
+// vector registers of one lane for one item format
+template <int PREC, int XDT>
+struct LaneVec {
+    static constexpr bool D2 = UseDot2<PREC, XDT>::v;
+    static constexpr int CPL = DlFmt<PREC>::CPL;
+    uint32_t xp[D2 ? 16 : 1];
+    float corr[CPL];
+    float p2e[CPL];
+    float v[D2 ? 1 : 32];
+    float vs[CPL];
+};
+
+// x (activation dtype, global) -> lane vector; chunk i of the lane is chunk cl + i * G of the row
+template <int PREC, int XDT>
+__device__ __forceinline__ void load_x(const void *x, int cl, int G, int C, LaneVec<PREC, XDT> &lv) {
+    constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = min(cl + i * G, C - 1);  // lanes past the row end compute on a copy, never stored
+        lv.p2e[i] = 1.0f;
+        lv.corr[i] = 0.f;
+        lv.vs[i] = 0.f;
+        if constexpr (XDT == MOEHIP_DT_F32) {
+            const float4 *src = reinterpret_cast<const float4 *>(x) + (size_t)c * (VPC / 4);
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < VPC / 4; ++m) {
+                const float4 f = src[m];
+                lv.v[i * VPC + 4 * m + 0] = f.x;
+                lv.v[i * VPC + 4 * m + 1] = f.y;
+                lv.v[i * VPC + 4 * m + 2] = f.z;
+                lv.v[i * VPC + 4 * m + 3] = f.w;
+                acc += (f.x + f.y) + (f.z + f.w);
+            }
+            lv.vs[i] = acc;
+        } else {
+            const uint4 *src = reinterpret_cast<const uint4 *>(x) + (size_t)c * (VPC / 8);
+            uint32_t w[VPC / 2];
+#pragma unroll
+            for (int m = 0; m < VPC / 8; ++m) {
+                const uint4 u = src[m];
+                w[4 * m + 0] = u.x;
+                w[4 * m + 1] = u.y;
+                w[4 * m + 2] = u.z;
+                w[4 * m + 3] = u.w;
+            }
+            if constexpr (LaneVec<PREC, XDT>::D2) {
+                if constexpr (XDT == MOEHIP_DT_F16) {
+                    pair_chunk<PREC>(w, lv.xp + i * DlFmt<PREC>::XPC, lv.corr[i]);
+                } else {  // bf16 -> fp16 scaled by a power of two
+                    float f[VPC];
+#pragma unroll
+                    for (int m = 0; m < VPC / 2; ++m) {
+                        f[2 * m] = bf16_to_f32(w[m] & 0xffffu);
+                        f[2 * m + 1] = bf16_to_f32(w[m] >> 16);
+                    }
+                    uint32_t hw[VPC / 2];
+                    lv.p2e[i] = scale_to_h<VPC>(f, hw);
+                    pair_chunk<PREC>(hw, lv.xp + i * DlFmt<PREC>::XPC, lv.corr[i]);
+                }
+            } else {
+                float acc = 0.f;
+#pragma unroll
+                for (int m = 0; m < VPC / 2; ++m) {
+                    const float a0 = XDT == MOEHIP_DT_F16 ? f16_to_f32(w[m] & 0xffffu) : bf16_to_f32(w[m] & 0xffffu);
+                    const float a1 = XDT == MOEHIP_DT_F16 ? f16_to_f32(w[m] >> 16) : bf16_to_f32(w[m] >> 16);
+                    lv.v[i * VPC + 2 * m] = a0;
+                    lv.v[i * VPC + 2 * m + 1] = a1;
+                    acc += a0 + a1;
+                }
+                lv.vs[i] = acc;
+            }
+        }
+    }
+}
+
+// h staged in LDS (piece-major: piece m of chunk c at (m * C + c) * 4) -> lane vector
+template <int PREC, int XDT>
+__device__ __forceinline__ void load_h(const float *s_h, int cl, int G, int C, LaneVec<PREC, XDT> &lv) {
+    constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = min(cl + i * G, C - 1);
+        lv.p2e[i] = 1.0f;
+        lv.corr[i] = 0.f;
+        lv.vs[i] = 0.f;
+        float f[VPC];
+#pragma unroll
+        for (int m = 0; m < VPC / 4; ++m) {
+            const float4 u = *reinterpret_cast<const float4 *>(s_h + (m * C + c) * 4);
+            f[4 * m + 0] = u.x;
+            f[4 * m + 1] = u.y;
+            f[4 * m + 2] = u.z;
+            f[4 * m + 3] = u.w;
+        }
+        if constexpr (LaneVec<PREC, XDT>::D2) {
+            uint32_t hw[VPC / 2];
+            lv.p2e[i] = scale_to_h<VPC>(f, hw);
+            pair_chunk<PREC>(hw, lv.xp + i * DlFmt<PREC>::XPC, lv.corr[i]);
+        } else {
+            float acc = 0.f;
+#pragma unroll
+            for (int m = 0; m < VPC; ++m) {
+                lv.v[i * VPC + m] = f[m];
+                acc += f[m];
+            }
+            lv.vs[i] = acc;
+        }
+    }
+}
+
+// sum over the lane's chunk i of weight * vector (before the group scale and 2^e)
+template <int PREC, int XDT>
+__device__ __forceinline__ float lane_dot(const uint4 q, const LaneVec<PREC, XDT> &lv, int i) {
+    if constexpr (LaneVec<PREC, XDT>::D2) {
+        return dot2_chunk<PREC>(q, lv.xp + i * DlFmt<PREC>::XPC, lv.corr[i]);
+    } else {
+        return chunk_dot<PREC>(q, lv.v + i * DlFmt<PREC>::VPC, lv.vs[i]);
+    }
+}
+
+// raw scale bits of chunk c of row `row` (int: fp16 group scale; fp8: fp32 block scale)
+template <int PREC>
+__device__ __forceinline__ uint32_t scale_bits(const uint8_t *sb, int row, int c, int cols, int gs) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) {
+        const int ng = cols / gs;
+        return reinterpret_cast<const uint16_t *>(sb)[(size_t)row * ng + (c * Fmt<PREC>::VPC) / gs];
+    } else if constexpr (PREC == MOEHIP_PREC_FP8) {
+        const int sc = (cols + 127) >> 7;
+        return reinterpret_cast<const uint32_t *>(sb)[(size_t)(row >> 7) * sc + ((c * 16) >> 7)];
+    } else {
+        return 0x3f800000u;
+    }
+}
+template <int PREC>
+__device__ __forceinline__ float scale_val(uint32_t bits) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return f16_to_f32(bits);
+    else return __uint_as_float(bits);
+}
+
+// ---------------------------------------------------------------------------------------
+// up item (one wave's share): NPU passes of RPW row pairs, h[r] = silu(gate_r . x) * (up_r . x)
+// ---------------------------------------------------------------------------------------
+template <int PREC, int XDT>
+__device__ __forceinline__ void up_rows(const uint8_t *qb, const uint8_t *sb, const LaneVec<PREC, XDT> &lv, int pair0,
+                                        int I, int H, int gs, int lg, uint64_t *hout, uint32_t tag, uint64_t *st) {
+    constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL, NPU = DlFmt<PREC>::NPU;
     const int lane = threadIdx.x & 63;
     const int G = 1 << lg, RPW = 64 >> lg;
     const int slot = lane >> lg, cl = lane & (G - 1);
     const int C = H / VPC;
     const size_t RB = (size_t)C * 16;
-    float v[CPL][VPC];
-    float vs[CPL];
+    uint4 qg[NPU][CPL], qu[NPU][CPL];
+    uint32_t sg[NPU][CPL], su[NPU][CPL];
+    // branch-free: out-of-range lanes load an in-range chunk and get a zero scale
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = min(cl + i * G, C - 1);
-        float acc = 0.f;
+    for (int p = 0; p < NPU; ++p) {
+        const int r0 = pair0 + p * RPW + slot;
+        const int r = min(r0, I - 1);
 #pragma unroll
-        for (int m = 0; m < NPC; ++m) {
-            const float4 p4 = *reinterpret_cast<const float4 *>(sv + (m * C + c) * 4);
-            v[i][4 * m + 0] = p4.x;
-            v[i][4 * m + 1] = p4.y;
-            v[i][4 * m + 2] = p4.z;
-            v[i][4 * m + 3] = p4.w;
-            acc += (p4.x + p4.y) + (p4.z + p4.w);
-        }
-        vs[i] = acc;
-    }
-    const int npass = (nrows + RPW - 1) / RPW;
-    for (int pb = 0; pb < npass; pb += D) {
-        uint4 qg[D][CPL], qu[D][CPL];
-        float sg[D][CPL], su[D][CPL];
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int rp = (pb + d) * RPW + slot;
-            const int r = r0 + rp;
-            const bool rok = (pb + d) < npass && rp < nrows && r < I;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) {
-                const int c = cl + i * G;
-                if (rok && c < C) {
-                    qg[d][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
-                    qu[d][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)(r + I) * RB + (size_t)c * 16);
-                    sg[d][i] = chunk_scale<PREC>(sb, r, c, H, gs);
-                    su[d][i] = chunk_scale<PREC>(sb, r + I, c, H, gs);
-                } else {
-                    qg[d][i] = make_uint4(0, 0, 0, 0);
-                    qu[d][i] = make_uint4(0, 0, 0, 0);
-                    sg[d][i] = 0.f;
-                    su[d][i] = 0.f;
-                }
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            float pg = 0.f, pu = 0.f;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) {
-                pg = fmaf(sg[d][i], chunk_dot<PREC>(qg[d][i], v[i], vs[i]), pg);
-                pu = fmaf(su[d][i], chunk_dot<PREC>(qu[d][i], v[i], vs[i]), pu);
-            }
-            pg = group_sum(pg, lg);
-            pu = group_sum(pu, lg);
-            const int rp = (pb + d) * RPW + slot;
-            const int r = r0 + rp;
-            if (cl == 0 && (pb + d) < npass && rp < nrows && r < I) st_co(hout + r, silu_mul(pg, pu));
+        for (int i = 0; i < CPL; ++i) {
+            const int c0 = cl + i * G;
+            const int c = min(c0, C - 1);
+            const bool ok = r0 < I && c0 < C;
+            qg[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
+            qu[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)(r + I) * RB + (size_t)c * 16);
+            const uint32_t a0 = scale_bits<PREC>(sb, r, c, H, gs), a1 = scale_bits<PREC>(sb, r + I, c, H, gs);
+            sg[p][i] = ok ? a0 : 0u;
+            su[p][i] = ok ? a1 : 0u;
         }
     }
+    if (st != nullptr) {  // profiling: separate the load latency from the arithmetic
+        __builtin_amdgcn_s_waitcnt(0);
+        stamp(st, 2);
+    }
+    // every pass's dot products first (independent: the compiler interleaves them), then the
+    // lane-group reductions step by step over all values, then h = silu(g) * u
+    float v[2 * NPU];
+#pragma unroll
+    for (int p = 0; p < NPU; ++p) {
+        float pg = 0.f, pu = 0.f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            pg = fmaf(scale_val<PREC>(sg[p][i]) * lv.p2e[i], lane_dot<PREC, XDT>(qg[p][i], lv, i), pg);
+            pu = fmaf(scale_val<PREC>(su[p][i]) * lv.p2e[i], lane_dot<PREC, XDT>(qu[p][i], lv, i), pu);
+        }
+        v[2 * p] = pg;
+        v[2 * p + 1] = pu;
+    }
+    grp_total_n<2 * NPU>(v, lg);
+    if (cl == G - 1) {
+#pragma unroll
+        for (int p = 0; p < NPU; ++p) {
+            const int r = pair0 + p * RPW + slot;
+            if (r < I) st_tag(hout + r, __float_as_uint(silu_mul(v[2 * p], v[2 * p + 1])), tag);
+        }
+    }
+    stamp(st, 3);
 }
 
+// ---------------------------------------------------------------------------------------
+// down item (one wave's share): weights loaded first, then (after the caller's wait) h and
+// NPD passes of RPW rows, partial[r] = wt * (down_r . h)
+// ---------------------------------------------------------------------------------------
 template <int PREC>
-__device__ __forceinline__ void down_rows(const uint8_t *qb, const uint8_t *sb, const float *sv, int r0, int nrows, int H, int I,
-                          int gs, int lg, float wt, float *pout) {
-    constexpr int VPC = Fmt<PREC>::VPC;
-    constexpr int NPC = VPC / 4;
-    constexpr int CPL = FusedCpl<PREC>::v;
-    constexpr int D = CPL >= 4 ? 1 : 4 / CPL;
+struct DownRegs {
+    uint4 q[DlFmt<PREC>::NPD][DlFmt<PREC>::CPL];
+    uint32_t s[DlFmt<PREC>::NPD][DlFmt<PREC>::CPL];
+};
+
+template <int PREC>
+__device__ __forceinline__ void down_load(const uint8_t *qb, const uint8_t *sb, int row0, int H, int I, int gs, int lg,
+                                          DownRegs<PREC> &d) {
+    constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL, NPD = DlFmt<PREC>::NPD;
     const int lane = threadIdx.x & 63;
     const int G = 1 << lg, RPW = 64 >> lg;
     const int slot = lane >> lg, cl = lane & (G - 1);
     const int C = I / VPC;
     const size_t RB = (size_t)C * 16;
-    float v[CPL][VPC];
-    float vs[CPL];
+    // branch-free: out-of-range lanes load an in-range chunk and get a zero scale
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        const int c = min(cl + i * G, C - 1);
+    for (int p = 0; p < NPD; ++p) {
+        const int r0 = row0 + p * RPW + slot;
+        const int r = min(r0, H - 1);
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+            const int c0 = cl + i * G;
+            const int c = min(c0, C - 1);
+            d.q[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
+            const uint32_t sv = scale_bits<PREC>(sb, r, c, I, gs);
+            d.s[p][i] = (r0 < H && c0 < C) ? sv : 0u;
+        }
+    }
+}
+
+template <int PREC, int XDT>
+__device__ __forceinline__ void down_rows(const DownRegs<PREC> &d, const LaneVec<PREC, XDT> &lv, int row0, int H,
+                                          int lg, float wt, uint64_t *pout, uint32_t tag) {
+    constexpr int CPL = DlFmt<PREC>::CPL, NPD = DlFmt<PREC>::NPD;
+    const int lane = threadIdx.x & 63;
+    const int G = 1 << lg, RPW = 64 >> lg;
+    const int slot = lane >> lg, cl = lane & (G - 1);
+    float v[NPD];
+#pragma unroll
+    for (int p = 0; p < NPD; ++p) {
         float acc = 0.f;
 #pragma unroll
-        for (int m = 0; m < NPC; ++m) {
-            const float4 p4 = *reinterpret_cast<const float4 *>(sv + (m * C + c) * 4);
-            v[i][4 * m + 0] = p4.x;
-            v[i][4 * m + 1] = p4.y;
-            v[i][4 * m + 2] = p4.z;
-            v[i][4 * m + 3] = p4.w;
-            acc += (p4.x + p4.y) + (p4.z + p4.w);
-        }
-        vs[i] = acc;
+        for (int i = 0; i < CPL; ++i)
+            acc = fmaf(scale_val<PREC>(d.s[p][i]) * lv.p2e[i], lane_dot<PREC, XDT>(d.q[p][i], lv, i), acc);
+        v[p] = acc;
     }
-    const int npass = (nrows + RPW - 1) / RPW;
-    for (int pb = 0; pb < npass; pb += D) {
-        uint4 qd[D][CPL];
-        float sd[D][CPL];
+    grp_total_n<NPD>(v, lg);
+    if (cl == G - 1) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int rr = (pb + d) * RPW + slot;
-            const int r = r0 + rr;
-            const bool rok = (pb + d) < npass && rr < nrows && r < H;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) {
-                const int c = cl + i * G;
-                if (rok && c < C) {
-                    qd[d][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
-                    sd[d][i] = chunk_scale<PREC>(sb, r, c, I, gs);
-                } else {
-                    qd[d][i] = make_uint4(0, 0, 0, 0);
-                    sd[d][i] = 0.f;
-                }
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) acc = fmaf(sd[d][i], chunk_dot<PREC>(qd[d][i], v[i], vs[i]), acc);
-            acc = group_sum(acc, lg);
-            const int rr = (pb + d) * RPW + slot;
-            const int r = r0 + rr;
-            if (cl == 0 && (pb + d) < npass && rr < nrows && r < H) st_co(pout + r, wt * acc);
+        for (int p = 0; p < NPD; ++p) {
+            const int r = row0 + p * RPW + slot;
+            if (r < H) st_tag(pout + r, __float_as_uint(wt * v[p]), tag);
         }
     }
 }
 
-__device__ __forceinline__ int vpc_dev(int prec) {
-    return prec == MOEHIP_PREC_INT4 ? 32 : (prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8) ? 16
-           : (prec == MOEHIP_PREC_F32 ? 4 : 8);
-}
-
-// log2 of the lanes per row for rows of `cols` values (32 values per lane)
-__device__ __forceinline__ int row_lg(int cols) {
-    const int lanes = (cols + 31) / 32;
-    int G = 1, lg = 0;
-    while (G < lanes && G < 64) G <<= 1, ++lg;
-    return lg;
-}
-
-// select element i of a small argument array without dynamic indexing (kernel arguments
-// indexed by a run-time value would be copied to private memory)
-template <typename T>
-__device__ __forceinline__ T pick4(const T (&v)[4], int i) {
-    return i == 0 ? v[0] : (i == 1 ? v[1] : (i == 2 ? v[2] : v[3]));
-}
-__device__ __forceinline__ int64_t pick_off(const int64_t (&v)[4][4], int p, int f) {
-    const int64_t r0 = f == 0 ? v[0][0] : (f == 1 ? v[0][1] : (f == 2 ? v[0][2] : v[0][3]));
-    const int64_t r1 = f == 0 ? v[1][0] : (f == 1 ? v[1][1] : (f == 2 ? v[1][2] : v[1][3]));
-    const int64_t r2 = f == 0 ? v[2][0] : (f == 1 ? v[2][1] : (f == 2 ? v[2][2] : v[2][3]));
-    const int64_t r3 = f == 0 ? v[3][0] : (f == 1 ? v[3][1] : (f == 2 ? v[3][2] : v[3][3]));
-    return p == 0 ? r0 : (p == 1 ? r1 : (p == 2 ? r2 : r3));
-}
-
 // ---------------------------------------------------------------------------------------
-// route tail: softmax / top-k / renorm / HOBBIT / resident copy / tables (wave 0 of one WG)
+// route tail: softmax / top-k / renorm / HOBBIT / resident copy / tables (wave 0 of one WG).
+// Logits and keys are staged in LDS (lane l handles l, l + 64, ...). Top-k: k rounds of a wave-wide maximum over
+// 32-bit keys; for 16-bit activations the key packs the order-preserving bits of the logit
+// above (1023 - index), so one maximum gives the largest logit and, among equal logits, the
+// lowest index (torch.topk / the reference order); fp32 logits take a second maximum for the
+// index among equal keys.
 // ---------------------------------------------------------------------------------------
+// words between record copies: P * k rows of 3 words, rounded up to 1 KB
+__host__ __device__ __forceinline__ size_t rec_stride_words(int P, int k) { return (size_t)((P * k * 24 + 1023) / 1024) * 128; }
+
 template <int XDT>
-__device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float *s_w, float *s_l, uint64_t *ts) {
-    const int lane = threadIdx.x;  // wave 0 only; s_l: E floats of LDS (+ 2 x 32 candidate slots)
+__device__ __forceinline__ uint32_t logit_key(float v, int c) {
+    if constexpr (XDT == MOEHIP_DT_F32) {
+        (void)c;
+        return fkey(v);
+    } else {
+        uint32_t b = XDT == MOEHIP_DT_F16 ? (uint32_t)f32_to_f16_rne(v) : (__float_as_uint(v) >> 16);
+        if (v == 0.f) b = 0u;
+        const uint32_t k16 = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+        return (k16 << 10) | (uint32_t)(1023 - c);
+    }
+}
+
+// record of table row jj (P * k rows, precision-major): 3 tagged words
+//   [0] = weight bits (0 = nothing to run), [1] / [2] = low / high half of the record address;
+// NREC copies, copy c of row jj at word c * rec_stride_words(P, k) + jj * 3
+template <int XDT>
+__device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int *s_idx, float *s_w, float *s_sorted,
+                                           float *s_buf, uint32_t *err, uint64_t *ts) {
+    const int lane = threadIdx.x;  // wave 0 only; s_buf: 2 * 1024 words of LDS (logits, keys)
     const int k = a.k, E = a.E;
-    const unsigned long long lt = (1ull << lane) - 1ull;  // lanes below this one
+    const int epl = (E + 63) >> 6;
+    float *s_lv = s_buf;
+    uint32_t *s_key = reinterpret_cast<uint32_t *>(s_buf + 1024);
 #define TS(i) do { if (ts != nullptr && lane == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
     TS(0);
+    if (ts != nullptr && lane == 0) ts[6] = __builtin_amdgcn_s_memtime();  // core clock, for the clock rate
+    int myc = 0;      // lane j < k: expert of rank j
+    float myw = 0.f;  // and its fp32 weight (rounded to the activation dtype)
+    int64_t rt[DL_MAXP] = {0, 0, 0, 0};  // and the addresses of its resident records
     if (a.Wr != nullptr) {
-        const float *logits = ws_ptr<float>(a, a.off_logits);
-        float m = -INFINITY;
-        for (int c = lane; c < E; c += 64) {
-            const float v = ld_co(logits + c);
-            s_l[c] = v;
-            m = fmaxf(m, v);
-            if (a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, v);
-        }
-        m = wave_max(m);
-        TS(1);
-        float sum = 0.f;
-        for (int c = lane; c < E; c += 64) sum += expf(s_l[c] - m);
-        sum = wave_sum(sum);
-        // k-th largest logit by radix select over order-preserving keys (MSB first)
-        uint32_t prefix = 0, mask = 0;
-        int need = k;
-        for (int b = 31; b >= 0; --b) {
-            const uint32_t bit = 1u << b, cand = prefix | bit, m2 = mask | bit;
-            int cnt = 0;
-            for (int c = lane; c < E; c += 64) cnt += (fkey(s_l[c]) & m2) == cand;
-            cnt = wave_sum_i(cnt);
-            if (cnt >= need) prefix = cand;
-            else need -= cnt;
-            mask = m2;
-        }
-        // the k winners: every key above the k-th, then the `need` lowest-index keys equal to it
-        float *cv = s_l + E;                              // candidate values
-        int *ci = reinterpret_cast<int *>(s_l + E + 32);  // candidate indices
-        int nsel = 0, neq = 0;
-        for (int c0 = 0; c0 < E; c0 += 64) {
-            const int c = c0 + lane;
-            const uint32_t key = c < E ? fkey(s_l[c]) : 0u;
-            const bool gt = c < E && key > prefix;
-            const bool eq = c < E && key == prefix;
-            const unsigned long long eqm = __ballot(eq);
-            const bool sel = gt || (eq && neq + __popcll(eqm & lt) < need);
-            const unsigned long long sm = __ballot(sel);
-            if (sel) {
-                const int pos = nsel + __popcll(sm & lt);
-                cv[pos] = s_l[c];
-                ci[pos] = c;
+        const uint64_t *logits = ws_ptr<uint64_t>(a, a.off_logits);
+        // every logit of this launch (written by the router items, smaller tickets)
+        uint32_t need = 0;
+        for (int i = 0; i < epl; ++i)
+            if (lane + 64 * i < E) need |= 1u << i;
+        int nap = 1;
+        for (int it = 0; it < WAIT_SPINS && __ballot(need != 0) != 0ull; ++it) {
+            for (int i = 0; i < epl; ++i) {
+                if (need & (1u << i)) {
+                    const int c = lane + 64 * i;
+                    const uint64_t v = ld_tag(logits + c);
+                    if (tag_ok(v, tag)) {
+                        const float l = __uint_as_float((uint32_t)v);
+                        s_lv[c] = l;
+                        s_key[c] = logit_key<XDT>(l, c);
+                        if (a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, l);
+                        need &= ~(1u << i);
+                    }
+                }
             }
-            nsel += __popcll(sm);
-            neq += __popcll(eqm);
+            if (__ballot(need != 0) != 0ull) backoff(nap);
+            if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
+        }
+        for (int i = 0; i < epl; ++i) {  // logits still missing after the wait: never chosen
+            if (need & (1u << i)) {
+                s_lv[lane + 64 * i] = -INFINITY;
+                s_key[lane + 64 * i] = 0u;
+            }
         }
         __builtin_amdgcn_wave_barrier();
-        // order the winners by (logit desc, index asc), probabilities, renorm, outputs
-        float p = 0.f;
-        int rank = 0, myidx = 0;
-        if (lane < k) {
-            const float v = cv[lane];
-            myidx = ci[lane];
-            for (int i = 0; i < k; ++i) {
-                const float o = cv[i];
-                rank += (o > v) || (o == v && ci[i] < myidx);
+        TS(1);
+        float myv = 0.f;
+        if (E <= 64) {
+            // one logit per lane: its rank is the number of larger keys (keys are distinct for
+            // 16-bit logits; fp32 ties go to the lower index)
+            for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t key = lane < E ? s_key[lane] : 0u;
+            const float lvv = lane < E ? s_lv[lane] : -INFINITY;
+            int rank = 0;
+#pragma unroll
+            for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast)
+                if (q < E) {
+                    const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
+                    const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
+                        else rank += ov[u] > key;
+                    }
+                }
             }
-            p = expf(v - m) / sum;
+            if (lane < E && rank < k) {
+                s_key[512 + rank] = (uint32_t)lane;
+                s_lv[512 + rank] = lvv;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane < k) {
+                myc = (int)s_key[512 + lane];
+                myv = s_lv[512 + lane];
+            }
         }
-        const float tot = a.renorm ? wave_sum(lane < k ? p : 0.f) : 1.f;
+        for (int r = 0; r < k && E > 64; ++r) {
+            uint32_t lb = 0u;
+            int lc = lane;
+            for (int i = 0; i < epl; ++i) {
+                const int c = lane + 64 * i;
+                const uint32_t kk = c < E ? s_key[c] : 0u;
+                if (kk > lb) lb = kk, lc = c;
+            }
+            const uint32_t M = wave_max_u32(lb);
+            int c;
+            if constexpr (XDT == MOEHIP_DT_F32) {
+                // among lanes holding the maximum key, the lowest expert index
+                const uint32_t cand = lb == M ? (uint32_t)(1023 - lc) : 0u;
+                c = 1023 - (int)wave_max_u32(cand);
+            } else {
+                (void)lc;
+                c = 1023 - (int)(M & 1023u);
+            }
+            c = min(c, E - 1);
+            const float v = s_lv[c];
+            __builtin_amdgcn_wave_barrier();
+            if (lane == (c & 63)) s_key[c] = 0u;
+            __builtin_amdgcn_wave_barrier();
+            if (lane == r) {
+                myc = c;
+                myv = v;
+            }
+        }
         TS(2);
+        if (lane < k && myc >= 0 && myc < E) {  // residency loads overlap the softmax below
+#pragma unroll
+            for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.rtab[(size_t)pi * E + myc] : 0;
+        }
+        const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
+        float sum = 0.f;
+        for (int i = 0; i < epl; ++i)
+            if (lane + 64 * i < E) sum += expf(s_lv[lane + 64 * i] - m);
+        sum = wave_sum(sum);
+        const float p = lane < k ? expf(myv - m) / sum : 0.f;
+        const float tot = a.renorm ? wave_sum(p) : 1.f;
         if (lane < k) {
             const float pw = a.renorm ? p / tot : p;
-            const float r = rnd_act<XDT>(pw);
-            s_idx[rank] = myidx;
-            s_w[rank] = r;
-            if (a.idx_out) a.idx_out[rank] = myidx;
-            if (a.w_out) st_act<XDT>(a.w_out, rank, pw);
-            if (a.w32_out) a.w32_out[rank] = r;
+            myw = rnd_act<XDT>(pw);
+            if (a.idx_out) a.idx_out[lane] = myc;
+            if (a.w_out) st_act<XDT>(a.w_out, lane, pw);
+            if (a.w32_out) a.w32_out[lane] = myw;
         }
     } else if (lane < k) {
-        s_idx[lane] = (int)a.idx_in[lane];
-        s_w[lane] = a.w32_in[lane];
+        myc = (int)a.idx_in[lane];
+        myw = a.w32_in[lane];
+        if (myc >= 0 && myc < E) {
+#pragma unroll
+            for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.rtab[(size_t)pi * E + myc] : 0;
+        }
     }
-    __builtin_amdgcn_wave_barrier();
     TS(3);
     // HOBBIT levels (moelab/policy.py:77-123), resident copy, tables (moelab/fullgraph.py:149-171)
-    float *s_sorted = s_l;  // reused: k floats
     const int j = lane;
     const bool act = j < k;
-    const int e = act ? s_idx[j] : 0;
-    const float wj = act ? s_w[j] : 0.f;
+    const int e = act ? myc : 0;
+    if (act) {
+        s_idx[j] = e;
+        s_w[j] = myw;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const float wj = act ? myw : 0.f;
     float tot = 0.f;
     for (int i = 0; i < k; ++i) tot += s_w[i];
     tot = fmaxf(tot, 1e-12f);
@@ -405,7 +746,6 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
             const float o = s_w[i] / tot;
             rank += (o > wn) || (o == wn && i < j);
         }
-        __builtin_amdgcn_wave_barrier();
         if (act) s_sorted[rank] = wn;
         __builtin_amdgcn_wave_barrier();
         float cs = 0.f;
@@ -417,24 +757,32 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
         skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
     }
     TS(4);
-    const int req = lvl == 0 ? a.lv2p[0] : (lvl == 1 ? a.lv2p[1] : a.lv2p[2]);
+    const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
+    const int req = lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2);
     int chosen = -1;
-    for (int pi = a.P - 1; pi >= 0; --pi) {
-        const bool avail = act && e >= 0 && e < E && a.rtab[(size_t)pi * E + e] != 0;
+#pragma unroll
+    for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
+        const bool avail = pi < a.P && rt[pi] != 0;
         if (avail && (pol.upgrade ? req >= pi : req == pi)) chosen = pi;
     }
-    TS(5);
     const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
     const bool is_miss = act && !skip && !usable;
-    int64_t *tab = ws_ptr<int64_t>(a, a.off_tab);
-    float *wtab = ws_ptr<float>(a, a.off_wtab);
+    uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec);
+    // the chosen copy (address, weight) of this row; compact loops keep the register use small
+    const bool sel = act && chosen >= 0 && !skip && usable;
+    const int64_t base = !sel ? 0 : (chosen == 0 ? rt[0] : (chosen == 1 ? rt[1] : (chosen == 2 ? rt[2] : rt[3])));
+    const uint32_t wbits = sel ? __float_as_uint(wj) : 0u;
     if (act) {
+#pragma unroll 1
         for (int pi = 0; pi < a.P; ++pi) {
-            const bool sel = chosen == pi && !skip && pick4(a.planned, pi) != 0;
-            const int64_t base = sel ? a.rtab[(size_t)pi * E + e] : 0;
-            for (int f = 0; f < 4; ++f)
-                st_co64(tab + ((size_t)pi * k + j) * 4 + f, sel ? base + pick_off(a.offs, pi, f) : 0);
-            st_co(wtab + (size_t)pi * k + j, sel ? wj : 0.f);
+            const bool mine = sel && chosen == pi;
+#pragma unroll 1
+            for (int cp = 0; cp < NREC; ++cp) {
+                uint64_t *r3 = rec + (size_t)cp * rec_stride_words(a.P, k) + ((size_t)pi * k + j) * 3;
+                st_tag(r3 + 1, mine ? (uint32_t)(uint64_t)base : 0u, tag);
+                st_tag(r3 + 2, mine ? (uint32_t)((uint64_t)base >> 32) : 0u, tag);
+                st_tag(r3 + 0, mine ? wbits : 0u, tag);
+            }
         }
         if (a.info) {
             a.info[j] = (float)e;
@@ -442,11 +790,245 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
             a.info[2 * k + j] = (float)lvl;
         }
     }
-    TS(6);
+    TS(5);
+    if (ts != nullptr && lane == 0) ts[7] = __builtin_amdgcn_s_memtime();
     const unsigned long long bal = __ballot(is_miss);
     if (j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
-    TS(7);
 #undef TS
+}
+
+// ---------------------------------------------------------------------------------------
+// router item: 4 expert rows (one per wave), each lane 32 consecutive values (H <= 2048)
+// ---------------------------------------------------------------------------------------
+template <int XDT>
+__device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t tag) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int e = t * 4 + wave;
+    if (e >= a.E) return;
+    constexpr int ESZ = XDT == MOEHIP_DT_F32 ? 4 : 2;
+    constexpr int NV = 32 * ESZ / 16;  // 16-byte vectors per lane
+    const int c0 = lane * 32;
+    float acc = 0.f;
+    if (c0 < a.H) {
+        const uint8_t *wp = reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ;
+        const uint8_t *xp = reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * ESZ;
+        uint4 wv[NV], xv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            wv[i] = reinterpret_cast<const uint4 *>(wp)[i];
+            xv[i] = reinterpret_cast<const uint4 *>(xp)[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+            const uint32_t xd[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (XDT == MOEHIP_DT_F32) {
+                    acc = fmaf(__uint_as_float(wd[q]), __uint_as_float(xd[q]), acc);
+                } else if constexpr (XDT == MOEHIP_DT_F16) {
+                    acc = fmaf(f16_to_f32(wd[q] & 0xffffu), f16_to_f32(xd[q] & 0xffffu), acc);
+                    acc = fmaf(f16_to_f32(wd[q] >> 16), f16_to_f32(xd[q] >> 16), acc);
+                } else {
+                    acc = fmaf(__uint_as_float(wd[q] << 16), __uint_as_float(xd[q] << 16), acc);
+                    acc = fmaf(__uint_as_float(wd[q] & 0xffff0000u), __uint_as_float(xd[q] & 0xffff0000u), acc);
+                }
+            }
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) st_tag(ws_ptr<uint64_t>(a, a.off_logits) + e, __float_as_uint(rnd_act<XDT>(acc)), tag);
+}
+
+// ---------------------------------------------------------------------------------------
+// up / down items of one precision
+// ---------------------------------------------------------------------------------------
+struct Route {
+    float w;
+    uint64_t base;
+};
+
+// wait for routing record jj (3 tagged words, lanes 0..2 of wave 0, copy blockIdx % NREC) and
+// share it through LDS; on expiry the row is treated as not routed (w = 0) and the error flag
+// is set. Every thread of the workgroup must call this.
+__device__ __forceinline__ Route wg_route(const LayerArgs &a, uint32_t tag, int jj, float *s_r, uint32_t *err) {
+    const int tid = threadIdx.x;
+    if (tid < 64) {
+        const uint64_t *r3 =
+            ws_ptr<uint64_t>(a, a.off_rec) + (size_t)(blockIdx.x % NREC) * rec_stride_words(a.P, a.k) + (size_t)jj * 3;
+        int nap = 1;
+        bool got = false;
+        uint32_t p = 0;
+        for (int it = 0; it < WAIT_SPINS; ++it) {
+            const uint64_t v = tid < 3 ? ld_tag(r3 + tid) : ((uint64_t)tag << 32);
+            if (__ballot(!tag_ok(v, tag)) == 0ull) {
+                p = (uint32_t)v;
+                got = true;
+                break;
+            }
+            backoff(nap, 16);  // the routing is microseconds away: poll gently
+        }
+        if (!got) {
+            p = 0u;
+            if (tid == 0) flag_error(err);
+        }
+        if (tid < 3) s_r[tid] = __uint_as_float(p);
+    }
+    __syncthreads();
+    Route r;
+    r.w = s_r[0];
+    r.base = ((uint64_t)__float_as_uint(s_r[2]) << 32) | __float_as_uint(s_r[1]);
+    if (r.base == 0) r.w = 0.f;
+    __syncthreads();  // s_r may be rewritten by the next item
+    return r;
+}
+
+template <int PREC, int XDT>
+__device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, float *s_r,
+                                        uint32_t *err, int item) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lg = pick4(a.lg_up, pi);
+    const int G = 1 << lg, RPW = 64 >> lg;
+    const int C = a.H / DlFmt<PREC>::VPC;
+    LaneVec<PREC, XDT> lv;
+    uint64_t *st = a.stage != nullptr ? a.stage + 8 * (size_t)item : nullptr;
+    load_x<PREC, XDT>(a.x, lane & (G - 1), G, C, lv);  // before the routing wait
+    stamp(st, 0);
+    const Route rt = wg_route(a, tag, jj, s_r, err);
+    stamp(st, 1);
+    if (rt.w == 0.f) return;
+    const int per_wave = DlFmt<PREC>::NPU * RPW;
+    const int pair0 = b * per_wave * 4 + wave * per_wave;
+    const uint8_t *qb = reinterpret_cast<const uint8_t *>(rt.base + pick_off(a.offs, pi, 0));
+    const uint8_t *sb = reinterpret_cast<const uint8_t *>(rt.base + pick_off(a.offs, pi, 1));
+    uint64_t *hout = ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I;
+    up_rows<PREC, XDT>(qb, sb, lv, pair0, a.I, a.H, pick4(a.gs_up, pi), lg, hout, tag, st);
+}
+
+// h row jj of this launch -> LDS (piece-major for chunks of VPC values); false on expiry
+template <int VPC>
+__device__ __forceinline__ bool stage_h(const uint64_t *h, int I, uint32_t tag, float *s_h, uint32_t *err) {
+    const int tid = threadIdx.x;
+    const int C = I / VPC;
+    int nap = 1;
+    // the last element comes from the row's last up item: wait for it with one lane before
+    // polling the whole row (keeps the polling traffic of waiting workgroups small)
+    if (tid == 0) {
+        for (int it = 0; it < WAIT_SPINS; ++it) {
+            if (tag_ok(ld_tag(h + I - 1), tag)) break;
+            backoff(nap);
+        }
+    }
+    __syncthreads();
+    nap = 1;
+    for (int it = 0; it < WAIT_SPINS; ++it) {
+        int missing = 0;
+        for (int i = tid; i < I; i += 256) {
+            const uint64_t v = ld_tag(h + i);
+            if (tag_ok(v, tag)) {
+                const int c = i / VPC, q = i % VPC;
+                s_h[((q >> 2) * C + c) * 4 + (q & 3)] = __uint_as_float((uint32_t)v);
+            } else {
+                missing = 1;
+            }
+        }
+        if (!__syncthreads_or(missing)) return true;
+        backoff(nap);
+    }
+    if (tid == 0) flag_error(err);
+    return false;
+}
+
+template <int PREC, int XDT>
+__device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, float *s_h,
+                                          float *s_wk, uint32_t *err, int item) {
+    uint64_t *st = a.stage != nullptr ? a.stage + 8 * (size_t)item : nullptr;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lg = pick4(a.lg_dn, pi);
+    const int G = 1 << lg, RPW = 64 >> lg;
+    const int per_wave = DlFmt<PREC>::NPD * RPW;
+    const int row0 = b * per_wave * 4 + wave * per_wave;
+    const int PK = a.P * a.k;
+    const Route rt0 = wg_route(a, tag, jj, s_wk, err);
+    stamp(st, 1);
+    const bool run = rt0.w != 0.f;
+    uint64_t *part = ws_ptr<uint64_t>(a, a.off_part);
+    if (run) {
+        DownRegs<PREC> d;
+        down_load<PREC>(reinterpret_cast<const uint8_t *>(rt0.base + pick_off(a.offs, pi, 2)),
+                        reinterpret_cast<const uint8_t *>(rt0.base + pick_off(a.offs, pi, 3)), row0, a.H, a.I,
+                        pick4(a.gs_dn, pi), lg, d);
+        if (st != nullptr) {
+            __builtin_amdgcn_s_waitcnt(0);
+            stamp(st, 2);
+        }
+        if (stage_h<DlFmt<PREC>::VPC>(ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I, a.I, tag, s_h, err)) {
+            stamp(st, 3);
+            LaneVec<PREC, XDT> lv;
+            load_h<PREC, XDT>(s_h, lane & (G - 1), G, a.I / DlFmt<PREC>::VPC, lv);
+            down_rows<PREC, XDT>(d, lv, row0, a.H, lg, rt0.w, part + (size_t)jj * a.H, tag);
+            stamp(st, 4);
+        }
+        __syncthreads();  // s_h is reused by the next item
+    }
+    if (jj != PK - 1) return;
+    // the last table row's items sum every row's partials in table order
+    const uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec);
+    if (tid < PK) {
+        float w = 0.f;
+        int nap = 1;
+        for (int it = 0; it < WAIT_SPINS; ++it) {
+            const uint64_t v = ld_tag(rec + (size_t)tid * 3);
+            if (tag_ok(v, tag)) {
+                w = __uint_as_float((uint32_t)v);
+                break;
+            }
+            backoff(nap);
+            if (it == WAIT_SPINS - 1) flag_error(err);
+        }
+        s_wk[tid] = w;
+    }
+    __syncthreads();
+    const int rows = per_wave * 4;
+    for (int rr = tid; rr < rows; rr += 256) {
+        const int r = b * rows + rr;
+        if (r >= a.H) continue;
+        float s = 0.f;
+        for (int q = 0; q < PK; ++q) {
+            if (s_wk[q] == 0.f) continue;
+            int nap = 1;
+            for (int it = 0; it < WAIT_SPINS; ++it) {
+                const uint64_t v = ld_tag(part + (size_t)q * a.H + r);
+                if (tag_ok(v, tag)) {
+                    s += __uint_as_float((uint32_t)v);
+                    break;
+                }
+                backoff(nap);
+                if (it == WAIT_SPINS - 1) flag_error(err);
+            }
+        }
+        if (a.accumulate) s += ld_act<XDT>(a.out, r);
+        if (a.add != nullptr) s += ld_act<XDT>(a.add, r);
+        st_act<XDT>(a.out, r, s);
+    }
+    stamp(st, 5);
+    // the last combining item to finish advances the launch generation: every item of this
+    // launch is complete at that point, and every workgroup read the generation before its items
+    __syncthreads();
+    if (tid == 0) {
+        __builtin_amdgcn_s_waitcnt(0);  // this item's output stores are done
+        if (add_co32(a.ws + W_DONE, 1u) == (uint32_t)(pick4(a.ndb, a.P - 1) - 1)) {
+            const uint32_t gen = tag - 1u, next = gen + 1u == 0xFFFFFFFFu ? 0u : gen + 1u;
+            st_co32(a.ws + W_DONE, 0u);
+            for (int q = 0; q < NGEN; ++q) st_co32(a.ws + W_GEN + 256 * q, next);
+        }
+    }
+}
+
+// rows per down item / row pairs per up item of a precision (host and device)
+__host__ __device__ __forceinline__ int down_item_rows(int prec, int lg) {
+    const int npd = prec == MOEHIP_PREC_INT4 ? 8 : ((prec == MOEHIP_PREC_F16 || prec == MOEHIP_PREC_BF16) ? 2 : 4);
+    return npd * (64 >> lg) * 4;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -454,213 +1036,56 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, int *s_idx, float
 // ---------------------------------------------------------------------------------------
 template <int XDT>
 __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
-    __shared__ __align__(16) float s_vec[DL_MAXH];  // x (up items) or h (down items), piece-major
-    __shared__ int s_item, s_next, s_flag, s_fmt, s_routed;
+    __shared__ uint32_t s_tag;
     __shared__ int s_idx[64];
     __shared__ float s_w[64];
-    __shared__ float s_wt[DL_MAXP * 32];          // route cached per workgroup: table weights
-    __shared__ uint64_t s_tab[DL_MAXP * 32 * 4];  // and addresses
-    const int tid = threadIdx.x, wave = tid >> 6;
+    __shared__ float s_sorted[64];
+    __shared__ float s_wk[DL_MAXP * 32];
+    __shared__ __align__(16) float s_h[DL_MAXROW];
+    const int tid = threadIdx.x;
     uint32_t *ws = a.ws;
     uint32_t *err = ws + W_ERR;
-    const int PK = a.P * a.k;
     const int NR = a.Wr != nullptr ? (a.E + 3) / 4 : 1;
-    const int NU = PK * a.nub;
-    const int ND = PK * a.ndb;
-    const int total = NR + NU + ND;
-    uint32_t *up_done = ws_ptr<uint32_t>(a, a.off_up);
-    uint32_t *dn_done = ws_ptr<uint32_t>(a, a.off_dn);
-    int64_t *tab = ws_ptr<int64_t>(a, a.off_tab);
-    float *wtab = ws_ptr<float>(a, a.off_wtab);
-    float *hbuf = ws_ptr<float>(a, a.off_h);
-    float *part = ws_ptr<float>(a, a.off_part);
-    if (tid == 0) {
-        s_fmt = -1;  // which layout s_vec holds: VPC of staged x, or -1
-        s_routed = 0;
-        s_next = (int)add_co32(ws + W_TICKET, 1u);
-    }
-    for (;;) {
-        __syncthreads();
-        if (tid == 0) {
-            // take the reserved ticket and reserve the next one (its round trip overlaps the work)
-            s_item = s_next;
-            s_next = s_item < total ? (int)add_co32(ws + W_TICKET, 1u) : total;
-        }
-        __syncthreads();
-        const int t = s_item;
-        if (t >= total) break;
+    const int total = NR + a.NU + a.ND;
+    if (tid == 0) s_tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
+    __syncthreads();
+    const uint32_t tag = uni((int)s_tag);
+    for (int t = blockIdx.x; t < total; t += gridDim.x) {
+        __syncthreads();  // LDS of the previous item is free
         uint64_t t_start = 0;
         if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
         if (t < NR) {
-            // ---------------- router rows ----------------
-            if (a.Wr != nullptr) {
-                const int e = t * 4 + wave;
-                const int lane = tid & 63;
-                if (e < a.E) {
-                    // each lane: 32 consecutive values (H <= 2048), all loads issued before use
-                    constexpr int ESZ = XDT == MOEHIP_DT_F32 ? 4 : 2;
-                    constexpr int NV = 32 * ESZ / 16;  // 16-byte vectors per lane
-                    const int c0 = lane * 32;
-                    float acc = 0.f;
-                    if (c0 < a.H) {
-                        const uint8_t *wp = reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ;
-                        const uint8_t *xp = reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * ESZ;
-                        uint4 wv[NV], xv[NV];
-#pragma unroll
-                        for (int i = 0; i < NV; ++i) {
-                            wv[i] = reinterpret_cast<const uint4 *>(wp)[i];
-                            xv[i] = reinterpret_cast<const uint4 *>(xp)[i];
-                        }
-#pragma unroll
-                        for (int i = 0; i < NV; ++i) {
-                            const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-                            const uint32_t xd[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                if constexpr (XDT == MOEHIP_DT_F32) {
-                                    acc = fmaf(__uint_as_float(wd[q]), __uint_as_float(xd[q]), acc);
-                                } else if constexpr (XDT == MOEHIP_DT_F16) {
-                                    acc = fmaf(f16_to_f32(wd[q] & 0xffffu), f16_to_f32(xd[q] & 0xffffu), acc);
-                                    acc = fmaf(f16_to_f32(wd[q] >> 16), f16_to_f32(xd[q] >> 16), acc);
-                                } else {
-                                    acc = fmaf(__uint_as_float(wd[q] << 16), __uint_as_float(xd[q] << 16), acc);
-                                    acc = fmaf(__uint_as_float(wd[q] & 0xffff0000u), __uint_as_float(xd[q] & 0xffff0000u), acc);
-                                }
-                            }
-                        }
-                    }
-                    acc = wave_sum(acc);
-                    if (lane == 0) st_co(ws_ptr<float>(a, a.off_logits) + e, rnd_act<XDT>(acc));
-                }
-            }
-            sync_release();
-            if (tid == 0) s_flag = (add_co32(ws + W_ROUTER, 1u) == (uint32_t)(NR - 1));
-            __syncthreads();
-            if (s_flag) {
-                if (wave == 0) route_tail<XDT>(a, s_idx, s_w, s_vec, a.trace ? a.trace + 3 * total : nullptr);
-                sync_release();
-                if (tid == 0) {
-                    if (a.trace) a.trace[3 * total + 8] = __builtin_amdgcn_s_memrealtime();
-                    st_co32(ws + W_READY, 1u);
-                    s_fmt = -1;  // s_vec held the logits: no staged x any more
-                }
-            }
-        } else if (t < NR + NU) {
+            // ---------------- router rows; the last router item also routes ----------------
+            if (a.Wr != nullptr) router_rows<XDT>(a, t, tag);
+            if (t == NR - 1 && tid < 64)
+                route_tail<XDT>(a, tag, s_idx, s_w, s_sorted, s_h, err, a.trace ? a.trace + 3 * total : nullptr);
+        } else if (t < NR + a.NU) {
             // ---------------- kernel-A rows ----------------
             const int u = t - NR;
-            const int jj = u / a.nub, rb = u % a.nub;
-            const int pi = jj / a.k;
-            const int prec = pick4(a.prec, pi);
-            const int vpc = vpc_dev(prec);
-            if (s_fmt != vpc) {  // stage x in the piece-major layout of this format
-                const int C = a.H / vpc;
-                const int npc = vpc / 4;
-                for (int i4 = tid; i4 < a.H / 4; i4 += 256) {
-                    const int dst = vec_slot(i4, npc, C);
-                    float4 p4;
-                    if constexpr (XDT == MOEHIP_DT_F32) {
-                        p4 = reinterpret_cast<const float4 *>(a.x)[i4];
-                    } else {
-                        const uint2 r = reinterpret_cast<const uint2 *>(a.x)[i4];
-                        if constexpr (XDT == MOEHIP_DT_F16) {
-                            p4 = make_float4(f16_to_f32(r.x & 0xffffu), f16_to_f32(r.x >> 16), f16_to_f32(r.y & 0xffffu),
-                                             f16_to_f32(r.y >> 16));
-                        } else {
-                            p4 = make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
-                                             __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
-                        }
-                    }
-                    *reinterpret_cast<float4 *>(s_vec + dst) = p4;
-                }
-                __syncthreads();
-                if (tid == 0) s_fmt = vpc;
-            }
-            if (!s_routed) {  // first item after the routing: cache the tables in LDS
-                if (tid == 0) wait_geq(ws + W_READY, 1u, err);
-                __syncthreads();
-                for (int i = tid; i < PK; i += 256) s_wt[i] = ld_co(wtab + i);
-                for (int i = tid; i < PK * 4; i += 256) s_tab[i] = (uint64_t)ld_co64(tab + i);
-                __syncthreads();
-                if (tid == 0) s_routed = 1;
-            }
-            const float wt = s_wt[jj];
-            if (wt != 0.f) {
-                const uint8_t *qb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 0]);
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 1]);
-                const int lg = row_lg(a.H);
-                const int r0 = rb * UP_ROWS + wave * (UP_ROWS / 4);
-                float *hout = hbuf + (size_t)jj * a.I;
-                const int gs = pick4(a.gs_up, pi);
-                constexpr int NR4 = UP_ROWS / 4;
-                switch (prec) {
-                    case MOEHIP_PREC_INT4: up_rows<MOEHIP_PREC_INT4>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
-                    case MOEHIP_PREC_INT8: up_rows<MOEHIP_PREC_INT8>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
-                    case MOEHIP_PREC_F16: up_rows<MOEHIP_PREC_F16>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
-                    case MOEHIP_PREC_BF16: up_rows<MOEHIP_PREC_BF16>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
-                    default: up_rows<MOEHIP_PREC_FP8>(qb, sb, s_vec, r0, NR4, a.I, a.H, gs, lg, hout); break;
-                }
-                sync_release();
-                if (tid == 0) add_co32(up_done + jj * CSTRIDE, 1u);
+            const int pi = block_of(a.up_base, a.P, u);
+            const int rem = u - pick4(a.up_base, pi);
+            const int nub = pick4(a.nub, pi);
+            const int jj = pi * a.k + rem / nub, b = rem % nub;
+            switch (pick4(a.prec, pi)) {
+                case MOEHIP_PREC_INT4: up_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
+                case MOEHIP_PREC_INT8: up_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
+                case MOEHIP_PREC_F16: up_item<MOEHIP_PREC_F16, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
+                case MOEHIP_PREC_BF16: up_item<MOEHIP_PREC_BF16, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
+                default: up_item<MOEHIP_PREC_FP8, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
             }
         } else {
-            // ---------------- kernel-B rows + ordered combine ----------------
-            const int d = t - NR - NU;
-            const int jj = d / a.ndb, rb = d % a.ndb;
-            const int pi = jj / a.k;
-            const int prec = pick4(a.prec, pi);
-            if (!s_routed) {
-                if (tid == 0) wait_geq(ws + W_READY, 1u, err);
-                __syncthreads();
-                for (int i = tid; i < PK; i += 256) s_wt[i] = ld_co(wtab + i);
-                for (int i = tid; i < PK * 4; i += 256) s_tab[i] = (uint64_t)ld_co64(tab + i);
-                __syncthreads();
-                if (tid == 0) s_routed = 1;
-            }
-            const float wt = s_wt[jj];
-            if (wt != 0.f) {
-                if (tid == 0) wait_geq(up_done + jj * CSTRIDE, (uint32_t)a.nub, err);
-                __syncthreads();
-                const int vpc = vpc_dev(prec);
-                const int C = a.I / vpc;
-                const int npc = vpc / 4;
-                const float *hj = hbuf + (size_t)jj * a.I;
-                for (int i4 = tid; i4 < a.I / 4; i4 += 256) {
-                    const int dst = vec_slot(i4, npc, C);
-                    s_vec[dst + 0] = ld_co(hj + 4 * i4 + 0);
-                    s_vec[dst + 1] = ld_co(hj + 4 * i4 + 1);
-                    s_vec[dst + 2] = ld_co(hj + 4 * i4 + 2);
-                    s_vec[dst + 3] = ld_co(hj + 4 * i4 + 3);
-                }
-                if (tid == 0) s_fmt = -1;
-                __syncthreads();
-                const uint8_t *qb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 2]);
-                const uint8_t *sb = reinterpret_cast<const uint8_t *>(s_tab[(size_t)jj * 4 + 3]);
-                const int lg = row_lg(a.I);
-                const int r0 = rb * DN_ROWS + wave * (DN_ROWS / 4);
-                float *pout = part + (size_t)jj * a.H;
-                const int gs = pick4(a.gs_dn, pi);
-                constexpr int NR4 = DN_ROWS / 4;
-                switch (prec) {
-                    case MOEHIP_PREC_INT4: down_rows<MOEHIP_PREC_INT4>(qb, sb, s_vec, r0, NR4, a.H, a.I, gs, lg, wt, pout); break;
-                    case MOEHIP_PREC_INT8: down_rows<MOEHIP_PREC_INT8>(qb, sb, s_vec, r0, NR4, a.H, a.I, gs, lg, wt, pout); break;
-                    case MOEHIP_PREC_F16: down_rows<MOEHIP_PREC_F16>(qb, sb, s_vec, r0, NR4, a.H, a.I, gs, lg, wt, pout); break;
-                    case MOEHIP_PREC_BF16: down_rows<MOEHIP_PREC_BF16>(qb, sb, s_vec, r0, NR4, a.H, a.I, gs, lg, wt, pout); break;
-                    default: down_rows<MOEHIP_PREC_FP8>(qb, sb, s_vec, r0, NR4, a.H, a.I, gs, lg, wt, pout); break;
-                }
-            }
-            sync_release();
-            if (tid == 0) s_flag = (add_co32(dn_done + rb * CSTRIDE, 1u) == (uint32_t)(PK - 1));
-            __syncthreads();
-            if (s_flag && tid < DN_ROWS) {
-                const int r = rb * DN_ROWS + tid;
-                if (r < a.H) {
-                    float s = 0.f;
-                    for (int q = 0; q < PK; ++q)
-                        if (s_wt[q] != 0.f) s += ld_co(part + (size_t)q * a.H + r);
-                    if (a.accumulate) s += ld_act<XDT>(a.out, r);
-                    if (a.add != nullptr) s += ld_act<XDT>(a.add, r);
-                    st_act<XDT>(a.out, r, s);
-                }
+            // ---------------- kernel-B rows (+ ordered combine) ----------------
+            const int dd = t - NR - a.NU;
+            const int pi = block_of(a.dn_base, a.P, dd);
+            const int rem = dd - pick4(a.dn_base, pi);
+            const int ndb = pick4(a.ndb, pi);
+            const int jj = pi * a.k + rem / ndb, b = rem % ndb;
+            switch (pick4(a.prec, pi)) {
+                case MOEHIP_PREC_INT4: down_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
+                case MOEHIP_PREC_INT8: down_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
+                case MOEHIP_PREC_F16: down_item<MOEHIP_PREC_F16, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
+                case MOEHIP_PREC_BF16: down_item<MOEHIP_PREC_BF16, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
+                default: down_item<MOEHIP_PREC_FP8, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
             }
         }
         if (a.trace != nullptr && tid == 0) {
@@ -669,25 +1094,23 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             a.trace[3 * t + 2] = blockIdx.x;
         }
     }
-    // every workgroup has taken its last ticket; the last one resets the counters
-    if (tid == 0) s_flag = (add_co32(ws + W_DONE, 1u) == gridDim.x - 1);
-    __syncthreads();
-    if (s_flag) {
-        for (int i = tid; i < PK; i += 256) st_co32(up_done + i * CSTRIDE, 0u);
-        for (int i = tid; i < a.ndb; i += 256) st_co32(dn_done + i * CSTRIDE, 0u);
-        if (tid == 0) {
-            st_co32(ws + W_TICKET, 0u);
-            st_co32(ws + W_ROUTER, 0u);
-            st_co32(ws + W_READY, 0u);
-            st_co32(ws + W_DONE, 0u);
-        }
-    }
 }
 
-// workspace layout (bytes)
+// ---------------------------------------------------------------------------------------
+// host side: item plans and workspace layout
+// ---------------------------------------------------------------------------------------
+static inline int cpl_host(int prec) { return 32 / vpc_of(prec); }
+// log2 of the lanes per row of `cols` values (CPL chunks of VPC values per lane)
+static inline int lg_for(int cols, int prec) {
+    const int lanes = (cols / vpc_of(prec) + cpl_host(prec) - 1) / cpl_host(prec);
+    int G = 1, lg = 0;
+    while (G < lanes && G < 64) G <<= 1, ++lg;
+    return lg;
+}
+static inline int up_item_pairs(int prec, int lg) { return (4 / cpl_host(prec)) * (64 >> lg) * 4; }
+
 struct DlLayout {
-    uint32_t up, dn, tab, wtab, logits, h, part, total;
-    int nub, ndb;
+    uint32_t rec, logits, h, part, total;
 };
 
 static inline uint32_t al256(size_t v) { return (uint32_t)((v + 255) / 256 * 256); }
@@ -695,28 +1118,58 @@ static inline uint32_t al256(size_t v) { return (uint32_t)((v + 255) / 256 * 256
 static DlLayout dl_layout(int P, int k, int E, int H, int I) {
     DlLayout L;
     const int PK = P * k;
-    L.nub = (I + UP_ROWS - 1) / UP_ROWS;
-    L.ndb = (H + DN_ROWS - 1) / DN_ROWS;
     size_t off = W_HDR * 4;
-    L.up = (uint32_t)off;
-    off += (size_t)PK * CSTRIDE * 4;
-    L.dn = (uint32_t)off;
-    off += (size_t)L.ndb * CSTRIDE * 4;
     off = al256(off);
-    L.tab = (uint32_t)off;
-    off += (size_t)PK * 32;
-    L.wtab = (uint32_t)off;
-    off += (size_t)PK * 4;
+    L.rec = (uint32_t)off;
+    off += (size_t)NREC * rec_stride_words(P, k) * 8;
+    off = al256(off);
     L.logits = (uint32_t)off;
-    off += (size_t)E * 4;
+    off += (size_t)E * 8;
     off = al256(off);
     L.h = (uint32_t)off;
-    off += (size_t)PK * I * 4;
+    off += (size_t)PK * I * 8;
     off = al256(off);
     L.part = (uint32_t)off;
-    off += (size_t)PK * H * 4;
+    off += (size_t)PK * H * 8;
     L.total = al256(off);
     return L;
+}
+
+// item plan of a layer: fills the plan fields of `a`, returns the number of work items
+static int dl_plan(const moehip_layer_desc *d, int with_router, LayerArgs *a) {
+    int nu = 0, nd = 0;
+    for (int p = 0; p < DL_MAXP; ++p) {
+        const bool on = p < d->P;
+        a->lg_up[p] = on ? lg_for(d->H, d->prec[p]) : 0;
+        a->lg_dn[p] = on ? lg_for(d->I, d->prec[p]) : 0;
+        a->nub[p] = a->ndb[p] = 1;
+        a->up_base[p] = nu;
+        a->dn_base[p] = nd;
+        if (on) {
+            const int upi = up_item_pairs(d->prec[p], a->lg_up[p]);
+            const int dpi = down_item_rows(d->prec[p], a->lg_dn[p]);
+            a->nub[p] = (d->I + upi - 1) / upi;
+            a->ndb[p] = (d->H + dpi - 1) / dpi;
+            nu += d->k * a->nub[p];
+            nd += d->k * a->ndb[p];
+        }
+    }
+    a->NU = nu;
+    a->ND = nd;
+    return (with_router ? (d->E + 3) / 4 : 1) + nu + nd;
+}
+
+// workgroups of k_decode_layer<DT> the current device holds at once (occupancy x CUs)
+template <int DT>
+static int dl_capacity(int *cap) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_decode_layer<DT>), 256,
+                                                     0) != hipSuccess)
+        return -1;
+    *cap = per_cu * cus;
+    return 0;
 }
 
 }  // namespace moehip
@@ -749,11 +1202,8 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
         const int pr = d->prec[p];
         MOEHIP_REQUIRE(pr >= MOEHIP_PREC_INT4 && pr <= MOEHIP_PREC_FP8 && pr != MOEHIP_PREC_F32,
                        "decode_layer: precision %d (fp32 records use the grouped kernels)", pr);
-        const int vpc = pr == MOEHIP_PREC_INT4 ? 32 : (pr == MOEHIP_PREC_INT8 || pr == MOEHIP_PREC_FP8) ? 16
-                        : (pr == MOEHIP_PREC_F32 ? 4 : 8);
-        (void)vpc;
         if (pr == MOEHIP_PREC_INT4 || pr == MOEHIP_PREC_INT8) {
-            const int vpc = pr == MOEHIP_PREC_INT4 ? 32 : 16;
+            const int vpc = vpc_of(pr);
             MOEHIP_REQUIRE(d->gs_up[p] > 0 && d->gs_up[p] % vpc == 0 && d->H % d->gs_up[p] == 0 && d->gs_dn[p] > 0 &&
                                d->gs_dn[p] % vpc == 0 && d->I % d->gs_dn[p] == 0,
                            "decode_layer: group sizes %d/%d need multiples of %d dividing H/I", d->gs_up[p],
@@ -771,12 +1221,14 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.w32_in = w32_in;
     a.rtab = rtab;
     for (int p = 0; p < DL_MAXP; ++p) {
-        for (int f = 0; f < 4; ++f) a.offs[p][f] = p < d->P ? d->offs[p][f] : 0;
-        a.prec[p] = p < d->P ? d->prec[p] : 0;
-        a.gs_up[p] = p < d->P ? d->gs_up[p] : 0;
-        a.gs_dn[p] = p < d->P ? d->gs_dn[p] : 0;
-        a.planned[p] = p < d->P ? d->planned[p] : 0;
+        const bool on = p < d->P;
+        for (int f = 0; f < 4; ++f) a.offs[p][f] = on ? d->offs[p][f] : 0;
+        a.prec[p] = on ? d->prec[p] : 0;
+        a.gs_up[p] = on ? d->gs_up[p] : 0;
+        a.gs_dn[p] = on ? d->gs_dn[p] : 0;
+        a.planned[p] = on ? d->planned[p] : 0;
     }
+    const int total = dl_plan(d, Wr != nullptr, &a);
     for (int i = 0; i < 3; ++i) a.lv2p[i] = d->lv2p[i];
     a.P = d->P;
     a.E = d->E;
@@ -795,19 +1247,25 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.info = info;
     a.miss = miss;
     a.ws = reinterpret_cast<uint32_t *>(ws);
-    a.nub = L.nub;
-    a.ndb = L.ndb;
-    a.off_up = L.up;
-    a.off_dn = L.dn;
-    a.off_tab = L.tab;
-    a.off_wtab = L.wtab;
+    a.off_rec = L.rec;
     a.off_logits = L.logits;
     a.off_h = L.h;
     a.off_part = L.part;
     a.trace = trace;
-    const int PK = d->P * d->k;
-    const int total = (Wr != nullptr ? (d->E + 3) / 4 : 1) + PK * (L.nub + L.ndb);
-    const int g = grid > 0 ? (grid < total ? grid : total) : total;
+    a.stage = trace != nullptr ? trace + 3 * (size_t)(total + 3) : nullptr;
+    int cap = 0;
+    int rc = -1;
+    switch (d->dtype) {
+        case MOEHIP_DT_F16: rc = dl_capacity<MOEHIP_DT_F16>(&cap); break;
+        case MOEHIP_DT_BF16: rc = dl_capacity<MOEHIP_DT_BF16>(&cap); break;
+        default: rc = dl_capacity<MOEHIP_DT_F32>(&cap); break;
+    }
+    if (rc != 0 || cap <= 0) {
+        set_error("decode_layer: occupancy query failed");
+        return MOEHIP_ELAUNCH;
+    }
+    int g = grid > 0 ? (grid < total ? grid : total) : total;
+    if (g > cap) g = cap;  // every workgroup must fit on the GPU at once (see the kernel's header)
     hipStream_t st = as_stream(stream);
     switch (d->dtype) {
         case MOEHIP_DT_F16: hipLaunchKernelGGL((k_decode_layer<MOEHIP_DT_F16>), dim3(g), dim3(256), 0, st, a); break;
@@ -815,6 +1273,12 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
         default: hipLaunchKernelGGL((k_decode_layer<MOEHIP_DT_F32>), dim3(g), dim3(256), 0, st, a); break;
     }
     return check_launch("decode_layer");
+}
+
+extern "C" int moehip_decode_layer_work_items(const moehip_layer_desc *d, int with_router) {
+    if (d == nullptr || d->P <= 0 || d->P > DL_MAXP) return -1;
+    LayerArgs a;
+    return dl_plan(d, with_router, &a);
 }
 
 extern "C" int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream) {

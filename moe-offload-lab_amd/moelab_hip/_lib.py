@@ -55,6 +55,7 @@ _SIGS = {
     "moehip_decode_layer": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                              _vp, _vp, _vp, ctypes.c_size_t, _i, _vp, _vp], _i),
     "moehip_decode_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
+    "moehip_decode_layer_work_items": ([ctypes.POINTER(LayerDesc), _i], _i),
     "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
 }
 

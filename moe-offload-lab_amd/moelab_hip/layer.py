@@ -120,7 +120,7 @@ class MoEDecoder:
         self.miss = torch.zeros(1, dtype=torch.float32, device=dev)
         self._pols = [self.policy.device_policy(l) for l in range(store.L)]
         self.grid = grid
-        self.trace = None  # optional (items + 3, 3) int64 device tensor: per-item (start, end, workgroup)
+        self.trace = None  # optional int64 device tensor of 3 * (items + 3) + 8 * items: per-item stamps
         self.fused = fused and all(store.layouts[p]["precision"] != "fp32" for p in precs) and H <= 2048 \
             and _dims(store.layouts[precs[0]])[1] <= 2048
         if self.fused:
@@ -151,11 +151,11 @@ class MoEDecoder:
 
     def work_items(self) -> int:
         """Number of work items of one fused launch (router rows, up blocks, down blocks)."""
-        d = self._descs[0]
-        nub = (d.I + 15) // 16
-        ndb = (d.H + 63) // 64
-        nr = (d.E + 3) // 4 if self.router_weights is not None else 1
-        return nr + d.P * d.k * (nub + ndb)
+        n = _lib.load().moehip_decode_layer_work_items(ctypes.byref(self._descs[0]),
+                                                        1 if self.router_weights is not None else 0)
+        if n < 0:
+            raise RuntimeError("moehip_decode_layer_work_items: bad layer description")
+        return n
 
     def check_error(self) -> None:
         """Raise if a bounded wait inside the fused kernel expired on this decoder's workspace."""
