@@ -17,10 +17,15 @@ algorithmic bytes per launch = 8 routed int4 records (3,342,336 B each: gate_up.
 live with HIP events on the stream it runs on, over launches that rotate through all tokens and
 layers.
 
+HBM traffic per launch (roofline.traffic) is read from the committed rocprofv3 counter summary
+profiles/k_decode_layer_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
+same counters on a plain copy of known size, `--copy-calibration`); null when that file is absent.
+
 CPU baseline: the oracle's restatement of moelab's CPU expert branch (dequantise to fp32,
 F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workload, host cores.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py --copy-calibration 256     # a plain 256 MiB device copy, 20 times (counter scale)
 """
 
 from __future__ import annotations
@@ -37,6 +42,32 @@ sys.path.insert(0, str(ROOT / "moe-offload-lab_amd"))
 
 H, I, E, K_TOP, L = 2048, 1024, 64, 8, 16
 HBM_PEAK_GBS = 8000.0
+PROFILE = ROOT / "profiles" / "k_decode_layer_olmoe_int4_bs1.md"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the fused kernel from the committed counter summary, or None."""
+    try:
+        for line in PROFILE.read_text().splitlines():
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1].split()[0]))
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_calibration(mib: int):
+    """A plain device-to-device copy of `mib` MiB, 20 times: the bytes per launch are known
+    exactly (read mib MiB, write mib MiB), so counters read on it scale the kernel's counters."""
+    import torch
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 20}), flush=True)
 
 
 def log(*a):
@@ -195,7 +226,11 @@ def main():
     ap.add_argument("--kernel-launches", type=int, default=4096)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the MoE-layer path here runs on a single MI355X "
               "(multi-GPU sharding is described, not run). Use --gpus 1.", file=sys.stderr)
@@ -229,7 +264,7 @@ def main():
         "kernel_us": round(r["kernel_us"], 3),
         "roofline": {
             "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "kernel": "k_decode_layer<f16> (router + HOBBIT table + 8 int4 experts + combine, one launch)",
             "bytes_per_launch": r["kernel_bytes"],
         },
