@@ -201,6 +201,24 @@ int moehip_decode_layer_work_items(const moehip_layer_desc *desc, int with_route
 int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
 
 /*
+ * T > 1 tokens (prefill chunks, batched decode) through the experts of one layer, int4 gs64
+ * records: the pairs (token, slot) sorted by expert (offsets (E+1), sorted_pos (T*k) = t*k+j,
+ * rank (T*k) = position of pair t*k+j in sorted_pos or -1, as written by moehip_dispatch), for
+ * each expert e with tab[e] != 0: h = silu(X_e gate^T) * (X_e up^T) and y = w_pair * (h down^T)
+ * on MFMA (fp16 operands, exact int4 values, fp32 accumulation and group scales), then
+ * out[t] = sum over the token's slots in slot order (+ out if accumulate) (+ add). tab (E, 4)
+ * int64 record field addresses (0 row = expert not resident: contributes nothing); x (T, H)
+ * and out (T, H) in xdtype (fp16 / bf16); w (T*k) fp32 routing weights. H, I multiples of 64,
+ * gs = 64. ws: moehip_grouped_gemm_workspace_bytes(), 256-B aligned.
+ * Replaces moelab/runtime.py:418-436 (`_run_grouped_tokens`, per-expert expert_ffn) and the
+ * T > 1 accumulation runtime.py:352-353 (`out.index_add_(0, tok, y * w)`).
+ */
+int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, int xdtype, int T, int H, int I, int k, int E,
+                        int gs, const int32_t *offsets, const int32_t *sorted_pos, const int32_t *rank, const float *w,
+                        void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream);
+size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I);
+
+/*
  * Checkpoint-style FP8 block quantisation of w (O, I) fp32: per 128 x 128 block
  * scale = amax / 448 (1.0 for an all-zero block), q (O, I) = e4m3fn(w / scale) (round to
  * nearest even, saturating at 448), s (ceil(O/128), ceil(I/128)) fp32 — the

@@ -190,6 +190,15 @@ __device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
 __device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x05040100u); }
 __device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); }
 
+// (d & mask) | magic in one v_and_or_b32 (the compiler otherwise splits it into two
+// instructions: gfx9 VOP3 encodings take no literal constants). Never feed the result straight
+// into an MFMA operand: the compiler does not insert hazard wait states for inline asm.
+__device__ __forceinline__ uint32_t and_or(uint32_t d, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(d), "s"(mask), "v"(magic));
+    return r;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 }  // namespace moehip

@@ -258,14 +258,6 @@ __device__ __forceinline__ float scale_to_h(const float *v, uint32_t *w) {
     return ldexpf(1.0f, e);
 }
 
-// (d & mask) | magic in one v_and_or_b32 (the compiler otherwise splits it into two
-// instructions: gfx9 VOP3 encodings take no literal constants)
-__device__ __forceinline__ uint32_t and_or(uint32_t d, uint32_t mask, uint32_t magic) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(d), "s"(mask), "v"(magic));
-    return r;
-}
-
 // chunk dot products sum(weight * v) for the dot2 formats (before the group scale)
 template <int PREC>
 __device__ __forceinline__ float dot2_chunk(const uint4 q, const uint32_t *xp, float corr) {

@@ -57,6 +57,9 @@ _SIGS = {
     "moehip_decode_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
     "moehip_decode_layer_work_items": ([ctypes.POINTER(LayerDesc), _i], _i),
     "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
+    "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                             ctypes.c_size_t, _vp], _i),
+    "moehip_grouped_gemm_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
 }
 
 EXPORTED = tuple(_SIGS)

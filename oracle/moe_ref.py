@@ -515,6 +515,22 @@ def moe_layer(x, idx, w, weights_of, skip=None, shared=None):
     return out
 
 
+def moe_layer_grouped(x, idx, w, weights_of, skip=None):
+    """moe_layer for many tokens evaluated expert by expert (runtime.py:418-436: per expert
+    y = expert_ffn(x[tok]) on the expert's tokens, then out.index_add_(tok, y * w),
+    runtime.py:352-353): the same float64 result up to summation order."""
+    x = np.asarray(x, np.float64)
+    idx = np.asarray(idx)
+    w = np.asarray(w, np.float64)
+    out = np.zeros_like(x)
+    keep = np.ones(idx.shape, bool) if skip is None else ~np.asarray(skip, bool)
+    for e in np.unique(idx[keep]):
+        tok, slot = np.nonzero((idx == e) & keep)
+        y = expert_ffn(x[tok], *weights_of(int(e)))
+        np.add.at(out, tok, w[tok, slot][:, None] * y)
+    return out
+
+
 def cpu_expert_path(x: np.ndarray, entries, layouts) -> np.ndarray:
     """The reference's CPU expert branch for one token (runtime.py:646-702, decode case):
     x in float32; per expert materialize(float32) -> expert_ffn -> out += w * y. `entries` is

@@ -1,0 +1,129 @@
+"""
+GPU parity of the T > 1 path (prefill chunks, batched decode): moehip_dispatch + the MFMA grouped
+GEMM against the oracle's expert-by-expert layer (oracle.moe_layer_grouped, pinned against
+transformers' OlmoeExperts in test_oracle.py), within the north-star tolerance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from moelab_hip.layer import ResidentStore
+from moelab_hip.prefill import GroupedTokens
+from moelab_hip.store import record_layout
+from test_gpu_parity import assert_layer_close
+
+pytestmark = pytest.mark.gpu
+
+
+class _Experts:
+    """E int4 experts of N(0, std) weights (each regenerated from its own seed), encoded on the
+    GPU, with the oracle's float view built on demand."""
+
+    def __init__(self, dev, H, I, E, seed, std=0.02):
+        self.H, self.I, self.E, self.seed, self.std = H, I, E, seed, std
+        self.store = ResidentStore({"int4": record_layout("int4", H, I, 64, scale="absmax")}, 1, E, dev)
+        for e in range(E):
+            gu, dn = self.weights(e)
+            self.store.encode("int4", 0, e, gu.to(dev), dn.to(dev))
+        self._mats = {}
+
+    def weights(self, e):
+        g = torch.Generator().manual_seed(self.seed * 7919 + e)
+        return (torch.randn(2 * self.I, self.H, generator=g) * self.std,
+                torch.randn(self.H, self.I, generator=g) * self.std)
+
+    def mats(self, e):
+        if e not in self._mats:
+            gu, dn = self.weights(e)
+            lay = O.record_layout("int4", self.H, self.I, 64, scale="absmax")
+            self._mats[e] = O.materialize(lay, O.encode_record(lay, gu.numpy(), dn.numpy(), "absmax"))
+        return self._mats[e]
+
+    def bases(self):
+        return self.store.rtab[0, 0].clone()
+
+
+def _routing(T, E, k, seed, renorm):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    w = torch.rand(T, k, generator=g) + 0.05
+    if renorm:
+        w = w / w.sum(1, keepdim=True)
+    return idx, w.float()
+
+
+def _run(dev, ex, x, idx, w, dtype, skip=None, missing=()):
+    T, k = idx.shape
+    gt = GroupedTokens(ex.store.layouts["int4"], ex.E, k, T, dev)
+    bases = ex.bases()
+    for e in missing:
+        bases[e] = 0
+    tab = gt.table(bases)
+    xd, idxd, wd = x.to(dev).contiguous(), idx.to(dev).contiguous(), w.to(dev).contiguous()
+    out = torch.zeros(T, ex.H, dtype=dtype, device=dev)
+    sk = None if skip is None else torch.from_numpy(skip.astype(np.uint8)).to(dev)
+    gt.run(xd, idxd, wd, tab, out, skip=sk)
+    torch.cuda.synchronize()
+    keep = np.zeros(idx.shape, bool) if skip is None else skip.copy()
+    for e in missing:
+        keep |= idx.numpy() == e
+    ref = O.moe_layer_grouped(x.float().numpy(), idx.numpy(), w.numpy().astype(np.float64), ex.mats, skip=keep)
+    return out.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_grouped_gemm_small(dev, dtype):
+    H, I, E, k, T = 256, 128, 8, 2, 40
+    ex = _Experts(dev, H, I, E, 1)
+    idx, w = _routing(T, E, k, 2, False)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(3)).to(dtype)
+    got, ref = _run(dev, ex, x, idx, w, dtype)
+    assert_layer_close(got, ref, dtype)
+
+
+def test_grouped_gemm_many_tokens_per_expert_skip_and_missing(dev):
+    """> 64 tokens per expert (several passes), skipped pairs and a non-resident expert."""
+    H, I, E, k, T = 512, 256, 4, 2, 200
+    dtype = torch.float16
+    ex = _Experts(dev, H, I, E, 4)
+    idx, w = _routing(T, E, k, 5, True)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(6)).to(dtype)
+    skip = np.zeros((T, k), bool)
+    skip[::5, 0] = True
+    got, ref = _run(dev, ex, x, idx, w, dtype, skip=skip, missing=(2,))
+    assert_layer_close(got, ref, dtype)
+
+
+def test_grouped_gemm_large_activations_bf16(dev):
+    """bf16 activations far outside fp16's range: the per-token power-of-two scaling keeps them."""
+    H, I, E, k, T = 256, 128, 4, 2, 24
+    dtype = torch.bfloat16
+    ex = _Experts(dev, H, I, E, 7)
+    idx, w = _routing(T, E, k, 8, False)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(9))
+    x[::2] *= 3.0e5  # |x| ~ 1e6 on even tokens
+    x[1::4] *= 1.0e-6
+    x = x.to(dtype)
+    got, ref = _run(dev, ex, x, idx, w, dtype)
+    # relative to each token's largest output: bf16 output rounding alone is up to 2^-9 of it;
+    # an overflow or a flush to zero of the huge or tiny rows would be ~1
+    scale = np.abs(ref).max(axis=1, keepdims=True)
+    err = np.abs(got - ref) / scale
+    assert err.max() < 2.0 ** -7, err.max()
+    assert np.isfinite(got).all() and (np.abs(got[1::4]).max(axis=1) > 0).all()
+
+
+def test_grouped_gemm_qwen3_30b_prefill_shape(dev):
+    """Qwen3-30B-A3B MoE layer: d_model 2048, 128 experts, top-8 renormalised, d_ff 768, a
+    512-token bf16 prefill chunk."""
+    H, I, E, k, T = 2048, 768, 128, 8, 512
+    dtype = torch.bfloat16
+    ex = _Experts(dev, H, I, E, 10)
+    idx, w = _routing(T, E, k, 11, True)
+    w = O.round_to(w.numpy(), "bfloat16").astype(np.float32)  # weights in the model dtype
+    w = torch.from_numpy(w)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(12)).to(dtype)
+    got, ref = _run(dev, ex, x, idx, w, dtype)
+    assert_layer_close(got, ref, dtype)

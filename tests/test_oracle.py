@@ -377,3 +377,32 @@ def test_cpu_expert_path_matches_float64_layer():
     got = O.cpu_expert_path(x, [("int4", blobs[e], ws[e]) for e in range(4)], {"int4": lay})
     ref = O.moe_layer(x, np.array([[0, 1, 2, 3]]), np.array([ws]), lambda e: mats[e])
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_moe_layer_grouped_matches_olmoe_experts():
+    """The expert-by-expert evaluation (prefill order) against transformers' OlmoeExperts, with
+    skipped pairs excluded like moe_layer."""
+    from transformers import OlmoeConfig
+    from transformers.models.olmoe.modeling_olmoe import OlmoeExperts
+
+    H, I, E, k, T = 64, 32, 8, 3, 20
+    lay, blobs, mats = _tiny_store("int4", H, I, E, 6)
+    cfg = OlmoeConfig(hidden_size=H, intermediate_size=I, num_experts=E, num_experts_per_tok=k)
+    ex = OlmoeExperts(cfg).double()
+    with torch.no_grad():
+        for e in range(E):
+            ex.gate_up_proj[e].copy_(torch.from_numpy(mats[e][0]))
+            ex.down_proj[e].copy_(torch.from_numpy(mats[e][1]))
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(T, H, generator=g, dtype=torch.float64)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)])
+    w = torch.rand(T, k, generator=g, dtype=torch.float64)
+    with torch.no_grad():
+        ref = ex(x, idx, w).numpy()
+    mine = O.moe_layer_grouped(x.numpy(), idx.numpy(), w.numpy(), lambda e: mats[e])
+    assert np.allclose(mine, ref, rtol=1e-10, atol=1e-12)
+    skip = np.zeros((T, k), bool)
+    skip[::3, 1] = True
+    a = O.moe_layer_grouped(x.numpy(), idx.numpy(), w.numpy(), lambda e: mats[e], skip=skip)
+    b = O.moe_layer(x.numpy(), idx.numpy(), w.numpy(), lambda e: mats[e], skip=skip)
+    assert np.allclose(a, b, rtol=1e-12, atol=1e-14)
