@@ -26,6 +26,8 @@ F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workl
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
     python bench.py --copy-calibration 256     # a plain 256 MiB device copy, 20 times (counter scale)
+    python bench.py --workload qwen3-30b-prefill   # the grouped-GEMM path: one Qwen3-30B-shaped
+                                                   # layer on a 512-token bf16 chunk (own JSON line)
 """
 
 from __future__ import annotations
@@ -180,6 +182,87 @@ def gpu_bench(args):
     }
 
 
+# Qwen3-30B-A3B-shaped prefill chunk (the grouped-GEMM path)
+QH, QI, QE, QK, QT, QL = 2048, 768, 128, 8, 512, 8
+MFMA_PEAK_TFS = 2500.0  # dense fp16/bf16 MFMA
+
+
+def prefill_bench(args):
+    """One Qwen3-30B-shaped MoE layer on a 512-token bf16 chunk: router -> dispatch -> grouped
+    GEMMs -> combine, rotating over QL layers of int4 records (8 x 128 x 2.5 MB = 2.6 GB, far
+    above the Infinity Cache)."""
+    import torch
+
+    from moelab_hip import _lib
+    from moelab_hip.layer import ResidentStore
+    from moelab_hip.prefill import GroupedTokens
+    from moelab_hip.store import record_layout
+
+    dev = torch.device("cuda:0")
+    _lib.check_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    lay = record_layout("int4", QH, QI, 64, scale="absmax")
+    store = ResidentStore({"int4": lay}, QL, QE, dev)
+    t0 = time.time()
+    store.fill_synthetic(g, std=0.02)
+    torch.cuda.synchronize()
+    log(f"[bench] encoded {QL * QE} int4 records ({store.bytes_resident / 1e9:.2f} GB) in {time.time() - t0:.1f} s")
+    Wr = [(torch.randn(QE, QH, device=dev, generator=g) * 0.02).bfloat16() for _ in range(QL)]
+    xs = torch.randn(QL, QT, QH, device=dev, generator=g).bfloat16()
+    outs = torch.zeros(QL, QT, QH, dtype=torch.bfloat16, device=dev)
+    gt = GroupedTokens(lay, QE, QK, QT, dev)
+    tabs = [gt.table(store.rtab[l, 0]) for l in range(QL)]
+    distinct = []
+    for l in range(QL):
+        _, idx, _, _ = gt.route(xs[l], Wr[l], True)
+        distinct.append(int(torch.unique(idx).numel()))
+    st = torch.cuda.current_stream(dev)
+
+    def one(l):
+        gt.layer(xs[l], Wr[l], True, tabs[l], outs[l])
+
+    for i in range(max(args.warmup // 20, QL)):
+        one(i % QL)
+    torch.cuda.synchronize()
+    n = max(QL, args.steps // 10)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(n):
+        one(i % QL)
+    b.record(st)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000 / n
+    rec = lay["record_bytes"]
+    nd = sum(distinct) / QL
+    alg = nd * rec + QE * QH * 2 + 2 * QT * QH * 2  # distinct experts + router + x/out
+    flops = 2 * QT * QK * 3 * QH * QI + 2 * QT * QE * QH
+    log(f"[bench] prefill layer: {us:.1f} us, {nd:.1f} distinct experts, {alg / us / 1e3:.0f} GB/s, "
+        f"{flops / us / 1e6:.1f} TFLOP/s")
+    return {"us": us, "n": n, "alg": alg, "flops": flops, "distinct": nd}
+
+
+def prefill_line(args):
+    r = prefill_bench(args)
+    gbs = r["alg"] / (r["us"] * 1e-6) / 1e9
+    tfs = r["flops"] / (r["us"] * 1e-6) / 1e12
+    return {
+        "metric": "int4 MoE-layer prefill tok/s, Qwen3-30B shape, 512-token chunk, 1 GPU",
+        "value": round(QT / (r["us"] * 1e-6), 1), "unit": "tok/s", "n_gpus": 1, "steps": r["n"],
+        "warmup": max(args.warmup // 20, QL), "ms_per_step": round(r["us"] / 1000, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int4", "data": "synthetic",
+        "config": {"workload": "Qwen3-30B-A3B-shaped MoE layer, 512-token bf16 prefill chunk, int4 gs64 experts",
+                   "d_model": QH, "experts": QE, "top_k": QK, "d_ff": QI, "layers_rotated": QL, "tokens": QT,
+                   "router": "softmax top-8, renormalised", "distinct_experts": r["distinct"]},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole layer: router + dispatch + k_gemm_up + k_gemm_down + combine",
+                     "bytes_per_launch": int(r["alg"])},
+        "mfma": {"achieved": round(tfs, 1), "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFS, 4),
+                 "flops_per_launch": r["flops"]},
+        "cpu_baseline": None,
+    }
+
+
 def cpu_baseline(seconds: float):
     """The oracle's CPU expert path (moelab/runtime.py:646-702) on a bounded sample."""
     import numpy as np
@@ -227,6 +310,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill"], default="olmoe-decode-bs1")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -237,6 +321,9 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.workload == "qwen3-30b-prefill":
+        print(json.dumps(prefill_line(args)), flush=True)
+        return
     r = gpu_bench(args)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {

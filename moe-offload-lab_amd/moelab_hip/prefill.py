@@ -37,6 +37,31 @@ class GroupedTokens:
         self.sorted_pos = torch.empty(max_tokens * k, dtype=torch.int32, device=self.device)
         self.rank = torch.empty(max_tokens * k, dtype=torch.int32, device=self.device)
         self.offs = torch.tensor(field_offsets(layout), dtype=torch.int64, device=self.device)
+        self._route_bufs = None
+
+    def route(self, x: torch.Tensor, Wr: torch.Tensor, renorm: bool):
+        """Router for the T rows of x (moehip_router_topk): returns (logits, idx, w, w32) views of
+        preallocated buffers (valid until the next call). Replaces the model's gate call on a
+        prefill chunk (transformers Qwen3MoeTopKRouter / OlmoeTopKRouter.forward, called by moelab
+        at runtime.py:909)."""
+        T = x.shape[0]
+        if T > self.max_tokens or Wr.shape != (self.E, self.H) or Wr.dtype != x.dtype:
+            raise RuntimeError(f"GroupedTokens.route: x {tuple(x.shape)} Wr {tuple(Wr.shape)} {Wr.dtype}")
+        if self._route_bufs is None or self._route_bufs[0].dtype != x.dtype:
+            n, E, k, d = self.max_tokens, self.E, self.k, self.device
+            self._route_bufs = (torch.empty(n, E, dtype=x.dtype, device=d), torch.empty(n, k, dtype=torch.int64, device=d),
+                                torch.empty(n, k, dtype=x.dtype, device=d), torch.empty(n, k, dtype=torch.float32, device=d))
+        logits, idx, w, w32 = (b[:T] for b in self._route_bufs)
+        _lib.call("moehip_router_topk", x.data_ptr(), Wr.data_ptr(), T, self.H, self.E, self.k, 1 if renorm else 0,
+                  _lib.dt_code(x.dtype), logits.data_ptr(), idx.data_ptr(), w.data_ptr(), w32.data_ptr(),
+                  _lib.stream_of(self.device))
+        return logits, idx, w, w32
+
+    def layer(self, x: torch.Tensor, Wr: torch.Tensor, renorm: bool, tab: torch.Tensor, out: torch.Tensor,
+              add: torch.Tensor | None = None) -> torch.Tensor:
+        """One MoE layer on a chunk: router, expert-sorted dispatch, grouped GEMMs, ordered combine."""
+        _, idx, _, w32 = self.route(x, Wr, renorm)
+        return self.run(x, idx, w32, tab, out, add=add)
 
     def table(self, bases: torch.Tensor) -> torch.Tensor:
         """(E, 4) field-address table from the (E,) record base addresses (0 = not resident)."""
