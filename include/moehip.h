@@ -227,6 +227,36 @@ size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I);
  */
 int moehip_quantize_fp8_block(const float *w, int O, int I, void *q, float *s, void *stream);
 
+/*
+ * Offload staging (pinned host records -> device record slots) on the copy stream.
+ * items[i]: src = pinned host address (hipHostMalloc / torch pin_memory), dst = device record
+ * slot, bytes (16-byte multiples, 16-byte aligned). mode MOEHIP_STAGE_KERNEL: one gather kernel
+ * for the whole batch that reads the host records directly over the host link (n <= 32; every
+ * source must be pinned, which is checked with hipPointerGetAttributes on its first and last
+ * byte); MOEHIP_STAGE_SDMA: one hipMemcpyAsync per item. Record the caller's event after it.
+ * Replaces moelab/runtime.py:310-326 `_to_fast` (one torch.empty + copy_ per record on
+ * copy_stream, runtime.py:186) for the records of a layer's misses or prefetch list
+ * (runtime.py:899-951 `_prefetch`).
+ */
+typedef struct moehip_copy {
+    const void *src;
+    void *dst;
+    uint64_t bytes;
+} moehip_copy;
+#define MOEHIP_STAGE_KERNEL 0
+#define MOEHIP_STAGE_SDMA 1
+int moehip_stage_records(const moehip_copy *items, int n, int mode, void *stream);
+
+/*
+ * tab[idx[i]] = val[i] for i < n <= 64, as one small kernel on `stream` (host arrays, copied into
+ * the launch): tab is a device int64 table of tab_len entries (a layer-major (L, P, E) record
+ * table). Enqueued on the copy stream after moehip_stage_records, an entry turns non-zero only
+ * once its record has landed; enqueued on the compute stream, a removal is ordered after the
+ * kernels that still read the old record. Replaces moelab/fullgraph.py:73-98
+ * (`DeviceTable.added/removed/upload`: host table edits + a whole-table H2D copy).
+ */
+int moehip_table_set(int64_t *tab, int64_t tab_len, const int64_t *idx, const int64_t *val, int n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,12 @@ class LayerDesc(ctypes.Structure):
                 ("offs", (ctypes.c_int64 * 4) * 4), ("pol", Policy)]
 
 
+class Copy(ctypes.Structure):
+    """moehip_copy: one host -> device record copy."""
+
+    _fields_ = [("src", _vp), ("dst", _vp), ("bytes", ctypes.c_uint64)]
+
+
 _SIGS = {
     "moehip_abi_version": ([], _i),
     "moehip_last_error": ([], ctypes.c_char_p),
@@ -60,6 +66,9 @@ _SIGS = {
     "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                              ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemm_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
+    "moehip_stage_records": ([ctypes.POINTER(Copy), _i, _i, _vp], _i),
+    "moehip_table_set": ([_vp, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64), _i,
+                          _vp], _i),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -1,0 +1,250 @@
+"""
+Host-side offload logic (no GPU): the LRFU TierCache and the HostPool against the behaviour
+moelab's own unit tests fix (moelab tests/test_units.py:88-152, 253-291, 376-413 and
+tests/test_a5.py:109-125), the LRFU closed form, and heap victims against a brute-force sort.
+"""
+
+import math
+import random
+
+import pytest
+import torch
+
+from moelab_hip.offload import HostPool, TierCache
+
+RANK = {"fp16": 0, "int8": 1, "int4": 2}.get
+
+
+def blob(n):
+    return torch.zeros(n, dtype=torch.uint8)
+
+
+def test_lrfu_score_closed_form():
+    """f after touches at clocks t_i, read at clock T: sum_i gamma^(T - t_i)."""
+    c = TierCache("t", "cpu", 1000, RANK, half_life=3.0)
+    e = c.insert((0, 0, "fp16"), blob(10))  # touch at 0
+    c.tick(2)
+    c.touch(e)  # at 2
+    c.tick(3)
+    c.touch(e)  # at 5
+    c.tick(4)   # read at 9
+    g = 0.5 ** (1 / 3.0)
+    assert c.score(e) == pytest.approx(g ** 9 + g ** 7 + g ** 4, rel=1e-12)
+    # half-life: with no touches the score halves every half_life ticks
+    s0 = c.score(e)
+    c.tick(3)
+    assert c.score(e) == pytest.approx(s0 / 2, rel=1e-12)
+
+
+def test_lrfu_evicts_coldest():
+    c = TierCache("t", "cpu", 300, RANK, half_life=4)
+    for e in range(3):
+        c.insert((0, e, "fp16"), blob(100))
+    for _ in range(3):
+        c.tick()
+        c.touch(c.entries[(0, 0, "fp16")])
+    c.tick()
+    c.insert((0, 9, "fp16"), blob(100))
+    assert (0, 0, "fp16") in c.entries and (0, 9, "fp16") in c.entries
+    assert len(c.entries) == 3 and c.stats.evictions == 1
+
+
+def test_lrfu_recency_beats_old_frequency():
+    c = TierCache("t", "cpu", 200, RANK, half_life=1)
+    c.insert((0, 0, "fp16"), blob(100))
+    for _ in range(3):
+        c.touch(c.entries[(0, 0, "fp16")])
+    c.clock += 20
+    c.insert((0, 1, "fp16"), blob(100))
+    c.insert((0, 2, "fp16"), blob(100))
+    assert (0, 0, "fp16") not in c.entries
+
+
+def test_precision_substitution():
+    c = TierCache("t", "cpu", 1000, RANK)
+    c.insert((2, 7, "fp16"), blob(10))
+    assert c.lookup(2, 7, "int4").key[2] == "fp16"  # a more precise copy serves
+    c2 = TierCache("t", "cpu", 1000, RANK)
+    c2.insert((2, 7, "int4"), blob(10))
+    assert c2.lookup(2, 7, "fp16") is None  # a less precise one does not
+    assert c2.lookup(2, 7, "int4", exact=True) is not None
+    assert c2.stats.hits == 1 and c2.stats.misses == 1
+    c2.lookup(2, 8, "int4", count=False)
+    assert c2.stats.misses == 1
+
+
+def test_pins_and_protect():
+    c = TierCache("t", "cpu", 300, RANK, pin_fraction=0.5)
+    c.insert((0, 0, "fp16"), blob(100), pinned=True)
+    c.insert((0, 1, "fp16"), blob(100))
+    c.insert((0, 2, "fp16"), blob(100))
+    assert c.insert((0, 3, "fp16"), blob(100), protect=frozenset({(0, 1, "fp16"), (0, 2, "fp16")})) is None
+    assert c.insert((0, 3, "fp16"), blob(100)) is not None
+    assert (0, 0, "fp16") in c.entries
+    assert c.insert((0, 4, "fp16"), blob(400)) is None
+    assert c.stats.rejected == 2
+
+
+def test_repin_hysteresis_and_max_swaps():
+    c = TierCache("t", "cpu", 10_000, RANK, pin_fraction=0.5, half_life=1000)
+    for e in range(5):
+        c.insert((0, e, "fp16"), blob(1000), pinned=True)
+    for e in range(5, 10):
+        c.insert((0, e, "fp16"), blob(1000))
+    for e in range(5, 10):
+        for _ in range(3):
+            c.touch(c.entries[(0, e, "fp16")])
+    swaps = c.repin(hysteresis=0.25, max_swaps=4)
+    assert len(swaps) == 4
+    assert sum(ent.pinned for ent in c.entries.values()) == 5
+    d = TierCache("t", "cpu", 2000, RANK, pin_fraction=0.5, half_life=1000)
+    d.insert((0, 0, "fp16"), blob(1000), pinned=True)
+    d.insert((0, 1, "fp16"), blob(1000))
+    d.entries[(0, 0, "fp16")].f = 10.0
+    d.entries[(0, 1, "fp16")].f = 11.0  # only 10 % hotter: no swap
+    assert d.repin() == []
+
+
+def test_heap_victims_match_sorted_scores():
+    """Brute force: every eviction removes an entry of the lowest score among the unpinned,
+    unprotected ones (the heap gives the same victims as a full sort)."""
+    rnd = random.Random(0)
+    c = TierCache("t", "cpu", 40 * 64, {"a": 0}.get, half_life=8.0, pin_fraction=0.25)
+    checked = 0
+    for step in range(3000):
+        r = rnd.random()
+        if r < 0.5:
+            key = (rnd.randrange(4), rnd.randrange(60), "a")
+            if key in c.entries:
+                c.touch(c.entries[key])
+                continue
+            protect = frozenset(rnd.sample(list(c.entries), min(3, len(c.entries)))) if c.entries else frozenset()
+            expect = None
+            if c.used + 64 > c.budget:
+                cands = sorted((e for e in c.entries.values() if not e.pinned and e.key not in protect), key=c.score)
+                expect = [round(c.score(cands[0]), 9)] if cands else None
+            before = {k: c.score(e) for k, e in c.entries.items()}
+            c.insert(key, blob(64), protect=protect, pinned=rnd.random() < 0.05)
+            gone = [k for k in before if k not in c.entries]
+            if expect is not None:
+                assert sorted(round(before[k], 9) for k in gone) == expect, step
+                assert not set(gone) & protect
+                checked += 1
+        elif r < 0.8:
+            c.tick()
+        elif r < 0.9 and c.entries:
+            c.unpin(rnd.choice(list(c.entries)))
+        elif c.entries:
+            c.pin(rnd.choice(list(c.entries)))
+    assert checked > 500 and c.used <= c.budget
+
+
+def test_stale_eviction_protects_current_pass():
+    for policy, victim in (("lrfu", (0, 1, "a")), ("stale", (0, 0, "a"))):
+        c = TierCache("t", "cpu", 3 * 64, {"a": 0}.get, eviction=policy)
+        old = c.insert((0, 0, "a"), blob(64))
+        for _ in range(5):  # old but much used: high LRFU score
+            c.touch(old)
+        c.tick()
+        c.insert((0, 1, "a"), blob(64))  # this pass
+        c.insert((0, 2, "a"), blob(64))
+        c.touch(c.entries[(0, 2, "a")])
+        c.insert((0, 3, "a"), blob(64))
+        assert {(0, 0, "a"), (0, 1, "a"), (0, 2, "a")} - set(c.entries) == {victim}, policy
+    with pytest.raises(ValueError):
+        TierCache("t", "cpu", 64, {"a": 0}.get, eviction="fifo")
+
+
+def test_listener_and_on_evict():
+    seen, freed = [], []
+
+    class L:
+        def added(self, e):
+            seen.append(("+", e.key))
+
+        def removed(self, e):
+            seen.append(("-", e.key))
+
+    c = TierCache("t", "cpu", 200, RANK, on_evict=freed.append)
+    c.listener = L()
+    a = blob(100)
+    c.insert((0, 0, "int4"), a)
+    c.insert((0, 1, "int4"), blob(100))
+    c.tick(5)
+    c.touch(c.entries[(0, 1, "int4")])
+    c.insert((0, 2, "int4"), blob(100))
+    assert seen == [("+", (0, 0, "int4")), ("+", (0, 1, "int4")), ("-", (0, 0, "int4")), ("+", (0, 2, "int4"))]
+    assert len(freed) == 1 and freed[0] is a
+    assert c.by_expert == {(0, 1): {"int4"}, (0, 2): {"int4"}}
+    c.clear()
+    assert c.used == 0 and not c.entries and not c.by_expert
+
+
+def test_host_pool_exact_slots_cap_and_quarantine():
+    pool = HostPool({"fp16": 3000, "int4": 800}, cap_bytes=64 * 1024, pin=False, log=lambda *a: None)
+    a = pool.acquire("fp16")
+    assert a.numel() == 3000 and pool.is_pooled(a)
+    assert pool.allocated & (pool.allocated - 1) == 0  # power-of-two slabs
+    assert a.data_ptr() % 4096 == 0 or pool.slabs[0].data_ptr() % 4096 == 0
+    pool.release(a)
+    pool.release(a)  # double release ignored
+    b = pool.acquire("fp16")
+    assert b.data_ptr() != a.data_ptr()  # quarantined until the next layer
+    pool.advance()
+    got = {pool.acquire("fp16").data_ptr() for _ in range(len(pool.free["fp16"]) + 1)}
+    assert a.data_ptr() in got
+    blobs = [pool.acquire("int4") for _ in range(200)]
+    assert pool.allocated <= pool.cap and pool.fallbacks > 0
+    assert all(x.numel() == 800 for x in blobs)
+
+
+def test_host_pool_event_gates_reuse():
+    class Ev:
+        def __init__(self):
+            self.done = False
+
+        def query(self):
+            return self.done
+
+    pool = HostPool({"int4": 1024}, cap_bytes=16 * 1024, pin=False, log=lambda *a: None)
+    slots = [pool.acquire("int4") for _ in range(16)]
+    ev = Ev()
+    pool.release(slots[0], ev)
+    pool.advance()
+    extra = pool.acquire("int4")
+    assert not pool.is_pooled(extra) and pool.fallbacks == 1  # the copy reading slot 0 is in flight
+    ev.done = True
+    assert pool.acquire("int4").data_ptr() == slots[0].data_ptr()
+
+
+def test_host_pool_recycles_free_slabs_across_precisions():
+    pool = HostPool({"int8": 6000, "int4": 3000}, cap_bytes=4 * 65536, pin=False, log=lambda *a: None)
+    lo = []
+    while True:
+        b = pool.acquire("int4")
+        if not pool.is_pooled(b):
+            break
+        lo.append(b)
+    assert pool.allocated == pool.cap and pool.free["int8"] == []
+    for b in lo:
+        pool.release(b)
+    pool.advance()
+    hi = [pool.acquire("int8") for _ in range(20)]
+    assert all(pool.is_pooled(x) for x in hi) and pool.reclaims > 0 and pool.fallbacks == 1
+    assert pool.allocated == pool.cap
+    assert len({x.data_ptr() for x in hi}) == 20
+    pool.close()
+    assert pool.allocated == 0 and "0.00" in pool.describe()
+
+
+def test_slab_size_rule():
+    """Slab = max(pow2 >= record, min(256 MiB, pow2 >= 16 records)), shrunk to the largest power
+    of two that fits under the cap."""
+    rb = 1_671_168  # a Qwen3-Next-shaped int4 record
+    pool = HostPool({"int4": rb}, cap_bytes=1 << 30, pin=False, log=lambda *a: None)
+    pool.acquire("int4")
+    assert pool.allocated == 1 << 25  # 16 records -> 26.7 MB -> 32 MiB
+    assert len(pool.free["int4"]) == (1 << 25) // rb - 1
+    small = HostPool({"int4": rb}, cap_bytes=5 * rb, pin=False, log=lambda *a: None)
+    small.acquire("int4")
+    assert small.allocated == 1 << int(math.log2(5 * rb))
