@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MOEHIP_ABI_VERSION 1
+#define MOEHIP_ABI_VERSION 2
 
 /* error codes */
 #define MOEHIP_OK 0
@@ -49,6 +49,8 @@ extern "C" {
 #define MOEHIP_DT_F32 2
 
 int moehip_abi_version(void);
+/* sizeof(moehip_layer_desc) as compiled into the library (a binding checks its own struct). */
+size_t moehip_layer_desc_bytes(void);
 const char *moehip_last_error(void);
 /* 0 if device `dev` is a gfx950 (MI355X-class) GPU, MOEHIP_ENODEV otherwise. */
 int moehip_device_check(int dev);
@@ -168,6 +170,13 @@ typedef struct moehip_layer_desc {
     int lv2p[3];        /* HOBBIT level -> precision index (moelab/policy.py:188-192) */
     int64_t offs[4][4]; /* byte offsets of [gate_up.q, gate_up.s, down.q, down.s] in a record */
     moehip_policy pol;
+    /* Qwen3-Next shared expert (transformers Qwen3NextSparseMoeBlock.forward, models/qwen3_next/
+     * modeling_qwen3_next.py:786-797): out += sigmoid(x . shared_gate) * FFN_s(x). shared_gate (H)
+     * in the activation dtype, NULL = no shared expert; shared_rec[p] = base address of the
+     * shared expert's record in precision p (0 = absent; the most precise present copy runs).
+     * With a shared expert the workspace is sized for k + 1 rows. */
+    const void *shared_gate;
+    int64_t shared_rec[4];
 } moehip_layer_desc;
 
 /*

@@ -32,6 +32,8 @@ extern "C" int moehip_abi_version(void) { return MOEHIP_ABI_VERSION; }
 
 extern "C" const char *moehip_last_error(void) { return moehip::g_err; }
 
+extern "C" size_t moehip_layer_desc_bytes(void) { return sizeof(moehip_layer_desc); }
+
 extern "C" int moehip_device_check(int dev) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {

@@ -71,6 +71,9 @@ struct LayerArgs {
     int dn_base[DL_MAXP];
     int lv2p[3];
     int P, E, k, H, I, renorm, accumulate;
+    int ks;                 // table rows per precision: k routed (+ 1 shared)
+    const void *sgate;      // (H) shared-expert gate vector or null
+    int64_t srec[DL_MAXP];  // shared-expert record per precision (0 = absent)
     int NU, ND;             // up / down items
     moehip_policy pol;
     void *out;              // (H) activation dtype
@@ -582,7 +585,8 @@ template <int XDT>
 __device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int *s_idx, float *s_w, float *s_sorted,
                                            float *s_buf, uint32_t *err, uint64_t *ts) {
     const int lane = threadIdx.x;  // wave 0 only; s_buf: 2 * 1024 words of LDS (logits, keys)
-    const int k = a.k, E = a.E;
+    const int k = a.k, E = a.E, ks = a.ks;
+    const bool has_sh = a.sgate != nullptr;
     const int epl = (E + 63) >> 6;
     float *s_lv = s_buf;
     uint32_t *s_key = reinterpret_cast<uint32_t *>(s_buf + 1024);
@@ -710,10 +714,34 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int
             for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.rtab[(size_t)pi * E + myc] : 0;
         }
     }
+    if (has_sh && lane == k) {
+        // the shared expert (row k): weight sigmoid(x . g) with x . g rounded to the activation
+        // dtype like the gate's output (modeling_qwen3_next.py:793-796), record from srec
+        const uint64_t *ls = ws_ptr<uint64_t>(a, a.off_logits) + E;
+        float l = 0.f;
+        bool got = false;
+        int nap = 1;
+        for (int it = 0; it < WAIT_SPINS; ++it) {
+            const uint64_t v = ld_tag(ls);
+            if (tag_ok(v, tag)) {
+                l = __uint_as_float((uint32_t)v);
+                got = true;
+                break;
+            }
+            backoff(nap);
+        }
+        if (!got) flag_error(err);
+        myc = -1;
+        myw = got ? rnd_act<XDT>(1.0f / (1.0f + expf(-l))) : 0.f;
+#pragma unroll
+        for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.srec[pi] : 0;
+    }
     TS(3);
     // HOBBIT levels (moelab/policy.py:77-123), resident copy, tables (moelab/fullgraph.py:149-171)
     const int j = lane;
-    const bool act = j < k;
+    const bool act = j < k;                  // a routed row
+    const bool shr = has_sh && j == k;       // the shared row: level 0, never skipped
+    const bool row = act || shr;
     const int e = act ? myc : 0;
     if (act) {
         s_idx[j] = e;
@@ -748,35 +776,41 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int
         if (s <= pol.t1) lvl = 0;
         skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
     }
+    if (shr) {
+        lvl = 0;
+        skip = false;
+    }
     TS(4);
     const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
-    const int req = lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2);
+    // the shared row takes its most precise present copy
+    const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
+    const bool upg = shr || pol.upgrade;
     int chosen = -1;
 #pragma unroll
     for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
         const bool avail = pi < a.P && rt[pi] != 0;
-        if (avail && (pol.upgrade ? req >= pi : req == pi)) chosen = pi;
+        if (avail && (upg ? req >= pi : req == pi)) chosen = pi;
     }
     const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
-    const bool is_miss = act && !skip && !usable;
+    const bool is_miss = row && !skip && !usable;
     uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec);
     // the chosen copy (address, weight) of this row; compact loops keep the register use small
-    const bool sel = act && chosen >= 0 && !skip && usable;
+    const bool sel = row && chosen >= 0 && !skip && usable;
     const int64_t base = !sel ? 0 : (chosen == 0 ? rt[0] : (chosen == 1 ? rt[1] : (chosen == 2 ? rt[2] : rt[3])));
-    const uint32_t wbits = sel ? __float_as_uint(wj) : 0u;
-    if (act) {
+    const uint32_t wbits = sel ? __float_as_uint(row ? myw : 0.f) : 0u;
+    if (row) {
 #pragma unroll 1
         for (int pi = 0; pi < a.P; ++pi) {
             const bool mine = sel && chosen == pi;
 #pragma unroll 1
             for (int cp = 0; cp < NREC; ++cp) {
-                uint64_t *r3 = rec + (size_t)cp * rec_stride_words(a.P, k) + ((size_t)pi * k + j) * 3;
+                uint64_t *r3 = rec + (size_t)cp * rec_stride_words(a.P, ks) + ((size_t)pi * ks + j) * 3;
                 st_tag(r3 + 1, mine ? (uint32_t)(uint64_t)base : 0u, tag);
                 st_tag(r3 + 2, mine ? (uint32_t)((uint64_t)base >> 32) : 0u, tag);
                 st_tag(r3 + 0, mine ? wbits : 0u, tag);
             }
         }
-        if (a.info) {
+        if (a.info && act) {
             a.info[j] = (float)e;
             a.info[k + j] = skip ? -2.f : (float)chosen;
             a.info[2 * k + j] = (float)lvl;
@@ -795,14 +829,18 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int
 template <int XDT>
 __device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t tag) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = t * 4 + wave;
-    if (e >= a.E) return;
+    // rows: the E router rows (with Wr), then the shared-expert gate as row E (with sgate)
+    const int r = t * 4 + wave;
+    const int nrows = (a.Wr != nullptr ? a.E : 0) + (a.sgate != nullptr ? 1 : 0);
+    if (r >= nrows) return;
+    const int e = a.Wr != nullptr ? r : a.E;
     constexpr int ESZ = XDT == MOEHIP_DT_F32 ? 4 : 2;
     constexpr int NV = 32 * ESZ / 16;  // 16-byte vectors per lane
     const int c0 = lane * 32;
     float acc = 0.f;
     if (c0 < a.H) {
-        const uint8_t *wp = reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ;
+        const uint8_t *wp = e < a.E ? reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ
+                                    : reinterpret_cast<const uint8_t *>(a.sgate) + (size_t)c0 * ESZ;
         const uint8_t *xp = reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * ESZ;
         uint4 wv[NV], xv[NV];
 #pragma unroll
@@ -847,7 +885,7 @@ __device__ __forceinline__ Route wg_route(const LayerArgs &a, uint32_t tag, int 
     const int tid = threadIdx.x;
     if (tid < 64) {
         const uint64_t *r3 =
-            ws_ptr<uint64_t>(a, a.off_rec) + (size_t)(blockIdx.x % NREC) * rec_stride_words(a.P, a.k) + (size_t)jj * 3;
+            ws_ptr<uint64_t>(a, a.off_rec) + (size_t)(blockIdx.x % NREC) * rec_stride_words(a.P, a.ks) + (size_t)jj * 3;
         int nap = 1;
         bool got = false;
         uint32_t p = 0;
@@ -940,7 +978,7 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     const int G = 1 << lg, RPW = 64 >> lg;
     const int per_wave = DlFmt<PREC>::NPD * RPW;
     const int row0 = b * per_wave * 4 + wave * per_wave;
-    const int PK = a.P * a.k;
+    const int PK = a.P * a.ks;
     const Route rt0 = wg_route(a, tag, jj, s_wk, err);
     stamp(st, 1);
     const bool run = rt0.w != 0.f;
@@ -1017,6 +1055,13 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     }
 }
 
+// work items of the router stage: 4 rows each (E router rows, + the shared gate row); at least
+// one, which also runs the route tail
+__host__ __device__ __forceinline__ int router_items(bool with_router, bool shared, int E) {
+    const int rows = (with_router ? E : 0) + (shared ? 1 : 0);
+    return rows > 0 ? (rows + 3) / 4 : 1;
+}
+
 // rows per down item / row pairs per up item of a precision (host and device)
 __host__ __device__ __forceinline__ int down_item_rows(int prec, int lg) {
     const int npd = prec == MOEHIP_PREC_INT4 ? 8 : ((prec == MOEHIP_PREC_F16 || prec == MOEHIP_PREC_BF16) ? 2 : 4);
@@ -1037,7 +1082,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
     const int tid = threadIdx.x;
     uint32_t *ws = a.ws;
     uint32_t *err = ws + W_ERR;
-    const int NR = a.Wr != nullptr ? (a.E + 3) / 4 : 1;
+    const int NR = router_items(a.Wr != nullptr, a.sgate != nullptr, a.E);
     const int total = NR + a.NU + a.ND;
     if (tid == 0) s_tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
     __syncthreads();
@@ -1048,7 +1093,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
         if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
         if (t < NR) {
             // ---------------- router rows; the last router item also routes ----------------
-            if (a.Wr != nullptr) router_rows<XDT>(a, t, tag);
+            if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag);
             if (t == NR - 1 && tid < 64)
                 route_tail<XDT>(a, tag, s_idx, s_w, s_sorted, s_h, err, a.trace ? a.trace + 3 * total : nullptr);
         } else if (t < NR + a.NU) {
@@ -1057,7 +1102,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             const int pi = block_of(a.up_base, a.P, u);
             const int rem = u - pick4(a.up_base, pi);
             const int nub = pick4(a.nub, pi);
-            const int jj = pi * a.k + rem / nub, b = rem % nub;
+            const int jj = pi * a.ks + rem / nub, b = rem % nub;
             switch (pick4(a.prec, pi)) {
                 case MOEHIP_PREC_INT4: up_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
                 case MOEHIP_PREC_INT8: up_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
@@ -1071,7 +1116,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             const int pi = block_of(a.dn_base, a.P, dd);
             const int rem = dd - pick4(a.dn_base, pi);
             const int ndb = pick4(a.ndb, pi);
-            const int jj = pi * a.k + rem / ndb, b = rem % ndb;
+            const int jj = pi * a.ks + rem / ndb, b = rem % ndb;
             switch (pick4(a.prec, pi)) {
                 case MOEHIP_PREC_INT4: down_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
                 case MOEHIP_PREC_INT8: down_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
@@ -1116,7 +1161,7 @@ static DlLayout dl_layout(int P, int k, int E, int H, int I) {
     off += (size_t)NREC * rec_stride_words(P, k) * 8;
     off = al256(off);
     L.logits = (uint32_t)off;
-    off += (size_t)E * 8;
+    off += (size_t)(E + 1) * 8;  // + the shared-expert gate
     off = al256(off);
     L.h = (uint32_t)off;
     off += (size_t)PK * I * 8;
@@ -1130,6 +1175,7 @@ static DlLayout dl_layout(int P, int k, int E, int H, int I) {
 // item plan of a layer: fills the plan fields of `a`, returns the number of work items
 static int dl_plan(const moehip_layer_desc *d, int with_router, LayerArgs *a) {
     int nu = 0, nd = 0;
+    const int ks = d->k + (d->shared_gate != nullptr ? 1 : 0);
     for (int p = 0; p < DL_MAXP; ++p) {
         const bool on = p < d->P;
         a->lg_up[p] = on ? lg_for(d->H, d->prec[p]) : 0;
@@ -1142,13 +1188,13 @@ static int dl_plan(const moehip_layer_desc *d, int with_router, LayerArgs *a) {
             const int dpi = down_item_rows(d->prec[p], a->lg_dn[p]);
             a->nub[p] = (d->I + upi - 1) / upi;
             a->ndb[p] = (d->H + dpi - 1) / dpi;
-            nu += d->k * a->nub[p];
-            nd += d->k * a->ndb[p];
+            nu += ks * a->nub[p];
+            nd += ks * a->ndb[p];
         }
     }
     a->NU = nu;
     a->ND = nd;
-    return (with_router ? (d->E + 3) / 4 : 1) + nu + nd;
+    return router_items(with_router != 0, d->shared_gate != nullptr, d->E) + nu + nd;
 }
 
 // workgroups of k_decode_layer<DT> the current device holds at once (occupancy x CUs)
@@ -1202,10 +1248,14 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
                            d->gs_dn[p], vpc);
         }
     }
-    const DlLayout L = dl_layout(d->P, d->k, d->E, d->H, d->I);
+    const int ks = d->k + (d->shared_gate != nullptr ? 1 : 0);
+    const DlLayout L = dl_layout(d->P, ks, d->E, d->H, d->I);
     MOEHIP_REQUIRE(ws_bytes >= L.total, "decode_layer: workspace %zu bytes < %u", ws_bytes, L.total);
     MOEHIP_REQUIRE(((uintptr_t)ws % 256) == 0, "decode_layer: workspace must be 256-byte aligned");
-    MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)Wr % 16) == 0, "decode_layer: x and Wr must be 16-byte aligned");
+    MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)d->shared_gate % 16) == 0,
+                   "decode_layer: x, Wr and the shared gate must be 16-byte aligned");
+    MOEHIP_REQUIRE(d->P * ks <= DL_MAXP * 32, "decode_layer: %d precisions x %d rows exceed %d table rows", d->P, ks,
+                   DL_MAXP * 32);
     LayerArgs a;
     a.x = x;
     a.Wr = Wr;
@@ -1225,6 +1275,9 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.P = d->P;
     a.E = d->E;
     a.k = d->k;
+    a.ks = ks;
+    a.sgate = d->shared_gate;
+    for (int p = 0; p < DL_MAXP; ++p) a.srec[p] = p < d->P ? d->shared_rec[p] : 0;
     a.H = d->H;
     a.I = d->I;
     a.renorm = d->renorm;

@@ -15,6 +15,7 @@ import torch
 
 LIB_PATH = Path(os.environ.get("MOEHIP_LIB", Path(__file__).resolve().parent / "libmoehip.so"))
 
+ABI_VERSION = 2
 PREC_CODES = {"int4": 0, "int8": 1, "fp16": 2, "bf16": 3, "fp32": 4, "fp8": 5}
 DT_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -34,7 +35,8 @@ class LayerDesc(ctypes.Structure):
 
     _fields_ = [("P", _i), ("E", _i), ("k", _i), ("H", _i), ("I", _i), ("dtype", _i), ("renorm", _i),
                 ("prec", _i * 4), ("gs_up", _i * 4), ("gs_dn", _i * 4), ("planned", _i * 4), ("lv2p", _i * 3),
-                ("offs", (ctypes.c_int64 * 4) * 4), ("pol", Policy)]
+                ("offs", (ctypes.c_int64 * 4) * 4), ("pol", Policy), ("shared_gate", _vp),
+                ("shared_rec", ctypes.c_int64 * 4)]
 
 
 class Copy(ctypes.Structure):
@@ -45,6 +47,7 @@ class Copy(ctypes.Structure):
 
 _SIGS = {
     "moehip_abi_version": ([], _i),
+    "moehip_layer_desc_bytes": ([], ctypes.c_size_t),
     "moehip_last_error": ([], ctypes.c_char_p),
     "moehip_device_check": ([_i], _i),
     "moehip_gemv_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
@@ -90,8 +93,8 @@ def load(path: Path | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
-    if lib.moehip_abi_version() != 1:
-        raise RuntimeError(f"libmoehip ABI {lib.moehip_abi_version()} != 1")
+    if lib.moehip_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libmoehip ABI {lib.moehip_abi_version()} != {ABI_VERSION}")
     _lib = lib
     return lib
 

@@ -87,8 +87,11 @@ class MoEDecoder:
 
     def __init__(self, store: ResidentStore, k: int, policy: PrecisionPolicy | None = None, dtype=torch.float16,
                  router_weights: list | None = None, renorm: bool = False, planned: list | None = None,
-                 fused: bool = True, grid: int = 0):
+                 fused: bool = True, grid: int = 0, shared: list | None = None):
+        """shared: per layer None or {"gate": (H,) tensor in dtype, "rec": {precision: record blob}}
+        for a Qwen3-Next shared expert (out += sigmoid(x . gate) * FFN_s(x)); fused path only."""
         self.store = store
+        self.shared = shared
         self.k = k
         self.policy = policy or PrecisionPolicy("lo")
         self.dtype = dtype
@@ -123,9 +126,12 @@ class MoEDecoder:
         self.trace = None  # optional int64 device tensor of 3 * (items + 3) + 8 * items: per-item stamps
         self.fused = fused and all(store.layouts[p]["precision"] != "fp32" for p in precs) and H <= 2048 \
             and _dims(store.layouts[precs[0]])[1] <= 2048
+        if shared is not None and not self.fused:
+            raise RuntimeError("MoEDecoder: the shared expert runs in the fused decode kernel only")
         if self.fused:
             self._descs = [self._desc(l) for l in range(store.L)]
-            nbytes = _lib.load().moehip_decode_layer_workspace_bytes(self.P, k, E, H, self._descs[0].I)
+            rows = k + (1 if shared is not None and any(s is not None for s in shared) else 0)
+            nbytes = _lib.load().moehip_decode_layer_workspace_bytes(self.P, rows, E, H, self._descs[0].I)
             self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
             self.err = torch.zeros(1, dtype=torch.int32, device=dev)
 
@@ -147,6 +153,15 @@ class MoEDecoder:
         for v in range(3):
             d.lv2p[v] = self.lv2p[v]
         d.pol = self._pols[layer]
+        sh = self.shared[layer] if self.shared is not None else None
+        if sh is not None:
+            g = sh["gate"]
+            if g.dtype != self.dtype or g.numel() != d.H or not g.is_contiguous() or g.device != st.device:
+                raise RuntimeError(f"shared gate of layer {layer}: ({d.H},) {self.dtype} contiguous on {st.device}")
+            d.shared_gate = g.data_ptr()
+            for pi, p in enumerate(st.precisions):
+                blob = sh["rec"].get(p)
+                d.shared_rec[pi] = 0 if blob is None else blob.data_ptr()
         return d
 
     def work_items(self) -> int:

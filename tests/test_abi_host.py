@@ -32,7 +32,8 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.moehip_abi_version() == 1
+    assert lib.moehip_abi_version() == 2
+    assert lib.moehip_layer_desc_bytes() == ctypes.sizeof(_lib.LayerDesc)
 
 
 def test_argument_validation_without_gpu():

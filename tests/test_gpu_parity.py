@@ -528,3 +528,47 @@ def test_fused_router_planted_ties(dev, k):
     assert np.allclose(dec.w32.cpu().numpy(), w, rtol=2.0 ** -10, atol=0)
     assert_layer_close(out.float().cpu().numpy(), ref, torch.float16)
     dec.check_error()
+
+
+@pytest.mark.parametrize("prec", ["int4", "fp8"])
+@pytest.mark.parametrize("routed", [True, False])
+def test_fused_qwen3next_shared_expert(dev, prec, routed):
+    """Qwen3-Next layer with its shared expert in the same launch: routed top-10 of 512
+    (renormalised) + sigmoid(x . g) * FFN_s(x), bf16; the gate logit and the sigmoid rounded to
+    bf16 as the module computes them (modeling_qwen3_next.py:786-797)."""
+    H, I, E, k = 2048, 512, 512, 10
+    dtype = torch.bfloat16
+    S = _Stack(dev, H, I, E, 1, [prec], 12, dtype=dtype)
+    lay = S.store.layouts[prec]
+    g = torch.Generator().manual_seed(77)
+    gu_s, dn_s = torch.randn(2 * I, H, generator=g) * 0.02, torch.randn(H, I, generator=g) * 0.02
+    sh_blob = torch.zeros(lay["record_bytes"], dtype=torch.uint8, device=dev)
+    encode_record_(lay, sh_blob, gu_s.to(dev), dn_s.to(dev))
+    gate = (torch.randn(H, generator=g) * 0.05).to(dtype)
+    olay = O.record_layout(prec, H, I, 64, scale="absmax")
+    mats_s = O.materialize(olay, O.encode_record(olay, gu_s.numpy(), dn_s.numpy(), "absmax"))
+    dec = MoEDecoder(S.store, k, PrecisionPolicy("lo"), dtype, router_weights=[S.Wr[0].to(dev)] if routed else None,
+                     renorm=True, shared=[{"gate": gate.to(dev), "rec": {prec: sh_blob}}])
+    for t in range(3):
+        x = torch.randn(1, H, generator=g).to(dtype)
+        out = torch.zeros(1, H, dtype=dtype, device=dev)
+        print(f"shared expert {prec} routed={routed} token {t}", flush=True)
+        if routed:
+            dec.layer(0, x.to(dev), out)
+            _, idx, w, ref = S.reference(0, x, k, True, O.Policy("lo"))
+        else:
+            idx = torch.randperm(E, generator=g)[:k].view(1, k).numpy()
+            w = O.round_to(np.random.default_rng(t).random((1, k)).astype(np.float32), "bfloat16")
+            dec.layer(0, x.to(dev), out, idx=torch.from_numpy(idx).to(dev),
+                      w32=torch.from_numpy(w.astype(np.float32)).to(dev))
+            ref = O.moe_layer(x.float().numpy(), idx, w.astype(np.float64), lambda e: S.mats(0, e, prec))
+        torch.cuda.synchronize()
+        xf = x.float().numpy().astype(np.float64)
+        logit = O.round_to((xf @ gate.float().numpy().astype(np.float64)).astype(np.float32), "bfloat16")
+        gs = O.round_to((1.0 / (1.0 + np.exp(-logit.astype(np.float64)))).astype(np.float32), "bfloat16")
+        ref = ref + gs.astype(np.float64)[:, None] * O.expert_ffn(xf, *mats_s)
+        if routed:
+            assert dec.idx.cpu().numpy().tolist() == idx.tolist()
+        assert_layer_close(out.float().cpu().numpy(), ref, dtype)
+        assert dec.miss.item() == 0
+    dec.check_error()
