@@ -217,7 +217,7 @@ int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
  * on MFMA (fp16 operands, exact int4 values, fp32 accumulation and group scales), then
  * out[t] = sum over the token's slots in slot order (+ out if accumulate) (+ add). tab (E, 4)
  * int64 record field addresses (0 row = expert not resident: contributes nothing); x (T, H)
- * and out (T, H) in xdtype (fp16 / bf16); w (T*k) fp32 routing weights. H, I multiples of 64,
+ * and out (T, H) in xdtype (fp16 / bf16); w (T*k) fp32 routing weights. H a multiple of 256, I of 128,
  * gs = 64. ws: moehip_grouped_gemm_workspace_bytes(), 256-B aligned.
  * Replaces moelab/runtime.py:418-436 (`_run_grouped_tokens`, per-expert expert_ffn) and the
  * T > 1 accumulation runtime.py:352-353 (`out.index_add_(0, tok, y * w)`).

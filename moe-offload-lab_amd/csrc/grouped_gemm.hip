@@ -2,402 +2,406 @@
 //
 // Replaces the reference's prefill expert path (moelab/runtime.py:418-436 `_run_grouped_tokens`
 // and :352-353: per expert y = expert_ffn(x[tok]), out.index_add_(tok, y * w)) for int4 gs64
-// records. The pairs (token, slot) are sorted by expert (moehip_dispatch); per expert the tokens
+// records. The (token, slot) pairs are sorted by expert (moehip_dispatch); per expert the tokens
 // form the M dimension of two GEMMs:
 //   up:   h (n_e, I) = silu(X_e gate^T) * (X_e up^T)     K = H, weight rows 2I (gate; up)
 //   down: y (n_e, H) = w_pair * (h down^T)               K = I, weight rows H
 // followed by an ordered combine out[t] = sum over the token's slots in slot order.
 //
-// MFMA: v_mfma_f32_16x16x32_f16. A = activations (16 tokens x 32 K), B = weights (32 K x 16
-// rows), D = 16 tokens x 16 rows in fp32. One K step of 64 = one int4 scale group: each lane
-// loads 8 bytes (16 nibbles) of its weight row, turns each 8 nibbles into fp16 1024 + n with
-// one v_and_or_b32 per pair (exact), runs the group's two MFMAs, and folds the group into its
-// fp32 accumulators as acc += scale * (D - 1032 * sum_k x_k) (the offset 1024 + 8 removed with
-// the group sum of the activations, the scale applied in fp32): the products and the scale are
-// exact, as in the reference's dequantise-then-matmul path.
+// MFMA: v_mfma_f32_32x32x16_f16: A = 32 tokens x 16 K (lane i + 32 (k / 8), element k % 8),
+// B = 16 K x 32 weight rows (same lane rule), D = 32 x 32 fp32 (row i at lane
+// j + 32 ((i / 4) % 2), element 4 (i / 8) + i % 4), accumulated over the whole K. In one int4
+// scale group (64 K) lane half h of weight row j holds bytes 16 h .. 16 h + 15 (one 16-byte
+// load) and dword m of them feeds MFMA m: its 8 nibbles become fp16 1024 + n (exact), then
+// n - 8 (exact) and s * (n - 8) (one fp16 rounding, relative error <= 2^-11; the reference's own
+// prefill path rounds the dequantised weights to the model dtype, 2^-8 for bf16).
 //
-// Activations: every token row is scaled by a power of two into fp16 range (exact for fp16 and
-// bf16 inputs; the factor is applied back to the outputs). h enters the down GEMM as an fp16
-// hi + lo pair (two MFMAs per step), i.e. ~22 bits of its fp32 value.
+// Operand A is fp16 in LDS: fp16 activations as they are, bf16 activations scaled per token by a
+// power of two 2^-e (the row's largest |x| in [2^14, 2^15), exact for bf16 values), h (fp32,
+// written by the up kernel with a per-pair maximum gathered by atomics) scaled per pair the
+// same way; the outputs are scaled back by 2^e.
 //
-// Each workgroup (4 waves) owns one expert and a block of weight rows (up: 128 h columns =
-// 128 gate + 128 up rows; down: 256 output rows), every wave 4 subtiles of 16 rows, for up to
-// 64 tokens per pass; activations of the next K step are staged into LDS (double buffered,
-// rows padded to 144 bytes so the fragment reads are bank-conflict free) while the current
-// step computes.
+// Each workgroup (4 waves) owns one expert and 256 weight rows (up: 128 gate + 128 up rows =
+// 128 h columns; down: 256 output rows); a wave owns 2 subtiles of 32 rows, for up to 64
+// tokens per pass (two 32-token M tiles). K advances in chunks (up: 4 groups, down: 2): a wave
+// keeps a ring of chunks of its weight rows in registers (16 KB in flight while it computes),
+// and the workgroup stages the activation chunk into LDS (double buffered, rows padded by 16
+// bytes, permuted into operand order) one chunk ahead. Workgroups of one expert land on one XCD
+// (its L2 then serves the expert's activation rows to all of them).
 
 #include "gemv_core.hpp"
 
 namespace moehip {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+// record bytes in the global address space: table entries are plain integers, and loads through
+// generic pointers would be flat loads, which also count against the LDS wait counter (every
+// LDS wait would then wait for every weight load in flight)
+typedef const __attribute__((address_space(1))) uint8_t gu8;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ gu8 *record_ptr(int64_t a) { return (gu8 *)(uintptr_t)a; }
+__device__ __forceinline__ uint4 gload16(gu8 *p) {
+    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
-constexpr int GG_MT = 4;            // 16-token M tiles per pass
-constexpr int GG_TOK = GG_MT * 16;  // tokens per pass
-constexpr int GG_NS = 4;            // 16-row N subtiles per wave
-constexpr int GG_KG = 64;           // K per step (= the int4 group size)
-constexpr int GG_LDW = 72;          // LDS row stride in halves (64 + 8: 144 bytes)
+constexpr int GG_KG = 64;     // K per scale group
+constexpr int GG_TOK = 64;    // tokens per pass (two 32-token M tiles)
+constexpr int GG_ROWS = 256;  // weight rows per workgroup
 
-// exponent e of a row so that max|row| * 2^-e lies in [2^14, 2^15) (0 for an all-zero row)
+// chunk geometry: NGC groups of 64 K; each of the 256 threads stages CK / 4 fp16 values of one
+// token (NV 16-byte loads)
+template <int NGC> struct GgChunk {
+    static constexpr int CK = NGC * GG_KG;  // K per chunk
+    static constexpr int LDA = CK + 8;      // LDS row stride in halves
+    static constexpr int VPT = CK / 4;      // values staged per thread
+    static constexpr int NV = VPT / 8;      // 16-byte loads per thread
+};
+
+// ---------------------------------------------------------------------------------------
+// weights: dword d of a row (K elements c0..c7 as nibbles) and the group scale s (fp16, both
+// halves) -> fp16 s * (n - 8) in operand order c0 c4 c1 c5 c2 c6 c3 c7: (d & mask) | magic =
+// fp16 1024 + n in one v_and_or_b32 (common.hpp and_or; its result feeds the compiler's packed
+// fp16 add, never an MFMA operand directly), - 1032 (exact), * s (one rounding).
+// ---------------------------------------------------------------------------------------
+struct DeqK {
+    uint32_t mask, magic;  // 0x000F000F, 0x64006400
+};
+
+__device__ __forceinline__ f16x8 wdeq8(uint32_t d, half2_t s2, DeqK k) {
+#pragma clang fp contract(off)
+    const half2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const uint32_t u0 = and_or(d, k.mask, k.magic);  // 1024 + n
+    const uint32_t u1 = and_or(d >> 4, k.mask, k.magic);
+    const uint32_t u2 = and_or(d >> 8, k.mask, k.magic);
+    const uint32_t u3 = and_or(d >> 12, k.mask, k.magic);
+    const half2_t h0 = (__builtin_bit_cast(half2_t, u0) + off) * s2;
+    const half2_t h1 = (__builtin_bit_cast(half2_t, u1) + off) * s2;
+    const half2_t h2 = (__builtin_bit_cast(half2_t, u2) + off) * s2;
+    const half2_t h3 = (__builtin_bit_cast(half2_t, u3) + off) * s2;
+    const uint4 u = make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                               __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
+    return __builtin_bit_cast(f16x8, u);
+}
+
+template <int NGC> struct WChunk {
+    uint4 q[2][NGC];       // subtile, group: this lane half's 16 bytes of its row
+    uint32_t s[2][NGC / 2];  // subtile: the NGC group scales (fp16 pairs)
+};
+
+template <int NGC>
+__device__ __forceinline__ void load_chunk(WChunk<NGC> &w, gu8 *const (&qp)[2], gu8 *const (&sp)[2], int c) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        gu8 *q = qp[t] + (size_t)c * (GgChunk<NGC>::CK / 2);
+#pragma unroll
+        for (int g = 0; g < NGC; ++g) w.q[t][g] = gload16(q + 32 * g);  // 32 bytes per group row: this half's 16
+        gu8 *s = sp[t] + (size_t)c * (NGC * 2);
+        if constexpr (NGC == 4) {
+            const u32x2_t v = *(const __attribute__((address_space(1))) u32x2_t *)s;
+            w.s[t][0] = v.x, w.s[t][1] = v.y;
+        } else {
+            w.s[t][0] = *(const __attribute__((address_space(1))) uint32_t *)s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// activation chunks (fp16): thread tid stages token tid / 4 of the pass, values VPT * (tid % 4) ..
+// of the chunk, permuted per 8 values into operand order (c0 c4 c1 c5 c2 c6 c3 c7), into LDS row
+// `tok`. Threads past the pass's tokens load a valid row too (no branch around the loads, which
+// keeps the compiler's load counting exact): MFMA rows are independent and those rows are never
+// stored.
+// ---------------------------------------------------------------------------------------
+template <int NGC>
+__device__ __forceinline__ void xs_load(const uint16_t *row, int c, uint4 (&v)[GgChunk<NGC>::NV]) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)c * GgChunk<NGC>::CK +
+                                                     (threadIdx.x & 3) * GgChunk<NGC>::VPT);
+#pragma unroll
+    for (int m = 0; m < GgChunk<NGC>::NV; ++m) v[m] = p[m];
+}
+
+template <int NGC>
+__device__ __forceinline__ void xs_store(const uint4 (&v)[GgChunk<NGC>::NV], uint16_t *s_a) {
+    const int tok = threadIdx.x >> 2, part = threadIdx.x & 3;
+    uint4 *dst = reinterpret_cast<uint4 *>(s_a + tok * GgChunk<NGC>::LDA + part * GgChunk<NGC>::VPT);
+#pragma unroll
+    for (int m = 0; m < GgChunk<NGC>::NV; ++m) {
+        const uint4 u = v[m];
+        dst[m] = make_uint4(lo_lo(u.x, u.z), hi_hi(u.x, u.z), lo_lo(u.y, u.w), hi_hi(u.y, u.w));
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// one chunk of MFMAs for a wave: NGC groups x 4 MFMAs x NM M tiles x 2 subtiles
+// ---------------------------------------------------------------------------------------
+template <int NGC, int NM>
+__device__ __forceinline__ void mma_chunk(const WChunk<NGC> &w, const uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < NGC; ++g) {
+        half2_t s2[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t sw = (w.s[t][g >> 1] >> (16 * (g & 1))) & 0xffffu;
+            s2[t] = __builtin_bit_cast(half2_t, sw | (sw << 16));
+        }
+        const uint16_t *ap = s_a + i * GgChunk<NGC>::LDA + g * GG_KG + h * 32;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const uint4 q0 = w.q[0][g], q1 = w.q[1][g];
+            const uint32_t d0 = m == 0 ? q0.x : (m == 1 ? q0.y : (m == 2 ? q0.z : q0.w));
+            const uint32_t d1 = m == 0 ? q1.x : (m == 1 ? q1.y : (m == 2 ? q1.z : q1.w));
+            const f16x8 b0 = wdeq8(d0, s2[0], dk), b1 = wdeq8(d1, s2[1], dk);
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const f16x8 a = *reinterpret_cast<const f16x8 *>(ap + mt * 32 * GgChunk<NGC>::LDA + 8 * m);
+                d[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b0, d[mt][0], 0, 0, 0);
+                d[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b1, d[mt][1], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// the K loop of one pass (nch chunks): queue order of the loads is X0, R0 .. R(RING-2), X1,
+// R(RING-1) | per chunk c: X(c + 2), R(c + RING): waiting for an activation chunk never waits
+// for the weight chunks issued after it, so RING - 1 weight chunks stay in flight. Every load
+// is issued unconditionally (chunk indices clamped to the last chunk: a few repeated loads at
+// the end hit L2): with loads under branches the compiler cannot count them and waits for all.
+// ---------------------------------------------------------------------------------------
+template <int NGC, int RING, int NM>
+__device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2], int nch, const uint16_t *srcrow,
+                                       uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
+    constexpr int ABUF = GG_TOK * GgChunk<NGC>::LDA;
+    const int cl = nch - 1;
+    WChunk<NGC> wr[RING];
+    uint4 xv[GgChunk<NGC>::NV];
+    xs_load<NGC>(srcrow, 0, xv);
+#pragma unroll
+    for (int u = 0; u + 1 < RING; ++u) load_chunk<NGC>(wr[u], qp, sp, min(u, cl));
+    xs_store<NGC>(xv, s_a);
+    xs_load<NGC>(srcrow, min(1, cl), xv);
+    load_chunk<NGC>(wr[RING - 1], qp, sp, min(RING - 1, cl));
+    __syncthreads();
+#pragma unroll 1
+    for (int c0 = 0; c0 < nch; c0 += RING) {
+#pragma unroll
+        for (int u = 0; u < RING; ++u) {
+            const int c = c0 + u;
+            const int b = c & 1;
+            if (c < nch) {
+                mma_chunk<NGC, NM>(wr[u], s_a + b * ABUF, dk, d);
+                if (c + 1 < nch) xs_store<NGC>(xv, s_a + (b ^ 1) * ABUF);
+            }
+            xs_load<NGC>(srcrow, min(c + 2, cl), xv);
+            load_chunk<NGC>(wr[u], qp, sp, min(c + RING, cl));
+            if (c < nch) __syncthreads();
+        }
+    }
+}
+
+// tile t -> (expert, block): the blocks of 8 consecutive experts interleave so that every tile of
+// one expert has the same t % 8 (workgroups go round-robin over the 8 XCDs)
+__device__ __forceinline__ bool tile_of(int t, int E, int NB, int &e, int &nb) {
+    const int eg = t / (8 * NB), r = t % (8 * NB);
+    e = eg * 8 + (r & 7);
+    nb = r >> 3;
+    return e < E;
+}
+
+// exponent e with max * 2^-e in [2^14, 2^15) (0 for 0, inf or nan)
 __device__ __forceinline__ int row_exp(float m) {
     return (m > 0.f && m <= 3.0e38f) ? max(ilogbf(m) - 14, -100) : 0;
 }
 
-// one wave per row: ex[r] = row_exp(max |x[r, :]|)
-template <int DT>
-__global__ __launch_bounds__(256) void k_row_exp(const void *__restrict__ x, int R, int C, int *__restrict__ ex) {
+// bf16 activations, one wave per row: xe[r] = row_exp(max |x[r]|) and x16[r] = fp16(x[r] * 2^-xe[r])
+// (exact for bf16 values in range); pmax[0..NP) = 0
+__global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, int T, int H, int *__restrict__ xe,
+                                              uint16_t *__restrict__ x16, uint32_t *__restrict__ pmax, int NP) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < NP; i += gridDim.x * 256) pmax[i] = 0u;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= R) return;
+    if (r >= T || x == nullptr) return;
     float m = 0.f;
-    for (int c = lane; c < C; c += 64) m = fmaxf(m, fabsf(ld_act<DT>(x, (size_t)r * C + c)));
+    for (int c = lane; c < H; c += 64) m = fmaxf(m, fabsf(bf16_to_f32(x[(size_t)r * H + c])));
     m = wave_max(m);
-    if (lane == 0) ex[r] = row_exp(m);
-}
-
-// 8 nibbles (one dword of an int4 row) -> fp16 (1024 + n) in the order c0 c4 c1 c5 c2 c6 c3 c7.
-// Plain C on purpose (not the inline-asm and_or of the GEMV kernels): the results feed MFMA
-// operands, and only compiler-generated instructions get the VALU-write -> MFMA-read wait
-// states inserted by the compiler's hazard recognizer.
-__device__ __forceinline__ f16x8 deq8(uint32_t d) {
-    uint4 u;
-    u.x = (d & 0x000F000Fu) | 0x64006400u;
-    u.y = ((d >> 4) & 0x000F000Fu) | 0x64006400u;
-    u.z = ((d >> 8) & 0x000F000Fu) | 0x64006400u;
-    u.w = ((d >> 12) & 0x000F000Fu) | 0x64006400u;
-    return __builtin_bit_cast(f16x8, u);
-}
-
-// 8 consecutive activation values -> fp16 pairs in the same order (c0,c4) (c1,c5) (c2,c6) (c3,c7)
-__device__ __forceinline__ uint4 perm8(const float *v) {
-    return make_uint4(pack_h2(v[0], v[4]), pack_h2(v[1], v[5]), pack_h2(v[2], v[6]), pack_h2(v[3], v[7]));
-}
-
-// Activation staging for one K step: thread tid -> token tid / 4, K values 16 * (tid % 4) ..+16
-// of the step (one lane-group slice: LDS positions 16 q .. 16 q + 16, two halves of 8), written
-// permuted as the MFMA fragments expect; the group sum of the fp16 values goes to xg[token].
-struct StageRegs {
-    float v[16];
-};
-
-// loads of the next step (activations x (DT) or h (fp32), row `row` scaled by 2^-e)
-template <int DT>
-__device__ __forceinline__ void stage_load(const void *src, size_t row, int ld, int k0, bool ok, StageRegs &r) {
-    const int part = threadIdx.x & 3;
-    const size_t base = row * (size_t)ld + k0 + 16 * part;
-    if constexpr (DT == MOEHIP_DT_F32) {
-        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(src) + base);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const float4 f = ok ? p[m] : make_float4(0.f, 0.f, 0.f, 0.f);
-            r.v[4 * m + 0] = f.x;
-            r.v[4 * m + 1] = f.y;
-            r.v[4 * m + 2] = f.z;
-            r.v[4 * m + 3] = f.w;
-        }
-    } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(src) + base);
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            const uint4 u = ok ? p[m] : make_uint4(0, 0, 0, 0);
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                r.v[8 * m + 2 * q] = DT == MOEHIP_DT_F16 ? f16_to_f32(w[q] & 0xffffu) : bf16_to_f32(w[q] & 0xffffu);
-                r.v[8 * m + 2 * q + 1] = DT == MOEHIP_DT_F16 ? f16_to_f32(w[q] >> 16) : bf16_to_f32(w[q] >> 16);
-            }
-        }
-    }
-}
-
-// scaled fp16 (hi, and lo = the rounding remainder when LO) into LDS + group sums
-template <bool LO>
-__device__ __forceinline__ void stage_store(const StageRegs &r, float down, _Float16 *s_hi, _Float16 *s_lo,
-                                            float *s_sum) {
-    const int tok = threadIdx.x >> 2, part = threadIdx.x & 3;
-    float hv[16], lv[16];
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const float v = r.v[i] * down;
-        hv[i] = f16_to_f32(f32_to_f16_rne(v));
-        lv[i] = LO ? f16_to_f32(f32_to_f16_rne(v - hv[i])) : 0.f;
-        sum += hv[i] + lv[i];
-    }
-    uint4 *dh = reinterpret_cast<uint4 *>(s_hi + tok * GG_LDW + 16 * part);
-    dh[0] = perm8(hv);
-    dh[1] = perm8(hv + 8);
-    if constexpr (LO) {
-        uint4 *dl = reinterpret_cast<uint4 *>(s_lo + tok * GG_LDW + 16 * part);
-        dl[0] = perm8(lv);
-        dl[1] = perm8(lv + 8);
-    }
-    sum += dpp_f<0xB1>(sum);  // the 4 threads of a token are one quad
-    sum += dpp_f<0x4E>(sum);
-    if (part == 0) s_sum[tok] = sum;
-}
-
-// one K step of MFMAs for a wave: nm valid M tiles, GG_NS weight subtiles
-template <bool LO>
-__device__ __forceinline__ void mma_step(const _Float16 *s_hi, const _Float16 *s_lo, const float *s_sum, const uint2 (&bq)[GG_NS],
-                                         const float (&sc)[GG_NS], int nm, f32x4 (&acc)[GG_MT][GG_NS]) {
-    const int lane = threadIdx.x & 63;
-    const int m = lane & 15, q = lane >> 4;
-    f16x8 b0[GG_NS], b1[GG_NS];
-#pragma unroll
-    for (int j = 0; j < GG_NS; ++j) {
-        b0[j] = deq8(bq[j].x);
-        b1[j] = deq8(bq[j].y);
-    }
-#pragma unroll
-    for (int mt = 0; mt < GG_MT; ++mt) {
-        if (mt >= nm) break;
-        const _Float16 *ah = s_hi + (mt * 16 + m) * GG_LDW + 16 * q;
-        const f16x8 a0 = *reinterpret_cast<const f16x8 *>(ah);
-        const f16x8 a1 = *reinterpret_cast<const f16x8 *>(ah + 8);
-        f16x8 l0, l1;
-        if constexpr (LO) {
-            const _Float16 *al = s_lo + (mt * 16 + m) * GG_LDW + 16 * q;
-            l0 = *reinterpret_cast<const f16x8 *>(al);
-            l1 = *reinterpret_cast<const f16x8 *>(al + 8);
-        }
-        const float4 xg = *reinterpret_cast<const float4 *>(s_sum + mt * 16 + 4 * q);
-        const float xgv[4] = {xg.x, xg.y, xg.z, xg.w};
-#pragma unroll
-        for (int j = 0; j < GG_NS; ++j) {
-            f32x4 d = {0.f, 0.f, 0.f, 0.f};
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0[j], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1[j], d, 0, 0, 0);
-            if constexpr (LO) {
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b0[j], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b1[j], d, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[mt][j][r] = fmaf(sc[j], fmaf(-1032.0f, xgv[r], d[r]), acc[mt][j][r]);
-        }
-    }
+    const int e = row_exp(m);
+    const float sc = ldexpf(1.0f, -e);
+    for (int c = lane; c < H; c += 64) x16[(size_t)r * H + c] = f32_to_f16_rne(bf16_to_f32(x[(size_t)r * H + c]) * sc);
+    if (lane == 0) xe[r] = e;
 }
 
 // ---------------------------------------------------------------------------------------
-// up: grid (ceil(I / 128), E). Wave w: h columns c0 = 128 bx + 32 w .. +32; subtiles 0, 1 =
-// gate rows c0 + 16 j, subtiles 2, 3 = up rows I + c0 + 16 (j - 2).
+// up: tiles (expert, 128 h columns); wave w: h columns nb*128 + 32 w + (lane % 32), subtile 0 =
+// gate rows, subtile 1 = up rows. Writes h (pairs, I) fp32 and pmax[pair] = max |h| (atomic).
 // ---------------------------------------------------------------------------------------
-template <int XDT>
-__global__ __launch_bounds__(256) void k_gemm_up(const void *__restrict__ x, const int *__restrict__ xe, int H, int I,
-                                                 int k, const int32_t *__restrict__ offsets,
-                                                 const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
-                                                 int gs, float *__restrict__ h) {
-    __shared__ __align__(16) _Float16 s_x[2][GG_TOK * GG_LDW];
-    __shared__ __align__(16) float s_sum[2][GG_TOK];
-    const int e = blockIdx.y;
+// x: fp16 activations (the caller's, or x16 with exponents xe for bf16 input; xe null = 0)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_up(
+    const uint16_t *__restrict__ x, const int *__restrict__ xe, int H, int I, int k, int E,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
+    float *__restrict__ hb, uint32_t *__restrict__ pmax, DeqK dk) {
+    constexpr int NGC = 2;
+    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<NGC>::LDA];
+    __shared__ int s_e[GG_TOK];
+    __shared__ uint32_t s_mx[GG_TOK];
+    const int NB = I / 128;
+    int e, nb;
+    if (!tile_of(blockIdx.x, E, NB, e, nb)) return;
     const int p0 = offsets[e], ne = offsets[e + 1] - p0;
-    const uint8_t *qb = reinterpret_cast<const uint8_t *>(tab[4 * e + 0]);
-    const uint16_t *sb = reinterpret_cast<const uint16_t *>(tab[4 * e + 1]);
+    gu8 *qb = record_ptr(tab[4 * e + 0]);
+    gu8 *sb = record_ptr(tab[4 * e + 1]);
     if (ne <= 0 || qb == nullptr) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c0 = blockIdx.x * 128 + wave * 32;
-    const size_t RB = (size_t)H / 2;
-    const int ng = H / gs;
-    const int nsteps = H / GG_KG;
-    int rowj[GG_NS];
-    bool okj[GG_NS];
-#pragma unroll
-    for (int j = 0; j < GG_NS; ++j) {
-        const int col = c0 + 16 * (j & 1) + (lane & 15);
-        okj[j] = col < I;
-        rowj[j] = (j < 2 ? 0 : I) + min(col, I - 1);
-    }
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int col = nb * 128 + 32 * wave + j;
+    const size_t RB = (size_t)H / 2, SB = (size_t)(H / GG_KG) * 2;
+    gu8 *const qp[2] = {qb + (size_t)col * RB + 16 * h, qb + (size_t)(I + col) * RB + 16 * h};
+    gu8 *const sp[2] = {sb + (size_t)col * SB, sb + (size_t)(I + col) * SB};
+    const int nch = H / GgChunk<NGC>::CK;
     for (int m0 = 0; m0 < ne; m0 += GG_TOK) {
-        const int mn = min(GG_TOK, ne - m0);
-        const int nm = (mn + 15) / 16;
-        // this thread's staging token
+        const int mn = min(GG_TOK, ne - m0), nm = (mn + 31) / 32;
         const int stok = tid >> 2;
         const bool sok = stok < mn;
-        const int t_row = sok ? sorted_pos[p0 + m0 + stok] / k : 0;
-        const float sdown = sok ? ldexpf(1.0f, -xe[t_row]) : 0.f;
-        f32x4 acc[GG_MT][GG_NS];
+        const int xr = sok ? sorted_pos[p0 + m0 + stok] / k : 0;
+        const int ex = (sok && xe != nullptr) ? xe[xr] : 0;
+        if ((tid & 3) == 0) s_e[stok] = ex;
+        if ((tid & 3) == 1) s_mx[stok] = 0u;  // ordered before their use by k_loop's barriers
+        f32x16 d[2][2];
 #pragma unroll
-        for (int mt = 0; mt < GG_MT; ++mt)
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int j = 0; j < GG_NS; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        StageRegs sr;
-        uint2 bq[GG_NS], bn[GG_NS];
-        uint32_t sraw[GG_NS], snext[GG_NS];
-        stage_load<XDT>(x, (size_t)t_row, H, 0, sok, sr);
+            for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
+        if (nm == 2) k_loop<NGC, 3, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        else k_loop<NGC, 3, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32; per-pair max
 #pragma unroll
-        for (int j = 0; j < GG_NS; ++j) {
-            bq[j] = *reinterpret_cast<const uint2 *>(qb + (size_t)rowj[j] * RB + 8 * (lane >> 4));
-            sraw[j] = sb[(size_t)rowj[j] * ng];
+        for (int mt = 0; mt < 2; ++mt) {
+            if (mt >= nm) break;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tok = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float f = ldexpf(1.0f, s_e[tok]);
+                const float hv = silu_mul(d[mt][0][r] * f, d[mt][1][r] * f);
+                if (tok < mn) hb[(size_t)(p0 + m0 + tok) * I + col] = hv;
+                float m = tok < mn ? fabsf(hv) : 0.f;
+                m = fmaxf(m, dpp_f<0xB1>(m));  // max over the 16-lane row (16 columns of one token)
+                m = fmaxf(m, dpp_f<0x4E>(m));
+                m = fmaxf(m, dpp_f<0x141>(m));
+                m = fmaxf(m, dpp_f<0x140>(m));
+                if ((lane & 15) == 0 && tok < mn) atomicMax(&s_mx[tok], __float_as_uint(m));
+            }
         }
-        stage_store<false>(sr, sdown, s_x[0], nullptr, s_sum[0]);
         __syncthreads();
-        for (int st = 0; st < nsteps; ++st) {
-            const int buf = st & 1;
-            const bool more = st + 1 < nsteps;
-            if (more) {  // next step's loads are in flight while this one computes
-                stage_load<XDT>(x, (size_t)t_row, H, (st + 1) * GG_KG, sok, sr);
-#pragma unroll
-                for (int j = 0; j < GG_NS; ++j) {
-                    bn[j] = *reinterpret_cast<const uint2 *>(qb + (size_t)rowj[j] * RB + (size_t)(st + 1) * 32 +
-                                                              8 * (lane >> 4));
-                    snext[j] = sb[(size_t)rowj[j] * ng + (st + 1) * GG_KG / gs];
-                }
-            }
-            float sc[GG_NS];
-#pragma unroll
-            for (int j = 0; j < GG_NS; ++j) sc[j] = okj[j] ? f16_to_f32(sraw[j]) : 0.f;
-            mma_step<false>(s_x[buf], nullptr, s_sum[buf], bq, sc, nm, acc);
-            if (more) {
-                stage_store<false>(sr, sdown, s_x[buf ^ 1], nullptr, s_sum[buf ^ 1]);
-#pragma unroll
-                for (int j = 0; j < GG_NS; ++j) {
-                    bq[j] = bn[j];
-                    sraw[j] = snext[j];
-                }
-            }
-            __syncthreads();
-        }
-        // epilogue: h = silu(gate) * up, scaled back by the token's 2^e
-#pragma unroll
-        for (int mt = 0; mt < GG_MT; ++mt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = mt * 16 + 4 * (lane >> 4) + r;
-                if (tok >= mn) continue;
-                const int p = p0 + m0 + tok;
-                const float up = ldexpf(1.0f, xe[sorted_pos[p] / k]);
-#pragma unroll
-                for (int jp = 0; jp < 2; ++jp) {
-                    const int col = c0 + 16 * jp + (lane & 15);
-                    if (col < I) h[(size_t)p * I + col] = silu_mul(acc[mt][jp][r] * up, acc[mt][jp + 2][r] * up);
-                }
-            }
-        }
+        if (tid < mn) atomicMax(&pmax[p0 + m0 + tid], s_mx[tid]);
         __syncthreads();
     }
 }
 
+// one wave per pair: he[p] = row_exp(pmax[p]), h16[p] = fp16(h[p] * 2^-he[p])
+__global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, const uint32_t *__restrict__ pmax, int NP,
+                                             int I, uint16_t *__restrict__ h16, int *__restrict__ he) {
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (p >= NP) return;
+    const int e = row_exp(__uint_as_float(pmax[p]));
+    const float sc = ldexpf(1.0f, -e);
+    const float4 *src = reinterpret_cast<const float4 *>(hb + (size_t)p * I);
+    uint2 *dst = reinterpret_cast<uint2 *>(h16 + (size_t)p * I);
+    for (int c = lane; c < I / 4; c += 64) {
+        const float4 v = src[c];
+        dst[c] = make_uint2(pack_h2(v.x * sc, v.y * sc), pack_h2(v.z * sc, v.w * sc));
+    }
+    if (lane == 0) he[p] = e;
+}
+
 // ---------------------------------------------------------------------------------------
-// down: grid (ceil(H / 256), E). Wave w: output rows r0 = 256 bx + 64 w + 16 j. h rows enter as
-// fp16 hi + lo scaled by the pair's 2^-e; y[p, row] = w[pair] * (down_row . h_p).
+// down: tiles (expert, 256 output rows); wave w: rows nb*256 + 64 w + 32 t + (lane % 32).
+// y[pair, row] = w[pair] * (down_row . h_pair)
 // ---------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_gemm_down(const float *__restrict__ h, const int *__restrict__ he, int H, int I,
-                                                   const int32_t *__restrict__ offsets,
-                                                   const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
-                                                   const float *__restrict__ w, int gs, float *__restrict__ y) {
-    __shared__ __align__(16) _Float16 s_hi[2][GG_TOK * GG_LDW];
-    __shared__ __align__(16) _Float16 s_lo[2][GG_TOK * GG_LDW];
-    __shared__ __align__(16) float s_sum[2][GG_TOK];
-    const int e = blockIdx.y;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_down(
+    const uint16_t *__restrict__ h16, const int *__restrict__ he, int H, int I, int E,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
+    const float *__restrict__ w, float *__restrict__ y, DeqK dk) {
+    constexpr int NGC = 2;
+    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<NGC>::LDA];
+    __shared__ float s_f[GG_TOK];  // w[pair] * 2^e
+    const int NB = H / GG_ROWS;
+    int e, nb;
+    if (!tile_of(blockIdx.x, E, NB, e, nb)) return;
     const int p0 = offsets[e], ne = offsets[e + 1] - p0;
     if (ne <= 0) return;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const uint8_t *qb = reinterpret_cast<const uint8_t *>(tab[4 * e + 2]);
-    const uint16_t *sb = reinterpret_cast<const uint16_t *>(tab[4 * e + 3]);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    gu8 *qb = record_ptr(tab[4 * e + 2]);
+    gu8 *sb = record_ptr(tab[4 * e + 3]);
+    const int row0 = nb * GG_ROWS + 64 * wave + j;
     if (qb == nullptr) {  // expert not resident: its pairs contribute nothing
-        for (int i = tid; i < ne * 256; i += 256) {
-            const int p = p0 + i / 256, row = blockIdx.x * 256 + i % 256;
-            if (row < H) y[(size_t)p * H + row] = 0.f;
-        }
+        for (int i = tid; i < ne * GG_ROWS; i += 256)
+            y[(size_t)(p0 + i / GG_ROWS) * H + nb * GG_ROWS + i % GG_ROWS] = 0.f;
         return;
     }
-    const size_t RB = (size_t)I / 2;
-    const int ng = I / gs;
-    const int nsteps = I / GG_KG;
-    int rowj[GG_NS];
-    bool okj[GG_NS];
-#pragma unroll
-    for (int j = 0; j < GG_NS; ++j) {
-        const int row = blockIdx.x * 256 + wave * 64 + 16 * j + (lane & 15);
-        okj[j] = row < H;
-        rowj[j] = min(row, H - 1);
-    }
+    const size_t RB = (size_t)I / 2, SB = (size_t)(I / GG_KG) * 2;
+    gu8 *const qp[2] = {qb + (size_t)row0 * RB + 16 * h, qb + (size_t)(row0 + 32) * RB + 16 * h};
+    gu8 *const sp[2] = {sb + (size_t)row0 * SB, sb + (size_t)(row0 + 32) * SB};
+    const int nch = I / GgChunk<NGC>::CK;
     for (int m0 = 0; m0 < ne; m0 += GG_TOK) {
-        const int mn = min(GG_TOK, ne - m0);
-        const int nm = (mn + 15) / 16;
+        const int mn = min(GG_TOK, ne - m0), nm = (mn + 31) / 32;
         const int stok = tid >> 2;
         const bool sok = stok < mn;
-        const size_t prow = (size_t)(p0 + m0 + min(stok, mn - 1));
-        const float sdown = sok ? ldexpf(1.0f, -he[prow]) : 0.f;
-        f32x4 acc[GG_MT][GG_NS];
+        const size_t pr = (size_t)(p0 + m0 + (sok ? stok : 0));
+        if ((tid & 3) == 0) s_f[stok] = sok ? w[sorted_pos[pr]] * ldexpf(1.0f, he[pr]) : 0.f;
+        f32x16 d[2][2];
 #pragma unroll
-        for (int mt = 0; mt < GG_MT; ++mt)
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int j = 0; j < GG_NS; ++j) acc[mt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        StageRegs sr;
-        uint2 bq[GG_NS], bn[GG_NS];
-        uint32_t sraw[GG_NS], snext[GG_NS];
-        stage_load<MOEHIP_DT_F32>(h, prow, I, 0, sok, sr);
+            for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
+        if (nm == 2) k_loop<NGC, 3, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        else k_loop<NGC, 3, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
 #pragma unroll
-        for (int j = 0; j < GG_NS; ++j) {
-            bq[j] = *reinterpret_cast<const uint2 *>(qb + (size_t)rowj[j] * RB + 8 * (lane >> 4));
-            sraw[j] = sb[(size_t)rowj[j] * ng];
-        }
-        stage_store<true>(sr, sdown, s_hi[0], s_lo[0], s_sum[0]);
-        __syncthreads();
-        for (int st = 0; st < nsteps; ++st) {
-            const int buf = st & 1;
-            const bool more = st + 1 < nsteps;
-            if (more) {
-                stage_load<MOEHIP_DT_F32>(h, prow, I, (st + 1) * GG_KG, sok, sr);
+        for (int mt = 0; mt < 2; ++mt) {
+            if (mt >= nm) break;
 #pragma unroll
-                for (int j = 0; j < GG_NS; ++j) {
-                    bn[j] = *reinterpret_cast<const uint2 *>(qb + (size_t)rowj[j] * RB + (size_t)(st + 1) * 32 +
-                                                              8 * (lane >> 4));
-                    snext[j] = sb[(size_t)rowj[j] * ng + (st + 1) * GG_KG / gs];
-                }
-            }
-            float sc[GG_NS];
-#pragma unroll
-            for (int j = 0; j < GG_NS; ++j) sc[j] = okj[j] ? f16_to_f32(sraw[j]) : 0.f;
-            mma_step<true>(s_hi[buf], s_lo[buf], s_sum[buf], bq, sc, nm, acc);
-            if (more) {
-                stage_store<true>(sr, sdown, s_hi[buf ^ 1], s_lo[buf ^ 1], s_sum[buf ^ 1]);
-#pragma unroll
-                for (int j = 0; j < GG_NS; ++j) {
-                    bq[j] = bn[j];
-                    sraw[j] = snext[j];
-                }
-            }
-            __syncthreads();
-        }
-#pragma unroll
-        for (int mt = 0; mt < GG_MT; ++mt) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tok = mt * 16 + 4 * (lane >> 4) + r;
+            for (int r = 0; r < 16; ++r) {
+                const int tok = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (tok >= mn) continue;
-                const int p = p0 + m0 + tok;
-                const float f = w[sorted_pos[p]] * ldexpf(1.0f, he[p]);
-#pragma unroll
-                for (int j = 0; j < GG_NS; ++j)
-                    if (okj[j]) y[(size_t)p * H + rowj[j]] = f * acc[mt][j][r];
+                const size_t p = (size_t)(p0 + m0 + tok);
+                const float f = s_f[tok];
+                y[p * H + row0] = f * d[mt][0][r];
+                y[p * H + row0 + 32] = f * d[mt][1][r];
             }
         }
-        __syncthreads();
+        __syncthreads();  // s_f of the next pass
     }
 }
 
-// out[t] = sum over slots j (in order) of y[rank[t k + j]] (+ out if accumulate) (+ add)
+// out[t] = sum over slots j (in order) of y[rank[t k + j]] (+ out if accumulate) (+ add):
+// one workgroup per token, 8 consecutive columns per thread
 template <int DT>
 __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__ y, const int32_t *__restrict__ rank,
                                                        int T, int k, int H, const void *__restrict__ add,
                                                        void *__restrict__ out, int accumulate) {
     const int t = blockIdx.x;
-    for (int c = threadIdx.x; c < H; c += 256) {
-        float s = 0.f;
-        for (int j = 0; j < k; ++j) {
-            const int p = rank[(size_t)t * k + j];
-            if (p >= 0) s += y[(size_t)p * H + c];
+    for (int c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int jj = 0; jj < k; ++jj) {
+            const int p = rank[(size_t)t * k + jj];
+            if (p < 0) continue;
+            const float4 *src = reinterpret_cast<const float4 *>(y + (size_t)p * H + c0);
+            const float4 a = src[0], b = src[1];
+            s[0] += a.x, s[1] += a.y, s[2] += a.z, s[3] += a.w;
+            s[4] += b.x, s[5] += b.y, s[6] += b.z, s[7] += b.w;
         }
-        if (accumulate) s += ld_act<DT>(out, (size_t)t * H + c);
-        if (add != nullptr) s += ld_act<DT>(add, (size_t)t * H + c);
-        st_act<DT>(out, (size_t)t * H + c, s);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            float v = s[q];
+            if (accumulate) v += ld_act<DT>(out, (size_t)t * H + c0 + q);
+            if (add != nullptr) v += ld_act<DT>(add, (size_t)t * H + c0 + q);
+            st_act<DT>(out, (size_t)t * H + c0 + q, v);
+        }
     }
 }
 
 struct GgLayout {
-    size_t xe, he, h, y, total;
+    size_t xe, x16, pmax, h, h16, he, y, total;
 };
 static GgLayout gg_layout(int T, int k, int H, int I) {
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -406,10 +410,16 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     size_t off = 0;
     L.xe = off;
     off = al(off + (size_t)T * 4);
-    L.he = off;
+    L.x16 = off;
+    off = al(off + (size_t)T * H * 2);
+    L.pmax = off;
     off = al(off + NP * 4);
     L.h = off;
     off = al(off + NP * I * 4);
+    L.h16 = off;
+    off = al(off + NP * I * 2);
+    L.he = off;
+    off = al(off + NP * 4);
     L.y = off;
     off = al(off + NP * H * 4);
     L.total = off;
@@ -432,8 +442,8 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
     MOEHIP_REQUIRE(tab && x && offsets && sorted_pos && rank && w && out && ws, "grouped_gemm: null pointer");
     MOEHIP_REQUIRE(prec == MOEHIP_PREC_INT4, "grouped_gemm: precision %d (int4 records)", prec);
     MOEHIP_REQUIRE(gs == GG_KG, "grouped_gemm: group size %d (64)", gs);
-    MOEHIP_REQUIRE(T > 0 && k > 0 && E > 0 && H > 0 && I > 0 && H % GG_KG == 0 && I % GG_KG == 0,
-                   "grouped_gemm: T=%d k=%d E=%d H=%d I=%d (H, I multiples of 64)", T, k, E, H, I);
+    MOEHIP_REQUIRE(T > 0 && k > 0 && E > 0 && H > 0 && I > 0 && H % GG_ROWS == 0 && I % 128 == 0,
+                   "grouped_gemm: T=%d k=%d E=%d H=%d I=%d (H a multiple of 256, I of 128)", T, k, E, H, I);
     MOEHIP_REQUIRE(xdtype == MOEHIP_DT_F16 || xdtype == MOEHIP_DT_BF16, "grouped_gemm: activation dtype %d", xdtype);
     MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0, "grouped_gemm: x must be 16-byte aligned");
     const GgLayout L = gg_layout(T, k, H, I);
@@ -441,23 +451,24 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
                    ws_bytes, L.total);
     uint8_t *wsb = reinterpret_cast<uint8_t *>(ws);
     int *xe = reinterpret_cast<int *>(wsb + L.xe);
-    int *he = reinterpret_cast<int *>(wsb + L.he);
-    float *h = reinterpret_cast<float *>(wsb + L.h);
+    uint32_t *pmax = reinterpret_cast<uint32_t *>(wsb + L.pmax);
+    float *hb = reinterpret_cast<float *>(wsb + L.h);
     float *y = reinterpret_cast<float *>(wsb + L.y);
     const int NP = T * k;
     hipStream_t st = as_stream(stream);
-    if (xdtype == MOEHIP_DT_F16) {
-        hipLaunchKernelGGL((k_row_exp<MOEHIP_DT_F16>), dim3((T + 3) / 4), dim3(256), 0, st, x, T, H, xe);
-        hipLaunchKernelGGL((k_gemm_up<MOEHIP_DT_F16>), dim3((I + 127) / 128, E), dim3(256), 0, st, x, xe, H, I, k,
-                           offsets, sorted_pos, tab, gs, h);
-    } else {
-        hipLaunchKernelGGL((k_row_exp<MOEHIP_DT_BF16>), dim3((T + 3) / 4), dim3(256), 0, st, x, T, H, xe);
-        hipLaunchKernelGGL((k_gemm_up<MOEHIP_DT_BF16>), dim3((I + 127) / 128, E), dim3(256), 0, st, x, xe, H, I, k,
-                           offsets, sorted_pos, tab, gs, h);
-    }
-    hipLaunchKernelGGL((k_row_exp<MOEHIP_DT_F32>), dim3((NP + 3) / 4), dim3(256), 0, st, h, NP, I, he);
-    hipLaunchKernelGGL(k_gemm_down, dim3((H + 255) / 256, E), dim3(256), 0, st, h, he, H, I, offsets, sorted_pos, tab, w,
-                       gs, y);
+    const int E8 = (E + 7) / 8 * 8;
+    const dim3 gu(E8 * (I / 128)), gd(E8 * (H / GG_ROWS));
+    const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);
+    uint16_t *x16 = reinterpret_cast<uint16_t *>(wsb + L.x16);
+    const DeqK dk = {0x000F000Fu, 0x64006400u};
+    const bool bf = xdtype == MOEHIP_DT_BF16;
+    hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, bf ? xs : nullptr, T, H, xe, x16, pmax, NP);
+    hipLaunchKernelGGL(k_gemm_up, gu, dim3(256), 0, st, bf ? x16 : xs, bf ? xe : nullptr, H, I, k, E, offsets,
+                       sorted_pos, tab, hb, pmax, dk);
+    uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
+    int *he = reinterpret_cast<int *>(wsb + L.he);
+    hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, pmax, NP, I, h16, he);
+    hipLaunchKernelGGL(k_gemm_down, gd, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk);
     if (xdtype == MOEHIP_DT_F16)
         hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_F16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
                            accumulate);
