@@ -199,6 +199,21 @@ __device__ __forceinline__ uint32_t and_or(uint32_t d, uint32_t mask, uint32_t m
     return r;
 }
 
+// Record bytes in the global address space. Record addresses come from integer tables; loads
+// through generic pointers would be flat loads, which also count against the LDS / scalar wait
+// counter (every LDS wait would then also wait for the weight loads in flight).
+typedef const __attribute__((address_space(1))) uint8_t gbyte;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ gbyte *gbytes(uint64_t a) { return (gbyte *)(uintptr_t)a; }
+__device__ __forceinline__ gbyte *gbytes(const void *p) { return (gbyte *)(uintptr_t)p; }
+__device__ __forceinline__ uint4 gld16(gbyte *p) {
+    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t gld4(gbyte *p) { return *(const __attribute__((address_space(1))) uint32_t *)p; }
+__device__ __forceinline__ uint32_t gld2(gbyte *p) { return *(const __attribute__((address_space(1))) uint16_t *)p; }
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 }  // namespace moehip

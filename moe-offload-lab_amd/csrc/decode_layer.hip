@@ -416,13 +416,13 @@ __device__ __forceinline__ float lane_dot(const uint4 q, const LaneVec<PREC, XDT
 
 // raw scale bits of chunk c of row `row` (int: fp16 group scale; fp8: fp32 block scale)
 template <int PREC>
-__device__ __forceinline__ uint32_t scale_bits(const uint8_t *sb, int row, int c, int cols, int gs) {
+__device__ __forceinline__ uint32_t scale_bits(gbyte *sb, int row, int c, int cols, int gs) {
     if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) {
         const int ng = cols / gs;
-        return reinterpret_cast<const uint16_t *>(sb)[(size_t)row * ng + (c * Fmt<PREC>::VPC) / gs];
+        return gld2(sb + 2 * ((size_t)row * ng + (c * Fmt<PREC>::VPC) / gs));
     } else if constexpr (PREC == MOEHIP_PREC_FP8) {
         const int sc = (cols + 127) >> 7;
-        return reinterpret_cast<const uint32_t *>(sb)[(size_t)(row >> 7) * sc + ((c * 16) >> 7)];
+        return gld4(sb + 4 * ((size_t)(row >> 7) * sc + ((c * 16) >> 7)));
     } else {
         return 0x3f800000u;
     }
@@ -437,7 +437,7 @@ __device__ __forceinline__ float scale_val(uint32_t bits) {
 // up item (one wave's share): NPU passes of RPW row pairs, h[r] = silu(gate_r . x) * (up_r . x)
 // ---------------------------------------------------------------------------------------
 template <int PREC, int XDT>
-__device__ __forceinline__ void up_rows(const uint8_t *qb, const uint8_t *sb, const LaneVec<PREC, XDT> &lv, int pair0,
+__device__ __forceinline__ void up_rows(gbyte *qb, gbyte *sb, const LaneVec<PREC, XDT> &lv, int pair0,
                                         int I, int H, int gs, int lg, uint64_t *hout, uint32_t tag, uint64_t *st) {
     constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL, NPU = DlFmt<PREC>::NPU;
     const int lane = threadIdx.x & 63;
@@ -457,8 +457,8 @@ __device__ __forceinline__ void up_rows(const uint8_t *qb, const uint8_t *sb, co
             const int c0 = cl + i * G;
             const int c = min(c0, C - 1);
             const bool ok = r0 < I && c0 < C;
-            qg[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
-            qu[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)(r + I) * RB + (size_t)c * 16);
+            qg[p][i] = gld16(qb + (size_t)r * RB + (size_t)c * 16);
+            qu[p][i] = gld16(qb + (size_t)(r + I) * RB + (size_t)c * 16);
             const uint32_t a0 = scale_bits<PREC>(sb, r, c, H, gs), a1 = scale_bits<PREC>(sb, r + I, c, H, gs);
             sg[p][i] = ok ? a0 : 0u;
             su[p][i] = ok ? a1 : 0u;
@@ -504,7 +504,7 @@ struct DownRegs {
 };
 
 template <int PREC>
-__device__ __forceinline__ void down_load(const uint8_t *qb, const uint8_t *sb, int row0, int H, int I, int gs, int lg,
+__device__ __forceinline__ void down_load(gbyte *qb, gbyte *sb, int row0, int H, int I, int gs, int lg,
                                           DownRegs<PREC> &d) {
     constexpr int VPC = DlFmt<PREC>::VPC, CPL = DlFmt<PREC>::CPL, NPD = DlFmt<PREC>::NPD;
     const int lane = threadIdx.x & 63;
@@ -521,7 +521,7 @@ __device__ __forceinline__ void down_load(const uint8_t *qb, const uint8_t *sb, 
         for (int i = 0; i < CPL; ++i) {
             const int c0 = cl + i * G;
             const int c = min(c0, C - 1);
-            d.q[p][i] = *reinterpret_cast<const uint4 *>(qb + (size_t)r * RB + (size_t)c * 16);
+            d.q[p][i] = gld16(qb + (size_t)r * RB + (size_t)c * 16);
             const uint32_t sv = scale_bits<PREC>(sb, r, c, I, gs);
             d.s[p][i] = (r0 < H && c0 < C) ? sv : 0u;
         }
@@ -929,8 +929,8 @@ __device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi
     if (rt.w == 0.f) return;
     const int per_wave = DlFmt<PREC>::NPU * RPW;
     const int pair0 = b * per_wave * 4 + wave * per_wave;
-    const uint8_t *qb = reinterpret_cast<const uint8_t *>(rt.base + pick_off(a.offs, pi, 0));
-    const uint8_t *sb = reinterpret_cast<const uint8_t *>(rt.base + pick_off(a.offs, pi, 1));
+    gbyte *qb = gbytes(rt.base + pick_off(a.offs, pi, 0));
+    gbyte *sb = gbytes(rt.base + pick_off(a.offs, pi, 1));
     uint64_t *hout = ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I;
     up_rows<PREC, XDT>(qb, sb, lv, pair0, a.I, a.H, pick4(a.gs_up, pi), lg, hout, tag, st);
 }
@@ -985,8 +985,8 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     uint64_t *part = ws_ptr<uint64_t>(a, a.off_part);
     if (run) {
         DownRegs<PREC> d;
-        down_load<PREC>(reinterpret_cast<const uint8_t *>(rt0.base + pick_off(a.offs, pi, 2)),
-                        reinterpret_cast<const uint8_t *>(rt0.base + pick_off(a.offs, pi, 3)), row0, a.H, a.I,
+        down_load<PREC>(gbytes(rt0.base + pick_off(a.offs, pi, 2)), gbytes(rt0.base + pick_off(a.offs, pi, 3)), row0,
+                        a.H, a.I,
                         pick4(a.gs_dn, pi), lg, d);
         if (st != nullptr) {
             __builtin_amdgcn_s_waitcnt(0);

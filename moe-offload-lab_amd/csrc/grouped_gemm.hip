@@ -35,17 +35,8 @@ namespace moehip {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-// record bytes in the global address space: table entries are plain integers, and loads through
-// generic pointers would be flat loads, which also count against the LDS wait counter (every
-// LDS wait would then wait for every weight load in flight)
-typedef const __attribute__((address_space(1))) uint8_t gu8;
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ gu8 *record_ptr(int64_t a) { return (gu8 *)(uintptr_t)a; }
-__device__ __forceinline__ uint4 gload16(gu8 *p) {
-    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
+typedef gbyte gu8;  // record bytes, global address space (common.hpp)
+__device__ __forceinline__ gu8 *record_ptr(int64_t a) { return gbytes((uint64_t)a); }
 
 constexpr int GG_KG = 64;     // K per scale group
 constexpr int GG_TOK = 64;    // tokens per pass (two 32-token M tiles)
@@ -97,7 +88,7 @@ __device__ __forceinline__ void load_chunk(WChunk<NGC> &w, gu8 *const (&qp)[2], 
     for (int t = 0; t < 2; ++t) {
         gu8 *q = qp[t] + (size_t)c * (GgChunk<NGC>::CK / 2);
 #pragma unroll
-        for (int g = 0; g < NGC; ++g) w.q[t][g] = gload16(q + 32 * g);  // 32 bytes per group row: this half's 16
+        for (int g = 0; g < NGC; ++g) w.q[t][g] = gld16(q + 32 * g);  // 32 bytes per group row: this half's 16
         gu8 *s = sp[t] + (size_t)c * (NGC * 2);
         if constexpr (NGC == 4) {
             const u32x2_t v = *(const __attribute__((address_space(1))) u32x2_t *)s;
