@@ -50,7 +50,7 @@ constexpr int WAIT_SPINS = 1 << 22;   // x ~0.3 us per poll: a wait gives up aft
 // generation 1 KB apart (read by every workgroup at start)
 constexpr int NGEN = 16;
 enum { W_DONE = 0, W_ERR = 32, W_GEN = 256, W_HDR = W_GEN + 256 * NGEN };
-constexpr int NREC = 16;  // copies of every routing record (spreads the polling over memory channels)
+constexpr int NREC = 8;   // copies of every routing record (spreads the polling over memory channels)
 
 struct LayerArgs {
     const void *x;          // (H) activation dtype
@@ -638,15 +638,14 @@ __device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int
             const float lvv = lane < E ? s_lv[lane] : -INFINITY;
             int rank = 0;
 #pragma unroll
-            for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast)
-                if (q < E) {
-                    const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
-                    const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+            for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast);
+                                               // keys past E are 0 and never count
+                const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
+                const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
-                        else rank += ov[u] > key;
-                    }
+                for (int u = 0; u < 4; ++u) {
+                    if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
+                    else rank += ov[u] > key;
                 }
             }
             if (lane < E && rank < k) {
