@@ -4,27 +4,38 @@
 //
 // Work distribution: the work items are ordered [router items: 4 expert rows each][up items]
 //   [down items], and workgroup b runs items b, b + grid, b + 2 grid, ... in that order. An item
-//   only waits on SMALLER items (the routing waits for the router rows, up items for the routing,
-//   down items for the h rows of their table row, the combining down items for the other rows'
-//   partial sums). The grid is at most what the GPU holds at once (occupancy x CUs), so every
-//   workgroup is, or eventually becomes, resident (other kernels' workgroups drain), and the
-//   smallest unfinished item always belongs to a resident workgroup whose earlier items are done:
-//   the launch always drains, with no shared counter to take items from. Every wait is also
-//   bounded (WAIT_SPINS polls); on expiry the workgroup records an error in the workspace,
-//   treats the missing data as absent and moves on, so no launch can hang.
+//   only waits on SMALLER items (up and down items for the router rows, down items for the h rows
+//   of their table row, the combining down items for the other rows' partial sums). The grid is at
+//   most what the GPU holds at once (occupancy x CUs), so every workgroup is, or eventually
+//   becomes, resident (other kernels' workgroups drain), and the smallest unfinished item always
+//   belongs to a resident workgroup whose earlier items are done: the launch always drains, with
+//   no shared counter to take items from. Every wait is also bounded (WAIT_SPINS polls); on expiry
+//   the workgroup records an error in the workspace, treats the missing data as absent and moves
+//   on, so no launch can hang.
+//
+// Routing is computed by EVERY workgroup that runs an up or down item, from the logits: wave 0
+// polls the E logits, ranks them, applies softmax / renorm / HOBBIT and picks each table row's
+// resident copy (from the record table, prefetched into LDS by the other waves while the logits
+// are awaited). Every workgroup computes the same routing bit for bit, so no routing record has
+// to travel between workgroups: the only exchange before the weight loads is the logits.
 //
 // Items are sized so that every lane holds its whole share of the item's weights (8 x 16 bytes)
-// in registers: an up item issues all its loads as soon as its routing record appears, and a
-// down item issues its loads BEFORE waiting for h, so the layer's weight bytes are all requested
+// in registers: an up item issues all its loads as soon as its routing is known, and a down
+// item issues its loads BEFORE waiting for h, so the layer's weight bytes are all requested
 // right after the routing and the dependency waits overlap the HBM transfers.
 //
 // Cross-workgroup data is TAGGED instead of guarded by counters: every exchanged value (logit,
-// routing record word, h element, partial output row) is one 64-bit word (launch tag << 32 |
-// payload) written with one agent-scope (sc1) atomic store, and a consumer polls the words it
-// needs until they carry this launch's tag. A producer never waits for its stores and nothing
-// needs resetting between launches: the tag is the workspace's launch generation + 1, read by
-// every workgroup at start (from one of NGEN copies) and advanced by the last combining item to
-// finish (every other item is complete by then).
+// h element, partial output row) is one 64-bit word (launch tag << 32 | payload) written with one
+// agent-scope (sc1) atomic store, and a consumer polls the words it needs (all of them at once,
+// then the missing ones again) until they carry this launch's tag. The logits are written in
+// NLC copies on different memory channels, so that hundreds of polling workgroups do not queue on
+// one channel. A producer never waits for its stores and nothing needs resetting between
+// launches: the tag is the workspace's launch generation + 1, read by every workgroup at start
+// (from one of NGEN copies). Each workgroup then counts itself in one of NSUB reader counters
+// (no return value, so nothing waits on it; one counter per workgroup would serialise ~10 ns
+// per workgroup on one address), and the router items, which finish early, wait until their
+// counters hold every workgroup of the grid, clear them, and the last of them advances the
+// generation: every workgroup of this launch holds its tag by then.
 //
 // Arithmetic (16-bit activations): weights are turned into fp16 pairs with the 1024 + n
 // magic-exponent trick (int4: n in the mantissa low bits, or 16 n for the odd nibble; int8:
@@ -44,13 +55,17 @@ namespace moehip {
 constexpr int DL_MAXP = 4;
 constexpr int DL_MAXROW = 2048;       // 64 lanes x 32 vector values per lane
 constexpr int WAIT_SPINS = 1 << 22;   // x ~0.3 us per poll: a wait gives up after ~1 s
-// header words, each on its own 128-byte line: ticket counter, finished workgroups, sticky
-// error flag, launch generation
-// header words: finished combining items, sticky error flag, and NGEN copies of the launch
+// header words (each on its own 128-byte line): NSUB reader counters of the launch generation,
+// sticky error flag, the count of drained reader counters, and NGEN copies of the launch
 // generation 1 KB apart (read by every workgroup at start)
 constexpr int NGEN = 16;
-enum { W_DONE = 0, W_ERR = 32, W_GEN = 256, W_HDR = W_GEN + 256 * NGEN };
-constexpr int NREC = 8;   // copies of every routing record (spreads the polling over memory channels)
+constexpr int NSUB = 16;
+enum { W_READ = 0, W_ERR = NSUB * 32, W_TOP = NSUB * 32 + 32, W_GEN = 1024, W_HDR = W_GEN + 256 * NGEN };
+constexpr int NLC = 16;        // copies of the logits (spreads the polling over memory channels)
+constexpr int RT_LDS = 1024;   // record-table entries (P * E) prefetched into LDS
+// 64-bit words between two copies of the logits (E routed + the shared gate): a whole number of
+// 256-byte blocks plus one, so that consecutive copies start on different channels
+__host__ __device__ __forceinline__ size_t logit_stride_words(int E) { return ((size_t)(E + 1) * 8 + 255) / 256 * 32 + 32; }
 
 struct LayerArgs {
     const void *x;          // (H) activation dtype
@@ -85,7 +100,7 @@ struct LayerArgs {
     float *info;            // (3, k) or null
     float *miss;            // (1) or null
     uint32_t *ws;           // workspace (zeroed once by the caller)
-    uint32_t off_rec, off_logits, off_h, off_part;  // byte offsets in ws of the tagged arrays
+    uint32_t off_logits, off_h, off_part;  // byte offsets in ws of the tagged arrays
     uint64_t *trace;        // optional per-item trace: [ticket] = (start, end, workgroup) or null
     uint64_t *stage;        // with trace: 8 stage stamps per item after the trace rows
 };
@@ -555,16 +570,17 @@ __device__ __forceinline__ void down_rows(const DownRegs<PREC> &d, const LaneVec
 }
 
 // ---------------------------------------------------------------------------------------
-// route tail: softmax / top-k / renorm / HOBBIT / resident copy / tables (wave 0 of one WG).
-// Logits and keys are staged in LDS (lane l handles l, l + 64, ...). Top-k: k rounds of a wave-wide maximum over
-// 32-bit keys; for 16-bit activations the key packs the order-preserving bits of the logit
-// above (1023 - index), so one maximum gives the largest logit and, among equal logits, the
-// lowest index (torch.topk / the reference order); fp32 logits take a second maximum for the
-// index among equal keys.
+// routing of this launch, computed by each workgroup that runs up / down items (all threads
+// call; waves 1-3 prefetch the record table into LDS while wave 0 polls the logits).
+// Softmax / top-k / renorm / HOBBIT / resident copy; the result is each table row's weight and
+// record address in LDS (s_rw / s_rb, P * ks rows precision-major; weight 0 = nothing to run).
+// Logits and keys are staged in LDS (lane l handles l, l + 64, ...). Top-k: for E <= 64 every
+// lane counts the keys above its own; otherwise k rounds of a wave-wide maximum over 32-bit keys.
+// For 16-bit activations the key packs the order-preserving bits of the logit above
+// (1023 - index), so the largest key is the largest logit and, among equal logits, the lowest
+// index (torch.topk / the reference order); fp32 logits break ties on the index explicitly.
+// The reporting workgroup (report = true) also writes the optional readouts.
 // ---------------------------------------------------------------------------------------
-// words between record copies: P * k rows of 3 words, rounded up to 1 KB
-__host__ __device__ __forceinline__ size_t rec_stride_words(int P, int k) { return (size_t)((P * k * 24 + 1023) / 1024) * 128; }
-
 template <int XDT>
 __device__ __forceinline__ uint32_t logit_key(float v, int c) {
     if constexpr (XDT == MOEHIP_DT_F32) {
@@ -578,247 +594,264 @@ __device__ __forceinline__ uint32_t logit_key(float v, int c) {
     }
 }
 
-// record of table row jj (P * k rows, precision-major): 3 tagged words
-//   [0] = weight bits (0 = nothing to run), [1] / [2] = low / high half of the record address;
-// NREC copies, copy c of row jj at word c * rec_stride_words(P, k) + jj * 3
+// LDS of one workgroup
+struct DlShared {
+    uint32_t tag;
+    int routed;
+    int idx[64];
+    float w[64];
+    float sorted[64];
+    float gl;                      // shared-expert gate logit
+    float rw[DL_MAXP * 32];        // table rows: weight (0 = nothing to run)
+    uint64_t rb[DL_MAXP * 32];     //             record address
+    float wk[DL_MAXP * 32];
+    int64_t rt[RT_LDS];            // prefetched record table (P, E)
+    __align__(16) float h[DL_MAXROW];  // staged h; logits and keys during the routing
+};
+
 template <int XDT>
-__device__ __forceinline__ void route_tail(const LayerArgs &a, uint32_t tag, int *s_idx, float *s_w, float *s_sorted,
-                                           float *s_buf, uint32_t *err, uint64_t *ts) {
-    const int lane = threadIdx.x;  // wave 0 only; s_buf: 2 * 1024 words of LDS (logits, keys)
-    const int k = a.k, E = a.E, ks = a.ks;
+__device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, DlShared &sh, uint32_t *err, bool report,
+                            uint64_t *ts) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int k = a.k, E = a.E, ks = a.ks, P = a.P;
     const bool has_sh = a.sgate != nullptr;
+    const bool pre = P * E <= RT_LDS;
     const int epl = (E + 63) >> 6;
-    float *s_lv = s_buf;
-    uint32_t *s_key = reinterpret_cast<uint32_t *>(s_buf + 1024);
+    float *s_lv = sh.h;
+    uint32_t *s_key = reinterpret_cast<uint32_t *>(sh.h + 1024);
 #define TS(i) do { if (ts != nullptr && lane == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-    TS(0);
-    if (ts != nullptr && lane == 0) ts[6] = __builtin_amdgcn_s_memtime();  // core clock, for the clock rate
-    int myc = 0;      // lane j < k: expert of rank j
-    float myw = 0.f;  // and its fp32 weight (rounded to the activation dtype)
-    int64_t rt[DL_MAXP] = {0, 0, 0, 0};  // and the addresses of its resident records
-    if (a.Wr != nullptr) {
-        const uint64_t *logits = ws_ptr<uint64_t>(a, a.off_logits);
-        // every logit of this launch (written by the router items, smaller tickets)
-        uint32_t need = 0;
-        for (int i = 0; i < epl; ++i)
-            if (lane + 64 * i < E) need |= 1u << i;
-        int nap = 1;
-        for (int it = 0; it < WAIT_SPINS && __ballot(need != 0) != 0ull; ++it) {
-            for (int i = 0; i < epl; ++i) {
-                if (need & (1u << i)) {
-                    const int c = lane + 64 * i;
-                    const uint64_t v = ld_tag(logits + c);
-                    if (tag_ok(v, tag)) {
-                        const float l = __uint_as_float((uint32_t)v);
+    if (wave != 0) {
+        if (pre)
+            for (int i = tid - 64; i < P * E; i += 192) sh.rt[i] = a.rtab[i];
+    } else {
+        TS(0);
+        if (a.Wr != nullptr || has_sh) {
+            // every logit of this launch (written by the router items, smaller tickets), all
+            // requested at once, then the missing ones again
+            const uint64_t *logits = ws_ptr<uint64_t>(a, a.off_logits) + (size_t)(blockIdx.x % NLC) * logit_stride_words(E);
+            uint32_t need = 0;
+            if (a.Wr != nullptr)
+                for (int i = 0; i < epl; ++i)
+                    if (lane + 64 * i < E) need |= 1u << i;
+            if (has_sh && lane == 0) need |= 1u << 31;
+            int nap = 1;
+            for (int it = 0; it < WAIT_SPINS && __ballot(need != 0) != 0ull; ++it) {
+                uint64_t v[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (i < epl && (need & (1u << i))) v[i] = ld_tag(logits + lane + 64 * i);
+                const uint64_t vg = (need >> 31) ? ld_tag(logits + E) : 0ull;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if (i < epl && (need & (1u << i)) && tag_ok(v[i], tag)) {
+                        const int c = lane + 64 * i;
+                        const float l = __uint_as_float((uint32_t)v[i]);
                         s_lv[c] = l;
                         s_key[c] = logit_key<XDT>(l, c);
-                        if (a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, l);
+                        if (report && a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, l);
                         need &= ~(1u << i);
                     }
                 }
+                if ((need >> 31) && tag_ok(vg, tag)) {
+                    sh.gl = __uint_as_float((uint32_t)vg);
+                    need &= ~(1u << 31);
+                }
+                if (__ballot(need != 0) != 0ull) backoff(nap, 2);
+                if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
             }
-            if (__ballot(need != 0) != 0ull) backoff(nap);
-            if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
+            if (a.Wr != nullptr)
+                for (int i = 0; i < epl; ++i) {  // logits still missing after the wait: never chosen
+                    if (need & (1u << i)) {
+                        s_lv[lane + 64 * i] = -INFINITY;
+                        s_key[lane + 64 * i] = 0u;
+                    }
+                }
+            if (need >> 31) sh.gl = -INFINITY;  // gate weight 0
         }
-        for (int i = 0; i < epl; ++i) {  // logits still missing after the wait: never chosen
-            if (need & (1u << i)) {
-                s_lv[lane + 64 * i] = -INFINITY;
-                s_key[lane + 64 * i] = 0u;
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    if (wave == 0) {
         TS(1);
-        float myv = 0.f;
-        if (E <= 64) {
-            // one logit per lane: its rank is the number of larger keys (keys are distinct for
-            // 16-bit logits; fp32 ties go to the lower index)
-            for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
-            __builtin_amdgcn_wave_barrier();
-            const uint32_t key = lane < E ? s_key[lane] : 0u;
-            const float lvv = lane < E ? s_lv[lane] : -INFINITY;
-            int rank = 0;
+        int myc = 0;      // lane j < k: expert of rank j
+        float myw = 0.f;  // and its fp32 weight (rounded to the activation dtype)
+        int64_t rt[DL_MAXP] = {0, 0, 0, 0};  // and the addresses of its resident records
+        if (a.Wr != nullptr) {
+            float myv = 0.f;
+            if (E <= 64) {
+                // one logit per lane: its rank is the number of larger keys (keys are distinct for
+                // 16-bit logits; fp32 ties go to the lower index)
+                for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
+                __builtin_amdgcn_wave_barrier();
+                const uint32_t key = lane < E ? s_key[lane] : 0u;
+                const float lvv = lane < E ? s_lv[lane] : -INFINITY;
+                int rank = 0;
 #pragma unroll
-            for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast);
-                                               // keys past E are 0 and never count
-                const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
-                const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+                for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast);
+                                                   // keys past E are 0 and never count
+                    const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
+                    const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
-                    else rank += ov[u] > key;
+                    for (int u = 0; u < 4; ++u) {
+                        if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
+                        else rank += ov[u] > key;
+                    }
+                }
+                if (lane < E && rank < k) {
+                    s_key[512 + rank] = (uint32_t)lane;
+                    s_lv[512 + rank] = lvv;
+                }
+                __builtin_amdgcn_wave_barrier();
+                if (lane < k) {
+                    myc = (int)s_key[512 + lane];
+                    myv = s_lv[512 + lane];
                 }
             }
-            if (lane < E && rank < k) {
-                s_key[512 + rank] = (uint32_t)lane;
-                s_lv[512 + rank] = lvv;
+            for (int r = 0; r < k && E > 64; ++r) {
+                uint32_t lb = 0u;
+                int lc = lane;
+                for (int i = 0; i < epl; ++i) {
+                    const int c = lane + 64 * i;
+                    const uint32_t kk = c < E ? s_key[c] : 0u;
+                    if (kk > lb) lb = kk, lc = c;
+                }
+                const uint32_t M = wave_max_u32(lb);
+                int c;
+                if constexpr (XDT == MOEHIP_DT_F32) {
+                    // among lanes holding the maximum key, the lowest expert index
+                    const uint32_t cand = lb == M ? (uint32_t)(1023 - lc) : 0u;
+                    c = 1023 - (int)wave_max_u32(cand);
+                } else {
+                    (void)lc;
+                    c = 1023 - (int)(M & 1023u);
+                }
+                c = min(c, E - 1);
+                const float v = s_lv[c];
+                __builtin_amdgcn_wave_barrier();
+                if (lane == (c & 63)) s_key[c] = 0u;
+                __builtin_amdgcn_wave_barrier();
+                if (lane == r) {
+                    myc = c;
+                    myv = v;
+                }
             }
-            __builtin_amdgcn_wave_barrier();
+            TS(2);
+            if (lane < k && myc >= 0 && myc < E) {  // record-table reads overlap the softmax below
+#pragma unroll
+                for (int pi = 0; pi < DL_MAXP; ++pi)
+                    rt[pi] = pi < P ? (pre ? sh.rt[pi * E + myc] : a.rtab[(size_t)pi * E + myc]) : 0;
+            }
+            const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
+            float sum = 0.f;
+            for (int i = 0; i < epl; ++i)
+                if (lane + 64 * i < E) sum += expf(s_lv[lane + 64 * i] - m);
+            sum = wave_sum(sum);
+            const float p = lane < k ? expf(myv - m) / sum : 0.f;
+            const float tot = a.renorm ? wave_sum(p) : 1.f;
             if (lane < k) {
-                myc = (int)s_key[512 + lane];
-                myv = s_lv[512 + lane];
+                const float pw = a.renorm ? p / tot : p;
+                myw = rnd_act<XDT>(pw);
+                if (report) {
+                    if (a.idx_out) a.idx_out[lane] = myc;
+                    if (a.w_out) st_act<XDT>(a.w_out, lane, pw);
+                    if (a.w32_out) a.w32_out[lane] = myw;
+                }
             }
-        }
-        for (int r = 0; r < k && E > 64; ++r) {
-            uint32_t lb = 0u;
-            int lc = lane;
-            for (int i = 0; i < epl; ++i) {
-                const int c = lane + 64 * i;
-                const uint32_t kk = c < E ? s_key[c] : 0u;
-                if (kk > lb) lb = kk, lc = c;
-            }
-            const uint32_t M = wave_max_u32(lb);
-            int c;
-            if constexpr (XDT == MOEHIP_DT_F32) {
-                // among lanes holding the maximum key, the lowest expert index
-                const uint32_t cand = lb == M ? (uint32_t)(1023 - lc) : 0u;
-                c = 1023 - (int)wave_max_u32(cand);
-            } else {
-                (void)lc;
-                c = 1023 - (int)(M & 1023u);
-            }
-            c = min(c, E - 1);
-            const float v = s_lv[c];
-            __builtin_amdgcn_wave_barrier();
-            if (lane == (c & 63)) s_key[c] = 0u;
-            __builtin_amdgcn_wave_barrier();
-            if (lane == r) {
-                myc = c;
-                myv = v;
-            }
-        }
-        TS(2);
-        if (lane < k && myc >= 0 && myc < E) {  // residency loads overlap the softmax below
+        } else if (lane < k) {
+            myc = (int)a.idx_in[lane];
+            myw = a.w32_in[lane];
+            if (myc >= 0 && myc < E) {
 #pragma unroll
-            for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.rtab[(size_t)pi * E + myc] : 0;
-        }
-        const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
-        float sum = 0.f;
-        for (int i = 0; i < epl; ++i)
-            if (lane + 64 * i < E) sum += expf(s_lv[lane + 64 * i] - m);
-        sum = wave_sum(sum);
-        const float p = lane < k ? expf(myv - m) / sum : 0.f;
-        const float tot = a.renorm ? wave_sum(p) : 1.f;
-        if (lane < k) {
-            const float pw = a.renorm ? p / tot : p;
-            myw = rnd_act<XDT>(pw);
-            if (a.idx_out) a.idx_out[lane] = myc;
-            if (a.w_out) st_act<XDT>(a.w_out, lane, pw);
-            if (a.w32_out) a.w32_out[lane] = myw;
-        }
-    } else if (lane < k) {
-        myc = (int)a.idx_in[lane];
-        myw = a.w32_in[lane];
-        if (myc >= 0 && myc < E) {
-#pragma unroll
-            for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.rtab[(size_t)pi * E + myc] : 0;
-        }
-    }
-    if (has_sh && lane == k) {
-        // the shared expert (row k): weight sigmoid(x . g) with x . g rounded to the activation
-        // dtype like the gate's output (modeling_qwen3_next.py:793-796), record from srec
-        const uint64_t *ls = ws_ptr<uint64_t>(a, a.off_logits) + E;
-        float l = 0.f;
-        bool got = false;
-        int nap = 1;
-        for (int it = 0; it < WAIT_SPINS; ++it) {
-            const uint64_t v = ld_tag(ls);
-            if (tag_ok(v, tag)) {
-                l = __uint_as_float((uint32_t)v);
-                got = true;
-                break;
+                for (int pi = 0; pi < DL_MAXP; ++pi)
+                    rt[pi] = pi < P ? (pre ? sh.rt[pi * E + myc] : a.rtab[(size_t)pi * E + myc]) : 0;
             }
-            backoff(nap);
         }
-        if (!got) flag_error(err);
-        myc = -1;
-        myw = got ? rnd_act<XDT>(1.0f / (1.0f + expf(-l))) : 0.f;
+        if (has_sh && lane == k) {
+            // the shared expert (row k): weight sigmoid(x . g) with x . g rounded to the activation
+            // dtype like the gate's output (modeling_qwen3_next.py:793-796), record from srec
+            const float l = sh.gl;
+            myc = -1;
+            myw = l == -INFINITY ? 0.f : rnd_act<XDT>(1.0f / (1.0f + expf(-l)));
 #pragma unroll
-        for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < a.P ? a.srec[pi] : 0;
-    }
-    TS(3);
-    // HOBBIT levels (moelab/policy.py:77-123), resident copy, tables (moelab/fullgraph.py:149-171)
-    const int j = lane;
-    const bool act = j < k;                  // a routed row
-    const bool shr = has_sh && j == k;       // the shared row: level 0, never skipped
-    const bool row = act || shr;
-    const int e = act ? myc : 0;
-    if (act) {
-        s_idx[j] = e;
-        s_w[j] = myw;
-    }
-    __builtin_amdgcn_wave_barrier();
-    const float wj = act ? myw : 0.f;
-    float tot = 0.f;
-    for (int i = 0; i < k; ++i) tot += s_w[i];
-    tot = fmaxf(tot, 1e-12f);
-    int lvl;
-    bool skip = false;
-    const moehip_policy pol = a.pol;
-    if (pol.mode == 1 || pol.protect) {
-        lvl = 0;
-    } else if (pol.mode == 2) {
-        lvl = 2;
-    } else {
-        const float wn = wj / tot;
-        int rank = 0;
-        for (int i = 0; i < k; ++i) {
-            const float o = s_w[i] / tot;
-            rank += (o > wn) || (o == wn && i < j);
+            for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < P ? a.srec[pi] : 0;
         }
-        if (act) s_sorted[rank] = wn;
+        TS(3);
+        // HOBBIT levels (moelab/policy.py:77-123), resident copy, tables (moelab/fullgraph.py:149-171)
+        const int j = lane;
+        const bool act = j < k;                  // a routed row
+        const bool shr = has_sh && j == k;       // the shared row: level 0, never skipped
+        const bool row = act || shr;
+        const int e = act ? myc : 0;
+        if (act) {
+            sh.idx[j] = e;
+            sh.w[j] = myw;
+        }
         __builtin_amdgcn_wave_barrier();
-        float cs = 0.f;
-        for (int r = 0; r <= rank && r < k; ++r) cs += s_sorted[r];
-        const float s = cs - wn;
-        lvl = 2;
-        if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
-        if (s <= pol.t1) lvl = 0;
-        skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
-    }
-    if (shr) {
-        lvl = 0;
-        skip = false;
-    }
-    TS(4);
-    const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
-    // the shared row takes its most precise present copy
-    const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
-    const bool upg = shr || pol.upgrade;
-    int chosen = -1;
+        const float wj = act ? myw : 0.f;
+        float tot = 0.f;
+        for (int i = 0; i < k; ++i) tot += sh.w[i];
+        tot = fmaxf(tot, 1e-12f);
+        int lvl;
+        bool skip = false;
+        const moehip_policy pol = a.pol;
+        if (pol.mode == 1 || pol.protect) {
+            lvl = 0;
+        } else if (pol.mode == 2) {
+            lvl = 2;
+        } else {
+            const float wn = wj / tot;
+            int rank = 0;
+            for (int i = 0; i < k; ++i) {
+                const float o = sh.w[i] / tot;
+                rank += (o > wn) || (o == wn && i < j);
+            }
+            if (act) sh.sorted[rank] = wn;
+            __builtin_amdgcn_wave_barrier();
+            float cs = 0.f;
+            for (int r = 0; r <= rank && r < k; ++r) cs += sh.sorted[r];
+            const float s = cs - wn;
+            lvl = 2;
+            if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
+            if (s <= pol.t1) lvl = 0;
+            skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
+        }
+        if (shr) {
+            lvl = 0;
+            skip = false;
+        }
+        TS(4);
+        const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
+        // the shared row takes its most precise present copy
+        const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
+        const bool upg = shr || pol.upgrade;
+        int chosen = -1;
 #pragma unroll
-    for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
-        const bool avail = pi < a.P && rt[pi] != 0;
-        if (avail && (upg ? req >= pi : req == pi)) chosen = pi;
-    }
-    const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
-    const bool is_miss = row && !skip && !usable;
-    uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec);
-    // the chosen copy (address, weight) of this row; compact loops keep the register use small
-    const bool sel = row && chosen >= 0 && !skip && usable;
-    const int64_t base = !sel ? 0 : (chosen == 0 ? rt[0] : (chosen == 1 ? rt[1] : (chosen == 2 ? rt[2] : rt[3])));
-    const uint32_t wbits = sel ? __float_as_uint(row ? myw : 0.f) : 0u;
-    if (row) {
-#pragma unroll 1
-        for (int pi = 0; pi < a.P; ++pi) {
-            const bool mine = sel && chosen == pi;
-#pragma unroll 1
-            for (int cp = 0; cp < NREC; ++cp) {
-                uint64_t *r3 = rec + (size_t)cp * rec_stride_words(a.P, ks) + ((size_t)pi * ks + j) * 3;
-                st_tag(r3 + 1, mine ? (uint32_t)(uint64_t)base : 0u, tag);
-                st_tag(r3 + 2, mine ? (uint32_t)((uint64_t)base >> 32) : 0u, tag);
-                st_tag(r3 + 0, mine ? wbits : 0u, tag);
+        for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
+            const bool avail = pi < P && rt[pi] != 0;
+            if (avail && (upg ? req >= pi : req == pi)) chosen = pi;
+        }
+        const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
+        const bool is_miss = row && !skip && !usable;
+        // the chosen copy (address, weight) of this row
+        const bool sel = row && chosen >= 0 && !skip && usable;
+        const int64_t base = !sel ? 0 : (chosen == 0 ? rt[0] : (chosen == 1 ? rt[1] : (chosen == 2 ? rt[2] : rt[3])));
+        if (row) {
+            for (int pi = 0; pi < P; ++pi) {
+                const bool mine = sel && chosen == pi;
+                sh.rw[pi * ks + j] = mine ? myw : 0.f;
+                sh.rb[pi * ks + j] = mine ? (uint64_t)base : 0ull;
+            }
+            if (report && a.info && act) {
+                a.info[j] = (float)e;
+                a.info[k + j] = skip ? -2.f : (float)chosen;
+                a.info[2 * k + j] = (float)lvl;
             }
         }
-        if (a.info && act) {
-            a.info[j] = (float)e;
-            a.info[k + j] = skip ? -2.f : (float)chosen;
-            a.info[2 * k + j] = (float)lvl;
-        }
+        const unsigned long long bal = __ballot(is_miss);
+        if (report && j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
+        if (j == 0) sh.routed = 1;
+        TS(5);
     }
-    TS(5);
-    if (ts != nullptr && lane == 0) ts[7] = __builtin_amdgcn_s_memtime();
-    const unsigned long long bal = __ballot(is_miss);
-    if (j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
+    __syncthreads();
 #undef TS
 }
 
@@ -866,7 +899,10 @@ __device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t 
         }
     }
     acc = wave_sum(acc);
-    if (lane == 0) st_tag(ws_ptr<uint64_t>(a, a.off_logits) + e, __float_as_uint(rnd_act<XDT>(acc)), tag);
+    // one copy per lane: lanes 0 .. NLC-1 store the same tagged logit into their copy
+    if (lane < NLC)
+        st_tag(ws_ptr<uint64_t>(a, a.off_logits) + (size_t)lane * logit_stride_words(a.E) + e,
+               __float_as_uint(rnd_act<XDT>(acc)), tag);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -877,43 +913,21 @@ struct Route {
     uint64_t base;
 };
 
-// wait for routing record jj (3 tagged words, lanes 0..2 of wave 0, copy blockIdx % NREC) and
-// share it through LDS; on expiry the row is treated as not routed (w = 0) and the error flag
-// is set. Every thread of the workgroup must call this.
-__device__ __forceinline__ Route wg_route(const LayerArgs &a, uint32_t tag, int jj, float *s_r, uint32_t *err) {
-    const int tid = threadIdx.x;
-    if (tid < 64) {
-        const uint64_t *r3 =
-            ws_ptr<uint64_t>(a, a.off_rec) + (size_t)(blockIdx.x % NREC) * rec_stride_words(a.P, a.ks) + (size_t)jj * 3;
-        int nap = 1;
-        bool got = false;
-        uint32_t p = 0;
-        for (int it = 0; it < WAIT_SPINS; ++it) {
-            const uint64_t v = tid < 3 ? ld_tag(r3 + tid) : ((uint64_t)tag << 32);
-            if (__ballot(!tag_ok(v, tag)) == 0ull) {
-                p = (uint32_t)v;
-                got = true;
-                break;
-            }
-            backoff(nap, 16);  // the routing is microseconds away: poll gently
-        }
-        if (!got) {
-            p = 0u;
-            if (tid == 0) flag_error(err);
-        }
-        if (tid < 3) s_r[tid] = __uint_as_float(p);
-    }
-    __syncthreads();
+// routing of table row jj (this launch's routing is in LDS): weight 0 = nothing to run
+template <int XDT>
+__device__ __forceinline__ Route wg_route(const LayerArgs &a, uint32_t tag, int jj, DlShared &sh, uint32_t *err) {
+    (void)tag;
+    (void)err;
     Route r;
-    r.w = s_r[0];
-    r.base = ((uint64_t)__float_as_uint(s_r[2]) << 32) | __float_as_uint(s_r[1]);
+    r.w = sh.rw[jj];
+    r.base = sh.rb[jj];
     if (r.base == 0) r.w = 0.f;
-    __syncthreads();  // s_r may be rewritten by the next item
     return r;
 }
 
-template <int PREC, int XDT>
-__device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, float *s_r,
+// LAZY: this workgroup computes the routing here, after requesting x (one-item workgroups)
+template <int PREC, int XDT, bool LAZY>
+__device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, DlShared &sh,
                                         uint32_t *err, int item) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lg = pick4(a.lg_up, pi);
@@ -923,7 +937,8 @@ __device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi
     uint64_t *st = a.stage != nullptr ? a.stage + 8 * (size_t)item : nullptr;
     load_x<PREC, XDT>(a.x, lane & (G - 1), G, C, lv);  // before the routing wait
     stamp(st, 0);
-    const Route rt = wg_route(a, tag, jj, s_r, err);
+    if (LAZY) route_local<XDT>(a, tag, sh, err, false, nullptr);
+    const Route rt = wg_route<XDT>(a, tag, jj, sh, err);
     stamp(st, 1);
     if (rt.w == 0.f) return;
     const int per_wave = DlFmt<PREC>::NPU * RPW;
@@ -934,43 +949,42 @@ __device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi
     up_rows<PREC, XDT>(qb, sb, lv, pair0, a.I, a.H, pick4(a.gs_up, pi), lg, hout, tag, st);
 }
 
-// h row jj of this launch -> LDS (piece-major for chunks of VPC values); false on expiry
+// h row jj of this launch -> LDS (piece-major for chunks of VPC values); false on expiry.
+// Every thread requests all its words at once, then only the missing ones again.
 template <int VPC>
 __device__ __forceinline__ bool stage_h(const uint64_t *h, int I, uint32_t tag, float *s_h, uint32_t *err) {
     const int tid = threadIdx.x;
     const int C = I / VPC;
+    constexpr int PER = DL_MAXROW / 256;  // words per thread (I <= 2048)
+    uint32_t need = 0;
+#pragma unroll
+    for (int m = 0; m < PER; ++m)
+        if (tid + 256 * m < I) need |= 1u << m;
     int nap = 1;
-    // the last element comes from the row's last up item: wait for it with one lane before
-    // polling the whole row (keeps the polling traffic of waiting workgroups small)
-    if (tid == 0) {
-        for (int it = 0; it < WAIT_SPINS; ++it) {
-            if (tag_ok(ld_tag(h + I - 1), tag)) break;
-            backoff(nap);
-        }
-    }
-    __syncthreads();
-    nap = 1;
     for (int it = 0; it < WAIT_SPINS; ++it) {
-        int missing = 0;
-        for (int i = tid; i < I; i += 256) {
-            const uint64_t v = ld_tag(h + i);
-            if (tag_ok(v, tag)) {
+        uint64_t v[PER];
+#pragma unroll
+        for (int m = 0; m < PER; ++m)
+            if (need & (1u << m)) v[m] = ld_tag(h + tid + 256 * m);
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            if ((need & (1u << m)) && tag_ok(v[m], tag)) {
+                const int i = tid + 256 * m;
                 const int c = i / VPC, q = i % VPC;
-                s_h[((q >> 2) * C + c) * 4 + (q & 3)] = __uint_as_float((uint32_t)v);
-            } else {
-                missing = 1;
+                s_h[((q >> 2) * C + c) * 4 + (q & 3)] = __uint_as_float((uint32_t)v[m]);
+                need &= ~(1u << m);
             }
         }
-        if (!__syncthreads_or(missing)) return true;
-        backoff(nap);
+        if (!__syncthreads_or(need != 0)) return true;
+        backoff(nap, 2);
     }
     if (tid == 0) flag_error(err);
     return false;
 }
 
-template <int PREC, int XDT>
-__device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, float *s_h,
-                                          float *s_wk, uint32_t *err, int item) {
+template <int PREC, int XDT, bool LAZY>
+__device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, DlShared &sh,
+                                          uint32_t *err, int item) {
     uint64_t *st = a.stage != nullptr ? a.stage + 8 * (size_t)item : nullptr;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lg = pick4(a.lg_dn, pi);
@@ -978,7 +992,8 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     const int per_wave = DlFmt<PREC>::NPD * RPW;
     const int row0 = b * per_wave * 4 + wave * per_wave;
     const int PK = a.P * a.ks;
-    const Route rt0 = wg_route(a, tag, jj, s_wk, err);
+    if (LAZY) route_local<XDT>(a, tag, sh, err, false, nullptr);
+    const Route rt0 = wg_route<XDT>(a, tag, jj, sh, err);
     stamp(st, 1);
     const bool run = rt0.w != 0.f;
     uint64_t *part = ws_ptr<uint64_t>(a, a.off_part);
@@ -991,66 +1006,113 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
             __builtin_amdgcn_s_waitcnt(0);
             stamp(st, 2);
         }
-        if (stage_h<DlFmt<PREC>::VPC>(ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I, a.I, tag, s_h, err)) {
+        if (stage_h<DlFmt<PREC>::VPC>(ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I, a.I, tag, sh.h, err)) {
             stamp(st, 3);
             LaneVec<PREC, XDT> lv;
-            load_h<PREC, XDT>(s_h, lane & (G - 1), G, a.I / DlFmt<PREC>::VPC, lv);
+            load_h<PREC, XDT>(sh.h, lane & (G - 1), G, a.I / DlFmt<PREC>::VPC, lv);
             down_rows<PREC, XDT>(d, lv, row0, a.H, lg, rt0.w, part + (size_t)jj * a.H, tag);
             stamp(st, 4);
         }
-        __syncthreads();  // s_h is reused by the next item
+        __syncthreads();  // sh.h is reused below and by the next item
     }
     if (jj != PK - 1) return;
-    // the last table row's items sum every row's partials in table order
-    const uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec);
-    if (tid < PK) {
-        float w = 0.f;
+    // the last table row's items sum every row's partials in table order. Table rows are taken
+    // in chunks that fit the LDS buffer; every thread requests its (table row, row) words of a
+    // chunk at once, then only the missing ones again.
+    const int rows = per_wave * 4;
+    const int r0 = b * rows;
+    float *s_part = sh.h;  // (chunk, rows)
+    constexpr int PER = DL_MAXROW / 256;
+    float acc[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) acc[u] = 0.f;
+    const int QC = max(1, DL_MAXROW / rows);
+    for (int q0 = 0; q0 < PK; q0 += QC) {
+        const int nq = min(QC, PK - q0), nw = nq * rows;
+        uint32_t need = 0;
+#pragma unroll
+        for (int m = 0; m < PER; ++m) {
+            const int i = tid + 256 * m;
+            if (i >= nw) continue;
+            const int q = q0 + i / rows, rr = i % rows;
+            if (sh.rw[q] != 0.f && sh.rb[q] != 0 && r0 + rr < a.H) need |= 1u << m;
+            else s_part[i] = 0.f;
+        }
         int nap = 1;
         for (int it = 0; it < WAIT_SPINS; ++it) {
-            const uint64_t v = ld_tag(rec + (size_t)tid * 3);
-            if (tag_ok(v, tag)) {
-                w = __uint_as_float((uint32_t)v);
-                break;
+            uint64_t v[PER];
+#pragma unroll
+            for (int m = 0; m < PER; ++m) {
+                const int i = tid + 256 * m;
+                if (need & (1u << m)) v[m] = ld_tag(part + (size_t)(q0 + i / rows) * a.H + r0 + i % rows);
             }
-            backoff(nap);
-            if (it == WAIT_SPINS - 1) flag_error(err);
-        }
-        s_wk[tid] = w;
-    }
-    __syncthreads();
-    const int rows = per_wave * 4;
-    for (int rr = tid; rr < rows; rr += 256) {
-        const int r = b * rows + rr;
-        if (r >= a.H) continue;
-        float s = 0.f;
-        for (int q = 0; q < PK; ++q) {
-            if (s_wk[q] == 0.f) continue;
-            int nap = 1;
-            for (int it = 0; it < WAIT_SPINS; ++it) {
-                const uint64_t v = ld_tag(part + (size_t)q * a.H + r);
-                if (tag_ok(v, tag)) {
-                    s += __uint_as_float((uint32_t)v);
-                    break;
+#pragma unroll
+            for (int m = 0; m < PER; ++m) {
+                if ((need & (1u << m)) && tag_ok(v[m], tag)) {
+                    s_part[tid + 256 * m] = __uint_as_float((uint32_t)v[m]);
+                    need &= ~(1u << m);
                 }
-                backoff(nap);
-                if (it == WAIT_SPINS - 1) flag_error(err);
+            }
+            if (!__syncthreads_or(need != 0)) break;
+            backoff(nap, 2);
+            if (it == WAIT_SPINS - 1) {  // give up: the missing partials count as 0
+                flag_error(err);
+#pragma unroll
+                for (int m = 0; m < PER; ++m)
+                    if (need & (1u << m)) s_part[tid + 256 * m] = 0.f;
+                __syncthreads();
             }
         }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int rr = tid + 256 * u;
+            if (rr < rows)
+                for (int qq = 0; qq < nq; ++qq) acc[u] += s_part[qq * rows + rr];
+        }
+        __syncthreads();  // s_part is rewritten by the next chunk
+    }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int rr = tid + 256 * u, r = r0 + rr;
+        if (rr >= rows || r >= a.H) continue;
+        float s = acc[u];
         if (a.accumulate) s += ld_act<XDT>(a.out, r);
         if (a.add != nullptr) s += ld_act<XDT>(a.add, r);
         st_act<XDT>(a.out, r, s);
     }
     stamp(st, 5);
-    // the last combining item to finish advances the launch generation: every item of this
-    // launch is complete at that point, and every workgroup read the generation before its items
-    __syncthreads();
-    if (tid == 0) {
-        __builtin_amdgcn_s_waitcnt(0);  // this item's output stores are done
-        if (add_co32(a.ws + W_DONE, 1u) == (uint32_t)(pick4(a.ndb, a.P - 1) - 1)) {
-            const uint32_t gen = tag - 1u, next = gen + 1u == 0xFFFFFFFFu ? 0u : gen + 1u;
-            st_co32(a.ws + W_DONE, 0u);
-            for (int q = 0; q < NGEN; ++q) st_co32(a.ws + W_GEN + 256 * q, next);
-        }
+    __syncthreads();  // sh.h is reused by the next item
+}
+
+// this workgroup holds its launch tag: count it in reader counter blockIdx % NSUB (a wave
+// other than wave 0, which routes; no return value)
+__device__ __forceinline__ void gen_read_done(uint32_t *ws) {
+    if (threadIdx.x == 192)
+        __hip_atomic_fetch_add(ws + W_READ + 32 * (blockIdx.x % NSUB), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// router item r of NR: wait until the reader counters q = r, r + NR, ... hold every workgroup of
+// the grid that counts there, clear them, and count them drained; the last drained counter
+// advances the launch generation (every workgroup of the launch has read it by then). Bounded:
+// on expiry the error flag is set and the generation is advanced all the same (a tag must never
+// be reused).
+__device__ __forceinline__ void gen_manage(uint32_t *ws, int r, int NR, uint32_t tag) {
+    const int q = threadIdx.x;
+    const int G = gridDim.x;
+    if (q >= NSUB || q >= G || q % NR != r) return;
+    const uint32_t nq = (uint32_t)((G - q + NSUB - 1) / NSUB);
+    int nap = 1;
+    for (int it = 0; it < WAIT_SPINS; ++it) {
+        if (ld_co32(ws + W_READ + 32 * q) >= nq) break;
+        backoff(nap);
+        if (it == WAIT_SPINS - 1) flag_error(ws + W_ERR);
+    }
+    st_co32(ws + W_READ + 32 * q, 0u);
+    const uint32_t used = (uint32_t)min(G, NSUB);
+    if (add_co32(ws + W_TOP, 1u) == used - 1u) {
+        const uint32_t gen = tag - 1u, next = gen + 1u == 0xFFFFFFFFu ? 0u : gen + 1u;
+        st_co32(ws + W_TOP, 0u);
+        for (int c = 0; c < NGEN; ++c) st_co32(ws + W_GEN + 256 * c, next);
     }
 }
 
@@ -1070,58 +1132,68 @@ __host__ __device__ __forceinline__ int down_item_rows(int prec, int lg) {
 // ---------------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------------
-template <int XDT>
+// PR = the record precision of a single-precision launch (its code only), or -1 for any mix
+template <int XDT, int PR>
 __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
-    __shared__ uint32_t s_tag;
-    __shared__ int s_idx[64];
-    __shared__ float s_w[64];
-    __shared__ float s_sorted[64];
-    __shared__ float s_wk[DL_MAXP * 32];
-    __shared__ __align__(16) float s_h[DL_MAXROW];
+    __shared__ DlShared sh;
     const int tid = threadIdx.x;
     uint32_t *ws = a.ws;
     uint32_t *err = ws + W_ERR;
     const int NR = router_items(a.Wr != nullptr, a.sgate != nullptr, a.E);
     const int total = NR + a.NU + a.ND;
-    if (tid == 0) s_tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
+    if (tid == 0) {
+        sh.tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
+        sh.routed = 0;
+    }
     __syncthreads();
-    const uint32_t tag = uni((int)s_tag);
+    const uint32_t tag = uni((int)sh.tag);
+    gen_read_done(ws);
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
         __syncthreads();  // LDS of the previous item is free
         uint64_t t_start = 0;
         if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
         if (t < NR) {
-            // ---------------- router rows; the last router item also routes ----------------
+            // ---------------- router rows; the last router item also reports the routing ----------------
             if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag);
-            if (t == NR - 1 && tid < 64)
-                route_tail<XDT>(a, tag, s_idx, s_w, s_sorted, s_h, err, a.trace ? a.trace + 3 * total : nullptr);
+            if (t == NR - 1) route_local<XDT>(a, tag, sh, err, true, a.trace ? a.trace + 3 * total : nullptr);
+            gen_manage(ws, t, NR, tag);
         } else if (t < NR + a.NU) {
+            if (!sh.routed) route_local<XDT>(a, tag, sh, err, false, nullptr);
             // ---------------- kernel-A rows ----------------
             const int u = t - NR;
             const int pi = block_of(a.up_base, a.P, u);
             const int rem = u - pick4(a.up_base, pi);
             const int nub = pick4(a.nub, pi);
             const int jj = pi * a.ks + rem / nub, b = rem % nub;
-            switch (pick4(a.prec, pi)) {
-                case MOEHIP_PREC_INT4: up_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
-                case MOEHIP_PREC_INT8: up_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
-                case MOEHIP_PREC_F16: up_item<MOEHIP_PREC_F16, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
-                case MOEHIP_PREC_BF16: up_item<MOEHIP_PREC_BF16, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
-                default: up_item<MOEHIP_PREC_FP8, XDT>(a, tag, pi, jj, b, s_wk, err, t); break;
+            if constexpr (PR >= 0) {
+                up_item<PR, XDT, false>(a, tag, pi, jj, b, sh, err, t);
+            } else {
+                switch (pick4(a.prec, pi)) {
+                    case MOEHIP_PREC_INT4: up_item<MOEHIP_PREC_INT4, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_INT8: up_item<MOEHIP_PREC_INT8, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_F16: up_item<MOEHIP_PREC_F16, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_BF16: up_item<MOEHIP_PREC_BF16, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    default: up_item<MOEHIP_PREC_FP8, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                }
             }
         } else {
+            if (!sh.routed) route_local<XDT>(a, tag, sh, err, false, nullptr);
             // ---------------- kernel-B rows (+ ordered combine) ----------------
             const int dd = t - NR - a.NU;
             const int pi = block_of(a.dn_base, a.P, dd);
             const int rem = dd - pick4(a.dn_base, pi);
             const int ndb = pick4(a.ndb, pi);
             const int jj = pi * a.ks + rem / ndb, b = rem % ndb;
-            switch (pick4(a.prec, pi)) {
-                case MOEHIP_PREC_INT4: down_item<MOEHIP_PREC_INT4, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
-                case MOEHIP_PREC_INT8: down_item<MOEHIP_PREC_INT8, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
-                case MOEHIP_PREC_F16: down_item<MOEHIP_PREC_F16, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
-                case MOEHIP_PREC_BF16: down_item<MOEHIP_PREC_BF16, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
-                default: down_item<MOEHIP_PREC_FP8, XDT>(a, tag, pi, jj, b, s_h, s_wk, err, t); break;
+            if constexpr (PR >= 0) {
+                down_item<PR, XDT, false>(a, tag, pi, jj, b, sh, err, t);
+            } else {
+                switch (pick4(a.prec, pi)) {
+                    case MOEHIP_PREC_INT4: down_item<MOEHIP_PREC_INT4, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_INT8: down_item<MOEHIP_PREC_INT8, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_F16: down_item<MOEHIP_PREC_F16, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    case MOEHIP_PREC_BF16: down_item<MOEHIP_PREC_BF16, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                    default: down_item<MOEHIP_PREC_FP8, XDT, false>(a, tag, pi, jj, b, sh, err, t); break;
+                }
             }
         }
         if (a.trace != nullptr && tid == 0) {
@@ -1129,6 +1201,69 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
             a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
             a.trace[3 * t + 2] = blockIdx.x;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// one-item kernel: a single-precision launch whose items all fit on the GPU at once runs one
+// item per workgroup (grid = items), with the code of its precision only and no item loop (the
+// compiler then keeps no loop state live across the items' code: fewer registers, more
+// workgroups per CU). Same items, routing, exchanges and generation handling as above.
+// ---------------------------------------------------------------------------------------
+// the kernel's argument block, re-derived from the kernarg segment pointer behind an empty asm
+// so that the compiler loads each argument where a phase uses it instead of at kernel entry
+// (arguments loaded at entry stay live in SGPRs through the whole kernel)
+typedef const __attribute__((address_space(4))) LayerArgs KLayerArgs;
+__device__ __forceinline__ const LayerArgs &kargs() {
+    KLayerArgs *p = (KLayerArgs *)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return *(const LayerArgs *)p;
+}
+
+template <int XDT, int PR>
+__global__ __launch_bounds__(256) void k_decode_tok(LayerArgs) {
+    __shared__ DlShared sh;
+    const int tid = threadIdx.x;
+    int NR, NU, total;
+    {
+        const LayerArgs &a = kargs();
+        NR = uni(router_items(a.Wr != nullptr, a.sgate != nullptr, a.E));
+        NU = uni(a.NU);
+        total = NR + NU + uni(a.ND);
+        if (tid == 0) {
+            sh.tag = ld_co32(a.ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
+            sh.routed = 0;
+        }
+    }
+    __syncthreads();
+    const uint32_t tag = uni((int)sh.tag);
+    gen_read_done(kargs().ws);
+    const int t = blockIdx.x;
+    uint64_t t_start = 0;
+    if (t < NR) {
+        const LayerArgs &a = kargs();
+        if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
+        if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag);
+        if (t == NR - 1) route_local<XDT>(a, tag, sh, a.ws + W_ERR, true, a.trace ? a.trace + 3 * total : nullptr);
+        gen_manage(a.ws, t, NR, tag);
+    } else if (t < NR + NU) {
+        const LayerArgs &a = kargs();
+        if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
+        const int u = t - NR;
+        const int nub = uni(a.nub[0]);
+        up_item<PR, XDT, true>(a, tag, 0, u / nub, u % nub, sh, a.ws + W_ERR, t);
+    } else {
+        const LayerArgs &a = kargs();
+        if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
+        const int dd = t - NR - NU;
+        const int ndb = uni(a.ndb[0]);
+        down_item<PR, XDT, true>(a, tag, 0, dd / ndb, dd % ndb, sh, a.ws + W_ERR, t);
+    }
+    const LayerArgs &a = kargs();
+    if (a.trace != nullptr && tid == 0) {
+        a.trace[3 * t + 0] = t_start;
+        a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
+        a.trace[3 * t + 2] = blockIdx.x;
     }
 }
 
@@ -1146,7 +1281,7 @@ static inline int lg_for(int cols, int prec) {
 static inline int up_item_pairs(int prec, int lg) { return (4 / cpl_host(prec)) * (64 >> lg) * 4; }
 
 struct DlLayout {
-    uint32_t rec, logits, h, part, total;
+    uint32_t logits, h, part, total;
 };
 
 static inline uint32_t al256(size_t v) { return (uint32_t)((v + 255) / 256 * 256); }
@@ -1156,11 +1291,8 @@ static DlLayout dl_layout(int P, int k, int E, int H, int I) {
     const int PK = P * k;
     size_t off = W_HDR * 4;
     off = al256(off);
-    L.rec = (uint32_t)off;
-    off += (size_t)NREC * rec_stride_words(P, k) * 8;
-    off = al256(off);
     L.logits = (uint32_t)off;
-    off += (size_t)(E + 1) * 8;  // + the shared-expert gate
+    off += (size_t)NLC * logit_stride_words(E) * 8;  // E routed + the shared-expert gate, NLC copies
     off = al256(off);
     L.h = (uint32_t)off;
     off += (size_t)PK * I * 8;
@@ -1196,14 +1328,35 @@ static int dl_plan(const moehip_layer_desc *d, int with_router, LayerArgs *a) {
     return router_items(with_router != 0, d->shared_gate != nullptr, d->E) + nu + nd;
 }
 
-// workgroups of k_decode_layer<DT> the current device holds at once (occupancy x CUs)
-template <int DT>
-static int dl_capacity(int *cap) {
+// the kernel instances of a launch: the one-item kernel of its precision (single-precision
+// launches), and the item-loop kernel (any mix, or more items than the GPU holds at once)
+typedef void (*DlKernel)(LayerArgs);
+template <int XDT>
+static DlKernel dl_tok_x(int prec0) {
+    switch (prec0) {
+        case MOEHIP_PREC_INT4: return k_decode_tok<XDT, MOEHIP_PREC_INT4>;
+        case MOEHIP_PREC_INT8: return k_decode_tok<XDT, MOEHIP_PREC_INT8>;
+        case MOEHIP_PREC_F16: return k_decode_tok<XDT, MOEHIP_PREC_F16>;
+        case MOEHIP_PREC_BF16: return k_decode_tok<XDT, MOEHIP_PREC_BF16>;
+        case MOEHIP_PREC_FP8: return k_decode_tok<XDT, MOEHIP_PREC_FP8>;
+        default: return nullptr;
+    }
+}
+static DlKernel dl_kernel(int dtype, bool tok, int prec0) {
+    switch (dtype) {
+        case MOEHIP_DT_F16: return tok ? dl_tok_x<MOEHIP_DT_F16>(prec0) : k_decode_layer<MOEHIP_DT_F16, -1>;
+        case MOEHIP_DT_BF16: return tok ? dl_tok_x<MOEHIP_DT_BF16>(prec0) : k_decode_layer<MOEHIP_DT_BF16, -1>;
+        default: return tok ? dl_tok_x<MOEHIP_DT_F32>(prec0) : k_decode_layer<MOEHIP_DT_F32, -1>;
+    }
+}
+
+// workgroups of a kernel instance the current device holds at once (occupancy x CUs)
+static int dl_capacity(DlKernel kern, int *cap) {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess) return -1;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&k_decode_layer<DT>), 256,
-                                                     0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256, 0) !=
+        hipSuccess)
         return -1;
     *cap = per_cu * cus;
     return 0;
@@ -1291,31 +1444,30 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.info = info;
     a.miss = miss;
     a.ws = reinterpret_cast<uint32_t *>(ws);
-    a.off_rec = L.rec;
     a.off_logits = L.logits;
     a.off_h = L.h;
     a.off_part = L.part;
     a.trace = trace;
     a.stage = trace != nullptr ? trace + 3 * (size_t)(total + 3) : nullptr;
+    // the one-item kernel when the launch has one precision, no grid was requested and all its
+    // items fit on the GPU at once; otherwise the item loop over at most that many workgroups
+    DlKernel kern = nullptr;
     int cap = 0;
-    int rc = -1;
-    switch (d->dtype) {
-        case MOEHIP_DT_F16: rc = dl_capacity<MOEHIP_DT_F16>(&cap); break;
-        case MOEHIP_DT_BF16: rc = dl_capacity<MOEHIP_DT_BF16>(&cap); break;
-        default: rc = dl_capacity<MOEHIP_DT_F32>(&cap); break;
+    if (d->P == 1 && (grid <= 0 || grid >= total)) {
+        kern = dl_kernel(d->dtype, true, d->prec[0]);
+        if (kern == nullptr || dl_capacity(kern, &cap) != 0 || cap < total) kern = nullptr;
     }
-    if (rc != 0 || cap <= 0) {
-        set_error("decode_layer: occupancy query failed");
-        return MOEHIP_ELAUNCH;
+    int g = total;
+    if (kern == nullptr) {
+        kern = dl_kernel(d->dtype, false, 0);
+        if (dl_capacity(kern, &cap) != 0 || cap <= 0) {
+            set_error("decode_layer: occupancy query failed");
+            return MOEHIP_ELAUNCH;
+        }
+        g = grid > 0 ? (grid < total ? grid : total) : total;
+        if (g > cap) g = cap;  // every workgroup must fit on the GPU at once (see the kernel's header)
     }
-    int g = grid > 0 ? (grid < total ? grid : total) : total;
-    if (g > cap) g = cap;  // every workgroup must fit on the GPU at once (see the kernel's header)
-    hipStream_t st = as_stream(stream);
-    switch (d->dtype) {
-        case MOEHIP_DT_F16: hipLaunchKernelGGL((k_decode_layer<MOEHIP_DT_F16>), dim3(g), dim3(256), 0, st, a); break;
-        case MOEHIP_DT_BF16: hipLaunchKernelGGL((k_decode_layer<MOEHIP_DT_BF16>), dim3(g), dim3(256), 0, st, a); break;
-        default: hipLaunchKernelGGL((k_decode_layer<MOEHIP_DT_F32>), dim3(g), dim3(256), 0, st, a); break;
-    }
+    hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, as_stream(stream), a);
     return check_launch("decode_layer");
 }
 
