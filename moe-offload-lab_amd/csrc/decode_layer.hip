@@ -61,8 +61,11 @@ constexpr int WAIT_SPINS = 1 << 22;   // x ~0.3 us per poll: a wait gives up aft
 constexpr int NGEN = 16;
 constexpr int NSUB = 16;
 enum { W_READ = 0, W_ERR = NSUB * 32, W_TOP = NSUB * 32 + 32, W_GEN = 1024, W_HDR = W_GEN + 256 * NGEN };
-constexpr int NLC = 16;        // copies of the logits (spreads the polling over memory channels)
+constexpr int NLC = 1;         // copies of the logits
 constexpr int RT_LDS = 1024;   // record-table entries (P * E) prefetched into LDS
+constexpr int REC_SHARED = 0xFFF;  // expert field of the shared row in a routing record
+constexpr int NRC = 8;             // copies of the routing record, REC_STRIDE words apart (4 KB + 128 B:
+constexpr int REC_STRIDE = 528;    // different pages and lines, so the pollers spread over channels)
 // 64-bit words between two copies of the logits (E routed + the shared gate): a whole number of
 // 256-byte blocks plus one, so that consecutive copies start on different channels
 __host__ __device__ __forceinline__ size_t logit_stride_words(int E) { return ((size_t)(E + 1) * 8 + 255) / 256 * 32 + 32; }
@@ -90,6 +93,8 @@ struct LayerArgs {
     const void *sgate;      // (H) shared-expert gate vector or null
     int64_t srec[DL_MAXP];  // shared-expert record per precision (0 = absent)
     int NU, ND;             // up / down items
+    uint32_t defer;         // one-item kernel: down items request their weights this many real-time
+                            // ticks (10 ns) after the routing, when the gate/up weights have streamed
     moehip_policy pol;
     void *out;              // (H) activation dtype
     const void *add;        // (H) activation dtype or null
@@ -100,7 +105,7 @@ struct LayerArgs {
     float *info;            // (3, k) or null
     float *miss;            // (1) or null
     uint32_t *ws;           // workspace (zeroed once by the caller)
-    uint32_t off_logits, off_h, off_part;  // byte offsets in ws of the tagged arrays
+    uint32_t off_rec, off_logits, off_h, off_part;  // byte offsets in ws of the tagged arrays
     uint64_t *trace;        // optional per-item trace: [ticket] = (start, end, workgroup) or null
     uint64_t *stage;        // with trace: 8 stage stamps per item after the trace rows
 };
@@ -180,8 +185,28 @@ __device__ __forceinline__ T *ws_ptr(const LayerArgs &a, uint32_t off) {
 }
 
 // profiling stamp i of the current item (thread 0, trace runs only)
+// Stamps are kept in LDS and written out once at the end of the item (stamp_flush): a global
+// store per stamp would make the wave's next memory wait also wait for that store's
+// acknowledgement (vmcnt counts stores), which distorts exactly the polls being timed.
+// Slots 0-7: the item's stages; 8-15: the routing stamps of the reporting workgroup.
+__device__ __forceinline__ uint64_t *stamp_buf() {
+    __shared__ uint64_t buf[16];
+    return buf;
+}
 __device__ __forceinline__ void stamp(uint64_t *st, int i) {
-    if (st != nullptr && threadIdx.x == 0) st[i] = __builtin_amdgcn_s_memrealtime();
+    if (st != nullptr && threadIdx.x == 0) stamp_buf()[i] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void stamp_clear() {
+    if (threadIdx.x < 16) stamp_buf()[threadIdx.x] = 0;
+}
+// after a barrier: thread 0 copies the item's stamps (and the routing stamps, if any) out
+__device__ __forceinline__ void stamp_flush(uint64_t *st, uint64_t *ts) {
+    if (threadIdx.x != 0) return;
+    const uint64_t *b = stamp_buf();
+    for (int i = 0; i < 8; ++i)
+        if (st != nullptr && b[i] != 0) st[i] = b[i];
+    for (int i = 0; i < 8; ++i)
+        if (ts != nullptr && b[8 + i] != 0) ts[i] = b[8 + i];
 }
 
 // Select element i of a small argument array without dynamic indexing. The elements pass
@@ -611,18 +636,22 @@ struct DlShared {
 
 template <int XDT>
 __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, DlShared &sh, uint32_t *err, bool report,
-                            uint64_t *ts) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+                            uint64_t *ts, uint64_t *ist = nullptr, bool publish = false) {
+    // the routing wave: blockIdx % 4, so that the routing waves of the workgroups sharing a CU
+    // run on different SIMDs; the other three waves prefetch the record table
+    const int tid = threadIdx.x, rwave = (tid >> 6) - (int)(blockIdx.x & 3u), lane = tid & 63;
     const int k = a.k, E = a.E, ks = a.ks, P = a.P;
     const bool has_sh = a.sgate != nullptr;
     const bool pre = P * E <= RT_LDS;
     const int epl = (E + 63) >> 6;
     float *s_lv = sh.h;
     uint32_t *s_key = reinterpret_cast<uint32_t *>(sh.h + 1024);
-#define TS(i) do { if (ts != nullptr && lane == 0) ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-    if (wave != 0) {
-        if (pre)
-            for (int i = tid - 64; i < P * E; i += 192) sh.rt[i] = a.rtab[i];
+#define TS(i) do { if (ts != nullptr && lane == 0) stamp_buf()[8 + (i)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+    if (rwave != 0) {
+        if (pre) {
+            const int o = (tid + 256 - 64 * (int)(blockIdx.x & 3u)) & 255;  // 64 .. 255 in the other waves
+            for (int i = o - 64; i < P * E; i += 192) sh.rt[i] = a.rtab[i];
+        }
     } else {
         TS(0);
         if (a.Wr != nullptr || has_sh) {
@@ -648,7 +677,6 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                         const float l = __uint_as_float((uint32_t)v[i]);
                         s_lv[c] = l;
                         s_key[c] = logit_key<XDT>(l, c);
-                        if (report && a.logits_out != nullptr) st_act<XDT>(a.logits_out, c, l);
                         need &= ~(1u << i);
                     }
                 }
@@ -667,33 +695,56 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                     }
                 }
             if (need >> 31) sh.gl = -INFINITY;  // gate weight 0
+            if (a.Wr != nullptr && E <= 64)
+                for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
         }
+        if (ist != nullptr && lane == 0) stamp_buf()[6] = __builtin_amdgcn_s_memrealtime();
     }
     __syncthreads();
-    if (wave == 0) {
+    // E <= 64 with 16-bit logits (distinct keys below 2^26): every wave counts, for each lane's
+    // key, the larger keys among its 16 ((key - other) >> 31 is 1 exactly when other > key);
+    // the routing wave adds the four counts up
+    int *s_prt = reinterpret_cast<int *>(sh.h + 256);
+    const bool rank4 = XDT != MOEHIP_DT_F32 && a.Wr != nullptr && E <= 64;
+    if (rank4) {
+        const int wv = tid >> 6;
+        const uint32_t key = lane < E ? s_key[lane] : 0u;
+        uint32_t part = 0;
+#pragma unroll
+        for (int q = 0; q < 16; q += 4) {
+            const uint4 o = *reinterpret_cast<const uint4 *>(s_key + 16 * wv + q);
+            part += ((key - o.x) >> 31) + ((key - o.y) >> 31) + ((key - o.z) >> 31) + ((key - o.w) >> 31);
+        }
+        s_prt[wv * 64 + lane] = (int)part;
+        __syncthreads();
+    }
+    if (rwave == 0) {
         TS(1);
         int myc = 0;      // lane j < k: expert of rank j
         float myw = 0.f;  // and its fp32 weight (rounded to the activation dtype)
+        float myp = 0.f;  // (its weight before the rounding, for w_out)
         int64_t rt[DL_MAXP] = {0, 0, 0, 0};  // and the addresses of its resident records
         if (a.Wr != nullptr) {
             float myv = 0.f;
             if (E <= 64) {
                 // one logit per lane: its rank is the number of larger keys (keys are distinct for
                 // 16-bit logits; fp32 ties go to the lower index)
-                for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
-                __builtin_amdgcn_wave_barrier();
                 const uint32_t key = lane < E ? s_key[lane] : 0u;
                 const float lvv = lane < E ? s_lv[lane] : -INFINITY;
                 int rank = 0;
+                if (rank4) {
+                    rank = s_prt[lane] + s_prt[64 + lane] + s_prt[128 + lane] + s_prt[192 + lane];
+                } else {
 #pragma unroll
-                for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS broadcast);
-                                                   // keys past E are 0 and never count
-                    const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
-                    const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
+                    for (int q = 0; q < 64; q += 4) {  // every lane reads the same 4 keys (LDS
+                                                       // broadcast); keys past E are 0, never counted
+                        const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q);
+                        const uint32_t ov[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
-                        else rank += ov[u] > key;
+                        for (int u = 0; u < 4; ++u) {
+                            if constexpr (XDT == MOEHIP_DT_F32) rank += (ov[u] > key) || (ov[u] == key && q + u < lane);
+                            else rank += ov[u] > key;
+                        }
                     }
                 }
                 if (lane < E && rank < k) {
@@ -748,13 +799,8 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
             const float p = lane < k ? expf(myv - m) / sum : 0.f;
             const float tot = a.renorm ? wave_sum(p) : 1.f;
             if (lane < k) {
-                const float pw = a.renorm ? p / tot : p;
-                myw = rnd_act<XDT>(pw);
-                if (report) {
-                    if (a.idx_out) a.idx_out[lane] = myc;
-                    if (a.w_out) st_act<XDT>(a.w_out, lane, pw);
-                    if (a.w32_out) a.w32_out[lane] = myw;
-                }
+                myp = a.renorm ? p / tot : p;
+                myw = rnd_act<XDT>(myp);
             }
         } else if (lane < k) {
             myc = (int)a.idx_in[lane];
@@ -840,37 +886,142 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                 sh.rw[pi * ks + j] = mine ? myw : 0.f;
                 sh.rb[pi * ks + j] = mine ? (uint64_t)base : 0ull;
             }
-            if (report && a.info && act) {
+        }
+        if (publish && row) {
+            // the routing record of a single-precision launch (route_fetch): valid bit, expert
+            // (REC_SHARED for the shared row) and the weight's bits in the activation dtype
+            const uint32_t wb = XDT == MOEHIP_DT_F16 ? (uint32_t)f32_to_f16_rne(myw) : (__float_as_uint(myw) >> 16);
+            const uint32_t pay = (sel ? 0x80000000u : 0u) | ((uint32_t)(shr ? REC_SHARED : e) << 16) | (sel ? wb : 0u);
+            for (int c = 0; c < NRC; ++c) st_tag(ws_ptr<uint64_t>(a, a.off_rec) + (size_t)c * REC_STRIDE + j, pay, tag);
+        }
+        // the readouts, after the record: a store makes the wave's next memory wait also wait for
+        // the store's acknowledgement, so none may precede the polls and the record
+        const unsigned long long bal = __ballot(is_miss);
+        if (report) {
+            if (a.logits_out != nullptr && a.Wr != nullptr)
+                for (int c = lane; c < E; c += 64) st_act<XDT>(a.logits_out, c, s_lv[c]);
+            if (act && a.Wr != nullptr) {
+                if (a.idx_out) a.idx_out[j] = myc;
+                if (a.w_out) st_act<XDT>(a.w_out, j, myp);
+                if (a.w32_out) a.w32_out[j] = myw;
+            }
+            if (a.info && act) {
                 a.info[j] = (float)e;
                 a.info[k + j] = skip ? -2.f : (float)chosen;
                 a.info[2 * k + j] = (float)lvl;
             }
+            if (j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
         }
-        const unsigned long long bal = __ballot(is_miss);
-        if (report && j == 0 && a.miss != nullptr) a.miss[0] += (float)__popcll(bal);
         if (j == 0) sh.routed = 1;
         TS(5);
+        if (ist != nullptr && lane == 0) stamp_buf()[7] = __builtin_amdgcn_s_memrealtime();
     }
     __syncthreads();
 #undef TS
+}
+
+// this workgroup holds its launch tag: count it in reader counter blockIdx % NSUB (a wave
+// other than wave 0, which routes; no return value)
+__device__ __forceinline__ void gen_read_done(uint32_t *ws) {
+    if (threadIdx.x == 192)
+        __hip_atomic_fetch_add(ws + W_READ + 32 * (blockIdx.x % NSUB), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// router item r of NR: wait until the reader counters q = r, r + NR, ... hold every workgroup of
+// the grid that counts there, clear them, and count them drained; the last drained counter
+// advances the launch generation (every workgroup of the launch has read it by then). Bounded:
+// on expiry the error flag is set and the generation is advanced all the same (a tag must never
+// be reused).
+__device__ __forceinline__ void gen_manage(uint32_t *ws, int r, int NR, uint32_t tag) {
+    const int q = threadIdx.x;
+    const int G = gridDim.x;
+    if (q >= NSUB || q >= G || q % NR != r) return;
+    const uint32_t nq = (uint32_t)((G - q + NSUB - 1) / NSUB);
+    int nap = 1;
+    for (int it = 0; it < WAIT_SPINS; ++it) {
+        if (ld_co32(ws + W_READ + 32 * q) >= nq) break;
+        backoff(nap);
+        if (it == WAIT_SPINS - 1) flag_error(ws + W_ERR);
+    }
+    st_co32(ws + W_READ + 32 * q, 0u);
+    const uint32_t used = (uint32_t)min(G, NSUB);
+    if (add_co32(ws + W_TOP, 1u) == used - 1u) {
+        const uint32_t gen = tag - 1u, next = gen + 1u == 0xFFFFFFFFu ? 0u : gen + 1u;
+        st_co32(ws + W_TOP, 0u);
+        for (int c = 0; c < NGEN; ++c) st_co32(ws + W_GEN + 256 * c, next);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// routing of a single-precision launch as published by the gathering workgroup (route_local
+// with publish): wave blockIdx % 4 polls the ks record words, the other waves prefetch the
+// record table into LDS, and each table row's weight and record address land in s_rw / s_rb.
+// On expiry a row counts as not routed (weight 0) and the error flag is set.
+// ---------------------------------------------------------------------------------------
+template <int XDT>
+__device__ __forceinline__ void route_fetch(const LayerArgs &a, uint32_t tag, DlShared &sh, uint32_t *err,
+                                            uint64_t *ist) {
+    const int tid = threadIdx.x, rwave = (tid >> 6) - (int)(blockIdx.x & 3u), lane = tid & 63;
+    const int E = a.E, ks = a.ks;
+    const bool pre = E <= RT_LDS;
+    if (rwave != 0) {
+        if (pre) {
+            const int o = (tid + 256 - 64 * (int)(blockIdx.x & 3u)) & 255;  // 64 .. 255 in the other waves
+            for (int i = o - 64; i < E; i += 192) sh.rt[i] = a.rtab[i];
+        }
+    } else {
+        const uint64_t *rec = ws_ptr<uint64_t>(a, a.off_rec) + (size_t)(blockIdx.x % NRC) * REC_STRIDE;
+        bool need = lane < ks;
+        uint32_t pay = 0;
+        int nap = 1;
+        for (int it = 0; it < WAIT_SPINS; ++it) {
+            if (need) {
+                const uint64_t v = ld_tag(rec + lane);
+                if (tag_ok(v, tag)) {
+                    pay = (uint32_t)v;
+                    need = false;
+                }
+            }
+            if (__ballot(need) == 0ull) break;
+            backoff(nap, 8);  // the record is microseconds away: poll gently
+            if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
+        }
+        if (lane < ks) sh.idx[lane] = (int)(need ? 0u : pay);
+        if (ist != nullptr && lane == 0) stamp_buf()[6] = __builtin_amdgcn_s_memrealtime();
+    }
+    __syncthreads();
+    if (rwave == 0) {
+        if (lane < ks) {
+            const uint32_t pay = (uint32_t)sh.idx[lane];
+            const int e = (int)((pay >> 16) & 0xFFFu);
+            const bool valid = (pay >> 31) != 0u && (e == REC_SHARED || e < E);
+            const float w = XDT == MOEHIP_DT_F16 ? f16_to_f32(pay & 0xFFFFu) : bf16_to_f32(pay & 0xFFFFu);
+            const int64_t base = !valid ? 0 : (e == REC_SHARED ? a.srec[0] : (pre ? sh.rt[e] : a.rtab[e]));
+            sh.rw[lane] = base != 0 ? w : 0.f;
+            sh.rb[lane] = (uint64_t)base;
+        }
+        if (lane == 0) sh.routed = 1;
+        if (ist != nullptr && lane == 0) stamp_buf()[7] = __builtin_amdgcn_s_memrealtime();
+    }
+    __syncthreads();
+    gen_read_done(a.ws);  // after the routing exchange, whose words it would otherwise queue with
 }
 
 // ---------------------------------------------------------------------------------------
 // router item: 4 expert rows (one per wave), each lane 32 consecutive values (H <= 2048)
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t tag) {
+__device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t tag, uint64_t *st, DlShared &sh) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     // rows: the E router rows (with Wr), then the shared-expert gate as row E (with sgate)
     const int r = t * 4 + wave;
     const int nrows = (a.Wr != nullptr ? a.E : 0) + (a.sgate != nullptr ? 1 : 0);
-    if (r >= nrows) return;
-    const int e = a.Wr != nullptr ? r : a.E;
+    const int e = a.Wr != nullptr ? r : a.E;  // logit index of this wave's row
     constexpr int ESZ = XDT == MOEHIP_DT_F32 ? 4 : 2;
     constexpr int NV = 32 * ESZ / 16;  // 16-byte vectors per lane
     const int c0 = lane * 32;
     float acc = 0.f;
-    if (c0 < a.H) {
+    if (r < nrows && c0 < a.H) {
         const uint8_t *wp = e < a.E ? reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)e * a.H + c0) * ESZ
                                     : reinterpret_cast<const uint8_t *>(a.sgate) + (size_t)c0 * ESZ;
         const uint8_t *xp = reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * ESZ;
@@ -899,10 +1050,20 @@ __device__ __forceinline__ void router_rows(const LayerArgs &a, int t, uint32_t 
         }
     }
     acc = wave_sum(acc);
-    // one copy per lane: lanes 0 .. NLC-1 store the same tagged logit into their copy
-    if (lane < NLC)
-        st_tag(ws_ptr<uint64_t>(a, a.off_logits) + (size_t)lane * logit_stride_words(a.E) + e,
-               __float_as_uint(rnd_act<XDT>(acc)), tag);
+    if (lane == 0) sh.wk[wave] = rnd_act<XDT>(acc);
+    stamp(st, 0);
+    __syncthreads();
+    // the item's (up to) 4 logits leave in ONE coalesced store (lanes 0..3 of wave 0): fewer
+    // partial-line writes to the lines every poller reads. The shared gate (row E) is the last
+    // router row, so its item holds no routed row after it.
+    const int rr = t * 4 + lane;
+    if (wave == 0 && lane < 4 && rr < nrows) {
+        const int ee = a.Wr != nullptr ? rr : a.E;
+        uint64_t *lg = ws_ptr<uint64_t>(a, a.off_logits);
+        for (int c = 0; c < NLC; ++c)
+            st_tag(lg + (size_t)c * logit_stride_words(a.E) + ee, __float_as_uint(sh.wk[lane]), tag);
+    }
+    stamp(st, 1);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -925,7 +1086,7 @@ __device__ __forceinline__ Route wg_route(const LayerArgs &a, uint32_t tag, int 
     return r;
 }
 
-// LAZY: this workgroup computes the routing here, after requesting x (one-item workgroups)
+// LAZY: this workgroup fetches the published routing here, after requesting x (one-item kernel)
 template <int PREC, int XDT, bool LAZY>
 __device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi, int jj, int b, DlShared &sh,
                                         uint32_t *err, int item) {
@@ -937,7 +1098,7 @@ __device__ __forceinline__ void up_item(const LayerArgs &a, uint32_t tag, int pi
     uint64_t *st = a.stage != nullptr ? a.stage + 8 * (size_t)item : nullptr;
     load_x<PREC, XDT>(a.x, lane & (G - 1), G, C, lv);  // before the routing wait
     stamp(st, 0);
-    if (LAZY) route_local<XDT>(a, tag, sh, err, false, nullptr);
+    if (LAZY) route_fetch<XDT>(a, tag, sh, err, st);
     const Route rt = wg_route<XDT>(a, tag, jj, sh, err);
     stamp(st, 1);
     if (rt.w == 0.f) return;
@@ -992,7 +1153,14 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     const int per_wave = DlFmt<PREC>::NPD * RPW;
     const int row0 = b * per_wave * 4 + wave * per_wave;
     const int PK = a.P * a.ks;
-    if (LAZY) route_local<XDT>(a, tag, sh, err, false, nullptr);
+    if (LAZY) {
+        route_fetch<XDT>(a, tag, sh, err, st);
+        // the gate/up weights first: requested together with these, they would share the HBM
+        // with weights that cannot be used before h exists anyway
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        const uint32_t defer = (uint32_t)uni((int)a.defer);
+        while (__builtin_amdgcn_s_memrealtime() - t0 < defer) __builtin_amdgcn_s_sleep(10);
+    }
     const Route rt0 = wg_route<XDT>(a, tag, jj, sh, err);
     stamp(st, 1);
     const bool run = rt0.w != 0.f;
@@ -1002,10 +1170,10 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
         down_load<PREC>(gbytes(rt0.base + pick_off(a.offs, pi, 2)), gbytes(rt0.base + pick_off(a.offs, pi, 3)), row0,
                         a.H, a.I,
                         pick4(a.gs_dn, pi), lg, d);
-        if (st != nullptr) {
-            __builtin_amdgcn_s_waitcnt(0);
-            stamp(st, 2);
-        }
+        // h is polled only once this wave's weights are in registers: polling earlier would
+        // compete with the weight stream and cannot let the rows start any sooner
+        __builtin_amdgcn_s_waitcnt(0);
+        stamp(st, 2);
         if (stage_h<DlFmt<PREC>::VPC>(ws_ptr<uint64_t>(a, a.off_h) + (size_t)jj * a.I, a.I, tag, sh.h, err)) {
             stamp(st, 3);
             LaneVec<PREC, XDT> lv;
@@ -1084,38 +1252,6 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
     __syncthreads();  // sh.h is reused by the next item
 }
 
-// this workgroup holds its launch tag: count it in reader counter blockIdx % NSUB (a wave
-// other than wave 0, which routes; no return value)
-__device__ __forceinline__ void gen_read_done(uint32_t *ws) {
-    if (threadIdx.x == 192)
-        __hip_atomic_fetch_add(ws + W_READ + 32 * (blockIdx.x % NSUB), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// router item r of NR: wait until the reader counters q = r, r + NR, ... hold every workgroup of
-// the grid that counts there, clear them, and count them drained; the last drained counter
-// advances the launch generation (every workgroup of the launch has read it by then). Bounded:
-// on expiry the error flag is set and the generation is advanced all the same (a tag must never
-// be reused).
-__device__ __forceinline__ void gen_manage(uint32_t *ws, int r, int NR, uint32_t tag) {
-    const int q = threadIdx.x;
-    const int G = gridDim.x;
-    if (q >= NSUB || q >= G || q % NR != r) return;
-    const uint32_t nq = (uint32_t)((G - q + NSUB - 1) / NSUB);
-    int nap = 1;
-    for (int it = 0; it < WAIT_SPINS; ++it) {
-        if (ld_co32(ws + W_READ + 32 * q) >= nq) break;
-        backoff(nap);
-        if (it == WAIT_SPINS - 1) flag_error(ws + W_ERR);
-    }
-    st_co32(ws + W_READ + 32 * q, 0u);
-    const uint32_t used = (uint32_t)min(G, NSUB);
-    if (add_co32(ws + W_TOP, 1u) == used - 1u) {
-        const uint32_t gen = tag - 1u, next = gen + 1u == 0xFFFFFFFFu ? 0u : gen + 1u;
-        st_co32(ws + W_TOP, 0u);
-        for (int c = 0; c < NGEN; ++c) st_co32(ws + W_GEN + 256 * c, next);
-    }
-}
-
 // work items of the router stage: 4 rows each (E router rows, + the shared gate row); at least
 // one, which also runs the route tail
 __host__ __device__ __forceinline__ int router_items(bool with_router, bool shared, int E) {
@@ -1151,11 +1287,15 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
     for (int t = blockIdx.x; t < total; t += gridDim.x) {
         __syncthreads();  // LDS of the previous item is free
         uint64_t t_start = 0;
-        if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
+        if (a.trace != nullptr) {
+            stamp_clear();
+            __syncthreads();
+            if (tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
+        }
         if (t < NR) {
             // ---------------- router rows; the last router item also reports the routing ----------------
-            if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag);
-            if (t == NR - 1) route_local<XDT>(a, tag, sh, err, true, a.trace ? a.trace + 3 * total : nullptr);
+            if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag, a.stage != nullptr ? a.stage + 8 * (size_t)t : nullptr, sh);
+            if (t == NR - 1) route_local<XDT>(a, tag, sh, err, true, a.trace ? a.stage + 8 * (size_t)total : nullptr);
             gen_manage(ws, t, NR, tag);
         } else if (t < NR + a.NU) {
             if (!sh.routed) route_local<XDT>(a, tag, sh, err, false, nullptr);
@@ -1196,10 +1336,14 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
                 }
             }
         }
-        if (a.trace != nullptr && tid == 0) {
-            a.trace[3 * t + 0] = t_start;
-            a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
-            a.trace[3 * t + 2] = blockIdx.x;
+        if (a.trace != nullptr) {
+            __syncthreads();
+            stamp_flush(a.stage + 8 * (size_t)t, t == NR - 1 ? a.stage + 8 * (size_t)total : nullptr);
+            if (tid == 0) {
+                a.trace[3 * t + 0] = t_start;
+                a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
+                a.trace[3 * t + 2] = blockIdx.x;
+            }
         }
     }
 }
@@ -1237,14 +1381,19 @@ __global__ __launch_bounds__(256) void k_decode_tok(LayerArgs) {
     }
     __syncthreads();
     const uint32_t tag = uni((int)sh.tag);
-    gen_read_done(kargs().ws);
     const int t = blockIdx.x;
     uint64_t t_start = 0;
+    if (kargs().trace != nullptr) {
+        stamp_clear();
+        __syncthreads();
+    }
     if (t < NR) {
         const LayerArgs &a = kargs();
         if (a.trace != nullptr && tid == 0) t_start = __builtin_amdgcn_s_memrealtime();
-        if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag);
-        if (t == NR - 1) route_local<XDT>(a, tag, sh, a.ws + W_ERR, true, a.trace ? a.trace + 3 * total : nullptr);
+        if (a.Wr != nullptr || a.sgate != nullptr) router_rows<XDT>(a, t, tag, a.stage != nullptr ? a.stage + 8 * (size_t)t : nullptr, sh);
+        if (t == NR - 1)
+            route_local<XDT>(a, tag, sh, a.ws + W_ERR, true, a.trace ? a.stage + 8 * (size_t)total : nullptr, nullptr, true);
+        gen_read_done(a.ws);
         gen_manage(a.ws, t, NR, tag);
     } else if (t < NR + NU) {
         const LayerArgs &a = kargs();
@@ -1260,10 +1409,14 @@ __global__ __launch_bounds__(256) void k_decode_tok(LayerArgs) {
         down_item<PR, XDT, true>(a, tag, 0, dd / ndb, dd % ndb, sh, a.ws + W_ERR, t);
     }
     const LayerArgs &a = kargs();
-    if (a.trace != nullptr && tid == 0) {
-        a.trace[3 * t + 0] = t_start;
-        a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
-        a.trace[3 * t + 2] = blockIdx.x;
+    if (a.trace != nullptr) {
+        __syncthreads();
+        stamp_flush(a.stage + 8 * (size_t)t, t == NR - 1 ? a.stage + 8 * (size_t)total : nullptr);
+        if (tid == 0) {
+            a.trace[3 * t + 0] = t_start;
+            a.trace[3 * t + 1] = __builtin_amdgcn_s_memrealtime();
+            a.trace[3 * t + 2] = blockIdx.x;
+        }
     }
 }
 
@@ -1281,7 +1434,7 @@ static inline int lg_for(int cols, int prec) {
 static inline int up_item_pairs(int prec, int lg) { return (4 / cpl_host(prec)) * (64 >> lg) * 4; }
 
 struct DlLayout {
-    uint32_t logits, h, part, total;
+    uint32_t rec, logits, h, part, total;
 };
 
 static inline uint32_t al256(size_t v) { return (uint32_t)((v + 255) / 256 * 256); }
@@ -1291,6 +1444,9 @@ static DlLayout dl_layout(int P, int k, int E, int H, int I) {
     const int PK = P * k;
     size_t off = W_HDR * 4;
     off = al256(off);
+    L.rec = (uint32_t)off;  // the routing record: one tagged word per table row, NRC copies
+    off += ((size_t)(NRC - 1) * REC_STRIDE + PK) * 8;
+    off = al256(off) + 4096;  // the logits on other pages than the record copies
     L.logits = (uint32_t)off;
     off += (size_t)NLC * logit_stride_words(E) * 8;  // E routed + the shared-expert gate, NLC copies
     off = al256(off);
@@ -1329,7 +1485,8 @@ static int dl_plan(const moehip_layer_desc *d, int with_router, LayerArgs *a) {
 }
 
 // the kernel instances of a launch: the one-item kernel of its precision (single-precision
-// launches), and the item-loop kernel (any mix, or more items than the GPU holds at once)
+// launches with 16-bit activations), and the item-loop kernel (any mix, fp32 activations, or
+// more items than the GPU holds at once)
 typedef void (*DlKernel)(LayerArgs);
 template <int XDT>
 static DlKernel dl_tok_x(int prec0) {
@@ -1346,7 +1503,7 @@ static DlKernel dl_kernel(int dtype, bool tok, int prec0) {
     switch (dtype) {
         case MOEHIP_DT_F16: return tok ? dl_tok_x<MOEHIP_DT_F16>(prec0) : k_decode_layer<MOEHIP_DT_F16, -1>;
         case MOEHIP_DT_BF16: return tok ? dl_tok_x<MOEHIP_DT_BF16>(prec0) : k_decode_layer<MOEHIP_DT_BF16, -1>;
-        default: return tok ? dl_tok_x<MOEHIP_DT_F32>(prec0) : k_decode_layer<MOEHIP_DT_F32, -1>;
+        default: return k_decode_layer<MOEHIP_DT_F32, -1>;  // (the routing record holds 16-bit weights)
     }
 }
 
@@ -1423,6 +1580,12 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
         a.planned[p] = on ? d->planned[p] : 0;
     }
     const int total = dl_plan(d, Wr != nullptr, &a);
+    {
+        // the time the HBM needs for the k routed gate/up blocks (q + scales) at 8 TB/s, in 10 ns
+        // ticks: single-precision launches only (one record kind)
+        const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
+        a.defer = d->P == 1 ? (uint32_t)(d->k * gu / 8.0e12 * 1.0e8) : 0u;
+    }
     for (int i = 0; i < 3; ++i) a.lv2p[i] = d->lv2p[i];
     a.P = d->P;
     a.E = d->E;
@@ -1444,6 +1607,7 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     a.info = info;
     a.miss = miss;
     a.ws = reinterpret_cast<uint32_t *>(ws);
+    a.off_rec = L.rec;
     a.off_logits = L.logits;
     a.off_h = L.h;
     a.off_part = L.part;
