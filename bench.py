@@ -18,7 +18,7 @@ live with HIP events on the stream it runs on, over launches that rotate through
 layers.
 
 HBM traffic per launch (roofline.traffic) is read from the committed rocprofv3 counter summary
-profiles/k_decode_layer_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
+profiles/k_decode_tok_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
 same counters on a plain copy of known size, `--copy-calibration`); null when that file is absent.
 
 CPU baseline: the oracle's restatement of moelab's CPU expert branch (dequantise to fp32,
@@ -45,7 +45,7 @@ sys.path.insert(0, str(ROOT / "moe-offload-lab_amd"))
 
 H, I, E, K_TOP, L = 2048, 1024, 64, 8, 16
 HBM_PEAK_GBS = 8000.0
-PROFILE = ROOT / "profiles" / "k_decode_layer_olmoe_int4_bs1.md"
+PROFILE = ROOT / "profiles" / "k_decode_tok_olmoe_int4_bs1.md"
 
 
 def measured_traffic():
@@ -530,7 +530,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "k_decode_layer<f16> (router + HOBBIT table + 8 int4 experts + combine, one launch)",
+            "kernel": "k_decode_tok<f16, int4> (router + HOBBIT table + 8 int4 experts + combine, one launch)",
             "bytes_per_launch": r["kernel_bytes"],
         },
         "cpu_baseline": cpu,
