@@ -264,6 +264,131 @@ def prefill_line(args):
     }
 
 
+# More decode configurations through the same fused kernel (their own JSON lines): the OLMoE stack
+# with two record precisions per expert (a weight-threshold precision rule), and the Qwen3-30B-A3B /
+# Qwen3-Next-80B-A3B layer shapes at batch 1.
+DECODE_SPECS = {
+    "olmoe-mixed-decode": dict(H=2048, I=1024, E=64, k=8, L=16, precs=["fp16", "int4"], dtype="float16",
+                               renorm=False, shared=False, policy=("weight", 0.15),
+                               desc="OLMoE-shaped 16-layer MoE stack, decode bs=1, each routed expert in fp16 "
+                                    "if its gate weight >= 0.15, else int4 gs64; fp16 and int4 records of "
+                                    "every expert resident"),
+    "qwen3-30b-decode": dict(H=2048, I=768, E=128, k=8, L=8, precs=["int4"], dtype="bfloat16", renorm=True,
+                             shared=False, policy=("lo",),
+                             desc="Qwen3-30B-A3B-shaped MoE layer, decode bs=1, int4 gs64 experts, 8 layers "
+                                  "rotated"),
+    "qwen3-next-decode-int4": dict(H=2048, I=512, E=512, k=10, L=8, precs=["int4"], dtype="bfloat16",
+                                   renorm=True, shared=True, policy=("lo",),
+                                   desc="Qwen3-Next-80B-A3B-shaped MoE layer, decode bs=1, 512 int4 gs64 experts "
+                                        "top-10 + sigmoid-gated shared expert, 8 layers rotated"),
+    "qwen3-next-decode-fp8": dict(H=2048, I=512, E=512, k=10, L=8, precs=["fp8"], dtype="bfloat16",
+                                  renorm=True, shared=True, policy=("lo",),
+                                  desc="Qwen3-Next-80B-A3B-shaped MoE layer, decode bs=1, 512 FP8 e4m3 experts "
+                                       "(128x128 block scales) top-10 + sigmoid-gated shared expert, 8 layers "
+                                       "rotated"),
+}
+
+
+def decode_line(args, name):
+    """One decode configuration: a HIP graph per token over L layers (fused kernel), 16 tokens;
+    algorithmic bytes per launch = the records the launch ran (from the kernel's per-row readout)
+    + router + shared gate + x/out."""
+    import torch
+
+    from moelab_hip import _lib
+    from moelab_hip.layer import MoEDecoder, ResidentStore
+    from moelab_hip.policy import PrecisionPolicy
+    from moelab_hip.store import encode_record_, record_layout
+
+    sp = DECODE_SPECS[name]
+    dev = torch.device("cuda:0")
+    _lib.check_device(dev)
+    H_, I_, E_, k_, L_ = sp["H"], sp["I"], sp["E"], sp["k"], sp["L"]
+    dt = getattr(torch, sp["dtype"])
+    g = torch.Generator(device=dev).manual_seed(0)
+    lays = {p: record_layout(p, H_, I_, 64, scale="absmax" if p in ("int4", "int8") else None) for p in sp["precs"]}
+    store = ResidentStore(lays, L_, E_, dev)
+    t0 = time.time()
+    store.fill_synthetic(g, std=0.02)
+    torch.cuda.synchronize()
+    log(f"[bench] {name}: {store.bytes_resident / 1e9:.2f} GB of records encoded in {time.time() - t0:.1f} s")
+    Wr = [(torch.randn(E_, H_, device=dev, generator=g) * 0.02).to(dt) for _ in range(L_)]
+    shared = None
+    if sp["shared"]:
+        shared = []
+        for _ in range(L_):
+            rec = {}
+            for p, lay in lays.items():
+                blob = torch.zeros(lay["record_bytes"], dtype=torch.uint8, device=dev)
+                encode_record_(lay, blob, torch.randn(2 * I_, H_, device=dev, generator=g) * 0.02,
+                               torch.randn(H_, I_, device=dev, generator=g) * 0.02)
+                rec[p] = blob
+            shared.append({"gate": (torch.randn(H_, device=dev, generator=g) * 0.05).to(dt), "rec": rec})
+    # upgrade=False: a level-2 request runs the int4 record even though the fp16 one is resident
+    pol = (PrecisionPolicy(sp["policy"][0], t1=sp["policy"][1], upgrade=False) if len(sp["policy"]) > 1
+           else PrecisionPolicy(sp["policy"][0]))
+    dec = MoEDecoder(store, k_, pol, dt, router_weights=Wr, renorm=sp["renorm"], shared=shared)
+    S = 16
+    xs = torch.randn(S, L_, 1, H_, device=dev, generator=g).to(dt)
+    outs = torch.zeros(S, L_, 1, H_, dtype=dt, device=dev)
+    # bytes each launch ran: one eager pass, reading the per-row readout after every layer
+    precs = store.precisions
+    run_bytes = 0
+    for s_ in range(S):
+        for l in range(L_):
+            dec.layer(l, xs[s_, l], outs[s_, l])
+            info = dec.info[l].cpu()
+            for j in range(k_):
+                c = int(info[1, j])
+                if c >= 0:
+                    run_bytes += lays[precs[c]]["record_bytes"]
+    if sp["shared"]:
+        run_bytes += S * L_ * lays[precs[0]]["record_bytes"]
+    alg = run_bytes / (S * L_) + E_ * H_ * 2 + (H_ * 2 if sp["shared"] else 0) + 2 * H_ * 2
+    if dec.miss.item() != 0:
+        raise RuntimeError("experts missing from the resident store")
+
+    def token(s_):
+        for l in range(L_):
+            dec.layer(l, xs[s_, l], outs[s_, l])
+
+    graphs = []
+    for s_ in range(S):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            token(s_)
+        graphs.append(gr)
+    for i in range(max(S, args.warmup // 4)):
+        graphs[i % S].replay()
+    torch.cuda.synchronize()
+    steps = max(S, args.steps // 4)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        graphs[i % S].replay()
+    b.record()
+    torch.cuda.synchronize()
+    dec.check_error()
+    ms = a.elapsed_time(b) / steps
+    layer_us = ms * 1000 / L_
+    gbs = alg / (layer_us * 1e-6) / 1e9
+    log(f"[bench] {name}: {layer_us:.2f} us per layer, {alg / 1e6:.2f} MB per launch, {gbs:.0f} GB/s")
+    return {
+        "metric": f"MoE-layer decode tok/s + % HBM roofline, {name}, bs=1, 1 GPU",
+        "value": round(1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": max(S, args.warmup // 4),
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "+".join(sp["precs"]), "data": "synthetic",
+        "config": {"workload": sp["desc"], "d_model": H_, "experts": E_, "top_k": k_, "d_ff": I_, "layers": L_,
+                   "batch": 1, "activations": sp["dtype"], "shared_expert": sp["shared"]},
+        "layer_us": round(layer_us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "fused decode layer (one launch per layer, HIP graph per token)",
+                     "bytes_per_launch": int(alg)},
+        "cpu_baseline": None,
+    }
+
+
 # Qwen3-Next-80B-A3B-shaped offloaded decode
 NH, NI, NE, NK = 2048, 512, 512, 10
 
@@ -480,7 +605,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
-    ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload"],
+    ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload",
+                                           *DECODE_SPECS],
                     default="olmoe-decode-bs1")
     ap.add_argument("--offload-layers", type=int, default=48)
     ap.add_argument("--offload-steps", type=int, default=256)
@@ -501,6 +627,9 @@ def main():
         return
     if args.workload == "qwen3-next-offload":
         print(json.dumps(offload_line(args)), flush=True)
+        return
+    if args.workload in DECODE_SPECS:
+        print(json.dumps(decode_line(args, args.workload)), flush=True)
         return
     r = gpu_bench(args)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)

@@ -113,8 +113,12 @@ int moehip_router_topk(const void *x, const void *Wr, int T, int H, int E, int k
 
 /* HOBBIT policy parameters (moelab/policy.py:50-58); t_mid/t2 < 0 mean "None". */
 typedef struct moehip_policy {
-    int mode;   /* 0 = hobbit, 1 = hi, 2 = lo */
-    float t1;    /* t1_for(layer) + 1e-6 rounded to fp32 (the slack of policy.py:120-122) */
+    int mode;   /* 0 = hobbit, 1 = hi, 2 = lo, 3 = weight threshold (see t1) */
+    float t1;    /* t1_for(layer) + 1e-6 rounded to fp32 (the slack of policy.py:120-122); for mode 3
+                  * the threshold itself: level 0 when an expert's routed weight (fp32, as rounded to
+                  * the activation dtype) is >= t1, else level 2. Mode 3 has no counterpart in
+                  * moelab's policy.py: it is the benchmark configurations' per-expert precision rule
+                  * ("fp16 if the gate weight is >= 0.15, else int4"). */
     float t_mid; /* t_mid + 1e-6, or < 0 */
     float t2;    /* t2 + 1e-6, or < 0 */
     int protect; /* 1 if the layer is protected (level 0) */

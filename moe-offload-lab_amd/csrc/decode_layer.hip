@@ -843,6 +843,8 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
             lvl = 0;
         } else if (pol.mode == 2) {
             lvl = 2;
+        } else if (pol.mode == 3) {
+            lvl = wj >= pol.t1 ? 0 : 2;  // weight threshold: the expert's own routed weight
         } else {
             const float wn = wj / tot;
             int rank = 0;

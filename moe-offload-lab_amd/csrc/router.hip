@@ -177,6 +177,8 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
         lvl = 0;
     } else if (pol.mode == 2) {
         lvl = 2;
+    } else if (pol.mode == 3) {
+        lvl = wj >= pol.t1 ? 0 : 2;  // weight threshold: the expert's own routed weight
     } else {
         // unimportance (policy.py:77-87): stable descending rank, s = cumsum(sorted) - own weight
         const float wn = wj / s_total;

@@ -15,12 +15,14 @@ import torch
 
 from ._lib import Policy
 
-MODES = ("hi", "lo", "hobbit")
+MODES = ("hi", "lo", "hobbit", "weight")
 
 
 @dataclass
 class PrecisionPolicy:
-    """policy.py:20-58."""
+    """policy.py:20-58. mode "weight" (not in moelab) is the benchmark configurations' rule: an
+    expert is served at level 0 (the most precise record) when its own routed weight is >= t1, else
+    at level 2; no skipping."""
 
     mode: str = "hobbit"
     t1: float = 0.6
@@ -80,6 +82,9 @@ class PrecisionPolicy:
         fixed = self._fixed(layer)
         if fixed is not None:
             return torch.full((T, k), fixed, dtype=torch.int8), none
+        if self.mode == "weight":  # level 0 when the expert's own weight reaches t1 (no skip)
+            w = weights.cpu().float()
+            return torch.where(w >= self.t1, 0, 2).to(torch.int8), none
         s = self.unimportance(weights.cpu())
         lvl = torch.full((T, k), 2, dtype=torch.int8)
         if self.t_mid is not None:
@@ -94,6 +99,9 @@ class PrecisionPolicy:
         fixed = self._fixed(layer)
         if fixed is not None:
             return [fixed] * k, [False] * k, [0.0] * k
+        if self.mode == "weight":
+            f32 = lambda v: float(torch.tensor(v, dtype=torch.float32))  # noqa: E731
+            return [0 if f32(w) >= f32(self.t1) else 2 for w in weights], [False] * k, [0.0] * k
         s = self.unimportance_one(weights)
         t1 = self.t1_for(layer) + 1e-6
         tm = None if self.t_mid is None else self.t_mid + 1e-6
@@ -117,8 +125,11 @@ class PrecisionPolicy:
 
     def device_policy(self, layer: int) -> Policy:
         """Parameters of moehip_decide_table for `layer`."""
-        mode = {"hobbit": 0, "hi": 1, "lo": 2}[self.mode]
+        mode = {"hobbit": 0, "hi": 1, "lo": 2, "weight": 3}[self.mode]
         f32 = lambda v: float(torch.tensor(v, dtype=torch.float32))  # noqa: E731
+        if self.mode == "weight":
+            return Policy(mode=mode, t1=f32(self.t1), t_mid=-1.0, t2=-1.0,
+                          protect=1 if layer in self.protect_layers else 0, upgrade=1 if self.allow_upgrade else 0)
         return Policy(mode=mode, t1=f32(self.t1_for(layer) + 1e-6),
                       t_mid=-1.0 if self.t_mid is None else f32(self.t_mid + 1e-6),
                       t2=-1.0 if self.t2 is None else f32(self.t2 + 1e-6),

@@ -395,6 +395,8 @@ class Policy:
         fixed = self._fixed(layer)
         if fixed is not None:
             return np.full((T, k), fixed, np.int8), none
+        if self.mode == "weight":  # the benchmark configurations' rule (not in moelab): w >= t1 -> level 0
+            return np.where(w >= np.float32(self.t1), 0, 2).astype(np.int8), none
         s = unimportance(w)
         lvl = np.full((T, k), 2, np.int8)
         if self.t_mid is not None:

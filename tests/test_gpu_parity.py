@@ -288,7 +288,8 @@ def test_router_planted_ties(dev):
 # HOBBIT decision + table, dispatch
 # ---------------------------------------------------------------------------------------
 @pytest.mark.parametrize("pol_kw", [dict(mode="hobbit", t1=0.6), dict(mode="hobbit", t1=0.3, t_mid=0.7, t2=0.9),
-                                    dict(mode="hi"), dict(mode="lo"), dict(mode="hobbit", t1=0.5, upgrade=False)])
+                                    dict(mode="hi"), dict(mode="lo"), dict(mode="hobbit", t1=0.5, upgrade=False),
+                                    dict(mode="weight", t1=0.3), dict(mode="weight", t1=0.3, upgrade=False)])
 def test_decide_table_matches_policy(dev, pol_kw):
     precs = ["fp16", "int8", "int4"]
     P, E, k = 3, 32, 8
@@ -412,22 +413,32 @@ class _Stack:
 
 
 @pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("mode", ["lo", "hobbit"])
+@pytest.mark.parametrize("mode", ["lo", "hobbit", "weight"])
 def test_decoder_layer_olmoe(dev, mode, fused):
+    """OLMoE layers; hobbit / weight: fp16 and int4 records of every expert, the level picks the
+    record (the weight rule with a threshold that splits this seed's top-8 into both kinds)."""
     H, I, E, k, L = 2048, 1024, 64, 8, 2
     dtype = torch.float16
-    precs = ["fp16", "int4"] if mode == "hobbit" else ["int4"]
+    precs = ["fp16", "int4"] if mode in ("hobbit", "weight") else ["int4"]
     S = _Stack(dev, H, I, E, L, precs, 100)
-    pol = PrecisionPolicy(mode, t1=0.5, upgrade=False)
+    xs = [torch.randn(1, H, generator=S.g).to(dtype) for _ in range(L)]
+    t1 = 0.5
+    if mode == "weight":  # the median routed weight of these tokens: both record kinds run
+        ws = [O.router(xs[l].float().numpy(), S.Wr[l].float().numpy(), k, False, "float16")[2] for l in range(L)]
+        t1 = float(np.median(np.concatenate([w.ravel() for w in ws])))
+    pol = PrecisionPolicy(mode, t1=t1, upgrade=False)
     dec = MoEDecoder(S.store, k, pol, dtype, router_weights=[w.to(dev) for w in S.Wr], fused=fused)
     assert dec.fused == fused
     for l in range(L):
-        x = torch.randn(1, H, generator=S.g).to(dtype)
+        x = xs[l]
         out = torch.zeros(1, H, dtype=dtype, device=dev)
         dec.layer(l, x.to(dev), out)
         torch.cuda.synchronize()
-        lo, idx, w, ref = S.reference(l, x, k, False, O.Policy(mode, t1=0.5))
+        lo, idx, w, ref = S.reference(l, x, k, False, O.Policy(mode, t1=t1))
         assert dec.idx.cpu().numpy().tolist() == idx.tolist()
+        if mode == "weight" and l == 0:  # the rows really split between the two record kinds
+            ch = dec.info[l, 1].cpu().numpy()
+            assert (ch == 0).any() and (ch == 1).any(), ch
         assert np.allclose(dec.w32.cpu().numpy(), w, rtol=2.0 ** -10, atol=0)
         assert_layer_close(out.float().cpu().numpy(), ref, dtype)
     assert dec.miss.item() == 0

@@ -406,3 +406,23 @@ def test_moe_layer_grouped_matches_olmoe_experts():
     a = O.moe_layer_grouped(x.numpy(), idx.numpy(), w.numpy(), lambda e: mats[e], skip=skip)
     b = O.moe_layer(x.numpy(), idx.numpy(), w.numpy(), lambda e: mats[e], skip=skip)
     assert np.allclose(a, b, rtol=1e-12, atol=1e-14)
+
+
+def test_weight_threshold_rule():
+    """The benchmark configurations' rule (fp16 if the gate weight is >= 0.15, else int4): level 0
+    exactly at and above the threshold in fp32, never a skip; the host policy agrees, one token and
+    batched, and packs the threshold without the HOBBIT slack."""
+    import torch
+
+    from moelab_hip.policy import PrecisionPolicy
+
+    w = np.array([[0.3, np.float32(0.15), np.nextafter(np.float32(0.15), np.float32(0)), 0.0, 1.0]], np.float32)
+    lvl, skip = O.Policy("weight", t1=0.15).levels(0, w)
+    assert lvl.tolist() == [[0, 0, 2, 2, 0]] and not skip.any()
+    pol = PrecisionPolicy("weight", t1=0.15)
+    hl, hs = pol.levels(0, torch.from_numpy(w))
+    assert hl.tolist() == lvl.tolist() and not hs.any()
+    l1, s1, _ = pol.levels_one(0, w[0].tolist())
+    assert l1 == lvl[0].tolist() and not any(s1)
+    dp = pol.device_policy(3)
+    assert dp.mode == 3 and dp.t1 == float(np.float32(0.15)) and dp.t2 < 0
