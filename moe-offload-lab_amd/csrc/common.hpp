@@ -211,6 +211,12 @@ __device__ __forceinline__ uint4 gld16(gbyte *p) {
     const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// streaming load (non-temporal hint) for weight bytes read once per launch: they then do not
+// displace the small, reused data (router weights, activations, exchange words) from the caches
+__device__ __forceinline__ uint4 gld16_nt(gbyte *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ uint32_t gld4(gbyte *p) { return *(const __attribute__((address_space(1))) uint32_t *)p; }
 __device__ __forceinline__ uint32_t gld2(gbyte *p) { return *(const __attribute__((address_space(1))) uint16_t *)p; }
 

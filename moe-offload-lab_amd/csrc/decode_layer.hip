@@ -497,8 +497,8 @@ __device__ __forceinline__ void up_rows(gbyte *qb, gbyte *sb, const LaneVec<PREC
             const int c0 = cl + i * G;
             const int c = min(c0, C - 1);
             const bool ok = r0 < I && c0 < C;
-            qg[p][i] = gld16(qb + (size_t)r * RB + (size_t)c * 16);
-            qu[p][i] = gld16(qb + (size_t)(r + I) * RB + (size_t)c * 16);
+            qg[p][i] = gld16_nt(qb + (size_t)r * RB + (size_t)c * 16);
+            qu[p][i] = gld16_nt(qb + (size_t)(r + I) * RB + (size_t)c * 16);
             const uint32_t a0 = scale_bits<PREC>(sb, r, c, H, gs), a1 = scale_bits<PREC>(sb, r + I, c, H, gs);
             sg[p][i] = ok ? a0 : 0u;
             su[p][i] = ok ? a1 : 0u;
@@ -561,7 +561,7 @@ __device__ __forceinline__ void down_load(gbyte *qb, gbyte *sb, int row0, int H,
         for (int i = 0; i < CPL; ++i) {
             const int c0 = cl + i * G;
             const int c = min(c0, C - 1);
-            d.q[p][i] = gld16(qb + (size_t)r * RB + (size_t)c * 16);
+            d.q[p][i] = gld16_nt(qb + (size_t)r * RB + (size_t)c * 16);
             const uint32_t sv = scale_bits<PREC>(sb, r, c, I, gs);
             d.s[p][i] = (r0 < H && c0 < C) ? sv : 0u;
         }
