@@ -82,7 +82,61 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
     }
 }
 
-// softmax + top-k + renorm for one token per wave (E <= 1024, k <= 32)
+// logits on MFMA (16-bit activations, T >= 16, H a multiple of 512, 16-byte aligned rows): one
+// workgroup per 16 tokens x 16 experts, each of its 4 waves a quarter of H through
+// v_mfma_f32_16x16x32 (A = 16 tokens x 32 K: lane row + 16 (k / 8), element k % 8; B likewise for
+// the 16 expert rows; D row 4 (lane / 16) + i, column lane % 16), the four partial tiles summed
+// in wave order in LDS (fixed order: the result does not depend on scheduling), one rounding
+typedef _Float16 rf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 rbf16x8 __attribute__((ext_vector_type(8)));
+typedef float rf32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+__device__ __forceinline__ rf32x4 router_mfma(const uint4 a, const uint4 b, const rf32x4 c) {
+    if constexpr (DT == MOEHIP_DT_F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rf16x8, a), __builtin_bit_cast(rf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rbf16x8, a), __builtin_bit_cast(rbf16x8, b), c, 0, 0, 0);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_router_logits_mfma(const void *__restrict__ x, const void *__restrict__ Wr,
+                                                            int T, int H, int E, void *__restrict__ logits) {
+    __shared__ float s_part[4][16][17];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+    const int r = lane & 15, kq = lane >> 4;
+    const uint16_t *xr = reinterpret_cast<const uint16_t *>(x) + (size_t)min(t0 + r, T - 1) * H + kq * 8;
+    const uint16_t *wr = reinterpret_cast<const uint16_t *>(Wr) + (size_t)min(e0 + r, E - 1) * H + kq * 8;
+    const int kw = H >> 2;
+    rf32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = wave * kw; k0 < (wave + 1) * kw; k0 += 128) {
+        uint4 av[4], bv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            av[u] = *reinterpret_cast<const uint4 *>(xr + k0 + 32 * u);
+            bv[u] = *reinterpret_cast<const uint4 *>(wr + k0 + 32 * u);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = router_mfma<DT>(av[u], bv[u], acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_part[wave][4 * kq + i][r] = acc[i];
+    __syncthreads();
+    const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
+    const float v = ((s_part[0][m][n] + s_part[1][m][n]) + s_part[2][m][n]) + s_part[3][m][n];
+    if (t0 + m < T && e0 + n < E) st_act<DT>(logits, (size_t)(t0 + m) * E + e0 + n, v);
+}
+
+// softmax + top-k + renorm for one token per wave (E <= 1024, k <= 32). 16-bit logits: k rounds of
+// a DPP wave maximum over 32-bit keys (order-preserving logit bits above 1023 - index: the largest
+// logit, the lowest index among equal logits); fp32 logits: value and index compared separately.
+__device__ __forceinline__ uint32_t topk_key16(uint32_t bits16, int c) {
+    const uint32_t b = (bits16 & 0x7fffu) == 0u ? 0u : bits16;  // -0 == +0
+    const uint32_t k16 = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+    return (k16 << 10) | (uint32_t)(1023 - c);
+}
+
 template <int DT>
 __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ logits, int T, int E, int k, int renorm,
                                                     int64_t *__restrict__ idx, void *__restrict__ wout,
@@ -92,11 +146,18 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
     __shared__ int s_idx[32];
     __shared__ float s_p[32];
     float lv[16];
+    uint32_t key[16];
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int c = lane + 64 * i;
-        lv[i] = c < E ? ld_act<DT>(logits, (size_t)t * E + min(c, E - 1)) : -INFINITY;
+        key[i] = 0u;
+        lv[i] = -INFINITY;
+        if (c < E) {
+            lv[i] = ld_act<DT>(logits, (size_t)t * E + c);
+            if constexpr (DT != MOEHIP_DT_F32)
+                key[i] = topk_key16(reinterpret_cast<const uint16_t *>(logits)[(size_t)t * E + c], c);
+        }
         m = fmaxf(m, lv[i]);
     }
     m = wave_max(m);
@@ -107,31 +168,50 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
         if (c < E) sum += expf(lv[i] - m);
     }
     sum = wave_sum(sum);
-    uint32_t taken = 0;
-    for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = INT_MAX;
+    if constexpr (DT != MOEHIP_DT_F32) {
+        for (int j = 0; j < k; ++j) {
+            uint32_t lb = 0u;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int c = lane + 64 * i;
-            if (c < E && !((taken >> i) & 1u) && (lv[i] > bv || (lv[i] == bv && c < bi))) {
-                bv = lv[i];
-                bi = c;
-            }
-        }
+            for (int i = 0; i < 16; ++i) lb = max(lb, key[i]);
+            const uint32_t M = wave_max_u32(lb);
+            const int c = 1023 - (int)(M & 1023u);
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ov = __shfl_xor(bv, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
+            for (int i = 0; i < 16; ++i)
+                if (key[i] == M) key[i] = 0u;  // keys are distinct: exactly one lane clears one
+            if (lane == 0) s_idx[j] = c;
         }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        if (lane == 0) {
-            s_idx[j] = bi;
-            s_p[j] = expf(bv - m) / sum;
+        __syncthreads();
+        if (lane < k) {
+            const int c = s_idx[lane];
+            s_p[lane] = expf(ld_act<DT>(logits, (size_t)t * E + c) - m) / sum;
+        }
+    } else {
+        uint32_t taken = 0;
+        for (int j = 0; j < k; ++j) {
+            float bv = -INFINITY;
+            int bi = INT_MAX;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int c = lane + 64 * i;
+                if (c < E && !((taken >> i) & 1u) && (lv[i] > bv || (lv[i] == bv && c < bi))) {
+                    bv = lv[i];
+                    bi = c;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (ov > bv || (ov == bv && oi < bi)) {
+                    bv = ov;
+                    bi = oi;
+                }
+            }
+            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+            if (lane == 0) {
+                s_idx[j] = bi;
+                s_p[j] = expf(bv - m) / sum;
+            }
         }
     }
     __syncthreads();
@@ -236,13 +316,18 @@ extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, i
     hipStream_t st = as_stream(stream);
     const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
     const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
+    // a real matrix product (16 tokens or more): MFMA tiles of 16 tokens x 16 experts
+    const bool mf = dtype != MOEHIP_DT_F32 && vec16 && T >= 16 && H % 512 == 0;
+    const dim3 gm((T + 15) / 16, (E + 15) / 16);
     switch (dtype) {
         case MOEHIP_DT_F16:
-            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_F16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
+            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
             break;
         case MOEHIP_DT_BF16:
-            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_BF16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_BF16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
+            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_BF16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_BF16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
             break;
         default:
