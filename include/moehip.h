@@ -232,6 +232,54 @@ int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, int xdtype,
 size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I);
 
 /*
+ * moehip_grouped_gemm over P record tables, one per record precision precs[p] (MOEHIP_PREC_INT4 /
+ * INT8 / FP8 / F16 / BF16): tabs (P, E, 4) int64, row (p, e) = the field addresses of expert e's
+ * record when the expert runs at precision p (as written by moehip_batch_vote), else 0. Pairs of
+ * experts with no non-zero row must carry rank -1 (moehip_batch_vote sets it). precs is a host
+ * array. Replaces, for any record precision and mixed precision per expert, moelab/runtime.py:
+ * 418-436 (`_run_grouped_tokens`: per expert, expert_ffn on its tokens at the voted precision)
+ * and the accumulation runtime.py:352-353.
+ */
+int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H,
+                              int I, int k, int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
+                              const int32_t *rank, const float *w, void *out, const void *add, int accumulate, void *ws,
+                              size_t ws_bytes, void *stream);
+
+/*
+ * HOBBIT levels of T tokens (moelab/policy.py:110-123 `levels`, the T > 1 branch of
+ * runtime.py:459-470): w32 (T, ks) fp32, the first k slots routed; levels (T, ks) int32 and skip
+ * (T, ks) uint8 (1 = skipped). Slots k..ks-1 (the shared expert) get level 0 and are never
+ * skipped. k <= ks <= 64.
+ */
+int moehip_batch_levels(const float *w32, int T, int k, int ks, const moehip_policy *pol, int32_t *levels,
+                        uint8_t *skip, void *stream);
+
+/*
+ * One precision per expert for T > 1 tokens (moelab/runtime.py:484-492 with policy.py:148-154
+ * `expert_level`: the most precise level requested by at least hi_vote of the expert's pairs,
+ * then level_to_precision through lv2p[3]), the resident copy (as moehip_decide_table: rtab
+ * (P, E) device base addresses, 0 = absent; upgrade from pol), and the tables of
+ * moehip_grouped_gemm_multi: tabs (P, E + has_shared, 4). Expert E is the shared expert when
+ * has_shared (records shared_rec[P], a host array). levels, offsets (E + has_shared + 1) and
+ * sorted_pos come from moehip_batch_levels and moehip_dispatch (over E + has_shared experts).
+ * An expert with no usable copy gets rank -1 on its pairs and adds their number to miss.
+ * info (E + has_shared) fp32 = chosen precision, -1 = missing, -2 = no pairs (may be NULL).
+ */
+int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_t *offsets, const int32_t *sorted_pos,
+                      double hi_vote, const moehip_policy *pol, const int *lv2p, const int64_t *rtab,
+                      const int64_t *shared_rec, int P, const int64_t *offs, const int *planned, int64_t *tabs,
+                      int32_t *rank, float *info, float *miss, void *stream);
+
+/*
+ * Qwen3-Next shared expert as slot k of every token (transformers Qwen3NextSparseMoeBlock.forward,
+ * models/qwen3_next/modeling_qwen3_next.py:786-797): idx_ext (T, k + 1) / w_ext (T, k + 1) =
+ * the routed idx (T, k) / w32 (T, k) followed by expert id E with weight sigmoid(x . gate), x .
+ * gate and the sigmoid each rounded to the activation dtype. x (T, H), gate (H) in dtype.
+ */
+int moehip_shared_slot(const void *x, const void *gate, int T, int H, int dtype, const int64_t *idx, const float *w32,
+                       int k, int E, int64_t *idx_ext, float *w_ext, void *stream);
+
+/*
  * Checkpoint-style FP8 block quantisation of w (O, I) fp32: per 128 x 128 block
  * scale = amax / 448 (1.0 for an all-zero block), q (O, I) = e4m3fn(w / scale) (round to
  * nearest even, saturating at 448), s (ceil(O/128), ceil(I/128)) fp32 — the

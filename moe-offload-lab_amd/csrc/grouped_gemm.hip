@@ -42,20 +42,29 @@ constexpr int GG_KG = 64;     // K per scale group
 constexpr int GG_TOK = 64;    // tokens per pass (two 32-token M tiles)
 constexpr int GG_ROWS = 256;  // weight rows per workgroup
 
-// chunk geometry: NGC groups of 64 K; each of the 256 threads stages CK / 4 fp16 values of one
-// token (NV 16-byte loads)
-template <int NGC> struct GgChunk {
-    static constexpr int CK = NGC * GG_KG;  // K per chunk
+// chunk geometry: CK values of K per chunk; a lane half covers CK / 2 of them, which is 32 bytes
+// of its weight row for every record precision (int4: CK 128 = two scale groups, one per half;
+// int8 / fp8: 64; fp16 / bf16: 32). Each of the 256 threads stages CK / 4 fp16 activation values
+// of one token (NV 16-byte loads).
+template <int CKV> struct GgChunk {
+    static constexpr int CK = CKV;          // K per chunk
     static constexpr int LDA = CK + 8;      // LDS row stride in halves
     static constexpr int VPT = CK / 4;      // values staged per thread
     static constexpr int NV = VPT / 8;      // 16-byte loads per thread
 };
+template <int PREC> struct GgPrec;
+template <> struct GgPrec<MOEHIP_PREC_INT4> { static constexpr int CK = 128, BITS = 4; };
+template <> struct GgPrec<MOEHIP_PREC_INT8> { static constexpr int CK = 64, BITS = 8; };
+template <> struct GgPrec<MOEHIP_PREC_FP8> { static constexpr int CK = 64, BITS = 8; };
+template <> struct GgPrec<MOEHIP_PREC_F16> { static constexpr int CK = 32, BITS = 16; };
+template <> struct GgPrec<MOEHIP_PREC_BF16> { static constexpr int CK = 32, BITS = 16; };
 
 // ---------------------------------------------------------------------------------------
-// weights: dword d of a row (K elements c0..c7 as nibbles) and the group scale s (fp16, both
-// halves) -> fp16 s * (n - 8) in operand order c0 c4 c1 c5 c2 c6 c3 c7: (d & mask) | magic =
-// fp16 1024 + n in one v_and_or_b32 (common.hpp and_or; its result feeds the compiler's packed
-// fp16 add, never an MFMA operand directly), - 1032 (exact), * s (one rounding).
+// weights -> fp16 B operands in operand order c0 c4 c1 c5 c2 c6 c3 c7 (the order the activation
+// chunks are stored in). int4: dword d of a row (K elements c0..c7 as nibbles) and the group
+// scale s (fp16, both halves): (d & mask) | magic = fp16 1024 + n in one v_and_or_b32 (common.hpp
+// and_or; its result feeds the compiler's packed fp16 add, never an MFMA operand directly),
+// - 1032 (exact), * s (one rounding).
 // ---------------------------------------------------------------------------------------
 struct DeqK {
     uint32_t mask, magic;  // 0x000F000F, 0x64006400
@@ -77,25 +86,109 @@ __device__ __forceinline__ f16x8 wdeq8(uint32_t d, half2_t s2, DeqK k) {
     return __builtin_bit_cast(f16x8, u);
 }
 
-template <int NGC> struct WChunk {
-    uint4 q[2][NGC];       // subtile, group: this lane half's 16 bytes of its row
-    uint32_t s[2][NGC / 2];  // subtile: the NGC group scales (fp16 pairs)
+// int8: bytes b0..b7 (K c0..c7) in dwords lo, hi. Pair i = (b_i, b_i+4) moved into the low bytes
+// of two halves by one v_perm_b32, the sign bit flipped and fp16 1024's high byte set by one xor
+// (fp16 1024 + q + 128, exact), - 1152 (exact), * s (one rounding).
+__device__ __forceinline__ f16x8 wdeq8_i8(uint32_t lo, uint32_t hi, half2_t s2) {
+#pragma clang fp contract(off)
+    const half2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + i) << 16) | (uint32_t)i;
+        const uint32_t u = __builtin_amdgcn_perm(hi, lo, sel) ^ 0x64806480u;
+        r[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2_t, u) + off) * s2);
+    }
+    return __builtin_bit_cast(f16x8, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// fp8 e4m3fn: pair i moved into the HIGH bytes of two halves (b << 8); (v & sign) | ((v >> 1) &
+// 0x3F80) is the fp16 of value * 2^-8 exactly (exponent bias 15 vs 7, subnormals included; the
+// format's only NaN code never occurs in a record), * fp16(block scale * 2^8) (one rounding).
+__device__ __forceinline__ f16x8 wdeq8_fp8(uint32_t lo, uint32_t hi, half2_t s2) {
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t sel = 0x000C000Cu | ((uint32_t)(4 + i) << 24) | ((uint32_t)i << 8);
+        const uint32_t v = __builtin_amdgcn_perm(hi, lo, sel);
+        const uint32_t u = and_or(v >> 1, 0x3F803F80u, v & 0x80008000u);
+        r[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, u) * s2);
+    }
+    return __builtin_bit_cast(f16x8, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// fp16 / bf16: halves c0..c7 in dwords d0..d3; pair i = (c_i, c_i+4) by one v_perm_b32; bf16 pairs
+// become fp16 through fp32 (exact for every value in fp16's normal range)
+template <int PREC>
+__device__ __forceinline__ f16x8 wdeq8_16(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3) {
+    uint32_t r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t lo = (i >> 1) == 0 ? d0 : d1, hi = (i >> 1) == 0 ? d2 : d3;
+        const uint32_t v = __builtin_amdgcn_perm(hi, lo, (i & 1) ? 0x07060302u : 0x05040100u);
+        if constexpr (PREC == MOEHIP_PREC_BF16) {
+            r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v << 16),
+                                                                          __uint_as_float(v & 0xffff0000u)));
+        } else {
+            r[i] = v;
+        }
+    }
+    return __builtin_bit_cast(f16x8, make_uint4(r[0], r[1], r[2], r[3]));
+}
+
+// one chunk of weights in registers: per subtile this lane half's 32 bytes of its row and the
+// raw scale (int4 / int8: fp16 group scale bits; fp8: fp32 block scale bits; fp16 / bf16: none)
+struct WChunk {
+    uint4 q[2][2];
+    uint32_t s[2];
 };
 
-template <int NGC>
-__device__ __forceinline__ void load_chunk(WChunk<NGC> &w, gu8 *const (&qp)[2], gu8 *const (&sp)[2], int c) {
+// qp[t]: the lane's row (subtile t) + 32 * half; sp[t]: its scale row (see gemm_rows)
+template <int PREC>
+__device__ __forceinline__ void load_chunk(WChunk &w, gu8 *const (&qp)[2], gu8 *const (&sp)[2], int c) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-        gu8 *q = qp[t] + (size_t)c * (GgChunk<NGC>::CK / 2);
-#pragma unroll
-        for (int g = 0; g < NGC; ++g) w.q[t][g] = gld16(q + 32 * g);  // 32 bytes per group row: this half's 16
-        gu8 *s = sp[t] + (size_t)c * (NGC * 2);
-        if constexpr (NGC == 4) {
-            const u32x2_t v = *(const __attribute__((address_space(1))) u32x2_t *)s;
-            w.s[t][0] = v.x, w.s[t][1] = v.y;
-        } else {
-            w.s[t][0] = *(const __attribute__((address_space(1))) uint32_t *)s;
-        }
+        gu8 *q = qp[t] + (size_t)c * 64;  // 64 bytes of a row per chunk for every precision
+        w.q[t][0] = gld16(q);
+        w.q[t][1] = gld16(q + 16);
+        if constexpr (PREC == MOEHIP_PREC_INT4)
+            w.s[t] = *(const __attribute__((address_space(1))) uint16_t *)(sp[t] + (size_t)c * 4);
+        else if constexpr (PREC == MOEHIP_PREC_INT8)
+            w.s[t] = *(const __attribute__((address_space(1))) uint16_t *)(sp[t] + (size_t)c * 2);
+        else if constexpr (PREC == MOEHIP_PREC_FP8)
+            w.s[t] = *(const __attribute__((address_space(1))) uint32_t *)(sp[t] + (size_t)(c >> 1) * 4);
+        else
+            w.s[t] = 0u;
+    }
+}
+
+// row pointers of one lane: q row `row` of a (rows, K) weight matrix at qb, offset by the lane
+// half's 32 bytes; scale row at sb (int4 / int8: fp16 (rows, K / 64); fp8: fp32 (rows / 128,
+// K / 128) blocks)
+template <int PREC>
+__device__ __forceinline__ void gemm_rows(gu8 *qb, gu8 *sb, int row, int K, int h, gu8 *&q, gu8 *&sc) {
+    q = qb + (size_t)row * ((size_t)K * GgPrec<PREC>::BITS / 8) + 32 * h;
+    if constexpr (PREC == MOEHIP_PREC_INT4) sc = sb + (size_t)row * (K / GG_KG) * 2 + 2 * h;
+    else if constexpr (PREC == MOEHIP_PREC_INT8) sc = sb + (size_t)row * (K / GG_KG) * 2;
+    else if constexpr (PREC == MOEHIP_PREC_FP8) sc = sb + (size_t)(row >> 7) * (K >> 7) * 4;
+    else sc = sb;
+}
+
+// B operand of MFMA step m of a chunk for one subtile (the lane's 8 dwords, natural K order)
+template <int PREC, int M>
+__device__ __forceinline__ f16x8 b_operand(const uint4 (&q)[2], uint32_t sraw, DeqK dk) {
+    const uint32_t dw[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+        const uint32_t sw = sraw & 0xffffu;
+        return wdeq8(dw[M], __builtin_bit_cast(half2_t, sw | (sw << 16)), dk);
+    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
+        const uint32_t sw = sraw & 0xffffu;
+        return wdeq8_i8(dw[2 * M], dw[2 * M + 1], __builtin_bit_cast(half2_t, sw | (sw << 16)));
+    } else if constexpr (PREC == MOEHIP_PREC_FP8) {
+        const uint32_t sw = f32_to_f16_rne(__uint_as_float(sraw) * 256.0f);
+        return wdeq8_fp8(dw[2 * M], dw[2 * M + 1], __builtin_bit_cast(half2_t, sw | (sw << 16)));
+    } else {
+        return wdeq8_16<PREC>(dw[4 * M], dw[4 * M + 1], dw[4 * M + 2], dw[4 * M + 3]);
     }
 }
 
@@ -106,54 +199,49 @@ __device__ __forceinline__ void load_chunk(WChunk<NGC> &w, gu8 *const (&qp)[2], 
 // keeps the compiler's load counting exact): MFMA rows are independent and those rows are never
 // stored.
 // ---------------------------------------------------------------------------------------
-template <int NGC>
-__device__ __forceinline__ void xs_load(const uint16_t *row, int c, uint4 (&v)[GgChunk<NGC>::NV]) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)c * GgChunk<NGC>::CK +
-                                                     (threadIdx.x & 3) * GgChunk<NGC>::VPT);
+template <int CK>
+__device__ __forceinline__ void xs_load(const uint16_t *row, int c, uint4 (&v)[GgChunk<CK>::NV]) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)c * CK + (threadIdx.x & 3) * GgChunk<CK>::VPT);
 #pragma unroll
-    for (int m = 0; m < GgChunk<NGC>::NV; ++m) v[m] = p[m];
+    for (int m = 0; m < GgChunk<CK>::NV; ++m) v[m] = p[m];
 }
 
-template <int NGC>
-__device__ __forceinline__ void xs_store(const uint4 (&v)[GgChunk<NGC>::NV], uint16_t *s_a) {
+template <int CK>
+__device__ __forceinline__ void xs_store(const uint4 (&v)[GgChunk<CK>::NV], uint16_t *s_a) {
     const int tok = threadIdx.x >> 2, part = threadIdx.x & 3;
-    uint4 *dst = reinterpret_cast<uint4 *>(s_a + tok * GgChunk<NGC>::LDA + part * GgChunk<NGC>::VPT);
+    uint4 *dst = reinterpret_cast<uint4 *>(s_a + tok * GgChunk<CK>::LDA + part * GgChunk<CK>::VPT);
 #pragma unroll
-    for (int m = 0; m < GgChunk<NGC>::NV; ++m) {
+    for (int m = 0; m < GgChunk<CK>::NV; ++m) {
         const uint4 u = v[m];
         dst[m] = make_uint4(lo_lo(u.x, u.z), hi_hi(u.x, u.z), lo_lo(u.y, u.w), hi_hi(u.y, u.w));
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// one chunk of MFMAs for a wave: NGC groups x 4 MFMAs x NM M tiles x 2 subtiles
+// one chunk of MFMAs for a wave: CK / 16 steps x NM M tiles x 2 subtiles. Step m of lane half h
+// covers K h * CK / 2 + 8 m .. + 7 of the chunk, in A (LDS) and B (registers) alike.
 // ---------------------------------------------------------------------------------------
-template <int NGC, int NM>
-__device__ __forceinline__ void mma_chunk(const WChunk<NGC> &w, const uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
-    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+template <int PREC, int NM, int M = 0>
+__device__ __forceinline__ void mma_steps(const WChunk &w, const uint16_t *ap, DeqK dk, f32x16 (&d)[2][2]) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    if constexpr (M < CK / 16) {
+        const f16x8 b0 = b_operand<PREC, M>(w.q[0], w.s[0], dk);
+        const f16x8 b1 = b_operand<PREC, M>(w.q[1], w.s[1], dk);
 #pragma unroll
-    for (int g = 0; g < NGC; ++g) {
-        half2_t s2[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const uint32_t sw = (w.s[t][g >> 1] >> (16 * (g & 1))) & 0xffffu;
-            s2[t] = __builtin_bit_cast(half2_t, sw | (sw << 16));
+        for (int mt = 0; mt < NM; ++mt) {
+            const f16x8 a = *reinterpret_cast<const f16x8 *>(ap + mt * 32 * GgChunk<CK>::LDA + 8 * M);
+            d[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b0, d[mt][0], 0, 0, 0);
+            d[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b1, d[mt][1], 0, 0, 0);
         }
-        const uint16_t *ap = s_a + i * GgChunk<NGC>::LDA + g * GG_KG + h * 32;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint4 q0 = w.q[0][g], q1 = w.q[1][g];
-            const uint32_t d0 = m == 0 ? q0.x : (m == 1 ? q0.y : (m == 2 ? q0.z : q0.w));
-            const uint32_t d1 = m == 0 ? q1.x : (m == 1 ? q1.y : (m == 2 ? q1.z : q1.w));
-            const f16x8 b0 = wdeq8(d0, s2[0], dk), b1 = wdeq8(d1, s2[1], dk);
-#pragma unroll
-            for (int mt = 0; mt < NM; ++mt) {
-                const f16x8 a = *reinterpret_cast<const f16x8 *>(ap + mt * 32 * GgChunk<NGC>::LDA + 8 * m);
-                d[mt][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b0, d[mt][0], 0, 0, 0);
-                d[mt][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b1, d[mt][1], 0, 0, 0);
-            }
-        }
+        mma_steps<PREC, NM, M + 1>(w, ap, dk, d);
     }
+}
+
+template <int PREC, int NM>
+__device__ __forceinline__ void mma_chunk(const WChunk &w, const uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    mma_steps<PREC, NM>(w, s_a + i * GgChunk<CK>::LDA + h * (CK / 2), dk, d);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -163,19 +251,20 @@ __device__ __forceinline__ void mma_chunk(const WChunk<NGC> &w, const uint16_t *
 // is issued unconditionally (chunk indices clamped to the last chunk: a few repeated loads at
 // the end hit L2): with loads under branches the compiler cannot count them and waits for all.
 // ---------------------------------------------------------------------------------------
-template <int NGC, int RING, int NM>
+template <int PREC, int RING, int NM>
 __device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2], int nch, const uint16_t *srcrow,
                                        uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
-    constexpr int ABUF = GG_TOK * GgChunk<NGC>::LDA;
+    constexpr int CK = GgPrec<PREC>::CK;
+    constexpr int ABUF = GG_TOK * GgChunk<CK>::LDA;
     const int cl = nch - 1;
-    WChunk<NGC> wr[RING];
-    uint4 xv[GgChunk<NGC>::NV];
-    xs_load<NGC>(srcrow, 0, xv);
+    WChunk wr[RING];
+    uint4 xv[GgChunk<CK>::NV];
+    xs_load<CK>(srcrow, 0, xv);
 #pragma unroll
-    for (int u = 0; u + 1 < RING; ++u) load_chunk<NGC>(wr[u], qp, sp, min(u, cl));
-    xs_store<NGC>(xv, s_a);
-    xs_load<NGC>(srcrow, min(1, cl), xv);
-    load_chunk<NGC>(wr[RING - 1], qp, sp, min(RING - 1, cl));
+    for (int u = 0; u + 1 < RING; ++u) load_chunk<PREC>(wr[u], qp, sp, min(u, cl));
+    xs_store<CK>(xv, s_a);
+    xs_load<CK>(srcrow, min(1, cl), xv);
+    load_chunk<PREC>(wr[RING - 1], qp, sp, min(RING - 1, cl));
     __syncthreads();
 #pragma unroll 1
     for (int c0 = 0; c0 < nch; c0 += RING) {
@@ -184,11 +273,11 @@ __device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2],
             const int c = c0 + u;
             const int b = c & 1;
             if (c < nch) {
-                mma_chunk<NGC, NM>(wr[u], s_a + b * ABUF, dk, d);
-                if (c + 1 < nch) xs_store<NGC>(xv, s_a + (b ^ 1) * ABUF);
+                mma_chunk<PREC, NM>(wr[u], s_a + b * ABUF, dk, d);
+                if (c + 1 < nch) xs_store<CK>(xv, s_a + (b ^ 1) * ABUF);
             }
-            xs_load<NGC>(srcrow, min(c + 2, cl), xv);
-            load_chunk<NGC>(wr[u], qp, sp, min(c + RING, cl));
+            xs_load<CK>(srcrow, min(c + 2, cl), xv);
+            load_chunk<PREC>(wr[u], qp, sp, min(c + RING, cl));
             if (c < nch) __syncthreads();
         }
     }
@@ -229,12 +318,13 @@ __global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, in
 // gate rows, subtile 1 = up rows. Writes h (pairs, I) fp32 and pmax[pair] = max |h| (atomic).
 // ---------------------------------------------------------------------------------------
 // x: fp16 activations (the caller's, or x16 with exponents xe for bf16 input; xe null = 0)
+template <int PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_up(
     const uint16_t *__restrict__ x, const int *__restrict__ xe, int H, int I, int k, int E,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
     float *__restrict__ hb, uint32_t *__restrict__ pmax, DeqK dk) {
-    constexpr int NGC = 2;
-    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<NGC>::LDA];
+    constexpr int CK = GgPrec<PREC>::CK;
+    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<CK>::LDA];
     __shared__ int s_e[GG_TOK];
     __shared__ uint32_t s_mx[GG_TOK];
     const int NB = I / 128;
@@ -246,10 +336,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (ne <= 0 || qb == nullptr) return;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
     const int col = nb * 128 + 32 * wave + j;
-    const size_t RB = (size_t)H / 2, SB = (size_t)(H / GG_KG) * 2;
-    gu8 *const qp[2] = {qb + (size_t)col * RB + 16 * h, qb + (size_t)(I + col) * RB + 16 * h};
-    gu8 *const sp[2] = {sb + (size_t)col * SB, sb + (size_t)(I + col) * SB};
-    const int nch = H / GgChunk<NGC>::CK;
+    gu8 *qp[2], *sp[2];
+    gemm_rows<PREC>(qb, sb, col, H, h, qp[0], sp[0]);
+    gemm_rows<PREC>(qb, sb, I + col, H, h, qp[1], sp[1]);
+    const int nch = H / CK;
     for (int m0 = 0; m0 < ne; m0 += GG_TOK) {
         const int mn = min(GG_TOK, ne - m0), nm = (mn + 31) / 32;
         const int stok = tid >> 2;
@@ -263,8 +353,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
-        if (nm == 2) k_loop<NGC, 3, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
-        else k_loop<NGC, 3, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        if (nm == 2) k_loop<PREC, 3, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        else k_loop<PREC, 3, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
         // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32; per-pair max
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -309,12 +399,13 @@ __global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, const
 // down: tiles (expert, 256 output rows); wave w: rows nb*256 + 64 w + 32 t + (lane % 32).
 // y[pair, row] = w[pair] * (down_row . h_pair)
 // ---------------------------------------------------------------------------------------
+template <int PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_down(
     const uint16_t *__restrict__ h16, const int *__restrict__ he, int H, int I, int E,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
-    const float *__restrict__ w, float *__restrict__ y, DeqK dk) {
-    constexpr int NGC = 2;
-    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<NGC>::LDA];
+    const float *__restrict__ w, float *__restrict__ y, DeqK dk, int zero_missing) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<CK>::LDA];
     __shared__ float s_f[GG_TOK];  // w[pair] * 2^e
     const int NB = H / GG_ROWS;
     int e, nb;
@@ -325,15 +416,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     gu8 *qb = record_ptr(tab[4 * e + 2]);
     gu8 *sb = record_ptr(tab[4 * e + 3]);
     const int row0 = nb * GG_ROWS + 64 * wave + j;
-    if (qb == nullptr) {  // expert not resident: its pairs contribute nothing
-        for (int i = tid; i < ne * GG_ROWS; i += 256)
-            y[(size_t)(p0 + i / GG_ROWS) * H + nb * GG_ROWS + i % GG_ROWS] = 0.f;
+    if (qb == nullptr) {  // expert not resident (single-table launches): its pairs contribute nothing
+        if (zero_missing)
+            for (int i = tid; i < ne * GG_ROWS; i += 256)
+                y[(size_t)(p0 + i / GG_ROWS) * H + nb * GG_ROWS + i % GG_ROWS] = 0.f;
         return;
     }
-    const size_t RB = (size_t)I / 2, SB = (size_t)(I / GG_KG) * 2;
-    gu8 *const qp[2] = {qb + (size_t)row0 * RB + 16 * h, qb + (size_t)(row0 + 32) * RB + 16 * h};
-    gu8 *const sp[2] = {sb + (size_t)row0 * SB, sb + (size_t)(row0 + 32) * SB};
-    const int nch = I / GgChunk<NGC>::CK;
+    gu8 *qp[2], *sp[2];
+    gemm_rows<PREC>(qb, sb, row0, I, h, qp[0], sp[0]);
+    gemm_rows<PREC>(qb, sb, row0 + 32, I, h, qp[1], sp[1]);
+    const int nch = I / CK;
     for (int m0 = 0; m0 < ne; m0 += GG_TOK) {
         const int mn = min(GG_TOK, ne - m0), nm = (mn + 31) / 32;
         const int stok = tid >> 2;
@@ -345,8 +437,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
-        if (nm == 2) k_loop<NGC, 3, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
-        else k_loop<NGC, 3, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        if (nm == 2) k_loop<PREC, 3, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        else k_loop<PREC, 3, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             if (mt >= nm) break;
@@ -426,12 +518,32 @@ extern "C" size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I
     return gg_layout(T, k, H, I).total;
 }
 
-extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, int xdtype, int T, int H, int I, int k,
-                                   int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
-                                   const int32_t *rank, const float *w, void *out, const void *add, int accumulate,
-                                   void *ws, size_t ws_bytes, void *stream) {
-    MOEHIP_REQUIRE(tab && x && offsets && sorted_pos && rank && w && out && ws, "grouped_gemm: null pointer");
-    MOEHIP_REQUIRE(prec == MOEHIP_PREC_INT4, "grouped_gemm: precision %d (int4 records)", prec);
+template <int PREC>
+static void launch_up(dim3 g, hipStream_t st, const uint16_t *x, const int *xe, int H, int I, int k, int E,
+                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *hb, uint32_t *pmax,
+                      DeqK dk) {
+    hipLaunchKernelGGL((k_gemm_up<PREC>), g, dim3(256), 0, st, x, xe, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk);
+}
+template <int PREC>
+static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *he, int H, int I, int E,
+                        const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, const float *w, float *y,
+                        DeqK dk, int zero_missing) {
+    hipLaunchKernelGGL((k_gemm_down<PREC>), g, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk,
+                       zero_missing);
+}
+
+static bool gg_prec_ok(int prec) {
+    return prec == MOEHIP_PREC_INT4 || prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8 ||
+           prec == MOEHIP_PREC_F16 || prec == MOEHIP_PREC_BF16;
+}
+
+// the layer on P record tables (one per precision, rows of experts not run at that precision 0)
+static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H, int I, int k,
+                  int E, int gs, const int32_t *offsets, const int32_t *sorted_pos, const int32_t *rank, const float *w,
+                  void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream, int zero_missing) {
+    MOEHIP_REQUIRE(tabs && x && offsets && sorted_pos && rank && w && out && ws && precs, "grouped_gemm: null pointer");
+    MOEHIP_REQUIRE(P >= 1 && P <= 4, "grouped_gemm: %d record tables (1..4)", P);
+    for (int p = 0; p < P; ++p) MOEHIP_REQUIRE(gg_prec_ok(precs[p]), "grouped_gemm: record precision %d", precs[p]);
     MOEHIP_REQUIRE(gs == GG_KG, "grouped_gemm: group size %d (64)", gs);
     MOEHIP_REQUIRE(T > 0 && k > 0 && E > 0 && H > 0 && I > 0 && H % GG_ROWS == 0 && I % 128 == 0,
                    "grouped_gemm: T=%d k=%d E=%d H=%d I=%d (H a multiple of 256, I of 128)", T, k, E, H, I);
@@ -453,13 +565,33 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
     uint16_t *x16 = reinterpret_cast<uint16_t *>(wsb + L.x16);
     const DeqK dk = {0x000F000Fu, 0x64006400u};
     const bool bf = xdtype == MOEHIP_DT_BF16;
+    const uint16_t *xa = bf ? x16 : xs;
+    const int *xea = bf ? xe : nullptr;
     hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, bf ? xs : nullptr, T, H, xe, x16, pmax, NP);
-    hipLaunchKernelGGL(k_gemm_up, gu, dim3(256), 0, st, bf ? x16 : xs, bf ? xe : nullptr, H, I, k, E, offsets,
-                       sorted_pos, tab, hb, pmax, dk);
+    for (int p = 0; p < P; ++p) {
+        const int64_t *tab = tabs + (size_t)p * E * 4;
+        switch (precs[p]) {
+            case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+            case MOEHIP_PREC_INT8: launch_up<MOEHIP_PREC_INT8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+            case MOEHIP_PREC_FP8: launch_up<MOEHIP_PREC_FP8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+            case MOEHIP_PREC_F16: launch_up<MOEHIP_PREC_F16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+            default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+        }
+    }
     uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
     int *he = reinterpret_cast<int *>(wsb + L.he);
     hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, pmax, NP, I, h16, he);
-    hipLaunchKernelGGL(k_gemm_down, gd, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk);
+    for (int p = 0; p < P; ++p) {
+        const int64_t *tab = tabs + (size_t)p * E * 4;
+        const int zm = zero_missing && P == 1;
+        switch (precs[p]) {
+            case MOEHIP_PREC_INT4: launch_down<MOEHIP_PREC_INT4>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_INT8: launch_down<MOEHIP_PREC_INT8>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_FP8: launch_down<MOEHIP_PREC_FP8>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_F16: launch_down<MOEHIP_PREC_F16>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            default: launch_down<MOEHIP_PREC_BF16>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+        }
+    }
     if (xdtype == MOEHIP_DT_F16)
         hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_F16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
                            accumulate);
@@ -467,4 +599,20 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
         hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_BF16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
                            accumulate);
     return check_launch("grouped_gemm");
+}
+
+extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, int xdtype, int T, int H, int I, int k,
+                                   int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
+                                   const int32_t *rank, const float *w, void *out, const void *add, int accumulate,
+                                   void *ws, size_t ws_bytes, void *stream) {
+    return gg_run(1, &prec, tab, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
+                  ws_bytes, stream, 1);
+}
+
+extern "C" int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T,
+                                         int H, int I, int k, int E, int gs, const int32_t *offsets,
+                                         const int32_t *sorted_pos, const int32_t *rank, const float *w, void *out,
+                                         const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream) {
+    return gg_run(P, precs, tabs, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
+                  ws_bytes, stream, 0);
 }

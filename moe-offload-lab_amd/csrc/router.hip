@@ -229,20 +229,15 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
     }
 }
 
-// HOBBIT levels + resident-copy choice + kernel tables for one token (k <= 64), one wave
-__global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__ idx, const float *__restrict__ w32,
-                                                     int k, moehip_policy pol, int lv0, int lv1, int lv2,
-                                                     const int64_t *__restrict__ rtab, int P, int E,
-                                                     const int64_t *__restrict__ offs, const int *__restrict__ planned,
-                                                     int64_t *__restrict__ tab, float *__restrict__ wtab,
-                                                     float *__restrict__ info, float *__restrict__ miss) {
-    const int j = threadIdx.x;
+// HOBBIT level and skip of slot j (< k <= 64) of one token: every thread of a 64-thread block calls
+// it (it synchronises the block); lanes j >= k pass wj = 0 and get a meaningless level.
+// policy.py:77-123 (unimportance over the normalised weights, stable descending rank), the fixed
+// modes (hi / lo / protected layer) and the weight threshold.
+__device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_policy &pol, int &lvl, bool &skip) {
     __shared__ float s_w[64];
     __shared__ float s_sorted[64];
     __shared__ float s_total;
     const bool act = j < k;
-    const int e = act ? (int)idx[j] : 0;
-    const float wj = act ? w32[j] : 0.f;
     s_w[j] = wj;
     __syncthreads();
     if (j == 0) {
@@ -251,8 +246,7 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
         s_total = fmaxf(tot, 1e-12f);
     }
     __syncthreads();
-    int lvl;
-    bool skip = false;
+    skip = false;
     if (pol.mode == 1 || pol.protect) {
         lvl = 0;
     } else if (pol.mode == 2) {
@@ -279,6 +273,22 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
         if (s <= pol.t1) lvl = 0;
         skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
     }
+}
+
+// HOBBIT levels + resident-copy choice + kernel tables for one token (k <= 64), one wave
+__global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__ idx, const float *__restrict__ w32,
+                                                     int k, moehip_policy pol, int lv0, int lv1, int lv2,
+                                                     const int64_t *__restrict__ rtab, int P, int E,
+                                                     const int64_t *__restrict__ offs, const int *__restrict__ planned,
+                                                     int64_t *__restrict__ tab, float *__restrict__ wtab,
+                                                     float *__restrict__ info, float *__restrict__ miss) {
+    const int j = threadIdx.x;
+    const bool act = j < k;
+    const int e = act ? (int)idx[j] : 0;
+    const float wj = act ? w32[j] : 0.f;
+    int lvl;
+    bool skip;
+    slot_level(j, k, wj, pol, lvl, skip);
     const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
     int chosen = -1;
     for (int pi = P - 1; pi >= 0; --pi) {
@@ -301,6 +311,103 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
     }
     const unsigned long long bal = __ballot(is_miss);
     if (j == 0 && miss != nullptr) miss[0] += (float)__popcll(bal);
+}
+
+// ---------------------------------------------------------------------------------------
+// T > 1 tokens (moelab/runtime.py:459-492 `_decide_general`): per-token levels and skip, then
+// after the expert-sorted dispatch one precision per expert by vote (policy.py:148-154) and the
+// per-precision record tables. The optional shared expert is slot k of every token (expert E).
+// ---------------------------------------------------------------------------------------
+
+// one block (one wave) per token: levels (T, ks) int32 and skip (T, ks) uint8; slot k < ks (the
+// shared expert) is level 0 and never skipped
+__global__ __launch_bounds__(64) void k_batch_levels(const float *__restrict__ w32, int k, int ks, moehip_policy pol,
+                                                     int32_t *__restrict__ levels, uint8_t *__restrict__ skip) {
+    const int t = blockIdx.x, j = threadIdx.x;
+    const float wj = j < k ? w32[(size_t)t * ks + j] : 0.f;
+    int lvl;
+    bool sk;
+    slot_level(j, k, wj, pol, lvl, sk);
+    if (j < k) {
+        levels[(size_t)t * ks + j] = lvl;
+        skip[(size_t)t * ks + j] = sk ? 1 : 0;
+    } else if (j < ks) {
+        levels[(size_t)t * ks + j] = 0;
+        skip[(size_t)t * ks + j] = 0;
+    }
+}
+
+struct SharedRecs {
+    int64_t r[4];
+};
+
+// one thread per expert (E routed + the shared one when has_shared): the most precise level
+// requested by at least hi_vote of its pairs, its precision (lv2p) and resident copy (as
+// k_decide_table), the table row of that precision (all other precisions' rows 0); an expert with
+// no usable copy gets rank -1 on its pairs (they contribute nothing) and counts them in miss.
+// info[e] = chosen precision, -1 = missing, -2 = no pairs.
+__global__ __launch_bounds__(64) void k_batch_vote(const int32_t *__restrict__ levels, int E, int has_shared,
+                                                   const int32_t *__restrict__ offsets,
+                                                   const int32_t *__restrict__ sorted_pos, double hi_vote, int upgrade,
+                                                   int lv0, int lv1, int lv2, const int64_t *__restrict__ rtab,
+                                                   SharedRecs srec, int P, const int64_t *__restrict__ offs,
+                                                   const int *__restrict__ planned, int64_t *__restrict__ tabs,
+                                                   int32_t *__restrict__ rank, float *__restrict__ info,
+                                                   float *__restrict__ miss) {
+    const int EA = E + (has_shared ? 1 : 0);
+    const int e = blockIdx.x * 64 + threadIdx.x;
+    if (e >= EA) return;
+    const int p0 = offsets[e], n = offsets[e + 1] - p0;
+    int chosen = -1;
+    if (n > 0) {
+        int c0 = 0, c1 = 0;
+        for (int i = 0; i < n; ++i) {
+            const int l = levels[sorted_pos[p0 + i]];
+            c0 += l <= 0;
+            c1 += l <= 1;
+        }
+        const double need = (hi_vote - 1e-9) * (double)n;
+        const int level = (double)c0 >= need ? 0 : ((double)c1 >= need ? 1 : 2);
+        const int req = level == 0 ? lv0 : (level == 1 ? lv1 : lv2);
+        for (int pi = P - 1; pi >= 0; --pi) {
+            const int64_t base = e < E ? rtab[(size_t)pi * E + e] : srec.r[pi];
+            if (base != 0 && (upgrade ? req >= pi : req == pi)) chosen = pi;
+        }
+        if (chosen >= 0 && !planned[chosen]) chosen = -1;
+    }
+    for (int pi = 0; pi < P; ++pi) {
+        const bool sel = chosen == pi;
+        const int64_t base = !sel ? 0 : (e < E ? rtab[(size_t)pi * E + e] : srec.r[pi]);
+        for (int f = 0; f < 4; ++f) tabs[((size_t)pi * EA + e) * 4 + f] = sel ? base + offs[pi * 4 + f] : 0;
+    }
+    if (n > 0 && chosen < 0) {
+        for (int i = 0; i < n; ++i) rank[sorted_pos[p0 + i]] = -1;
+        if (miss != nullptr) atomicAdd(miss, (float)n);
+    }
+    if (info != nullptr) info[e] = n == 0 ? -2.f : (float)chosen;
+}
+
+// one wave per token: the routed slots copied into (T, k + 1) arrays and slot k = the shared
+// expert (id E) with weight sigmoid(x . g), x . g rounded to the activation dtype like the shared
+// gate's output and the sigmoid rounded to it too (transformers modeling_qwen3_next.py:793-796)
+template <int DT>
+__global__ __launch_bounds__(64) void k_shared_slot(const void *__restrict__ x, const void *__restrict__ g, int H,
+                                                    const int64_t *__restrict__ idx, const float *__restrict__ w32,
+                                                    int k, int E, int64_t *__restrict__ idx_ext,
+                                                    float *__restrict__ w_ext) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    float acc = 0.f;
+    for (int c = lane; c < H; c += 64) acc += ld_act<DT>(x, (size_t)t * H + c) * ld_act<DT>(g, c);
+    acc = wave_sum(acc);
+    const int ks = k + 1;
+    if (lane < k) {
+        idx_ext[(size_t)t * ks + lane] = idx[(size_t)t * k + lane];
+        w_ext[(size_t)t * ks + lane] = w32[(size_t)t * k + lane];
+    } else if (lane == k) {
+        const float l = rnd_act<DT>(acc);
+        idx_ext[(size_t)t * ks + k] = E;
+        w_ext[(size_t)t * ks + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
+    }
 }
 
 }  // namespace moehip
@@ -349,4 +456,53 @@ extern "C" int moehip_decide_table(const int64_t *idx, const float *w32, int k, 
     hipLaunchKernelGGL(k_decide_table, dim3(1), dim3(64), 0, as_stream(stream), idx, w32, k, *pol, lv2p[0], lv2p[1],
                        lv2p[2], rtab, P, E, offs, planned, tab, wtab, info, miss);
     return check_launch("decide_table");
+}
+
+extern "C" int moehip_batch_levels(const float *w32, int T, int k, int ks, const moehip_policy *pol, int32_t *levels,
+                                   uint8_t *skip, void *stream) {
+    MOEHIP_REQUIRE(w32 && pol && levels && skip, "batch_levels: null pointer");
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 64 && ks >= k && ks <= 64, "batch_levels: T=%d k=%d ks=%d", T, k, ks);
+    hipLaunchKernelGGL(k_batch_levels, dim3(T), dim3(64), 0, as_stream(stream), w32, k, ks, *pol, levels, skip);
+    return check_launch("batch_levels");
+}
+
+extern "C" int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_t *offsets,
+                                 const int32_t *sorted_pos, double hi_vote, const moehip_policy *pol, const int *lv2p,
+                                 const int64_t *rtab, const int64_t *shared_rec, int P, const int64_t *offs,
+                                 const int *planned, int64_t *tabs, int32_t *rank, float *info, float *miss,
+                                 void *stream) {
+    MOEHIP_REQUIRE(levels && offsets && sorted_pos && pol && lv2p && rtab && offs && planned && tabs && rank,
+                   "batch_vote: null pointer");
+    MOEHIP_REQUIRE(E > 0 && P > 0 && P <= 4, "batch_vote: E=%d P=%d (1..4 precisions)", E, P);
+    MOEHIP_REQUIRE(!has_shared || shared_rec != nullptr, "batch_vote: shared expert without records");
+    for (int i = 0; i < 3; ++i) MOEHIP_REQUIRE(lv2p[i] >= 0 && lv2p[i] < P, "batch_vote: lv2p[%d]=%d", i, lv2p[i]);
+    SharedRecs sr = {{0, 0, 0, 0}};
+    if (has_shared)
+        for (int p = 0; p < P; ++p) sr.r[p] = shared_rec[p];
+    const int EA = E + (has_shared ? 1 : 0);
+    hipLaunchKernelGGL(k_batch_vote, dim3((EA + 63) / 64), dim3(64), 0, as_stream(stream), levels, E, has_shared ? 1 : 0,
+                       offsets, sorted_pos, hi_vote, pol->upgrade, lv2p[0], lv2p[1], lv2p[2], rtab, sr, P, offs, planned,
+                       tabs, rank, info, miss);
+    return check_launch("batch_vote");
+}
+
+extern "C" int moehip_shared_slot(const void *x, const void *gate, int T, int H, int dtype, const int64_t *idx,
+                                  const float *w32, int k, int E, int64_t *idx_ext, float *w_ext, void *stream) {
+    MOEHIP_REQUIRE(x && gate && idx && w32 && idx_ext && w_ext, "shared_slot: null pointer");
+    MOEHIP_REQUIRE(T > 0 && H > 0 && k > 0 && k < 64 && E > 0, "shared_slot: T=%d H=%d k=%d E=%d", T, H, k, E);
+    hipStream_t st = as_stream(stream);
+    switch (dtype) {
+        case MOEHIP_DT_F16:
+            hipLaunchKernelGGL((k_shared_slot<MOEHIP_DT_F16>), dim3(T), dim3(64), 0, st, x, gate, H, idx, w32, k, E, idx_ext, w_ext);
+            break;
+        case MOEHIP_DT_BF16:
+            hipLaunchKernelGGL((k_shared_slot<MOEHIP_DT_BF16>), dim3(T), dim3(64), 0, st, x, gate, H, idx, w32, k, E, idx_ext, w_ext);
+            break;
+        case MOEHIP_DT_F32:
+            hipLaunchKernelGGL((k_shared_slot<MOEHIP_DT_F32>), dim3(T), dim3(64), 0, st, x, gate, H, idx, w32, k, E, idx_ext, w_ext);
+            break;
+        default:
+            MOEHIP_REQUIRE(false, "shared_slot: dtype %d", dtype);
+    }
+    return check_launch("shared_slot");
 }

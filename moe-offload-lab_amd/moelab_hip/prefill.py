@@ -11,6 +11,8 @@ the host.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -88,5 +90,134 @@ class GroupedTokens:
         _lib.call("moehip_grouped_gemm", _lib.prec_code("int4"), tab.data_ptr(), x.data_ptr(), _lib.dt_code(x.dtype), T,
                   self.H, self.I, self.k, self.E, 64, self.offsets.data_ptr(), self.sorted_pos.data_ptr(),
                   self.rank.data_ptr(), w32.data_ptr(), out.data_ptr(), _lib.ptr(add), 1 if accumulate else 0,
+                  self.ws.data_ptr(), self.ws.numel(), stream)
+        return out
+
+
+class GroupedLayer:
+    """T > 1 tokens (batched decode of a few tokens, prefill chunks) through the MoE layers of a
+    `ResidentStore` on the GPU, any record precision and one precision per expert.
+
+    Replaces moelab/runtime.py:459-492 (`_decide_general`: per-token HOBBIT levels and skip,
+    stable expert sort, one precision per expert by `expert_level` vote, policy.py:148-154) and
+    runtime.py:418-436 (`_run_grouped_tokens`) for every precision the store holds. Per layer, all
+    on the device and capturable (no host round trip):
+      1. router on the T rows (moehip_router_topk), unless idx / w32 are given
+      2. Qwen3-Next shared expert as slot k of every token (moehip_shared_slot), when present
+      3. levels and skip per (token, slot)            (moehip_batch_levels)
+      4. expert-sorted dispatch of the kept pairs     (moehip_dispatch)
+      5. vote, resident copy, per-precision tables    (moehip_batch_vote)
+      6. grouped GEMMs per precision + ordered combine (moehip_grouped_gemm_multi)
+    `shared`: per layer None or {"gate": (H,) tensor in dtype, "rec": {precision: record blob}}
+    (the same form as MoEDecoder's). `info[layer]` (E + 1) holds the precision index each expert
+    ran at (-1 missing, -2 no pairs); `miss` counts pairs of experts with no usable copy."""
+
+    def __init__(self, store, k: int, max_tokens: int, policy=None, dtype=torch.float16,
+                 router_weights: list | None = None, renorm: bool = False, shared: list | None = None,
+                 planned: list | None = None):
+        from .policy import PrecisionPolicy, level_to_precision
+
+        self.store, self.k, self.max_tokens = store, k, max_tokens
+        self.policy = policy or PrecisionPolicy("lo")
+        self.dtype, self.renorm, self.router_weights = dtype, renorm, router_weights
+        self.shared = shared
+        precs = store.precisions
+        self.P = len(precs)
+        if self.P > 4:
+            raise RuntimeError("GroupedLayer: at most 4 record precisions")
+        self.H, self.I = dims(store.layouts[precs[0]])
+        for p in precs:
+            lay = store.layouts[p]
+            if dims(lay) != (self.H, self.I):
+                raise RuntimeError(f"GroupedLayer: precision {p} has dims {dims(lay)} != {(self.H, self.I)}")
+            if lay["precision"] not in ("int4", "int8", "fp8", "fp16", "bf16"):
+                raise RuntimeError(f"GroupedLayer: {lay['precision']} records are not supported (int4/int8/fp8/fp16/bf16)")
+            if lay["precision"] in ("int4", "int8") and group_size_of(lay) != (64, 64):
+                raise RuntimeError(f"GroupedLayer: {p} records need group size 64, got {group_size_of(lay)}")
+        self.device = store.device
+        _lib.check_device(self.device)
+        lib = _lib.load()
+        d, E = self.device, store.E
+        self.E = E
+        self.has_shared = shared is not None and any(s is not None for s in shared)
+        ks = k + (1 if self.has_shared else 0)
+        EA = E + (1 if self.has_shared else 0)
+        self.ks_max, self.EA_max = ks, EA
+        n = max_tokens
+        self.logits = torch.empty(n, E, dtype=dtype, device=d)
+        self.idx = torch.empty(n, k, dtype=torch.int64, device=d)
+        self.w = torch.empty(n, k, dtype=dtype, device=d)
+        self.w32 = torch.empty(n, k, dtype=torch.float32, device=d)
+        self.idx_ext = torch.empty(n, ks, dtype=torch.int64, device=d)
+        self.w_ext = torch.empty(n, ks, dtype=torch.float32, device=d)
+        self.levels = torch.empty(n, ks, dtype=torch.int32, device=d)
+        self.skip = torch.empty(n, ks, dtype=torch.uint8, device=d)
+        self.counts = torch.empty(EA, dtype=torch.int32, device=d)
+        self.offsets = torch.empty(EA + 1, dtype=torch.int32, device=d)
+        self.sorted_pos = torch.empty(n * ks, dtype=torch.int32, device=d)
+        self.rank = torch.empty(n * ks, dtype=torch.int32, device=d)
+        self.tabs = torch.zeros(self.P, EA, 4, dtype=torch.int64, device=d)
+        self.info = torch.zeros(store.L, EA, dtype=torch.float32, device=d)
+        self.miss = torch.zeros(1, dtype=torch.float32, device=d)
+        self.offs = torch.tensor([field_offsets(store.layouts[p]) for p in precs], dtype=torch.int64, device=d)
+        planned = set(planned if planned is not None else precs)
+        self.planned_dev = torch.tensor([1 if p in planned else 0 for p in precs], dtype=torch.int32, device=d)
+        self.lv2p = (ctypes.c_int * 3)(*[precs.index(level_to_precision(v, precs)) for v in range(3)])
+        self.precs_arr = (ctypes.c_int * self.P)(*[_lib.prec_code(store.layouts[p]["precision"]) for p in precs])
+        self._pols = [self.policy.device_policy(l) for l in range(store.L)]
+        self._srec = []
+        for l in range(store.L):
+            sh = shared[l] if shared is not None else None
+            if sh is None:
+                self._srec.append(None)
+                continue
+            g = sh["gate"]
+            if g.dtype != dtype or g.numel() != self.H or not g.is_contiguous() or g.device != d:
+                raise RuntimeError(f"shared gate of layer {l}: ({self.H},) {dtype} contiguous on {d}")
+            self._srec.append((ctypes.c_int64 * self.P)(*[0 if sh["rec"].get(p) is None else sh["rec"][p].data_ptr()
+                                                          for p in precs]))
+        nbytes = lib.moehip_grouped_gemm_workspace_bytes(max_tokens, ks, self.H, self.I)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=d)
+
+    def layer(self, layer: int, x: torch.Tensor, out: torch.Tensor, idx: torch.Tensor | None = None,
+              w32: torch.Tensor | None = None, add: torch.Tensor | None = None) -> torch.Tensor:
+        """out (T, H) = MoE layer `layer` on x (T, H) (+ add). With idx (T, k) int64 / w32 (T, k)
+        fp32 given, the router is skipped."""
+        T, k, st = x.shape[0], self.k, self.store
+        if T > self.max_tokens or x.shape[1] != self.H or x.dtype != self.dtype or not x.is_contiguous():
+            raise RuntimeError(f"GroupedLayer.layer: x {tuple(x.shape)} {x.dtype} (max_tokens {self.max_tokens}, "
+                               f"H {self.H}, {self.dtype}, contiguous)")
+        if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise RuntimeError("GroupedLayer.layer: out must be a contiguous tensor like x")
+        stream = _lib.stream_of(self.device)
+        if idx is None:
+            Wr = self.router_weights[layer]
+            _lib.call("moehip_router_topk", x.data_ptr(), Wr.data_ptr(), T, self.H, self.E, k,
+                      1 if self.renorm else 0, _lib.dt_code(x.dtype), self.logits.data_ptr(), self.idx.data_ptr(),
+                      self.w.data_ptr(), self.w32.data_ptr(), stream)
+            idx, w32 = self.idx[:T], self.w32[:T]
+        elif idx.shape != (T, k) or w32.shape != (T, k) or idx.dtype != torch.int64 or w32.dtype != torch.float32 \
+                or not idx.is_contiguous() or not w32.is_contiguous():
+            raise RuntimeError("GroupedLayer.layer: idx (T, k) int64 and w32 (T, k) float32, contiguous")
+        srec = self._srec[layer]
+        if srec is not None:
+            g = self.shared[layer]["gate"]
+            _lib.call("moehip_shared_slot", x.data_ptr(), g.data_ptr(), T, self.H, _lib.dt_code(x.dtype),
+                      idx.data_ptr(), w32.data_ptr(), k, self.E, self.idx_ext.data_ptr(), self.w_ext.data_ptr(), stream)
+            pidx, pw, ks, EA = self.idx_ext, self.w_ext, k + 1, self.E + 1
+        else:
+            pidx, pw, ks, EA = idx, w32, k, self.E
+        _lib.call("moehip_batch_levels", pw.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
+                  self.levels.data_ptr(), self.skip.data_ptr(), stream)
+        _lib.call("moehip_dispatch", pidx.data_ptr(), self.skip.data_ptr(), T, ks, EA, self.counts.data_ptr(),
+                  self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(), stream)
+        _lib.call("moehip_batch_vote", self.levels.data_ptr(), self.E, 1 if srec is not None else 0,
+                  self.offsets.data_ptr(), self.sorted_pos.data_ptr(), float(self.policy.hi_vote),
+                  ctypes.byref(self._pols[layer]), self.lv2p, st.rtab[layer].data_ptr(), srec, self.P,
+                  self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(), self.rank.data_ptr(),
+                  self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
+        _lib.call("moehip_grouped_gemm_multi", self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(),
+                  _lib.dt_code(x.dtype), T, self.H, self.I, ks, EA, 64, self.offsets.data_ptr(),
+                  self.sorted_pos.data_ptr(), self.rank.data_ptr(), pw.data_ptr(), out.data_ptr(), _lib.ptr(add), 0,
                   self.ws.data_ptr(), self.ws.numel(), stream)
         return out

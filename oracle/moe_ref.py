@@ -478,6 +478,22 @@ def dispatch(idx: np.ndarray, E: int, skip: np.ndarray | None = None):
     return se, sp, counts, offsets
 
 
+def decide_general(policy: "Policy", layer: int, idx: np.ndarray, w32: np.ndarray, precisions: list):
+    """runtime.py:459-492 (`_decide_general`, T > 1): per-token levels and skip
+    (policy.levels, policy.py:110-123), then for every expert with kept pairs, in ascending id,
+    the vote policy.expert_level over its pairs' levels (policy.py:148-154) and
+    level_to_precision (policy.py:188-192). Returns (skip (T, k) bool, {expert: (level,
+    precision)})."""
+    idx = np.asarray(idx, np.int64)
+    lvl, skip = policy.levels(layer, np.asarray(w32, np.float32))
+    keep = ~np.asarray(skip, bool)
+    out = {}
+    for e in np.unique(idx[keep]):
+        lev = policy.expert_level(lvl[(idx == e) & keep])
+        out[int(e)] = (lev, level_to_precision(lev, precisions))
+    return np.asarray(skip, bool), out
+
+
 def silu(v):
     return v / (1.0 + np.exp(-v))
 

@@ -211,6 +211,25 @@ def test_per_layer_t1_and_level_to_precision():
     assert [O.level_to_precision(v, ["fp16", "int8", "int4"]) for v in (0, 1, 2)] == ["fp16", "int8", "int4"]
 
 
+def test_decide_general_vote_by_hand():
+    """runtime.py:459-492 on three tokens worked by hand. With t1 = 0.6 each token's best expert has
+    s = 0 (level 0) and the others s >= 0.6 (level 2); t2 = 0.9 skips s > 0.9 at level 2.
+    token 0: w [0.7, 0.2, 0.1] -> s [0, .7, .9]    -> levels [0, 2, 2], no skip (.9 is not > .9 + 1e-6)
+    token 1: w [0.5, 0.45, 0.05] -> s [0, .5, .95] -> levels [0, 0, 2], skip slot 2
+    token 2: w [0.4, 0.35, 0.25] -> s [0, .4, .75] -> levels [0, 0, 2]
+    idx: e3 gets (t0 lvl 0, t1 lvl 0) -> 0; e5 gets (t0 lvl 2, t2 lvl 0) -> 0 (1 of 2 >= 0.5);
+    e7 gets (t0 lvl 2, t2 lvl 2) -> 2; e1 gets (t1 lvl 0, t2 lvl 0) -> 0; e9 only the skipped pair."""
+    pol = O.Policy("hobbit", t1=0.6, t2=0.9)
+    idx = np.array([[3, 5, 7], [1, 3, 9], [5, 1, 7]])
+    w = np.array([[0.7, 0.2, 0.1], [0.5, 0.45, 0.05], [0.4, 0.35, 0.25]], np.float32)
+    skip, dec = O.decide_general(pol, 0, idx, w, ["fp16", "int4"])
+    assert skip.tolist() == [[False, False, False], [False, False, True], [False, False, False]]
+    assert dec == {1: (0, "fp16"), 3: (0, "fp16"), 5: (0, "fp16"), 7: (2, "int4")}
+    # a stricter vote: e5 (1 of 2 at level 0) no longer reaches 0.75
+    pol.hi_vote = 0.75
+    assert O.decide_general(pol, 0, idx, w, ["fp16", "int4"])[1][5] == (2, "int4")
+
+
 def test_t_mid_levels():
     w = np.array([[0.5, 0.3, 0.15, 0.05]], np.float32)  # s = 0, .5, .8, .95
     lvl, skip = O.Policy("hobbit", t1=0.3, t_mid=0.85, t2=0.9).levels(0, w)
