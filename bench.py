@@ -288,22 +288,36 @@ DECODE_SPECS = {
                                        "rotated"),
 }
 
+# batched decode (T > 1 tokens per step): the grouped path over the resident store
+BATCH_SPECS = {
+    "olmoe-mixed-decode-bs8": dict(DECODE_SPECS["olmoe-mixed-decode"], batch=8,
+                                   desc="OLMoE-shaped 16-layer MoE stack, decode bs=8, each (token, expert) "
+                                        "requesting fp16 if its gate weight >= 0.15, else int4 gs64, one "
+                                        "precision per expert by vote; fp16 and int4 records of every expert "
+                                        "resident"),
+    "qwen3-next-decode-int4-bs32": dict(DECODE_SPECS["qwen3-next-decode-int4"], batch=32,
+                                        desc="Qwen3-Next-80B-A3B-shaped MoE layer, decode bs=32, 512 int4 gs64 "
+                                             "experts top-10 + sigmoid-gated shared expert, 8 layers rotated"),
+    "qwen3-next-decode-fp8-bs32": dict(DECODE_SPECS["qwen3-next-decode-fp8"], batch=32,
+                                       desc="Qwen3-Next-80B-A3B-shaped MoE layer, decode bs=32, 512 FP8 e4m3 "
+                                            "experts (128x128 block scales) top-10 + sigmoid-gated shared "
+                                            "expert, 8 layers rotated"),
+}
 
-def decode_line(args, name):
-    """One decode configuration: a HIP graph per token over L layers (fused kernel), 16 tokens;
-    algorithmic bytes per launch = the records the launch ran (from the kernel's per-row readout)
-    + router + shared gate + x/out."""
+
+def _decode_setup(sp, name):
+    """Resident store of L layers x E experts in each precision of the spec (synthetic N(0, 0.02)
+    weights), router weights, shared experts and the precision policy."""
     import torch
 
     from moelab_hip import _lib
-    from moelab_hip.layer import MoEDecoder, ResidentStore
+    from moelab_hip.layer import ResidentStore
     from moelab_hip.policy import PrecisionPolicy
     from moelab_hip.store import encode_record_, record_layout
 
-    sp = DECODE_SPECS[name]
     dev = torch.device("cuda:0")
     _lib.check_device(dev)
-    H_, I_, E_, k_, L_ = sp["H"], sp["I"], sp["E"], sp["k"], sp["L"]
+    H_, I_, E_, L_ = sp["H"], sp["I"], sp["E"], sp["L"]
     dt = getattr(torch, sp["dtype"])
     g = torch.Generator(device=dev).manual_seed(0)
     lays = {p: record_layout(p, H_, I_, 64, scale="absmax" if p in ("int4", "int8") else None) for p in sp["precs"]}
@@ -327,6 +341,20 @@ def decode_line(args, name):
     # upgrade=False: a level-2 request runs the int4 record even though the fp16 one is resident
     pol = (PrecisionPolicy(sp["policy"][0], t1=sp["policy"][1], upgrade=False) if len(sp["policy"]) > 1
            else PrecisionPolicy(sp["policy"][0]))
+    return dev, dt, g, lays, store, Wr, shared, pol
+
+
+def decode_line(args, name):
+    """One decode configuration: a HIP graph per token over L layers (fused kernel), 16 tokens;
+    algorithmic bytes per launch = the records the launch ran (from the kernel's per-row readout)
+    + router + shared gate + x/out."""
+    import torch
+
+    from moelab_hip.layer import MoEDecoder
+
+    sp = DECODE_SPECS[name]
+    H_, I_, E_, k_, L_ = sp["H"], sp["I"], sp["E"], sp["k"], sp["L"]
+    dev, dt, g, lays, store, Wr, shared, pol = _decode_setup(sp, name)
     dec = MoEDecoder(store, k_, pol, dt, router_weights=Wr, renorm=sp["renorm"], shared=shared)
     S = 16
     xs = torch.randn(S, L_, 1, H_, device=dev, generator=g).to(dt)
@@ -384,6 +412,82 @@ def decode_line(args, name):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "fused decode layer (one launch per layer, HIP graph per token)",
+                     "bytes_per_launch": int(alg)},
+        "cpu_baseline": None,
+    }
+
+
+def batch_line(args, name):
+    """Batched decode: B tokens per step through L layers on the grouped path (GroupedLayer: router,
+    levels, dispatch, per-expert vote, grouped GEMMs per precision, ordered combine), a HIP graph
+    per step, 8 distinct batches. Algorithmic bytes per layer = the distinct (expert, precision)
+    records the layer ran (from the vote's readout) + shared record + router + shared gate +
+    B x (x + out)."""
+    import torch
+
+    from moelab_hip.prefill import GroupedLayer
+
+    sp = BATCH_SPECS[name]
+    H_, I_, E_, k_, L_, B = sp["H"], sp["I"], sp["E"], sp["k"], sp["L"], sp["batch"]
+    dev, dt, g, lays, store, Wr, shared, pol = _decode_setup(sp, name)
+    gl = GroupedLayer(store, k_, B, pol, dt, router_weights=Wr, renorm=sp["renorm"], shared=shared)
+    S = 8
+    xs = torch.randn(S, L_, B, H_, device=dev, generator=g).to(dt)
+    outs = torch.zeros(S, L_, B, H_, dtype=dt, device=dev)
+    precs = store.precisions
+    run_bytes, distinct = 0, 0
+    for s_ in range(S):
+        for l in range(L_):
+            gl.layer(l, xs[s_, l], outs[s_, l])
+            info = gl.info[l].cpu()
+            for e in range(info.numel()):
+                c = int(info[e])
+                if c >= 0:
+                    run_bytes += lays[precs[c]]["record_bytes"]
+                    distinct += 1 if e < E_ else 0
+    if gl.miss.item() != 0:
+        raise RuntimeError("experts missing from the resident store")
+    alg = run_bytes / (S * L_) + E_ * H_ * 2 + (H_ * 2 if sp["shared"] else 0) + B * 2 * H_ * 2
+
+    def step(s_):
+        for l in range(L_):
+            gl.layer(l, xs[s_, l], outs[s_, l])
+
+    graphs = []
+    for s_ in range(S):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            step(s_)
+        graphs.append(gr)
+    warm = max(S, args.warmup // 8)
+    for i in range(warm):
+        graphs[i % S].replay()
+    torch.cuda.synchronize()
+    steps = max(S, args.steps // 8)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        graphs[i % S].replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    layer_us = ms * 1000 / L_
+    gbs = alg / (layer_us * 1e-6) / 1e9
+    log(f"[bench] {name}: {layer_us:.2f} us per layer, {alg / 1e6:.2f} MB per layer, {gbs:.0f} GB/s, "
+        f"{distinct / (S * L_):.1f} distinct routed experts per layer")
+    return {
+        "metric": f"MoE-layer decode tok/s + % HBM roofline, {name}, bs={B}, 1 GPU",
+        "value": round(B * 1000.0 / ms, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "+".join(sp["precs"]), "data": "synthetic",
+        "config": {"workload": sp["desc"], "d_model": H_, "experts": E_, "top_k": k_, "d_ff": I_, "layers": L_,
+                   "batch": B, "activations": sp["dtype"], "shared_expert": sp["shared"],
+                   "distinct_experts_per_layer": round(distinct / (S * L_), 2)},
+        "layer_us": round(layer_us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole layer: router + levels + dispatch + vote + k_gemm_up/down per precision "
+                               "+ combine (HIP graph per step)",
                      "bytes_per_launch": int(alg)},
         "cpu_baseline": None,
     }
@@ -606,7 +710,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload",
-                                           *DECODE_SPECS],
+                                           *DECODE_SPECS, *BATCH_SPECS],
                     default="olmoe-decode-bs1")
     ap.add_argument("--offload-layers", type=int, default=48)
     ap.add_argument("--offload-steps", type=int, default=256)
@@ -630,6 +734,9 @@ def main():
         return
     if args.workload in DECODE_SPECS:
         print(json.dumps(decode_line(args, args.workload)), flush=True)
+        return
+    if args.workload in BATCH_SPECS:
+        print(json.dumps(batch_line(args, args.workload)), flush=True)
         return
     r = gpu_bench(args)
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
