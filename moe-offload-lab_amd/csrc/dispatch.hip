@@ -1,75 +1,125 @@
 // Token-to-expert dispatch: counting sort of the routed pairs by expert, stable in pair order
 // (moelab/runtime.py:471-482: keep = ~skip, argsort(flat_e, stable=True), unique_consecutive).
 //
-// One workgroup of 1024 threads. Counts come from LDS atomics (exact), offsets from an LDS
-// scan, and each pair's rank among the earlier pairs of its expert from wave ballots: lanes of a
-// wave that hold the same expert id are matched bit by bit, and the 16 waves of a chunk then
-// claim their slots in wave order, so the result does not depend on scheduling.
+// One workgroup of 16 waves; wave w owns the contiguous pair segment [w * SEG, (w + 1) * SEG) and
+// walks it in pair order, 64 pairs at a time. In a 64-pair step the lanes holding the same
+// expert are matched by ebits ballots; the group's last lane updates the wave's own count of that
+// expert (no atomics, no cross-wave order to enforce). Pass 1 builds the per-wave counts
+// cnt[w][e]; one thread per expert turns its column into the wave starts, the experts' totals
+// are scanned (a shuffle scan per wave plus the wave totals), and pass 2 walks the segments again,
+// placing each pair at start[w][e] + its rank. Positions are stable in pair order.
 
 #include "common.hpp"
 
 namespace moehip {
 
+constexpr int DP_WAVES = 16;
+constexpr int DP_PRE = 8;  // 64-pair steps per wave whose expert ids are loaded up front
+
+// expert of pair p if it is kept (p < p1, not skipped, id in range), else -1
+__device__ __forceinline__ int pair_expert(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip, int p,
+                                           int p1, int E) {
+    if (p >= p1) return -1;
+    const int64_t e = idx[p];
+    return ((skip == nullptr || skip[p] == 0) && e >= 0 && e < E) ? (int)e : -1;
+}
+
+// positions of this 64-pair step: m = lanes with the same expert, r = rank among them
+__device__ __forceinline__ void match_lanes(int e, bool valid, int ebits, int lane, uint64_t &m, int &r) {
+    m = __ballot(valid);
+    for (int b = 0; b < ebits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+    }
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    r = __popcll(m & lt);
+}
+
 __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip,
                                                    int NP, int E, int ebits, int32_t *__restrict__ counts,
                                                    int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
                                                    int32_t *__restrict__ rank) {
-    __shared__ int s_cnt[1024];
-    __shared__ int s_run[1024];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    for (int e = tid; e < E; e += 1024) s_cnt[e] = 0;
+    extern __shared__ int s_cnt[];  // [DP_WAVES][E]: counts, then each wave's start per expert
+    __shared__ int s_wtot[DP_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int SEG = (NP + DP_WAVES - 1) / DP_WAVES;
+    const int p0 = wave * SEG, p1 = min(NP, p0 + SEG);
+    for (int i = tid; i < DP_WAVES * E; i += 1024) s_cnt[i] = 0;
     __syncthreads();
-    for (int p = tid; p < NP; p += 1024) {
-        const int64_t e = idx[p];
-        if ((skip == nullptr || skip[p] == 0) && e >= 0 && e < E) atomicAdd(&s_cnt[(int)e], 1);
+    int *mine = s_cnt + wave * E;
+    // the expert of each of the first DP_PRE steps' pairs, loaded at once (-1 = not a kept pair)
+    int pre[DP_PRE];
+#pragma unroll
+    for (int i = 0; i < DP_PRE; ++i) pre[i] = pair_expert(idx, skip, p0 + 64 * i + lane, p1, E);
+    // pass 1: per-wave counts (only the wave itself touches its row)
+    for (int base = p0, step = 0; base < p1; base += 64, ++step) {
+        const int p = base + lane;
+        int ev = -1;
+#pragma unroll
+        for (int i = 0; i < DP_PRE; ++i)
+            if (step == i) ev = pre[i];
+        if (step >= DP_PRE) ev = pair_expert(idx, skip, p, p1, E);
+        const bool valid = ev >= 0;
+        const int e = valid ? ev : 0;
+        uint64_t m;
+        int r;
+        match_lanes(e, valid, ebits, lane, m, r);
+        if (valid && r == __popcll(m) - 1) mine[e] += r + 1;
+        __builtin_amdgcn_wave_barrier();  // the row update is seen by the wave's next step
     }
     __syncthreads();
-    // inclusive Hillis-Steele scan over E entries (in s_run), then exclusive offsets
-    for (int e = tid; e < E; e += 1024) s_run[e] = s_cnt[e];
-    __syncthreads();
-    for (int off = 1; off < E; off <<= 1) {
-        int add = 0;
-        if (tid < E && tid >= off) add = s_run[tid - off];
-        __syncthreads();
-        if (tid < E) s_run[tid] += add;
-        __syncthreads();
-    }
+    // per expert: column prefix over the waves (wave starts relative to the expert's offset)
+    int tot = 0;  // E <= 1024: thread e owns expert e
     if (tid < E) {
-        const int excl = s_run[tid] - s_cnt[tid];
-        counts[tid] = s_cnt[tid];
-        offsets[tid] = excl;
-        if (tid == E - 1) offsets[E] = s_run[tid];
+        for (int w = 0; w < DP_WAVES; ++w) {
+            const int c = s_cnt[w * E + tid];
+            s_cnt[w * E + tid] = tot;
+            tot += c;
+        }
+        counts[tid] = tot;
     }
+    // exclusive scan of the experts' totals: 64 experts per wave, then the waves' totals
+    int incl = tot;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+    }
+    if (lane == 63) s_wtot[wave] = incl;
     __syncthreads();
-    const int total = s_run[E - 1];
+    int wbase = 0;
+    for (int w = 0; w < wave; ++w) wbase += s_wtot[w];
+    const int excl = wbase + incl - tot;
+    if (tid < E) {
+        offsets[tid] = excl;
+        for (int w = 0; w < DP_WAVES; ++w) s_cnt[w * E + tid] += excl;
+        if (tid == E - 1) offsets[E] = excl + tot;
+    }
+    int total = 0;
+    for (int w = 0; w < DP_WAVES; ++w) total += s_wtot[w];
     __syncthreads();
-    if (tid < E) s_run[tid] = s_run[tid] - s_cnt[tid];  // running insertion point per expert
-    __syncthreads();
-    const unsigned long long lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int base = 0; base < NP; base += 1024) {
-        const int p = base + tid;
-        const int64_t e64 = p < NP ? idx[p] : -1;
-        const bool valid = p < NP && (skip == nullptr || skip[p] == 0) && e64 >= 0 && e64 < E;
-        const int e = valid ? (int)e64 : 0;
-        unsigned long long m = __ballot(valid);
-        for (int b = 0; b < ebits; ++b) {
-            const bool bit = (e >> b) & 1;
-            const unsigned long long bal = __ballot(bit);
-            m &= bit ? bal : ~bal;
+    // pass 2: placement
+    for (int base = p0, step = 0; base < p1; base += 64, ++step) {
+        const int p = base + lane;
+        int ev = -1;
+#pragma unroll
+        for (int i = 0; i < DP_PRE; ++i)
+            if (step == i) ev = pre[i];
+        if (step >= DP_PRE) ev = pair_expert(idx, skip, p, p1, E);
+        const bool valid = ev >= 0;
+        const int e = valid ? ev : 0;
+        uint64_t m;
+        int r;
+        match_lanes(e, valid, ebits, lane, m, r);
+        if (valid) {
+            const int pos = mine[e] + r;
+            sorted_pos[pos] = p;
+            rank[p] = pos;
         }
-        const int r_in_wave = __popcll(m & lt);
-        const int c_in_wave = __popcll(m);
-        for (int w = 0; w < 16; ++w) {
-            __syncthreads();
-            if (wave == w && valid) {
-                const int pos = s_run[e] + r_in_wave;
-                sorted_pos[pos] = p;
-                rank[p] = pos;
-                if (r_in_wave == c_in_wave - 1) s_run[e] = pos + 1;
-            }
-        }
-        if (p < NP && !valid) rank[p] = -1;
+        __builtin_amdgcn_wave_barrier();
+        if (valid && r == __popcll(m) - 1) mine[e] += r + 1;
+        __builtin_amdgcn_wave_barrier();
+        if (p < p1 && !valid) rank[p] = -1;
     }
     for (int i = total + tid; i < NP; i += 1024) sorted_pos[i] = -1;
 }
@@ -85,7 +135,15 @@ extern "C" int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, i
                    "dispatch: bad sizes T=%d k=%d E=%d", T, k, E);
     int ebits = 0;
     while ((1 << ebits) < E) ++ebits;
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, as_stream(stream), idx, skip, T * k, E, ebits, counts,
+    const size_t lds = (size_t)DP_WAVES * E * sizeof(int);
+    static bool big_lds = false;  // more than 64 KiB of dynamic LDS must be enabled once per kernel
+    if (lds > 60 * 1024 && !big_lds) {
+        MOEHIP_REQUIRE(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_dispatch),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess,
+                       "dispatch: cannot enable %zu bytes of LDS", lds);
+        big_lds = true;
+    }
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), lds, as_stream(stream), idx, skip, T * k, E, ebits, counts,
                        offsets, sorted_pos, rank);
     return check_launch("dispatch");
 }

@@ -298,18 +298,34 @@ __device__ __forceinline__ int row_exp(float m) {
 }
 
 // bf16 activations, one wave per row: xe[r] = row_exp(max |x[r]|) and x16[r] = fp16(x[r] * 2^-xe[r])
-// (exact for bf16 values in range); pmax[0..NP) = 0
+// (exact for bf16 values in range), 8 values per 16-byte load and store; pmax[0..NP) = 0.
+// H is a multiple of 8.
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
 __global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, int T, int H, int *__restrict__ xe,
                                               uint16_t *__restrict__ x16, uint32_t *__restrict__ pmax, int NP) {
     for (int i = blockIdx.x * 256 + threadIdx.x; i < NP; i += gridDim.x * 256) pmax[i] = 0u;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (r >= T || x == nullptr) return;
+    const uint4 *src = reinterpret_cast<const uint4 *>(x + (size_t)r * H);
+    uint4 *dst = reinterpret_cast<uint4 *>(x16 + (size_t)r * H);
+    const int nv = H / 8;
     float m = 0.f;
-    for (int c = lane; c < H; c += 64) m = fmaxf(m, fabsf(bf16_to_f32(x[(size_t)r * H + c])));
+    for (int c = lane; c < nv; c += 64) {
+        const uint4 v = src[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf16_lo(w[i])), fabsf(bf16_hi(w[i]))));
+    }
     m = wave_max(m);
     const int e = row_exp(m);
     const float sc = ldexpf(1.0f, -e);
-    for (int c = lane; c < H; c += 64) x16[(size_t)r * H + c] = f32_to_f16_rne(bf16_to_f32(x[(size_t)r * H + c]) * sc);
+    for (int c = lane; c < nv; c += 64) {
+        const uint4 v = src[c];
+        dst[c] = make_uint4(pack_h2(bf16_lo(v.x) * sc, bf16_hi(v.x) * sc), pack_h2(bf16_lo(v.y) * sc, bf16_hi(v.y) * sc),
+                            pack_h2(bf16_lo(v.z) * sc, bf16_hi(v.z) * sc), pack_h2(bf16_lo(v.w) * sc, bf16_hi(v.w) * sc));
+    }
     if (lane == 0) xe[r] = e;
 }
 
@@ -353,8 +369,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
-        if (nm == 2) k_loop<PREC, 3, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
-        else k_loop<PREC, 3, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        if (nm == 2) k_loop<PREC, 2, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
+        else k_loop<PREC, 2, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
         // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32; per-pair max
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -437,8 +453,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
-        if (nm == 2) k_loop<PREC, 3, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
-        else k_loop<PREC, 3, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        if (nm == 2) k_loop<PREC, 2, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        else k_loop<PREC, 2, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             if (mt >= nm) break;

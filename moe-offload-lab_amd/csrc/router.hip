@@ -110,7 +110,19 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(const void *__restri
     const uint16_t *wr = reinterpret_cast<const uint16_t *>(Wr) + (size_t)min(e0 + r, E - 1) * H + kq * 8;
     const int kw = H >> 2;
     rf32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = wave * kw; k0 < (wave + 1) * kw; k0 += 128) {
+    int k0 = wave * kw;
+    const int kend = (wave + 1) * kw;
+    for (; k0 + 512 <= kend; k0 += 512) {  // 32 loads in flight at once
+        uint4 av[16], bv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            av[u] = *reinterpret_cast<const uint4 *>(xr + k0 + 32 * u);
+            bv[u] = *reinterpret_cast<const uint4 *>(wr + k0 + 32 * u);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc = router_mfma<DT>(av[u], bv[u], acc);
+    }
+    for (; k0 < kend; k0 += 128) {
         uint4 av[4], bv[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -169,22 +181,42 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
     }
     sum = wave_sum(sum);
     if constexpr (DT != MOEHIP_DT_F32) {
+        int myc = 0;
+        uint32_t myk = 0u;
         for (int j = 0; j < k; ++j) {
             uint32_t lb = 0u;
 #pragma unroll
             for (int i = 0; i < 16; ++i) lb = max(lb, key[i]);
             const uint32_t M = wave_max_u32(lb);
-            const int c = 1023 - (int)(M & 1023u);
 #pragma unroll
             for (int i = 0; i < 16; ++i)
                 if (key[i] == M) key[i] = 0u;  // keys are distinct: exactly one lane clears one
-            if (lane == 0) s_idx[j] = c;
+            if (lane == j) {
+                myc = 1023 - (int)(M & 1023u);
+                myk = M >> 10;
+            }
         }
-        __syncthreads();
         if (lane < k) {
-            const int c = s_idx[lane];
-            s_p[lane] = expf(ld_act<DT>(logits, (size_t)t * E + c) - m) / sum;
+            // the logit from its key (the inverse of topk_key16; -0 came back as +0, same value)
+            const uint32_t b = (myk & 0x8000u) ? (myk & 0x7fffu) : (~myk & 0xffffu);
+            const float v = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
+            const float p = expf(v - m) / sum;
+            s_p[lane] = p;
+            s_idx[lane] = myc;
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float tot = 0.f;
+        if (renorm)
+            for (int j = 0; j < k; ++j) tot += s_p[j];
+        if (lane < k) {
+            const float p = renorm ? s_p[lane] / tot : s_p[lane];
+            idx[(size_t)t * k + lane] = myc;
+            const float r = rnd_act<DT>(p);
+            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
+            if (w32 != nullptr) w32[(size_t)t * k + lane] = r;
+        }
+        return;
     } else {
         uint32_t taken = 0;
         for (int j = 0; j < k; ++j) {
