@@ -246,6 +246,18 @@ int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, cons
                               size_t ws_bytes, void *stream);
 
 /*
+ * moehip_grouped_gemm_multi with the expert products as batched dequant GEMVs instead of MFMA
+ * tiles (for few tokens per expert: batched decode): weight rows streamed whole with 16-byte
+ * loads and read once per launch however many tokens the expert has, v_dot2_f32_f16 products
+ * against each token's activations; same arguments, workspace and results up to fp32 summation
+ * order. Replaces the same reference code as moehip_grouped_gemm_multi.
+ */
+int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H,
+                              int I, int k, int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
+                              const int32_t *rank, const float *w, void *out, const void *add, int accumulate, void *ws,
+                              size_t ws_bytes, void *stream);
+
+/*
  * HOBBIT levels of T tokens (moelab/policy.py:110-123 `levels`, the T > 1 branch of
  * runtime.py:459-470): w32 (T, ks) fp32, the first k slots routed; levels (T, ks) int32 and skip
  * (T, ks) uint8 (1 = skipped). Slots k..ks-1 (the shared expert) get level 0 and are never

@@ -298,14 +298,13 @@ __device__ __forceinline__ int row_exp(float m) {
 }
 
 // bf16 activations, one wave per row: xe[r] = row_exp(max |x[r]|) and x16[r] = fp16(x[r] * 2^-xe[r])
-// (exact for bf16 values in range), 8 values per 16-byte load and store; pmax[0..NP) = 0.
+// (exact for bf16 values in range), 8 values per 16-byte load and store.
 // H is a multiple of 8.
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
 __global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, int T, int H, int *__restrict__ xe,
-                                              uint16_t *__restrict__ x16, uint32_t *__restrict__ pmax, int NP) {
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < NP; i += gridDim.x * 256) pmax[i] = 0u;
+                                              uint16_t *__restrict__ x16) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (r >= T || x == nullptr) return;
     const uint4 *src = reinterpret_cast<const uint4 *>(x + (size_t)r * H);
@@ -331,18 +330,17 @@ __global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, in
 
 // ---------------------------------------------------------------------------------------
 // up: tiles (expert, 128 h columns); wave w: h columns nb*128 + 32 w + (lane % 32), subtile 0 =
-// gate rows, subtile 1 = up rows. Writes h (pairs, I) fp32 and pmax[pair] = max |h| (atomic).
+// gate rows, subtile 1 = up rows. Writes h (pairs, I) fp32.
 // ---------------------------------------------------------------------------------------
 // x: fp16 activations (the caller's, or x16 with exponents xe for bf16 input; xe null = 0)
 template <int PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_up(
     const uint16_t *__restrict__ x, const int *__restrict__ xe, int H, int I, int k, int E,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
-    float *__restrict__ hb, uint32_t *__restrict__ pmax, DeqK dk) {
+    float *__restrict__ hb, DeqK dk) {
     constexpr int CK = GgPrec<PREC>::CK;
     __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<CK>::LDA];
     __shared__ int s_e[GG_TOK];
-    __shared__ uint32_t s_mx[GG_TOK];
     const int NB = I / 128;
     int e, nb;
     if (!tile_of(blockIdx.x, E, NB, e, nb)) return;
@@ -363,7 +361,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int xr = sok ? sorted_pos[p0 + m0 + stok] / k : 0;
         const int ex = (sok && xe != nullptr) ? xe[xr] : 0;
         if ((tid & 3) == 0) s_e[stok] = ex;
-        if ((tid & 3) == 1) s_mx[stok] = 0u;  // ordered before their use by k_loop's barriers
         f32x16 d[2][2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
@@ -371,7 +368,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
         if (nm == 2) k_loop<PREC, 2, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
         else k_loop<PREC, 2, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
-        // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32; per-pair max
+        // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             if (mt >= nm) break;
@@ -381,34 +378,286 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const float f = ldexpf(1.0f, s_e[tok]);
                 const float hv = silu_mul(d[mt][0][r] * f, d[mt][1][r] * f);
                 if (tok < mn) hb[(size_t)(p0 + m0 + tok) * I + col] = hv;
-                float m = tok < mn ? fabsf(hv) : 0.f;
-                m = fmaxf(m, dpp_f<0xB1>(m));  // max over the 16-lane row (16 columns of one token)
-                m = fmaxf(m, dpp_f<0x4E>(m));
-                m = fmaxf(m, dpp_f<0x141>(m));
-                m = fmaxf(m, dpp_f<0x140>(m));
-                if ((lane & 15) == 0 && tok < mn) atomicMax(&s_mx[tok], __float_as_uint(m));
             }
         }
-        __syncthreads();
-        if (tid < mn) atomicMax(&pmax[p0 + m0 + tid], s_mx[tid]);
-        __syncthreads();
+        __syncthreads();  // s_e of the next pass
     }
 }
 
-// one wave per pair: he[p] = row_exp(pmax[p]), h16[p] = fp16(h[p] * 2^-he[p])
-__global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, const uint32_t *__restrict__ pmax, int NP,
-                                             int I, uint16_t *__restrict__ h16, int *__restrict__ he) {
+// one wave per pair: he[p] = row_exp(max |h[p]|), h16[p] = fp16(h[p] * 2^-he[p])
+__global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, int NP, int I, uint16_t *__restrict__ h16,
+                                             int *__restrict__ he) {
     const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (p >= NP) return;
-    const int e = row_exp(__uint_as_float(pmax[p]));
-    const float sc = ldexpf(1.0f, -e);
     const float4 *src = reinterpret_cast<const float4 *>(hb + (size_t)p * I);
+    float m = 0.f;
+    for (int c = lane; c < I / 4; c += 64) {
+        const float4 v = src[c];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    const int e = row_exp(wave_max(m));
+    const float sc = ldexpf(1.0f, -e);
     uint2 *dst = reinterpret_cast<uint2 *>(h16 + (size_t)p * I);
     for (int c = lane; c < I / 4; c += 64) {
         const float4 v = src[c];
         dst[c] = make_uint2(pack_h2(v.x * sc, v.y * sc), pack_h2(v.z * sc, v.w * sc));
     }
     if (lane == 0) he[p] = e;
+}
+
+// ---------------------------------------------------------------------------------------
+// Batched GEMV for few tokens per expert (batched decode): the same h / y as the MFMA kernels,
+// computed with v_dot2_f32_f16 against weights streamed in whole rows. A row of K values is
+// C = K / VPC chunks of 16 bytes; G = 2^lg lanes share a row, lane cl owning chunks cl + i G
+// (i < CPL), so RPW = 64 / G rows per wave pass and P passes per wave, every load of the P passes
+// issued before any is used. A chunk's B values come from the MFMA path's converters (operand
+// order c0 c4 c1 c5 c2 c6 c3 c7 per 8 values, one fp16 rounding of the scaled weight); the lane's
+// activation slice of each token is permuted the same way when it is loaded. The expert's tokens
+// run GV_NT at a time against the weights held in registers (weights are read once however many
+// tokens the expert has).
+// ---------------------------------------------------------------------------------------
+constexpr int GV_NT = 4;
+constexpr int GV_TG = GV_NT;  // tokens of one expert per workgroup (more tokens: more work items)
+constexpr int GV_MAXROWS = 512; // rows of one workgroup (their outputs are staged in LDS)
+
+// raw scale of chunk c of a row (int4 / int8: fp16 bits of its group; fp8: fp32 bits of its block)
+template <int PREC>
+__device__ __forceinline__ uint32_t gv_scale(gu8 *sb, int row, int c, int K) {
+    constexpr int VPC = Fmt<PREC>::VPC;
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8)
+        return *(const __attribute__((address_space(1))) uint16_t *)(sb + ((size_t)row * (K / GG_KG) + (c * VPC) / GG_KG) * 2);
+    else if constexpr (PREC == MOEHIP_PREC_FP8)
+        return *(const __attribute__((address_space(1))) uint32_t *)(sb + ((size_t)(row >> 7) * (K >> 7) + ((c * VPC) >> 7)) * 4);
+    else
+        return 0u;
+}
+
+// the chunk's VPC values as fp16 pairs in operand order (VPC / 2 dwords)
+template <int PREC>
+__device__ __forceinline__ void gv_deq(const uint4 q, uint32_t sraw, DeqK dk, uint32_t *wv) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+        const uint32_t sw = sraw & 0xffffu;
+        const half2_t s2 = __builtin_bit_cast(half2_t, sw | (sw << 16));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint4 u = __builtin_bit_cast(uint4, wdeq8(d[b], s2, dk));
+            wv[4 * b] = u.x, wv[4 * b + 1] = u.y, wv[4 * b + 2] = u.z, wv[4 * b + 3] = u.w;
+        }
+    } else if constexpr (PREC == MOEHIP_PREC_INT8 || PREC == MOEHIP_PREC_FP8) {
+        uint32_t sw;
+        if constexpr (PREC == MOEHIP_PREC_INT8) sw = sraw & 0xffffu;
+        else sw = f32_to_f16_rne(__uint_as_float(sraw) * 256.0f);
+        const half2_t s2 = __builtin_bit_cast(half2_t, sw | (sw << 16));
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint4 u = __builtin_bit_cast(uint4, PREC == MOEHIP_PREC_INT8 ? wdeq8_i8(d[2 * b], d[2 * b + 1], s2)
+                                                                              : wdeq8_fp8(d[2 * b], d[2 * b + 1], s2));
+            wv[4 * b] = u.x, wv[4 * b + 1] = u.y, wv[4 * b + 2] = u.z, wv[4 * b + 3] = u.w;
+        }
+    } else {
+        const uint4 u = __builtin_bit_cast(uint4, wdeq8_16<PREC>(d[0], d[1], d[2], d[3]));
+        wv[0] = u.x, wv[1] = u.y, wv[2] = u.z, wv[3] = u.w;
+    }
+}
+
+// activation slice of chunk c of a row of K fp16 values (VPC / 8 16-byte loads), and its
+// permutation into operand order (VPC / 2 dwords), done once the weight loads are issued
+template <int VPC>
+__device__ __forceinline__ void gv_slice_load(const uint16_t *row, int c, uint4 *raw) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)c * VPC);
+#pragma unroll
+    for (int b = 0; b < VPC / 8; ++b) raw[b] = p[b];
+}
+template <int VPC>
+__device__ __forceinline__ void gv_slice_perm(const uint4 *raw, uint32_t *xv) {
+#pragma unroll
+    for (int b = 0; b < VPC / 8; ++b) {
+        const uint4 u = raw[b];
+        xv[4 * b] = lo_lo(u.x, u.z), xv[4 * b + 1] = hi_hi(u.x, u.z);
+        xv[4 * b + 2] = lo_lo(u.y, u.w), xv[4 * b + 3] = hi_hi(u.y, u.w);
+    }
+}
+
+// NG row groups of 4 P RPW rows from r0 (gate and up rows for UP) of one expert, against up to
+// GV_NT of its tokens; UP: h[pair, r] = silu(gate . x) * (up . x); else y[pair, r] = w 2^he (down . h).
+// The loads of group g + 1 are issued before group g is computed (two register buffers).
+template <int PREC, int CPL, int P, bool UP>
+__device__ __forceinline__ void gv_rows(const uint16_t *act, const int *ae, int K, int rows, int I, int k, int p0,
+                                        int nt, const int32_t *sorted_pos, gu8 *qb, gu8 *sb, int lg, int r0, int NG,
+                                        const float *w, float *out, int ostride, DeqK dk) {
+    constexpr int VPC = Fmt<PREC>::VPC, ND = VPC / 2, NM = UP ? 2 : 1;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int G = 1 << lg, RPW = 64 >> lg, slot = lane >> lg, cl = lane & (G - 1);
+    const int C = K / VPC;
+    const size_t RB = (size_t)C * 16;
+    const int GROWS = 4 * P * RPW;  // rows per group
+    __shared__ float s_out[GV_NT][GV_MAXROWS];
+    // the tokens first (their loads do not queue behind the weights'), then the activation slices
+    int pr[GV_NT], src[GV_NT];
+#pragma unroll
+    for (int t = 0; t < GV_NT; ++t) {
+        pr[t] = p0 + min(t, nt - 1);
+        src[t] = UP ? sorted_pos[pr[t]] / k : pr[t];  // UP: the token's row of x; else the pair's h
+    }
+    uint4 xr[GV_NT][CPL][VPC / 8];
+    float f[GV_NT];
+#pragma unroll
+    for (int t = 0; t < GV_NT; ++t) {
+        const uint16_t *row = act + (size_t)src[t] * K;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) gv_slice_load<VPC>(row, min(cl + i * G, C - 1), xr[t][i]);
+        const int ex = ae != nullptr ? ae[src[t]] : 0;
+        f[t] = UP ? ldexpf(1.0f, ex) : w[sorted_pos[pr[t]]] * ldexpf(1.0f, ex);
+    }
+    uint4 q[2][P][NM][CPL];
+    uint32_t sr[2][P][NM][CPL];
+    auto load = [&](int buf, int g) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int r = min(r0 + g * GROWS + (wave * P + p) * RPW + slot, rows - 1);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const int row = r + m * I;  // UP: gate row r, up row I + r
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) {
+                    // every load unconditional (clamped chunk): a load under a lane-dependent
+                    // branch is waited for before the next one is issued
+                    const int c = min(cl + i * G, C - 1);
+                    q[buf][p][m][i] = gld16(qb + (size_t)row * RB + (size_t)c * 16);
+                    sr[buf][p][m][i] = gv_scale<PREC>(sb, row, c, K);
+                }
+            }
+        }
+    };
+    load(0, 0);
+    uint32_t xv[GV_NT][CPL][ND];
+#pragma unroll
+    for (int t = 0; t < GV_NT; ++t)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) gv_slice_perm<VPC>(xr[t][i], xv[t][i]);
+    auto compute = [&](int buf, int g) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            float acc[NM][GV_NT];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+#pragma unroll
+                for (int t = 0; t < GV_NT; ++t) acc[m][t] = 0.f;
+#pragma unroll
+                for (int i = 0; i < CPL; ++i) {
+                    // lanes past the row's chunks (G > C / CPL) use zero bytes and scale 0: nothing
+                    const bool ok = cl + i * G < C;
+                    uint32_t wv[ND];
+                    gv_deq<PREC>(ok ? q[buf][p][m][i] : make_uint4(0u, 0u, 0u, 0u), ok ? sr[buf][p][m][i] : 0u, dk,
+                                 wv);
+#pragma unroll
+                    for (int t = 0; t < GV_NT; ++t) {
+                        if (t < nt) {
+#pragma unroll
+                            for (int j = 0; j < ND; ++j) acc[m][t] = dot2h(wv[j], xv[t][i][j], acc[m][t]);
+                        }
+                    }
+                }
+            }
+            const int r = r0 + g * GROWS + (wave * P + p) * RPW + slot;
+#pragma unroll
+            for (int t = 0; t < GV_NT; ++t) {
+                if (t < nt) {
+                    const float a0 = group_sum(acc[0][t], lg);
+                    if constexpr (UP) {
+                        const float a1 = group_sum(acc[NM - 1][t], lg);
+                        const float hv = silu_mul(a0 * f[t], a1 * f[t]);
+                        if (cl == 0) s_out[t][r - r0] = hv;
+                    } else {
+                        if (cl == 0) s_out[t][r - r0] = f[t] * a0;
+                    }
+                }
+            }
+        }
+    };
+    for (int g = 0; g < NG; g += 2) {
+        if (g + 1 < NG) load(1, g + 1);
+        compute(0, g);
+        if (g + 1 < NG) {
+            if (g + 2 < NG) load(0, g + 2);
+            compute(1, g + 1);
+        }
+    }
+    // the outputs, written once the weight stream is done (a store makes every later wait for
+    // a load also wait for the store's acknowledgement)
+    __syncthreads();
+    const int nrows = min(NG * GROWS, rows - r0);
+    for (int i = threadIdx.x; i < nt * nrows; i += 256) {
+        const int t = i / nrows, rr = i - t * nrows;
+        out[(size_t)(p0 + t) * ostride + r0 + rr] = s_out[t][rr];
+    }
+}
+
+// work items of the batched GEMVs: (expert, token group of GV_TG) for every expert with pairs, in
+// expert order (one workgroup, exclusive scan of ceil(n_e / GV_TG)); items[NP] = their number
+__global__ __launch_bounds__(1024) void k_gv_items(const int32_t *__restrict__ offsets, int E, int NP,
+                                                   int32_t *__restrict__ items) {
+    __shared__ int s_w[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int base = 0;
+    for (int e0 = 0; e0 < E; e0 += 1024) {
+        const int e = e0 + tid;
+        const int n = e < E ? offsets[e + 1] - offsets[e] : 0;
+        const int nz = (n + GV_TG - 1) / GV_TG;
+        int incl = nz;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        if (lane == 63) s_w[wave] = incl;
+        __syncthreads();
+        int wb = base, tot = base;
+        for (int w = 0; w < 16; ++w) {
+            if (w < wave) wb += s_w[w];
+            tot += s_w[w];
+        }
+        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
+        base = tot;
+        __syncthreads();
+    }
+    if (tid == 0) items[NP] = base;
+}
+
+// grid (row blocks, NP): block (b, i) covers rows [b * NG * 4 P RPW, ...) of work item i (expert e,
+// its tokens [z * GV_TG, (z + 1) * GV_TG)) when i < items[NP]
+template <int PREC, int CPL, int P>
+__global__ __launch_bounds__(256) void k_gemv_up(const uint16_t *__restrict__ x, const int *__restrict__ xe, int H,
+                                                 int I, int k, const int32_t *__restrict__ items, int NP,
+                                                 const int32_t *__restrict__ offsets,
+                                                 const int32_t *__restrict__ sorted_pos,
+                                                 const int64_t *__restrict__ tab, float *__restrict__ hb, DeqK dk,
+                                                 int lg, int NG) {
+    if ((int)blockIdx.y >= items[NP]) return;
+    const int it = items[blockIdx.y], e = it >> 8;
+    const int p0 = offsets[e] + (it & 255) * GV_TG, ne = min(GV_TG, offsets[e + 1] - p0);
+    gu8 *qb = record_ptr(tab[4 * e + 0]);
+    if (ne <= 0 || qb == nullptr) return;
+    const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
+    gv_rows<PREC, CPL, P, true>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 1]), lg, r0, NG,
+                                nullptr, hb, I, dk);
+}
+
+template <int PREC, int CPL, int P>
+__global__ __launch_bounds__(256) void k_gemv_down(const uint16_t *__restrict__ h16, const int *__restrict__ he, int H,
+                                                   int I, const int32_t *__restrict__ items, int NP,
+                                                   const int32_t *__restrict__ offsets,
+                                                   const int32_t *__restrict__ sorted_pos,
+                                                   const int64_t *__restrict__ tab, const float *__restrict__ w,
+                                                   float *__restrict__ y, DeqK dk, int lg, int NG) {
+    if ((int)blockIdx.y >= items[NP]) return;
+    const int it = items[blockIdx.y], e = it >> 8;
+    const int p0 = offsets[e] + (it & 255) * GV_TG, ne = min(GV_TG, offsets[e + 1] - p0);
+    gu8 *qb = record_ptr(tab[4 * e + 2]);
+    if (ne <= 0 || qb == nullptr) return;
+    const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
+    gv_rows<PREC, CPL, P, false>(h16, he, I, H, 0, 1, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 3]), lg, r0, NG,
+                                 w, y, H, dk);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -500,7 +749,7 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
 }
 
 struct GgLayout {
-    size_t xe, x16, pmax, h, h16, he, y, total;
+    size_t xe, x16, h, h16, he, y, items, total;
 };
 static GgLayout gg_layout(int T, int k, int H, int I) {
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -511,8 +760,6 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     off = al(off + (size_t)T * 4);
     L.x16 = off;
     off = al(off + (size_t)T * H * 2);
-    L.pmax = off;
-    off = al(off + NP * 4);
     L.h = off;
     off = al(off + NP * I * 4);
     L.h16 = off;
@@ -521,6 +768,8 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     off = al(off + NP * 4);
     L.y = off;
     off = al(off + NP * H * 4);
+    L.items = off;
+    off = al(off + (NP + 1) * 4);
     L.total = off;
     return L;
 }
@@ -536,9 +785,8 @@ extern "C" size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I
 
 template <int PREC>
 static void launch_up(dim3 g, hipStream_t st, const uint16_t *x, const int *xe, int H, int I, int k, int E,
-                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *hb, uint32_t *pmax,
-                      DeqK dk) {
-    hipLaunchKernelGGL((k_gemm_up<PREC>), g, dim3(256), 0, st, x, xe, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk);
+                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *hb, DeqK dk) {
+    hipLaunchKernelGGL((k_gemm_up<PREC>), g, dim3(256), 0, st, x, xe, H, I, k, E, offsets, sorted_pos, tab, hb, dk);
 }
 template <int PREC>
 static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *he, int H, int I, int E,
@@ -546,6 +794,73 @@ static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *
                         DeqK dk, int zero_missing) {
     hipLaunchKernelGGL((k_gemm_down<PREC>), g, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk,
                        zero_missing);
+}
+
+// batched GEMV launch geometry for rows of K values: G = 2^lg lanes per row, CPL chunks per lane,
+// P passes per wave (P * CPL = 4 16-byte loads per lane and matrix in flight)
+struct GvGeo {
+    int lg, cpl, p, rows_per_block;
+};
+static GvGeo gv_geo(int prec, int K) {
+    const int vpc = prec == MOEHIP_PREC_INT4 ? 32 : ((prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8) ? 16 : 8);
+    const int C = K / vpc;
+    int lg = 0;
+    while ((1 << lg) < C && lg < 6) ++lg;
+    GvGeo g;
+    g.lg = lg;
+    g.cpl = (C + (1 << lg) - 1) >> lg;
+    g.p = g.cpl >= 4 ? 1 : 4 / g.cpl;
+    g.rows_per_block = 4 * g.p * (64 >> lg);
+    return g;
+}
+
+template <int PREC, int CPL>
+static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const uint16_t *act, const int *ae,
+                          int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
+                          float *out, const float *w, DeqK dk) {
+    constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
+    // row groups per workgroup: up to 128 KiB of weights and GV_MAXROWS rows, while the pairs
+    // (an upper bound of the work items) still give about two workgroups per CU slot
+    const int groups = (rows + g.rows_per_block - 1) / g.rows_per_block;
+    const int row_bytes = (up ? 2 : 1) * (up ? H : I) * (PREC == MOEHIP_PREC_INT4 ? 1 : (PREC == MOEHIP_PREC_INT8 || PREC == MOEHIP_PREC_FP8 ? 2 : 4)) / 2;
+    int ng = max(1, min(groups, (128 << 10) / max(1, g.rows_per_block * row_bytes)));
+    ng = max(1, min(ng, GV_MAXROWS / g.rows_per_block));
+    ng = max(1, min(ng, groups * NP / 2048));
+    const dim3 grid((groups + ng - 1) / ng, NP);
+    if (up)
+        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P>), grid, dim3(256), 0, st, act, ae, H, I, k, items, NP, offsets,
+                           sorted_pos, tab, out, dk, g.lg, ng);
+    else
+        hipLaunchKernelGGL((k_gemv_down<PREC, CPL, P>), grid, dim3(256), 0, st, act, ae, H, I, items, NP, offsets,
+                           sorted_pos, tab, w, out, dk, g.lg, ng);
+}
+
+template <int PREC>
+static void launch_gv(bool up, const int32_t *items, int NP, hipStream_t st, const uint16_t *act, const int *ae, int H, int I, int k,
+                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
+                      const float *w, DeqK dk) {
+    const GvGeo g = gv_geo(PREC, up ? H : I);
+    const int rows = up ? I : H;
+    if (g.rows_per_block > GV_MAXROWS) return;  // unreachable for K >= 128 (checked by the caller)
+    switch (g.cpl) {
+        case 1: launch_gv_cpl<PREC, 1>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case 2: launch_gv_cpl<PREC, 2>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case 3:
+        case 4: launch_gv_cpl<PREC, 4>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        default: launch_gv_cpl<PREC, 8>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+    }
+}
+
+static void launch_gv_prec(int prec, bool up, const int32_t *items, int NP, hipStream_t st, const uint16_t *act, const int *ae, int H, int I,
+                           int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
+                           const float *w, DeqK dk) {
+    switch (prec) {
+        case MOEHIP_PREC_INT4: launch_gv<MOEHIP_PREC_INT4>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_INT8: launch_gv<MOEHIP_PREC_INT8>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_FP8: launch_gv<MOEHIP_PREC_FP8>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_F16: launch_gv<MOEHIP_PREC_F16>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        default: launch_gv<MOEHIP_PREC_BF16>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+    }
 }
 
 static bool gg_prec_ok(int prec) {
@@ -556,7 +871,8 @@ static bool gg_prec_ok(int prec) {
 // the layer on P record tables (one per precision, rows of experts not run at that precision 0)
 static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H, int I, int k,
                   int E, int gs, const int32_t *offsets, const int32_t *sorted_pos, const int32_t *rank, const float *w,
-                  void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream, int zero_missing) {
+                  void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream, int zero_missing,
+                  int gemv) {
     MOEHIP_REQUIRE(tabs && x && offsets && sorted_pos && rank && w && out && ws && precs, "grouped_gemm: null pointer");
     MOEHIP_REQUIRE(P >= 1 && P <= 4, "grouped_gemm: %d record tables (1..4)", P);
     for (int p = 0; p < P; ++p) MOEHIP_REQUIRE(gg_prec_ok(precs[p]), "grouped_gemm: record precision %d", precs[p]);
@@ -570,7 +886,6 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
                    ws_bytes, L.total);
     uint8_t *wsb = reinterpret_cast<uint8_t *>(ws);
     int *xe = reinterpret_cast<int *>(wsb + L.xe);
-    uint32_t *pmax = reinterpret_cast<uint32_t *>(wsb + L.pmax);
     float *hb = reinterpret_cast<float *>(wsb + L.h);
     float *y = reinterpret_cast<float *>(wsb + L.y);
     const int NP = T * k;
@@ -583,21 +898,28 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     const bool bf = xdtype == MOEHIP_DT_BF16;
     const uint16_t *xa = bf ? x16 : xs;
     const int *xea = bf ? xe : nullptr;
-    hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, bf ? xs : nullptr, T, H, xe, x16, pmax, NP);
-    for (int p = 0; p < P; ++p) {
+    if (bf) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
+    int32_t *items = reinterpret_cast<int32_t *>(wsb + L.items);
+    if (gemv) hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, items);
+    for (int p = 0; p < P && gemv; ++p)
+        launch_gv_prec(precs[p], true, items, NP, st, xa, xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
+                       dk);
+    for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         switch (precs[p]) {
-            case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
-            case MOEHIP_PREC_INT8: launch_up<MOEHIP_PREC_INT8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
-            case MOEHIP_PREC_FP8: launch_up<MOEHIP_PREC_FP8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
-            case MOEHIP_PREC_F16: launch_up<MOEHIP_PREC_F16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
-            default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, pmax, dk); break;
+            case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
+            case MOEHIP_PREC_INT8: launch_up<MOEHIP_PREC_INT8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
+            case MOEHIP_PREC_FP8: launch_up<MOEHIP_PREC_FP8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
+            case MOEHIP_PREC_F16: launch_up<MOEHIP_PREC_F16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
+            default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
         }
     }
     uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
     int *he = reinterpret_cast<int *>(wsb + L.he);
-    hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, pmax, NP, I, h16, he);
-    for (int p = 0; p < P; ++p) {
+    hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
+    for (int p = 0; p < P && gemv; ++p)
+        launch_gv_prec(precs[p], false, items, NP, st, h16, he, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, y, w, dk);
+    for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         const int zm = zero_missing && P == 1;
         switch (precs[p]) {
@@ -622,7 +944,7 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
                                    const int32_t *rank, const float *w, void *out, const void *add, int accumulate,
                                    void *ws, size_t ws_bytes, void *stream) {
     return gg_run(1, &prec, tab, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
-                  ws_bytes, stream, 1);
+                  ws_bytes, stream, 1, 0);
 }
 
 extern "C" int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T,
@@ -630,5 +952,13 @@ extern "C" int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t 
                                          const int32_t *sorted_pos, const int32_t *rank, const float *w, void *out,
                                          const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream) {
     return gg_run(P, precs, tabs, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
-                  ws_bytes, stream, 0);
+                  ws_bytes, stream, 0, 0);
+}
+
+extern "C" int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T,
+                                         int H, int I, int k, int E, int gs, const int32_t *offsets,
+                                         const int32_t *sorted_pos, const int32_t *rank, const float *w, void *out,
+                                         const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream) {
+    return gg_run(P, precs, tabs, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
+                  ws_bytes, stream, 0, 1);
 }

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const void *__restrict__ 
     }
 }
 
-// logits on MFMA (16-bit activations, T >= 16, H a multiple of 512, 16-byte aligned rows): one
+// logits on MFMA (16-bit activations, T >= 4, H a multiple of 512, 16-byte aligned rows): one
 // workgroup per 16 tokens x 16 experts, each of its 4 waves a quarter of H through
 // v_mfma_f32_16x16x32 (A = 16 tokens x 32 K: lane row + 16 (k / 8), element k % 8; B likewise for
 // the 16 expert rows; D row 4 (lane / 16) + i, column lane % 16), the four partial tiles summed
@@ -455,8 +455,8 @@ extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, i
     hipStream_t st = as_stream(stream);
     const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
     const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
-    // a real matrix product (16 tokens or more): MFMA tiles of 16 tokens x 16 experts
-    const bool mf = dtype != MOEHIP_DT_F32 && vec16 && T >= 16 && H % 512 == 0;
+    // a matrix product (4 tokens or more): MFMA tiles of 16 tokens x 16 experts
+    const bool mf = dtype != MOEHIP_DT_F32 && vec16 && T >= 4 && H % 512 == 0;
     const dim3 gm((T + 15) / 16, (E + 15) / 16);
     switch (dtype) {
         case MOEHIP_DT_F16:

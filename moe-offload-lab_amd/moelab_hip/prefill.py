@@ -107,15 +107,19 @@ class GroupedLayer:
       3. levels and skip per (token, slot)            (moehip_batch_levels)
       4. expert-sorted dispatch of the kept pairs     (moehip_dispatch)
       5. vote, resident copy, per-precision tables    (moehip_batch_vote)
-      6. grouped GEMMs per precision + ordered combine (moehip_grouped_gemm_multi)
+      6. expert products per precision + ordered combine: batched dequant GEMVs for up to
+         `gemv_tokens` tokens (moehip_grouped_gemv_multi), MFMA tiles beyond
+         (moehip_grouped_gemm_multi)
     `shared`: per layer None or {"gate": (H,) tensor in dtype, "rec": {precision: record blob}}
     (the same form as MoEDecoder's). `info[layer]` (E + 1) holds the precision index each expert
     ran at (-1 missing, -2 no pairs); `miss` counts pairs of experts with no usable copy."""
 
     def __init__(self, store, k: int, max_tokens: int, policy=None, dtype=torch.float16,
                  router_weights: list | None = None, renorm: bool = False, shared: list | None = None,
-                 planned: list | None = None):
+                 planned: list | None = None, gemv_tokens: int = 64):
         from .policy import PrecisionPolicy, level_to_precision
+
+        self.gemv_tokens = gemv_tokens
 
         self.store, self.k, self.max_tokens = store, k, max_tokens
         self.policy = policy or PrecisionPolicy("lo")
@@ -216,7 +220,8 @@ class GroupedLayer:
                   ctypes.byref(self._pols[layer]), self.lv2p, st.rtab[layer].data_ptr(), srec, self.P,
                   self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(), self.rank.data_ptr(),
                   self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
-        _lib.call("moehip_grouped_gemm_multi", self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(),
+        entry = "moehip_grouped_gemv_multi" if T <= self.gemv_tokens else "moehip_grouped_gemm_multi"
+        _lib.call(entry, self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(),
                   _lib.dt_code(x.dtype), T, self.H, self.I, ks, EA, 64, self.offsets.data_ptr(),
                   self.sorted_pos.data_ptr(), self.rank.data_ptr(), pw.data_ptr(), out.data_ptr(), _lib.ptr(add), 0,
                   self.ws.data_ptr(), self.ws.numel(), stream)

@@ -50,17 +50,23 @@ def _routing(T, E, k, seed, renorm=False):
     return idx, w.float()
 
 
+# GEMV: batched dequant GEMVs (the path for few tokens per expert); MFMA: the grouped GEMM tiles
+PATHS = {"gemv": 64, "mfma": 0}
+
+
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("prec", ["int4", "int8", "fp8", "fp16", "bf16"])
-def test_grouped_layer_each_record_precision(dev, prec, dtype):
-    """One record precision through the generic grouped GEMM (T = 24 tokens, top-2 of 8)."""
+def test_grouped_layer_each_record_precision(dev, prec, dtype, path):
+    """One record precision (T = 24 tokens, top-2 of 8: ~6 tokens per expert, more than one
+    4-token pass of the GEMV path)."""
     H, I, E, k, T = 512, 256, 8, 2, 24
     st = _store(dev, [prec], H, I, E, 1)
-    gl = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype)
+    gl = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype, gemv_tokens=PATHS[path])
     idx, w = _routing(T, E, k, 2)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(3)).to(dtype)
     out = torch.zeros(T, H, dtype=dtype, device=dev)
-    print(f"grouped layer {prec} {dtype}", flush=True)
+    print(f"grouped layer {prec} {dtype} {path}", flush=True)
     gl.layer(0, x.to(dev), out, idx.to(dev), w.to(dev))
     torch.cuda.synchronize()
     ref = O.moe_layer(x.float().numpy(), idx.numpy(), w.numpy().astype(np.float64), lambda e: _mats(st, prec, 0, e))
@@ -71,8 +77,9 @@ def test_grouped_layer_each_record_precision(dev, prec, dtype):
     assert gl.miss.item() == 0
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("mode", ["weight", "hobbit"])
-def test_grouped_layer_mixed_precision_vote(dev, mode):
+def test_grouped_layer_mixed_precision_vote(dev, mode, path):
     """OLMoE-shaped batched decode, 8 tokens, fp16 + int4 records: the per-token rule (weight
     threshold at the median routed weight, or HOBBIT t1 = 0.6 with t2 = 0.8, which always skips
     each token's last expert), the vote per expert (hi_vote 0.5), and each expert's tokens computed
@@ -89,9 +96,9 @@ def test_grouped_layer_mixed_precision_vote(dev, mode):
         pol, opol = PrecisionPolicy("weight", t1=t1, upgrade=False), O.Policy("weight", t1=t1)
     else:
         pol, opol = PrecisionPolicy("hobbit", t1=0.6, t2=0.8, upgrade=False), O.Policy("hobbit", t1=0.6, t2=0.8)
-    gl = GroupedLayer(st, k, T, pol, dtype, router_weights=[Wr.to(dev)])
+    gl = GroupedLayer(st, k, T, pol, dtype, router_weights=[Wr.to(dev)], gemv_tokens=PATHS[path])
     out = torch.zeros(T, H, dtype=dtype, device=dev)
-    print(f"mixed vote {mode}", flush=True)
+    print(f"mixed vote {mode} {path}", flush=True)
     gl.layer(0, x.to(dev), out)
     torch.cuda.synchronize()
     idx_d = gl.idx[:T].cpu().numpy()
@@ -110,8 +117,9 @@ def test_grouped_layer_mixed_precision_vote(dev, mode):
     assert skip.any() == (mode == "hobbit")
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("prec", ["int4", "fp8"])
-def test_grouped_layer_qwen3next_shared_expert(dev, prec):
+def test_grouped_layer_qwen3next_shared_expert(dev, prec, path):
     """Qwen3-Next-shaped batched decode, 32 tokens: routed top-10 of 512 (renormalised) plus the
     sigmoid-gated shared expert, bf16; gate logit and sigmoid rounded to bf16 as the module does
     (modeling_qwen3_next.py:786-797)."""
@@ -126,10 +134,10 @@ def test_grouped_layer_qwen3next_shared_expert(dev, prec):
     gate = (torch.randn(H, generator=g) * 0.05).to(dtype)
     Wr = (torch.randn(E, H, generator=g) * 0.02).to(dtype)
     gl = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype, router_weights=[Wr.to(dev)], renorm=True,
-                      shared=[{"gate": gate.to(dev), "rec": {prec: sh_blob}}])
+                      shared=[{"gate": gate.to(dev), "rec": {prec: sh_blob}}], gemv_tokens=PATHS[path])
     x = torch.randn(T, H, generator=g).to(dtype)
     out = torch.zeros(T, H, dtype=dtype, device=dev)
-    print(f"shared expert batch {prec}", flush=True)
+    print(f"shared expert batch {prec} {path}", flush=True)
     gl.layer(0, x.to(dev), out)
     torch.cuda.synchronize()
     logits, idx, w, _ = O.router(x.float().numpy(), Wr.float().numpy(), k, True, "bfloat16")
