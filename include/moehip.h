@@ -283,6 +283,18 @@ int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_
                       int32_t *rank, float *info, float *miss, void *stream);
 
 /*
+ * moehip_batch_levels + moehip_dispatch + moehip_batch_vote in one launch (one workgroup; the same
+ * arguments and results): w32 / idx are (T, ks) with the shared expert (id E) as the last slot
+ * when has_shared. T * ks <= 65536, E + has_shared <= 1025. For batched decode, where each of
+ * those steps is a few microseconds of launch latency.
+ */
+int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int ks, const moehip_policy *pol,
+                        int32_t *levels, uint8_t *skip, int E, int has_shared, int32_t *counts, int32_t *offsets,
+                        int32_t *sorted_pos, int32_t *rank, double hi_vote, const int *lv2p, const int64_t *rtab,
+                        const int64_t *shared_rec, int P, const int64_t *offs, const int *planned, int64_t *tabs,
+                        float *info, float *miss, void *stream);
+
+/*
  * Qwen3-Next shared expert as slot k of every token (transformers Qwen3NextSparseMoeBlock.forward,
  * models/qwen3_next/modeling_qwen3_next.py:786-797): idx_ext (T, k + 1) / w_ext (T, k + 1) =
  * the routed idx (T, k) / w32 (T, k) followed by expert id E with weight sigmoid(x . gate), x .

@@ -9,7 +9,7 @@
 // are scanned (a shuffle scan per wave plus the wave totals), and pass 2 walks the segments again,
 // placing each pair at start[w][e] + its rank. Positions are stable in pair order.
 
-#include "common.hpp"
+#include "decide.hpp"
 
 namespace moehip {
 
@@ -36,12 +36,11 @@ __device__ __forceinline__ void match_lanes(int e, bool valid, int ebits, int la
     r = __popcll(m & lt);
 }
 
-__global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip,
-                                                   int NP, int E, int ebits, int32_t *__restrict__ counts,
-                                                   int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
-                                                   int32_t *__restrict__ rank) {
-    extern __shared__ int s_cnt[];  // [DP_WAVES][E]: counts, then each wave's start per expert
-    __shared__ int s_wtot[DP_WAVES];
+// the dispatch by one workgroup of 1024 threads; s_cnt: DP_WAVES * E ints of LDS
+__device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip, int NP,
+                                            int E, int ebits, int32_t *__restrict__ counts,
+                                            int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
+                                            int32_t *__restrict__ rank, int *s_cnt, int *s_wtot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int SEG = (NP + DP_WAVES - 1) / DP_WAVES;
     const int p0 = wave * SEG, p1 = min(NP, p0 + SEG);
@@ -124,9 +123,93 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ i
     for (int i = total + tid; i < NP; i += 1024) sorted_pos[i] = -1;
 }
 
+__global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip,
+                                                   int NP, int E, int ebits, int32_t *__restrict__ counts,
+                                                   int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
+                                                   int32_t *__restrict__ rank) {
+    extern __shared__ int s_cnt[];  // [DP_WAVES][E]: counts, then each wave's start per expert
+    __shared__ int s_wtot[DP_WAVES];
+    dispatch_wg(idx, skip, NP, E, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
+}
+
+// The whole T > 1 decision in one workgroup (batched decode, where every step is latency-bound):
+// levels per (token, slot) (one wave per token, slot_level), the dispatch of the kept pairs over
+// the E + has_shared experts, and the vote / copy / tables per expert (vote_expert); the same
+// results as moehip_batch_levels + moehip_dispatch + moehip_batch_vote.
+__global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__ w, const int64_t *__restrict__ idx,
+                                                       int T, int k, int ks, moehip_policy pol,
+                                                       int32_t *__restrict__ levels, uint8_t *__restrict__ skip, int E,
+                                                       int has_shared, int ebits, int32_t *__restrict__ counts,
+                                                       int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
+                                                       int32_t *__restrict__ rank, double hi_vote, int lv0, int lv1,
+                                                       int lv2, const int64_t *__restrict__ rtab, SharedRecs srec, int P,
+                                                       const int64_t *__restrict__ offs, const int *__restrict__ planned,
+                                                       int64_t *__restrict__ tabs, float *__restrict__ info,
+                                                       float *__restrict__ miss) {
+    extern __shared__ int s_cnt[];
+    __shared__ int s_wtot[DP_WAVES];
+    __shared__ float s_w[DP_WAVES][64], s_sorted[DP_WAVES][64], s_total[DP_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int EA = E + (has_shared ? 1 : 0);
+    for (int t = wave; t < T; t += DP_WAVES) {
+        const float wj = lane < k ? w[(size_t)t * ks + lane] : 0.f;
+        int lvl;
+        bool sk;
+        slot_level(lane, k, wj, pol, s_w[wave], s_sorted[wave], &s_total[wave], lvl, sk);
+        if (lane < k) {
+            levels[(size_t)t * ks + lane] = lvl;
+            skip[(size_t)t * ks + lane] = sk ? 1 : 0;
+        } else if (lane < ks) {  // the shared expert: level 0, never skipped
+            levels[(size_t)t * ks + lane] = 0;
+            skip[(size_t)t * ks + lane] = 0;
+        }
+        wave_sync();  // the wave's LDS is reused for its next token
+    }
+    __syncthreads();
+    dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
+    __syncthreads();
+    for (int e = tid; e < EA; e += 1024)
+        vote_expert(e, levels, E, has_shared, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec, P,
+                    offs, planned, tabs, rank, info, miss);
+}
+
 }  // namespace moehip
 
 using namespace moehip;
+
+static bool enable_big_lds(const void *fn, size_t lds) {
+    if (lds <= 60 * 1024) return true;
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
+}
+
+extern "C" int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int ks, const moehip_policy *pol,
+                                   int32_t *levels, uint8_t *skip, int E, int has_shared, int32_t *counts,
+                                   int32_t *offsets, int32_t *sorted_pos, int32_t *rank, double hi_vote,
+                                   const int *lv2p, const int64_t *rtab, const int64_t *shared_rec, int P,
+                                   const int64_t *offs, const int *planned, int64_t *tabs, float *info, float *miss,
+                                   void *stream) {
+    MOEHIP_REQUIRE(w32 && idx && pol && levels && skip && counts && offsets && sorted_pos && rank && lv2p && rtab &&
+                       offs && planned && tabs,
+                   "batch_decide: null pointer");
+    const int EA = E + (has_shared ? 1 : 0);
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 64 && ks >= k && ks <= 64 && (long)T * ks <= 65536 && E > 0 && EA <= 1025 &&
+                       P > 0 && P <= 4,
+                   "batch_decide: bad sizes T=%d k=%d ks=%d E=%d P=%d", T, k, ks, E, P);
+    MOEHIP_REQUIRE(!has_shared || shared_rec != nullptr, "batch_decide: shared expert without records");
+    for (int i = 0; i < 3; ++i) MOEHIP_REQUIRE(lv2p[i] >= 0 && lv2p[i] < P, "batch_decide: lv2p[%d]=%d", i, lv2p[i]);
+    SharedRecs sr = {{0, 0, 0, 0}};
+    if (has_shared)
+        for (int p = 0; p < P; ++p) sr.r[p] = shared_rec[p];
+    int ebits = 0;
+    while ((1 << ebits) < EA) ++ebits;
+    const size_t lds = (size_t)DP_WAVES * EA * sizeof(int);
+    MOEHIP_REQUIRE(enable_big_lds(reinterpret_cast<const void *>(&k_batch_decide), lds),
+                   "batch_decide: cannot enable %zu bytes of LDS", lds);
+    hipLaunchKernelGGL(k_batch_decide, dim3(1), dim3(1024), lds, as_stream(stream), w32, idx, T, k, ks, *pol, levels,
+                       skip, E, has_shared ? 1 : 0, ebits, counts, offsets, sorted_pos, rank, hi_vote, lv2p[0], lv2p[1],
+                       lv2p[2], rtab, sr, P, offs, planned, tabs, info, miss);
+    return check_launch("batch_decide");
+}
 
 extern "C" int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E, int32_t *counts,
                                int32_t *offsets, int32_t *sorted_pos, int32_t *rank, void *stream) {

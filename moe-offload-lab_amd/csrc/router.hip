@@ -9,7 +9,7 @@
 
 #include <limits.h>
 
-#include "common.hpp"
+#include "decide.hpp"
 
 namespace moehip {
 
@@ -261,52 +261,6 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
     }
 }
 
-// HOBBIT level and skip of slot j (< k <= 64) of one token: every thread of a 64-thread block calls
-// it (it synchronises the block); lanes j >= k pass wj = 0 and get a meaningless level.
-// policy.py:77-123 (unimportance over the normalised weights, stable descending rank), the fixed
-// modes (hi / lo / protected layer) and the weight threshold.
-__device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_policy &pol, int &lvl, bool &skip) {
-    __shared__ float s_w[64];
-    __shared__ float s_sorted[64];
-    __shared__ float s_total;
-    const bool act = j < k;
-    s_w[j] = wj;
-    __syncthreads();
-    if (j == 0) {
-        float tot = 0.f;
-        for (int i = 0; i < k; ++i) tot += s_w[i];
-        s_total = fmaxf(tot, 1e-12f);
-    }
-    __syncthreads();
-    skip = false;
-    if (pol.mode == 1 || pol.protect) {
-        lvl = 0;
-    } else if (pol.mode == 2) {
-        lvl = 2;
-    } else if (pol.mode == 3) {
-        lvl = wj >= pol.t1 ? 0 : 2;  // weight threshold: the expert's own routed weight
-    } else {
-        // unimportance (policy.py:77-87): stable descending rank, s = cumsum(sorted) - own weight
-        const float wn = wj / s_total;
-        s_w[j] = wn;
-        __syncthreads();
-        int rank = 0;
-        for (int i = 0; i < k; ++i) {
-            const float o = s_w[i];
-            rank += (o > wn) || (o == wn && i < j);
-        }
-        if (act) s_sorted[rank] = wn;
-        __syncthreads();
-        float cs = 0.f;
-        for (int r = 0; r <= rank && r < k; ++r) cs += s_sorted[r];
-        const float s = cs - wn;
-        lvl = 2;
-        if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
-        if (s <= pol.t1) lvl = 0;
-        skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
-    }
-}
-
 // HOBBIT levels + resident-copy choice + kernel tables for one token (k <= 64), one wave
 __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__ idx, const float *__restrict__ w32,
                                                      int k, moehip_policy pol, int lv0, int lv1, int lv2,
@@ -318,9 +272,10 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
     const bool act = j < k;
     const int e = act ? (int)idx[j] : 0;
     const float wj = act ? w32[j] : 0.f;
+    __shared__ float s_w[64], s_sorted[64], s_total[1];
     int lvl;
     bool skip;
-    slot_level(j, k, wj, pol, lvl, skip);
+    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, skip);
     const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
     int chosen = -1;
     for (int pi = P - 1; pi >= 0; --pi) {
@@ -357,9 +312,10 @@ __global__ __launch_bounds__(64) void k_batch_levels(const float *__restrict__ w
                                                      int32_t *__restrict__ levels, uint8_t *__restrict__ skip) {
     const int t = blockIdx.x, j = threadIdx.x;
     const float wj = j < k ? w32[(size_t)t * ks + j] : 0.f;
+    __shared__ float s_w[64], s_sorted[64], s_total[1];
     int lvl;
     bool sk;
-    slot_level(j, k, wj, pol, lvl, sk);
+    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, sk);
     if (j < k) {
         levels[(size_t)t * ks + j] = lvl;
         skip[(size_t)t * ks + j] = sk ? 1 : 0;
@@ -369,15 +325,7 @@ __global__ __launch_bounds__(64) void k_batch_levels(const float *__restrict__ w
     }
 }
 
-struct SharedRecs {
-    int64_t r[4];
-};
-
-// one thread per expert (E routed + the shared one when has_shared): the most precise level
-// requested by at least hi_vote of its pairs, its precision (lv2p) and resident copy (as
-// k_decide_table), the table row of that precision (all other precisions' rows 0); an expert with
-// no usable copy gets rank -1 on its pairs (they contribute nothing) and counts them in miss.
-// info[e] = chosen precision, -1 = missing, -2 = no pairs.
+// one thread per expert (E routed + the shared one when has_shared): vote_expert (decide.hpp)
 __global__ __launch_bounds__(64) void k_batch_vote(const int32_t *__restrict__ levels, int E, int has_shared,
                                                    const int32_t *__restrict__ offsets,
                                                    const int32_t *__restrict__ sorted_pos, double hi_vote, int upgrade,
@@ -386,37 +334,10 @@ __global__ __launch_bounds__(64) void k_batch_vote(const int32_t *__restrict__ l
                                                    const int *__restrict__ planned, int64_t *__restrict__ tabs,
                                                    int32_t *__restrict__ rank, float *__restrict__ info,
                                                    float *__restrict__ miss) {
-    const int EA = E + (has_shared ? 1 : 0);
     const int e = blockIdx.x * 64 + threadIdx.x;
-    if (e >= EA) return;
-    const int p0 = offsets[e], n = offsets[e + 1] - p0;
-    int chosen = -1;
-    if (n > 0) {
-        int c0 = 0, c1 = 0;
-        for (int i = 0; i < n; ++i) {
-            const int l = levels[sorted_pos[p0 + i]];
-            c0 += l <= 0;
-            c1 += l <= 1;
-        }
-        const double need = (hi_vote - 1e-9) * (double)n;
-        const int level = (double)c0 >= need ? 0 : ((double)c1 >= need ? 1 : 2);
-        const int req = level == 0 ? lv0 : (level == 1 ? lv1 : lv2);
-        for (int pi = P - 1; pi >= 0; --pi) {
-            const int64_t base = e < E ? rtab[(size_t)pi * E + e] : srec.r[pi];
-            if (base != 0 && (upgrade ? req >= pi : req == pi)) chosen = pi;
-        }
-        if (chosen >= 0 && !planned[chosen]) chosen = -1;
-    }
-    for (int pi = 0; pi < P; ++pi) {
-        const bool sel = chosen == pi;
-        const int64_t base = !sel ? 0 : (e < E ? rtab[(size_t)pi * E + e] : srec.r[pi]);
-        for (int f = 0; f < 4; ++f) tabs[((size_t)pi * EA + e) * 4 + f] = sel ? base + offs[pi * 4 + f] : 0;
-    }
-    if (n > 0 && chosen < 0) {
-        for (int i = 0; i < n; ++i) rank[sorted_pos[p0 + i]] = -1;
-        if (miss != nullptr) atomicAdd(miss, (float)n);
-    }
-    if (info != nullptr) info[e] = n == 0 ? -2.f : (float)chosen;
+    if (e < E + (has_shared ? 1 : 0))
+        vote_expert(e, levels, E, has_shared, offsets, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, rtab, srec, P, offs,
+                    planned, tabs, rank, info, miss);
 }
 
 // one wave per token: the routed slots copied into (T, k + 1) arrays and slot k = the shared
@@ -429,7 +350,25 @@ __global__ __launch_bounds__(64) void k_shared_slot(const void *__restrict__ x, 
                                                     float *__restrict__ w_ext) {
     const int t = blockIdx.x, lane = threadIdx.x;
     float acc = 0.f;
-    for (int c = lane; c < H; c += 64) acc += ld_act<DT>(x, (size_t)t * H + c) * ld_act<DT>(g, c);
+    if (DT != MOEHIP_DT_F32 && H % 8 == 0) {  // 8 values per 16-byte load (x and g 16-byte aligned)
+        const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + (size_t)t * H);
+        const uint4 *gr = reinterpret_cast<const uint4 *>(g);
+        for (int c = lane; c < H / 8; c += 64) {
+            const uint4 xv = xr[c], gv = gr[c];
+            const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)xa[i]) : __uint_as_float(xa[i] << 16);
+                const float x1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(xa[i] >> 16)) : __uint_as_float(xa[i] & 0xffff0000u);
+                const float g0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)ga[i]) : __uint_as_float(ga[i] << 16);
+                const float g1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(ga[i] >> 16)) : __uint_as_float(ga[i] & 0xffff0000u);
+                acc = fmaf(x0, g0, acc);
+                acc = fmaf(x1, g1, acc);
+            }
+        }
+    } else {
+        for (int c = lane; c < H; c += 64) acc += ld_act<DT>(x, (size_t)t * H + c) * ld_act<DT>(g, c);
+    }
     acc = wave_sum(acc);
     const int ks = k + 1;
     if (lane < k) {
@@ -522,6 +461,7 @@ extern "C" int moehip_shared_slot(const void *x, const void *gate, int T, int H,
                                   const float *w32, int k, int E, int64_t *idx_ext, float *w_ext, void *stream) {
     MOEHIP_REQUIRE(x && gate && idx && w32 && idx_ext && w_ext, "shared_slot: null pointer");
     MOEHIP_REQUIRE(T > 0 && H > 0 && k > 0 && k < 64 && E > 0, "shared_slot: T=%d H=%d k=%d E=%d", T, H, k, E);
+    MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)gate % 16) == 0, "shared_slot: x and gate must be 16-byte aligned");
     hipStream_t st = as_stream(stream);
     switch (dtype) {
         case MOEHIP_DT_F16:

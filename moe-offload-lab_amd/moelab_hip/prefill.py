@@ -107,6 +107,7 @@ class GroupedLayer:
       3. levels and skip per (token, slot)            (moehip_batch_levels)
       4. expert-sorted dispatch of the kept pairs     (moehip_dispatch)
       5. vote, resident copy, per-precision tables    (moehip_batch_vote)
+         (3-5 in one launch, moehip_batch_decide, unless fused_decide=False)
       6. expert products per precision + ordered combine: batched dequant GEMVs for up to
          `gemv_tokens` tokens (moehip_grouped_gemv_multi), MFMA tiles beyond
          (moehip_grouped_gemm_multi)
@@ -116,10 +117,11 @@ class GroupedLayer:
 
     def __init__(self, store, k: int, max_tokens: int, policy=None, dtype=torch.float16,
                  router_weights: list | None = None, renorm: bool = False, shared: list | None = None,
-                 planned: list | None = None, gemv_tokens: int = 64):
+                 planned: list | None = None, gemv_tokens: int = 64, fused_decide: bool = True):
         from .policy import PrecisionPolicy, level_to_precision
 
         self.gemv_tokens = gemv_tokens
+        self.fused_decide = fused_decide
 
         self.store, self.k, self.max_tokens = store, k, max_tokens
         self.policy = policy or PrecisionPolicy("lo")
@@ -211,15 +213,23 @@ class GroupedLayer:
             pidx, pw, ks, EA = self.idx_ext, self.w_ext, k + 1, self.E + 1
         else:
             pidx, pw, ks, EA = idx, w32, k, self.E
-        _lib.call("moehip_batch_levels", pw.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
-                  self.levels.data_ptr(), self.skip.data_ptr(), stream)
-        _lib.call("moehip_dispatch", pidx.data_ptr(), self.skip.data_ptr(), T, ks, EA, self.counts.data_ptr(),
-                  self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(), stream)
-        _lib.call("moehip_batch_vote", self.levels.data_ptr(), self.E, 1 if srec is not None else 0,
-                  self.offsets.data_ptr(), self.sorted_pos.data_ptr(), float(self.policy.hi_vote),
-                  ctypes.byref(self._pols[layer]), self.lv2p, st.rtab[layer].data_ptr(), srec, self.P,
-                  self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(), self.rank.data_ptr(),
-                  self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
+        if self.fused_decide:
+            _lib.call("moehip_batch_decide", pw.data_ptr(), pidx.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
+                      self.levels.data_ptr(), self.skip.data_ptr(), self.E, 1 if srec is not None else 0,
+                      self.counts.data_ptr(), self.offsets.data_ptr(), self.sorted_pos.data_ptr(),
+                      self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p, st.rtab[layer].data_ptr(), srec,
+                      self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(),
+                      self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
+        else:
+            _lib.call("moehip_batch_levels", pw.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
+                      self.levels.data_ptr(), self.skip.data_ptr(), stream)
+            _lib.call("moehip_dispatch", pidx.data_ptr(), self.skip.data_ptr(), T, ks, EA, self.counts.data_ptr(),
+                      self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(), stream)
+            _lib.call("moehip_batch_vote", self.levels.data_ptr(), self.E, 1 if srec is not None else 0,
+                      self.offsets.data_ptr(), self.sorted_pos.data_ptr(), float(self.policy.hi_vote),
+                      ctypes.byref(self._pols[layer]), self.lv2p, st.rtab[layer].data_ptr(), srec, self.P,
+                      self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(), self.rank.data_ptr(),
+                      self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
         entry = "moehip_grouped_gemv_multi" if T <= self.gemv_tokens else "moehip_grouped_gemm_multi"
         _lib.call(entry, self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(),
                   _lib.dt_code(x.dtype), T, self.H, self.I, ks, EA, 64, self.offsets.data_ptr(),

@@ -77,9 +77,10 @@ def test_grouped_layer_each_record_precision(dev, prec, dtype, path):
     assert gl.miss.item() == 0
 
 
+@pytest.mark.parametrize("fused_decide", [True, False])
 @pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("mode", ["weight", "hobbit"])
-def test_grouped_layer_mixed_precision_vote(dev, mode, path):
+def test_grouped_layer_mixed_precision_vote(dev, mode, path, fused_decide):
     """OLMoE-shaped batched decode, 8 tokens, fp16 + int4 records: the per-token rule (weight
     threshold at the median routed weight, or HOBBIT t1 = 0.6 with t2 = 0.8, which always skips
     each token's last expert), the vote per expert (hi_vote 0.5), and each expert's tokens computed
@@ -96,7 +97,8 @@ def test_grouped_layer_mixed_precision_vote(dev, mode, path):
         pol, opol = PrecisionPolicy("weight", t1=t1, upgrade=False), O.Policy("weight", t1=t1)
     else:
         pol, opol = PrecisionPolicy("hobbit", t1=0.6, t2=0.8, upgrade=False), O.Policy("hobbit", t1=0.6, t2=0.8)
-    gl = GroupedLayer(st, k, T, pol, dtype, router_weights=[Wr.to(dev)], gemv_tokens=PATHS[path])
+    gl = GroupedLayer(st, k, T, pol, dtype, router_weights=[Wr.to(dev)], gemv_tokens=PATHS[path],
+                      fused_decide=fused_decide)
     out = torch.zeros(T, H, dtype=dtype, device=dev)
     print(f"mixed vote {mode} {path}", flush=True)
     gl.layer(0, x.to(dev), out)
@@ -117,9 +119,10 @@ def test_grouped_layer_mixed_precision_vote(dev, mode, path):
     assert skip.any() == (mode == "hobbit")
 
 
+@pytest.mark.parametrize("fused_decide", [True, False])
 @pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("prec", ["int4", "fp8"])
-def test_grouped_layer_qwen3next_shared_expert(dev, prec, path):
+def test_grouped_layer_qwen3next_shared_expert(dev, prec, path, fused_decide):
     """Qwen3-Next-shaped batched decode, 32 tokens: routed top-10 of 512 (renormalised) plus the
     sigmoid-gated shared expert, bf16; gate logit and sigmoid rounded to bf16 as the module does
     (modeling_qwen3_next.py:786-797)."""
@@ -134,7 +137,8 @@ def test_grouped_layer_qwen3next_shared_expert(dev, prec, path):
     gate = (torch.randn(H, generator=g) * 0.05).to(dtype)
     Wr = (torch.randn(E, H, generator=g) * 0.02).to(dtype)
     gl = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype, router_weights=[Wr.to(dev)], renorm=True,
-                      shared=[{"gate": gate.to(dev), "rec": {prec: sh_blob}}], gemv_tokens=PATHS[path])
+                      shared=[{"gate": gate.to(dev), "rec": {prec: sh_blob}}], gemv_tokens=PATHS[path],
+                      fused_decide=fused_decide)
     x = torch.randn(T, H, generator=g).to(dtype)
     out = torch.zeros(T, H, dtype=dtype, device=dev)
     print(f"shared expert batch {prec} {path}", flush=True)
