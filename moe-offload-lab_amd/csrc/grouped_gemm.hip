@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, int N
 // run GV_NT at a time against the weights held in registers (weights are read once however many
 // tokens the expert has).
 // ---------------------------------------------------------------------------------------
-constexpr int GV_NT = 4;
+constexpr int GV_NT = 1;
 constexpr int GV_TG = GV_NT;  // tokens of one expert per workgroup (more tokens: more work items)
 constexpr int GV_MAXROWS = 512; // rows of one workgroup (their outputs are staged in LDS)
 
