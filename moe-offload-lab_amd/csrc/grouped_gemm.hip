@@ -483,7 +483,7 @@ __device__ __forceinline__ void gv_slice_perm(const uint4 *raw, uint32_t *xv) {
 // GV_NT of its tokens; UP: h[pair, r] = silu(gate . x) * (up . x); else y[pair, r] = w 2^he (down . h).
 // The loads of group g + 1 are issued before group g is computed (two register buffers).
 template <int PREC, int CPL, int P, bool UP>
-__device__ __forceinline__ void gv_rows(const uint16_t *act, const int *ae, int K, int rows, int I, int k, int p0,
+__device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, int rows, int I, int k, int p0,
                                         int nt, const int32_t *sorted_pos, gu8 *qb, gu8 *sb, int lg, int r0, int NG,
                                         const float *w, float *out, int ostride, DeqK dk) {
     constexpr int VPC = Fmt<PREC>::VPC, ND = VPC / 2, NM = UP ? 2 : 1;
@@ -500,15 +500,23 @@ __device__ __forceinline__ void gv_rows(const uint16_t *act, const int *ae, int 
         pr[t] = p0 + min(t, nt - 1);
         src[t] = UP ? sorted_pos[pr[t]] / k : pr[t];  // UP: the token's row of x; else the pair's h
     }
-    uint4 xr[GV_NT][CPL][VPC / 8];
+    // UP: fp16 activation slices (the token's power of two in f); DOWN: fp32 h slices, each chunk
+    // scaled into fp16 by its own power of two (fe) once the weights are requested
+    constexpr int XW = UP ? VPC / 8 : VPC / 4;  // 16-byte loads per chunk
+    uint4 xr[GV_NT][CPL][XW];
     float f[GV_NT];
 #pragma unroll
     for (int t = 0; t < GV_NT; ++t) {
-        const uint16_t *row = act + (size_t)src[t] * K;
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) gv_slice_load<VPC>(row, min(cl + i * G, C - 1), xr[t][i]);
-        const int ex = ae != nullptr ? ae[src[t]] : 0;
-        f[t] = UP ? ldexpf(1.0f, ex) : w[sorted_pos[pr[t]]] * ldexpf(1.0f, ex);
+        for (int i = 0; i < CPL; ++i) {
+            const int c = min(cl + i * G, C - 1);
+            const uint4 *p = UP ? reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(act) + (size_t)src[t] * K + (size_t)c * VPC)
+                                : reinterpret_cast<const uint4 *>(reinterpret_cast<const float *>(act) + (size_t)src[t] * K + (size_t)c * VPC);
+#pragma unroll
+            for (int b = 0; b < XW; ++b) xr[t][i][b] = p[b];
+        }
+        if constexpr (UP) f[t] = ldexpf(1.0f, ae != nullptr ? ae[src[t]] : 0);
+        else f[t] = w[sorted_pos[pr[t]]];
     }
     uint4 q[2][P][NM][CPL];
     uint32_t sr[2][P][NM][CPL];
@@ -532,10 +540,28 @@ __device__ __forceinline__ void gv_rows(const uint16_t *act, const int *ae, int 
     };
     load(0, 0);
     uint32_t xv[GV_NT][CPL][ND];
+    float fe[GV_NT][CPL];
 #pragma unroll
     for (int t = 0; t < GV_NT; ++t)
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) gv_slice_perm<VPC>(xr[t][i], xv[t][i]);
+        for (int i = 0; i < CPL; ++i) {
+            if constexpr (UP) {
+                gv_slice_perm<VPC>(xr[t][i], xv[t][i]);
+                fe[t][i] = 1.0f;
+            } else {
+                const float *v = reinterpret_cast<const float *>(xr[t][i]);
+                float m = 0.f;
+#pragma unroll
+                for (int q = 0; q < VPC; ++q) m = fmaxf(m, fabsf(v[q]));
+                const int e = row_exp(m);
+                const float sc = ldexpf(1.0f, -e);
+                fe[t][i] = ldexpf(1.0f, e);
+#pragma unroll
+                for (int b = 0; b < VPC / 8; ++b)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) xv[t][i][4 * b + q] = pack_h2(v[8 * b + q] * sc, v[8 * b + q + 4] * sc);
+            }
+        }
     auto compute = [&](int buf, int g) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -554,8 +580,15 @@ __device__ __forceinline__ void gv_rows(const uint16_t *act, const int *ae, int 
 #pragma unroll
                     for (int t = 0; t < GV_NT; ++t) {
                         if (t < nt) {
+                            if constexpr (UP) {
 #pragma unroll
-                            for (int j = 0; j < ND; ++j) acc[m][t] = dot2h(wv[j], xv[t][i][j], acc[m][t]);
+                                for (int j = 0; j < ND; ++j) acc[m][t] = dot2h(wv[j], xv[t][i][j], acc[m][t]);
+                            } else {
+                                float pc = 0.f;
+#pragma unroll
+                                for (int j = 0; j < ND; ++j) pc = dot2h(wv[j], xv[t][i][j], pc);
+                                acc[m][t] = fmaf(pc, fe[t][i], acc[m][t]);
+                            }
                         }
                     }
                 }
@@ -644,7 +677,7 @@ __global__ __launch_bounds__(256) void k_gemv_up(const uint16_t *__restrict__ x,
 }
 
 template <int PREC, int CPL, int P>
-__global__ __launch_bounds__(256) void k_gemv_down(const uint16_t *__restrict__ h16, const int *__restrict__ he, int H,
+__global__ __launch_bounds__(256) void k_gemv_down(const float *__restrict__ hb, int H,
                                                    int I, const int32_t *__restrict__ items, int NP,
                                                    const int32_t *__restrict__ offsets,
                                                    const int32_t *__restrict__ sorted_pos,
@@ -656,7 +689,7 @@ __global__ __launch_bounds__(256) void k_gemv_down(const uint16_t *__restrict__ 
     gu8 *qb = record_ptr(tab[4 * e + 2]);
     if (ne <= 0 || qb == nullptr) return;
     const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
-    gv_rows<PREC, CPL, P, false>(h16, he, I, H, 0, 1, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 3]), lg, r0, NG,
+    gv_rows<PREC, CPL, P, false>(hb, nullptr, I, H, 0, 1, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 3]), lg, r0, NG,
                                  w, y, H, dk);
 }
 
@@ -815,7 +848,7 @@ static GvGeo gv_geo(int prec, int K) {
 }
 
 template <int PREC, int CPL>
-static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const uint16_t *act, const int *ae,
+static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
                           int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
                           float *out, const float *w, DeqK dk) {
     constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
@@ -828,15 +861,17 @@ static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const
     ng = max(1, min(ng, groups * NP / 2048));
     const dim3 grid((groups + ng - 1) / ng, NP);
     if (up)
-        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P>), grid, dim3(256), 0, st, act, ae, H, I, k, items, NP, offsets,
+        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act), ae,
+                           H, I, k, items, NP, offsets,
                            sorted_pos, tab, out, dk, g.lg, ng);
     else
-        hipLaunchKernelGGL((k_gemv_down<PREC, CPL, P>), grid, dim3(256), 0, st, act, ae, H, I, items, NP, offsets,
+        hipLaunchKernelGGL((k_gemv_down<PREC, CPL, P>), grid, dim3(256), 0, st, reinterpret_cast<const float *>(act), H, I,
+                           items, NP, offsets,
                            sorted_pos, tab, w, out, dk, g.lg, ng);
 }
 
 template <int PREC>
-static void launch_gv(bool up, const int32_t *items, int NP, hipStream_t st, const uint16_t *act, const int *ae, int H, int I, int k,
+static void launch_gv(bool up, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I, int k,
                       const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
                       const float *w, DeqK dk) {
     const GvGeo g = gv_geo(PREC, up ? H : I);
@@ -851,7 +886,7 @@ static void launch_gv(bool up, const int32_t *items, int NP, hipStream_t st, con
     }
 }
 
-static void launch_gv_prec(int prec, bool up, const int32_t *items, int NP, hipStream_t st, const uint16_t *act, const int *ae, int H, int I,
+static void launch_gv_prec(int prec, bool up, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I,
                            int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
                            const float *w, DeqK dk) {
     switch (prec) {
@@ -916,9 +951,11 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     }
     uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
     int *he = reinterpret_cast<int *>(wsb + L.he);
-    hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
+    // the MFMA down kernels read h as fp16 with a per-pair power of two; the GEMVs read the fp32 rows
+    if (!gemv) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
     for (int p = 0; p < P && gemv; ++p)
-        launch_gv_prec(precs[p], false, items, NP, st, h16, he, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, y, w, dk);
+        launch_gv_prec(precs[p], false, items, NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
+                       y, w, dk);
     for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         const int zm = zero_missing && P == 1;
