@@ -250,12 +250,13 @@ int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, cons
  * tiles (for few tokens per expert: batched decode): weight rows streamed whole with 16-byte
  * loads and read once per launch however many tokens the expert has, v_dot2_f32_f16 products
  * against each token's activations; same arguments, workspace and results up to fp32 summation
- * order. Replaces the same reference code as moehip_grouped_gemm_multi.
+ * order. items: the work list written by moehip_batch_route_decide (T * k + 1 int32), or NULL to
+ * build it here. Replaces the same reference code as moehip_grouped_gemm_multi.
  */
 int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H,
                               int I, int k, int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
                               const int32_t *rank, const float *w, void *out, const void *add, int accumulate, void *ws,
-                              size_t ws_bytes, void *stream);
+                              size_t ws_bytes, const int32_t *items, void *stream);
 
 /*
  * HOBBIT levels of T tokens (moelab/policy.py:110-123 `levels`, the T > 1 branch of
@@ -293,6 +294,28 @@ int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int 
                         int32_t *sorted_pos, int32_t *rank, double hi_vote, const int *lv2p, const int64_t *rtab,
                         const int64_t *shared_rec, int P, const int64_t *offs, const int *planned, int64_t *tabs,
                         float *info, float *miss, void *stream);
+
+/*
+ * The logits part of moehip_router_topk alone: logits (T, E) = x Wr^T rounded to dtype (the gate's
+ * F.linear, transformers modeling_olmoe.py:343), for moehip_batch_route_decide.
+ */
+int moehip_router_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits, void *stream);
+
+/*
+ * Batched decode from the router logits to the GEMV work list in one launch (one workgroup):
+ * softmax top-k per token (as moehip_router_topk: idx (T, k) int64, w_out (T, k) in dtype or NULL,
+ * w32 (T, k) fp32 holding dtype values), the shared expert as slot k when gate != NULL (as
+ * moehip_shared_slot: idx_ext / w_ext (T, k + 1); x (T, H) and gate (H) 16-byte aligned), then
+ * moehip_batch_decide, and the work list of moehip_grouped_gemv_multi (items, T * ks + 1 int32, or
+ * NULL). logits (T, E) fp16 / bf16, E <= 1024, k <= 32.
+ */
+int moehip_batch_route_decide(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
+                              const void *gate, int H, int64_t *idx, void *w_out, float *w32, int64_t *idx_ext,
+                              float *w_ext, const moehip_policy *pol, int32_t *levels, uint8_t *skip, int32_t *counts,
+                              int32_t *offsets, int32_t *sorted_pos, int32_t *rank, double hi_vote, const int *lv2p,
+                              const int64_t *rtab, const int64_t *shared_rec, int P, const int64_t *offs,
+                              const int *planned, int64_t *tabs, float *info, float *miss, int32_t *items,
+                              void *stream);
 
 /*
  * Qwen3-Next shared expert as slot k of every token (transformers Qwen3NextSparseMoeBlock.forward,

@@ -105,4 +105,102 @@ __device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E,
     if (info != nullptr) info[e] = n == 0 ? -2.f : (float)chosen;
 }
 
+
+// tokens per batched-GEMV work item (the work list written by the decision kernels and read by
+// the GEMV kernels)
+constexpr int GV_TOKENS = 1;
+
+// order-preserving 32-bit key of a 16-bit logit (bits16) at index c < 1024: the logit bits above
+// 1023 - c, so the largest logit wins and equal logits go to the lowest index; -0 == +0
+__device__ __forceinline__ uint32_t topk_key16(uint32_t bits16, int c) {
+    const uint32_t b = (bits16 & 0x7fffu) == 0u ? 0u : bits16;
+    const uint32_t k16 = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+    return (k16 << 10) | (uint32_t)(1023 - c);
+}
+
+// softmax top-k of one token's E logits (16-bit DT, E <= 1024, k <= 32) by one wave: fp32 softmax,
+// k rounds of a DPP wave maximum over the keys, optional renorm (the serial sum in slot order);
+// lane j < k gets its expert and its final fp32 weight. s_p: 32 floats of the wave's LDS.
+// transformers OlmoeTopKRouter.forward (modeling_olmoe.py:337-346) and Qwen3MoeTopKRouter.
+template <int DT>
+__device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E, int k, int renorm, float *s_p,
+                                          int &myc, float &myp) {
+    const int lane = threadIdx.x & 63;
+    const uint16_t *lr = reinterpret_cast<const uint16_t *>(logits) + row * E;
+    float lv[16];
+    uint32_t key[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = lane + 64 * i;
+        key[i] = 0u;
+        lv[i] = -INFINITY;
+        if (c < E) {
+            const uint32_t b = lr[c];
+            lv[i] = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
+            key[i] = topk_key16(b, c);
+        }
+        m = fmaxf(m, lv[i]);
+    }
+    m = wave_max(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < E) sum += expf(lv[i] - m);
+    sum = wave_sum(sum);
+    uint32_t myk = 0u;
+    myc = 0;
+    for (int j = 0; j < k; ++j) {
+        uint32_t lb = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) lb = max(lb, key[i]);
+        const uint32_t M = wave_max_u32(lb);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (key[i] == M) key[i] = 0u;  // keys are distinct: exactly one lane clears one
+        if (lane == j) {
+            myc = 1023 - (int)(M & 1023u);
+            myk = M >> 10;
+        }
+    }
+    float p = 0.f;
+    if (lane < k) {
+        // the logit from its key (the inverse of topk_key16; -0 came back as +0, same value)
+        const uint32_t b = (myk & 0x8000u) ? (myk & 0x7fffu) : (~myk & 0xffffu);
+        const float v = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
+        p = expf(v - m) / sum;
+        s_p[lane] = p;
+    }
+    wave_sync();
+    float tot = 0.f;
+    if (renorm)
+        for (int j = 0; j < k; ++j) tot += s_p[j];
+    myp = renorm ? p / tot : p;
+    wave_sync();  // s_p is free for the wave's next token
+}
+
+// x[t] . g over H values (16-bit DT: 8 per 16-byte load; x and g 16-byte aligned, H % 8 == 0), by
+// one wave, fp32, every lane gets the sum
+template <int DT>
+__device__ __forceinline__ float gate_dot_wave(const void *x, const void *g, int t, int H) {
+    const int lane = threadIdx.x & 63;
+    float acc = 0.f;
+    const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + (size_t)t * H);
+    const uint4 *gr = reinterpret_cast<const uint4 *>(g);
+    for (int c = lane; c < H / 8; c += 64) {
+        const uint4 xv = xr[c], gv = gr[c];
+        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gv.x, gv.y, gv.z, gv.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)xa[i]) : __uint_as_float(xa[i] << 16);
+            const float x1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(xa[i] >> 16)) : __uint_as_float(xa[i] & 0xffff0000u);
+            const float g0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)ga[i]) : __uint_as_float(ga[i] << 16);
+            const float g1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(ga[i] >> 16)) : __uint_as_float(ga[i] & 0xffff0000u);
+            acc = fmaf(x0, g0, acc);
+            acc = fmaf(x1, g1, acc);
+        }
+    }
+    return wave_sum(acc);
+}
+
 }  // namespace moehip

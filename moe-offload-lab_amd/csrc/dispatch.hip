@@ -177,6 +177,103 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
 
 using namespace moehip;
 
+// Batched decode, everything between the router logits and the expert products in one workgroup:
+// softmax top-k per token (one wave per token, topk_wave), the shared expert as slot k (its gate
+// x . g and sigmoid rounded to the activation dtype), levels, dispatch, vote / copy / tables, and
+// the work list of the batched GEMVs (one item per GV_TOKENS tokens of an expert, in expert order;
+// items[T * ks] = their number). Same results as moehip_router_topk (its top-k part) +
+// moehip_shared_slot + moehip_batch_decide + the GEMVs' own work list.
+template <int DT>
+__global__ __launch_bounds__(1024) void k_batch_route_decide(
+    const void *__restrict__ logits, int E, int k, int renorm, const void *__restrict__ x,
+    const void *__restrict__ gate, int H, int T, int64_t *__restrict__ idx, void *__restrict__ wout,
+    float *__restrict__ w32, int64_t *__restrict__ idx_ext, float *__restrict__ w_ext, moehip_policy pol,
+    int32_t *__restrict__ levels, uint8_t *__restrict__ skip, int ebits, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos, int32_t *__restrict__ rank, double hi_vote,
+    int lv0, int lv1, int lv2, const int64_t *__restrict__ rtab, SharedRecs srec, int P,
+    const int64_t *__restrict__ offs, const int *__restrict__ planned, int64_t *__restrict__ tabs,
+    float *__restrict__ info, float *__restrict__ miss, int32_t *__restrict__ items) {
+    extern __shared__ int s_cnt[];
+    __shared__ int s_wtot[DP_WAVES];
+    __shared__ float s_w[DP_WAVES][64], s_sorted[DP_WAVES][64], s_total[DP_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool shared = gate != nullptr;
+    const int ks = k + (shared ? 1 : 0), EA = E + (shared ? 1 : 0);
+    int64_t *pidx = shared ? idx_ext : idx;
+    float *pw = shared ? w_ext : w32;
+    // routing of every token
+    for (int t = wave; t < T; t += DP_WAVES) {
+        int myc;
+        float p;
+        topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_w[wave], myc, p);
+        const float r = rnd_act<DT>(p);
+        if (lane < k) {
+            idx[(size_t)t * k + lane] = myc;
+            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
+            w32[(size_t)t * k + lane] = r;
+            if (shared) {
+                idx_ext[(size_t)t * ks + lane] = myc;
+                w_ext[(size_t)t * ks + lane] = r;
+            }
+        }
+        if (shared) {
+            const float l = rnd_act<DT>(gate_dot_wave<DT>(x, gate, t, H));
+            if (lane == k) {
+                idx_ext[(size_t)t * ks + k] = E;
+                w_ext[(size_t)t * ks + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
+            }
+        }
+    }
+    __syncthreads();
+    // levels
+    for (int t = wave; t < T; t += DP_WAVES) {
+        const float wj = lane < k ? pw[(size_t)t * ks + lane] : 0.f;
+        int lvl;
+        bool sk;
+        slot_level(lane, k, wj, pol, s_w[wave], s_sorted[wave], &s_total[wave], lvl, sk);
+        if (lane < k) {
+            levels[(size_t)t * ks + lane] = lvl;
+            skip[(size_t)t * ks + lane] = sk ? 1 : 0;
+        } else if (lane < ks) {  // the shared expert: level 0, never skipped
+            levels[(size_t)t * ks + lane] = 0;
+            skip[(size_t)t * ks + lane] = 0;
+        }
+        wave_sync();
+    }
+    __syncthreads();
+    dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
+    __syncthreads();
+    for (int e = tid; e < EA; e += 1024)
+        vote_expert(e, levels, E, shared ? 1 : 0, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec,
+                    P, offs, planned, tabs, rank, info, miss);
+    if (items == nullptr) return;
+    // the work list: exclusive scan of ceil(n_e / GV_TOKENS) over the experts (the offsets are
+    // this workgroup's own writes, ordered by the barrier)
+    __syncthreads();
+    int base = 0;
+    for (int e0 = 0; e0 < EA; e0 += 1024) {
+        const int e = e0 + tid;
+        const int n = e < EA ? offsets[e + 1] - offsets[e] : 0;
+        const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
+        int incl = nz;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        if (lane == 63) s_wtot[wave] = incl;
+        __syncthreads();
+        int wb = base, tot = base;
+        for (int w = 0; w < DP_WAVES; ++w) {
+            if (w < wave) wb += s_wtot[w];
+            tot += s_wtot[w];
+        }
+        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
+        base = tot;
+        __syncthreads();
+    }
+    if (tid == 0) items[T * ks] = base;
+}
+
 static bool enable_big_lds(const void *fn, size_t lds) {
     if (lds <= 60 * 1024) return true;
     return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
@@ -209,6 +306,52 @@ extern "C" int moehip_batch_decide(const float *w32, const int64_t *idx, int T, 
                        skip, E, has_shared ? 1 : 0, ebits, counts, offsets, sorted_pos, rank, hi_vote, lv2p[0], lv2p[1],
                        lv2p[2], rtab, sr, P, offs, planned, tabs, info, miss);
     return check_launch("batch_decide");
+}
+
+extern "C" int moehip_batch_route_decide(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
+                                         const void *gate, int H, int64_t *idx, void *w_out, float *w32,
+                                         int64_t *idx_ext, float *w_ext, const moehip_policy *pol, int32_t *levels,
+                                         uint8_t *skip, int32_t *counts, int32_t *offsets, int32_t *sorted_pos,
+                                         int32_t *rank, double hi_vote, const int *lv2p, const int64_t *rtab,
+                                         const int64_t *shared_rec, int P, const int64_t *offs, const int *planned,
+                                         int64_t *tabs, float *info, float *miss, int32_t *items, void *stream) {
+    MOEHIP_REQUIRE(logits && idx && w32 && pol && levels && skip && counts && offsets && sorted_pos && rank && lv2p &&
+                       rtab && offs && planned && tabs,
+                   "batch_route_decide: null pointer");
+    MOEHIP_REQUIRE(dtype == MOEHIP_DT_F16 || dtype == MOEHIP_DT_BF16, "batch_route_decide: logits dtype %d", dtype);
+    const bool shared = gate != nullptr;
+    const int ks = k + (shared ? 1 : 0), EA = E + (shared ? 1 : 0);
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 32 && k <= E && E <= 1024 && (long)T * ks <= 65536 && P > 0 && P <= 4,
+                   "batch_route_decide: bad sizes T=%d E=%d k=%d P=%d", T, E, k, P);
+    MOEHIP_REQUIRE(!shared || (x && idx_ext && w_ext && shared_rec && H % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
+                               ((uintptr_t)gate % 16) == 0),
+                   "batch_route_decide: shared expert needs x, aligned gate, idx_ext, w_ext and records");
+    MOEHIP_REQUIRE(items == nullptr || (long)T * ks <= 256L * GV_TOKENS * EA,
+                   "batch_route_decide: work list limits (256 items per expert)");
+    for (int i = 0; i < 3; ++i) MOEHIP_REQUIRE(lv2p[i] >= 0 && lv2p[i] < P, "batch_route_decide: lv2p[%d]=%d", i, lv2p[i]);
+    SharedRecs sr = {{0, 0, 0, 0}};
+    if (shared)
+        for (int p = 0; p < P; ++p) sr.r[p] = shared_rec[p];
+    int ebits = 0;
+    while ((1 << ebits) < EA) ++ebits;
+    const size_t lds = (size_t)DP_WAVES * EA * sizeof(int);
+    hipStream_t st = as_stream(stream);
+    if (dtype == MOEHIP_DT_F16) {
+        MOEHIP_REQUIRE(enable_big_lds(reinterpret_cast<const void *>(&k_batch_route_decide<MOEHIP_DT_F16>), lds),
+                       "batch_route_decide: cannot enable %zu bytes of LDS", lds);
+        hipLaunchKernelGGL((k_batch_route_decide<MOEHIP_DT_F16>), dim3(1), dim3(1024), lds, st, logits, E, k, renorm, x,
+                           gate, H, T, idx, w_out, w32, idx_ext, w_ext, *pol, levels, skip, ebits, counts, offsets,
+                           sorted_pos, rank, hi_vote, lv2p[0], lv2p[1], lv2p[2], rtab, sr, P, offs, planned, tabs, info,
+                           miss, items);
+    } else {
+        MOEHIP_REQUIRE(enable_big_lds(reinterpret_cast<const void *>(&k_batch_route_decide<MOEHIP_DT_BF16>), lds),
+                       "batch_route_decide: cannot enable %zu bytes of LDS", lds);
+        hipLaunchKernelGGL((k_batch_route_decide<MOEHIP_DT_BF16>), dim3(1), dim3(1024), lds, st, logits, E, k, renorm,
+                           x, gate, H, T, idx, w_out, w32, idx_ext, w_ext, *pol, levels, skip, ebits, counts, offsets,
+                           sorted_pos, rank, hi_vote, lv2p[0], lv2p[1], lv2p[2], rtab, sr, P, offs, planned, tabs, info,
+                           miss, items);
+    }
+    return check_launch("batch_route_decide");
 }
 
 extern "C" int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E, int32_t *counts,

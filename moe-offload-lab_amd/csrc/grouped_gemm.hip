@@ -30,6 +30,7 @@
 // (its L2 then serves the expert's activation rows to all of them).
 
 #include "gemv_core.hpp"
+#include "decide.hpp"
 
 namespace moehip {
 
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, int N
 // run GV_NT at a time against the weights held in registers (weights are read once however many
 // tokens the expert has).
 // ---------------------------------------------------------------------------------------
-constexpr int GV_NT = 1;
+constexpr int GV_NT = GV_TOKENS;  // tokens per work item (decide.hpp: the decision kernels write the same list)
 constexpr int GV_TG = GV_NT;  // tokens of one expert per workgroup (more tokens: more work items)
 constexpr int GV_MAXROWS = 512; // rows of one workgroup (their outputs are staged in LDS)
 
@@ -907,7 +908,7 @@ static bool gg_prec_ok(int prec) {
 static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H, int I, int k,
                   int E, int gs, const int32_t *offsets, const int32_t *sorted_pos, const int32_t *rank, const float *w,
                   void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream, int zero_missing,
-                  int gemv) {
+                  int gemv, const int32_t *items_in = nullptr) {
     MOEHIP_REQUIRE(tabs && x && offsets && sorted_pos && rank && w && out && ws && precs, "grouped_gemm: null pointer");
     MOEHIP_REQUIRE(P >= 1 && P <= 4, "grouped_gemm: %d record tables (1..4)", P);
     for (int p = 0; p < P; ++p) MOEHIP_REQUIRE(gg_prec_ok(precs[p]), "grouped_gemm: record precision %d", precs[p]);
@@ -934,8 +935,10 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     const uint16_t *xa = bf ? x16 : xs;
     const int *xea = bf ? xe : nullptr;
     if (bf) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
+    // the work list: the caller's (written by moehip_batch_route_decide) or built here
     int32_t *items = reinterpret_cast<int32_t *>(wsb + L.items);
-    if (gemv) hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, items);
+    if (gemv && items_in == nullptr) hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, items);
+    if (items_in != nullptr) items = const_cast<int32_t *>(items_in);
     for (int p = 0; p < P && gemv; ++p)
         launch_gv_prec(precs[p], true, items, NP, st, xa, xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
@@ -995,7 +998,9 @@ extern "C" int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t 
 extern "C" int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T,
                                          int H, int I, int k, int E, int gs, const int32_t *offsets,
                                          const int32_t *sorted_pos, const int32_t *rank, const float *w, void *out,
-                                         const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream) {
+                                         const void *add, int accumulate, void *ws, size_t ws_bytes,
+                                         const int32_t *items, void *stream) {
+    MOEHIP_REQUIRE((long)T * k <= 256L * GV_TOKENS * E, "grouped_gemv: work list limits (256 items per expert)");
     return gg_run(P, precs, tabs, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
-                  ws_bytes, stream, 0, 1);
+                  ws_bytes, stream, 0, 1, items);
 }

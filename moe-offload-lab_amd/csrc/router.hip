@@ -143,11 +143,6 @@ __global__ __launch_bounds__(256) void k_router_logits_mfma(const void *__restri
 // softmax + top-k + renorm for one token per wave (E <= 1024, k <= 32). 16-bit logits: k rounds of
 // a DPP wave maximum over 32-bit keys (order-preserving logit bits above 1023 - index: the largest
 // logit, the lowest index among equal logits); fp32 logits: value and index compared separately.
-__device__ __forceinline__ uint32_t topk_key16(uint32_t bits16, int c) {
-    const uint32_t b = (bits16 & 0x7fffu) == 0u ? 0u : bits16;  // -0 == +0
-    const uint32_t k16 = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-    return (k16 << 10) | (uint32_t)(1023 - c);
-}
 
 template <int DT>
 __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ logits, int T, int E, int k, int renorm,
@@ -157,93 +152,57 @@ __global__ __launch_bounds__(64) void k_router_topk(const void *__restrict__ log
     const int lane = threadIdx.x;
     __shared__ int s_idx[32];
     __shared__ float s_p[32];
+    if constexpr (DT != MOEHIP_DT_F32) {
+        int myc;
+        float p;
+        topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_p, myc, p);
+        if (lane < k) {
+            idx[(size_t)t * k + lane] = myc;
+            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
+            if (w32 != nullptr) w32[(size_t)t * k + lane] = rnd_act<DT>(p);
+        }
+        return;
+    }
+    // fp32 logits: value and index compared separately (no 16-bit keys)
     float lv[16];
-    uint32_t key[16];
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int c = lane + 64 * i;
-        key[i] = 0u;
-        lv[i] = -INFINITY;
-        if (c < E) {
-            lv[i] = ld_act<DT>(logits, (size_t)t * E + c);
-            if constexpr (DT != MOEHIP_DT_F32)
-                key[i] = topk_key16(reinterpret_cast<const uint16_t *>(logits)[(size_t)t * E + c], c);
-        }
+        lv[i] = c < E ? ld_act<DT>(logits, (size_t)t * E + c) : -INFINITY;
         m = fmaxf(m, lv[i]);
     }
     m = wave_max(m);
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int c = lane + 64 * i;
-        if (c < E) sum += expf(lv[i] - m);
-    }
+    for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < E) sum += expf(lv[i] - m);
     sum = wave_sum(sum);
-    if constexpr (DT != MOEHIP_DT_F32) {
-        int myc = 0;
-        uint32_t myk = 0u;
-        for (int j = 0; j < k; ++j) {
-            uint32_t lb = 0u;
+    uint32_t taken = 0;
+    for (int j = 0; j < k; ++j) {
+        float bv = -INFINITY;
+        int bi = INT_MAX;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) lb = max(lb, key[i]);
-            const uint32_t M = wave_max_u32(lb);
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (key[i] == M) key[i] = 0u;  // keys are distinct: exactly one lane clears one
-            if (lane == j) {
-                myc = 1023 - (int)(M & 1023u);
-                myk = M >> 10;
+        for (int i = 0; i < 16; ++i) {
+            const int c = lane + 64 * i;
+            if (c < E && !((taken >> i) & 1u) && (lv[i] > bv || (lv[i] == bv && c < bi))) {
+                bv = lv[i];
+                bi = c;
             }
         }
-        if (lane < k) {
-            // the logit from its key (the inverse of topk_key16; -0 came back as +0, same value)
-            const uint32_t b = (myk & 0x8000u) ? (myk & 0x7fffu) : (~myk & 0xffffu);
-            const float v = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
-            const float p = expf(v - m) / sum;
-            s_p[lane] = p;
-            s_idx[lane] = myc;
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        float tot = 0.f;
-        if (renorm)
-            for (int j = 0; j < k; ++j) tot += s_p[j];
-        if (lane < k) {
-            const float p = renorm ? s_p[lane] / tot : s_p[lane];
-            idx[(size_t)t * k + lane] = myc;
-            const float r = rnd_act<DT>(p);
-            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
-            if (w32 != nullptr) w32[(size_t)t * k + lane] = r;
-        }
-        return;
-    } else {
-        uint32_t taken = 0;
-        for (int j = 0; j < k; ++j) {
-            float bv = -INFINITY;
-            int bi = INT_MAX;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int c = lane + 64 * i;
-                if (c < E && !((taken >> i) & 1u) && (lv[i] > bv || (lv[i] == bv && c < bi))) {
-                    bv = lv[i];
-                    bi = c;
-                }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-            if (lane == 0) {
-                s_idx[j] = bi;
-                s_p[j] = expf(bv - m) / sum;
-            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == 0) {
+            s_idx[j] = bi;
+            s_p[j] = expf(bv - m) / sum;
         }
     }
     __syncthreads();
@@ -350,26 +309,13 @@ __global__ __launch_bounds__(64) void k_shared_slot(const void *__restrict__ x, 
                                                     float *__restrict__ w_ext) {
     const int t = blockIdx.x, lane = threadIdx.x;
     float acc = 0.f;
-    if (DT != MOEHIP_DT_F32 && H % 8 == 0) {  // 8 values per 16-byte load (x and g 16-byte aligned)
-        const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + (size_t)t * H);
-        const uint4 *gr = reinterpret_cast<const uint4 *>(g);
-        for (int c = lane; c < H / 8; c += 64) {
-            const uint4 xv = xr[c], gv = gr[c];
-            const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gv.x, gv.y, gv.z, gv.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)xa[i]) : __uint_as_float(xa[i] << 16);
-                const float x1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(xa[i] >> 16)) : __uint_as_float(xa[i] & 0xffff0000u);
-                const float g0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)ga[i]) : __uint_as_float(ga[i] << 16);
-                const float g1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(ga[i] >> 16)) : __uint_as_float(ga[i] & 0xffff0000u);
-                acc = fmaf(x0, g0, acc);
-                acc = fmaf(x1, g1, acc);
-            }
-        }
-    } else {
-        for (int c = lane; c < H; c += 64) acc += ld_act<DT>(x, (size_t)t * H + c) * ld_act<DT>(g, c);
+    if constexpr (DT != MOEHIP_DT_F32) {
+        if (H % 8 == 0) acc = gate_dot_wave<DT>(x, g, t, H);
     }
-    acc = wave_sum(acc);
+    if (DT == MOEHIP_DT_F32 || H % 8 != 0) {
+        for (int c = lane; c < H; c += 64) acc += ld_act<DT>(x, (size_t)t * H + c) * ld_act<DT>(g, c);
+        acc = wave_sum(acc);
+    }
     const int ks = k + 1;
     if (lane < k) {
         idx_ext[(size_t)t * ks + lane] = idx[(size_t)t * k + lane];
@@ -385,6 +331,29 @@ __global__ __launch_bounds__(64) void k_shared_slot(const void *__restrict__ x, 
 
 using namespace moehip;
 
+// logits (T, E) = x Wr^T rounded to dtype: MFMA tiles from 4 tokens (16-bit, H a multiple of 512,
+// 16-byte aligned rows), VALU GEMVs otherwise
+static void launch_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits,
+                          hipStream_t st) {
+    const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
+    const bool mf = dtype != MOEHIP_DT_F32 && vec16 && T >= 4 && H % 512 == 0;
+    const dim3 gm((T + 15) / 16, (E + 15) / 16);
+    switch (dtype) {
+        case MOEHIP_DT_F16:
+            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_F16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
+            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            break;
+        case MOEHIP_DT_BF16:
+            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_BF16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
+            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_BF16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
+            break;
+        default:
+            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F32>), g1, dim3(256), 0, st, x, Wr, T, H, E, 0, logits);
+            break;
+    }
+}
+
 extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, int E, int k, int renorm, int dtype,
                                   void *logits, int64_t *idx, void *w, float *w32, void *stream) {
     MOEHIP_REQUIRE(x && Wr && logits && idx, "router_topk: null pointer");
@@ -392,28 +361,28 @@ extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, i
     MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E,
                    "router_topk: bad sizes T=%d H=%d E=%d k=%d", T, H, E, k);
     hipStream_t st = as_stream(stream);
-    const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
-    const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
-    // a matrix product (4 tokens or more): MFMA tiles of 16 tokens x 16 experts
-    const bool mf = dtype != MOEHIP_DT_F32 && vec16 && T >= 4 && H % 512 == 0;
-    const dim3 gm((T + 15) / 16, (E + 15) / 16);
+    launch_logits(x, Wr, T, H, E, dtype, logits, st);
     switch (dtype) {
         case MOEHIP_DT_F16:
-            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_F16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
-            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
             break;
         case MOEHIP_DT_BF16:
-            if (mf) hipLaunchKernelGGL((k_router_logits_mfma<MOEHIP_DT_BF16>), gm, dim3(256), 0, st, x, Wr, T, H, E, logits);
-            else hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_BF16>), g1, dim3(256), 0, st, x, Wr, T, H, E, vec16, logits);
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_BF16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
             break;
         default:
-            hipLaunchKernelGGL((k_router_logits<MOEHIP_DT_F32>), g1, dim3(256), 0, st, x, Wr, T, H, E, 0, logits);
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F32>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
             break;
     }
     return check_launch("router");
+}
+
+extern "C" int moehip_router_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits,
+                                    void *stream) {
+    MOEHIP_REQUIRE(x && Wr && logits, "router_logits: null pointer");
+    MOEHIP_REQUIRE(dtype >= MOEHIP_DT_F16 && dtype <= MOEHIP_DT_F32, "router_logits: bad dtype %d", dtype);
+    MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024, "router_logits: bad sizes T=%d H=%d E=%d", T, H, E);
+    launch_logits(x, Wr, T, H, E, dtype, logits, as_stream(stream));
+    return check_launch("router_logits");
 }
 
 extern "C" int moehip_decide_table(const int64_t *idx, const float *w32, int k, const moehip_policy *pol,

@@ -72,7 +72,11 @@ _SIGS = {
     "moehip_grouped_gemm_multi": ([_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                    _vp, ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemv_multi": ([_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
-                                   _vp, ctypes.c_size_t, _vp], _i),
+                                   _vp, ctypes.c_size_t, _vp, _vp], _i),
+    "moehip_router_logits": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp], _i),
+    "moehip_batch_route_decide": ([_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp,
+                                   ctypes.POINTER(Policy), _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_double, _vp, _vp,
+                                   _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_batch_levels": ([_vp, _i, _i, _i, ctypes.POINTER(Policy), _vp, _vp, _vp], _i),
     "moehip_batch_vote": ([_vp, _i, _i, _vp, _vp, ctypes.c_double, ctypes.POINTER(Policy), _vp, _vp, _vp, _i, _vp,
                            _vp, _vp, _vp, _vp, _vp, _vp], _i),

@@ -107,7 +107,10 @@ class GroupedLayer:
       3. levels and skip per (token, slot)            (moehip_batch_levels)
       4. expert-sorted dispatch of the kept pairs     (moehip_dispatch)
       5. vote, resident copy, per-precision tables    (moehip_batch_vote)
-         (3-5 in one launch, moehip_batch_decide, unless fused_decide=False)
+         with fused_decide (the default): 3-5 in one launch (moehip_batch_decide), and, when the
+         router runs here on up to route_fused_tokens 16-bit tokens, the top-k, 2, 3-5 and the
+         GEMVs' work list in one launch after the logits (moehip_router_logits +
+         moehip_batch_route_decide)
       6. expert products per precision + ordered combine: batched dequant GEMVs for up to
          `gemv_tokens` tokens (moehip_grouped_gemv_multi), MFMA tiles beyond
          (moehip_grouped_gemm_multi)
@@ -117,11 +120,16 @@ class GroupedLayer:
 
     def __init__(self, store, k: int, max_tokens: int, policy=None, dtype=torch.float16,
                  router_weights: list | None = None, renorm: bool = False, shared: list | None = None,
-                 planned: list | None = None, gemv_tokens: int = 64, fused_decide: bool = True):
+                 planned: list | None = None, gemv_tokens: int = 64, fused_decide: bool = True,
+                 route_fused_tokens: int = 16):
         from .policy import PrecisionPolicy, level_to_precision
 
         self.gemv_tokens = gemv_tokens
         self.fused_decide = fused_decide
+        # up to this many tokens the top-k, shared slot, decision and work list run in the one
+        # workgroup of moehip_batch_route_decide; beyond, the top-k and shared slot spread over one
+        # wave per token in launches of their own
+        self.route_fused_tokens = route_fused_tokens
 
         self.store, self.k, self.max_tokens = store, k, max_tokens
         self.policy = policy or PrecisionPolicy("lo")
@@ -163,6 +171,7 @@ class GroupedLayer:
         self.sorted_pos = torch.empty(n * ks, dtype=torch.int32, device=d)
         self.rank = torch.empty(n * ks, dtype=torch.int32, device=d)
         self.tabs = torch.zeros(self.P, EA, 4, dtype=torch.int64, device=d)
+        self.items = torch.empty(n * ks + 1, dtype=torch.int32, device=d)
         self.info = torch.zeros(store.L, EA, dtype=torch.float32, device=d)
         self.miss = torch.zeros(1, dtype=torch.float32, device=d)
         self.offs = torch.tensor([field_offsets(store.layouts[p]) for p in precs], dtype=torch.int64, device=d)
@@ -196,6 +205,10 @@ class GroupedLayer:
         if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise RuntimeError("GroupedLayer.layer: out must be a contiguous tensor like x")
         stream = _lib.stream_of(self.device)
+        srec = self._srec[layer]
+        if idx is None and self.fused_decide and x.dtype in (torch.float16, torch.bfloat16) \
+                and T <= self.route_fused_tokens:
+            return self._layer_routed(layer, x, out, add, srec, stream)
         if idx is None:
             Wr = self.router_weights[layer]
             _lib.call("moehip_router_topk", x.data_ptr(), Wr.data_ptr(), T, self.H, self.E, k,
@@ -205,7 +218,6 @@ class GroupedLayer:
         elif idx.shape != (T, k) or w32.shape != (T, k) or idx.dtype != torch.int64 or w32.dtype != torch.float32 \
                 or not idx.is_contiguous() or not w32.is_contiguous():
             raise RuntimeError("GroupedLayer.layer: idx (T, k) int64 and w32 (T, k) float32, contiguous")
-        srec = self._srec[layer]
         if srec is not None:
             g = self.shared[layer]["gate"]
             _lib.call("moehip_shared_slot", x.data_ptr(), g.data_ptr(), T, self.H, _lib.dt_code(x.dtype),
@@ -230,9 +242,41 @@ class GroupedLayer:
                       ctypes.byref(self._pols[layer]), self.lv2p, st.rtab[layer].data_ptr(), srec, self.P,
                       self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(), self.rank.data_ptr(),
                       self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
-        entry = "moehip_grouped_gemv_multi" if T <= self.gemv_tokens else "moehip_grouped_gemm_multi"
-        _lib.call(entry, self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(),
-                  _lib.dt_code(x.dtype), T, self.H, self.I, ks, EA, 64, self.offsets.data_ptr(),
-                  self.sorted_pos.data_ptr(), self.rank.data_ptr(), pw.data_ptr(), out.data_ptr(), _lib.ptr(add), 0,
-                  self.ws.data_ptr(), self.ws.numel(), stream)
+        args = (self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(), _lib.dt_code(x.dtype), T, self.H,
+                self.I, ks, EA, 64, self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(),
+                pw.data_ptr(), out.data_ptr(), _lib.ptr(add), 0, self.ws.data_ptr(), self.ws.numel())
+        if T <= self.gemv_tokens:
+            _lib.call("moehip_grouped_gemv_multi", *args, None, stream)  # the work list is built there
+        else:
+            _lib.call("moehip_grouped_gemm_multi", *args, stream)
+        return out
+
+    def _layer_routed(self, layer, x, out, add, srec, stream):
+        """The layer with the router run here: logits, then one launch from the logits to the work
+        list of the GEMVs (moehip_batch_route_decide), then the expert products."""
+        T, k, st = x.shape[0], self.k, self.store
+        shared = srec is not None
+        ks, EA = (k + 1, self.E + 1) if shared else (k, self.E)
+        Wr = self.router_weights[layer]
+        dt = _lib.dt_code(x.dtype)
+        _lib.call("moehip_router_logits", x.data_ptr(), Wr.data_ptr(), T, self.H, self.E, dt, self.logits.data_ptr(),
+                  stream)
+        g = self.shared[layer]["gate"] if shared else None
+        gemv = T <= self.gemv_tokens
+        _lib.call("moehip_batch_route_decide", self.logits.data_ptr(), dt, T, self.E, k, 1 if self.renorm else 0,
+                  x.data_ptr(), _lib.ptr(g), self.H, self.idx.data_ptr(), self.w.data_ptr(), self.w32.data_ptr(),
+                  self.idx_ext.data_ptr(), self.w_ext.data_ptr(), ctypes.byref(self._pols[layer]),
+                  self.levels.data_ptr(), self.skip.data_ptr(), self.counts.data_ptr(), self.offsets.data_ptr(),
+                  self.sorted_pos.data_ptr(), self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p,
+                  st.rtab[layer].data_ptr(), srec, self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(),
+                  self.tabs.data_ptr(), self.info[layer].data_ptr(), self.miss.data_ptr(),
+                  self.items.data_ptr() if gemv else None, stream)
+        pw = self.w_ext if shared else self.w32
+        args = (self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(), dt, T, self.H, self.I, ks, EA, 64,
+                self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(), pw.data_ptr(),
+                out.data_ptr(), _lib.ptr(add), 0, self.ws.data_ptr(), self.ws.numel())
+        if gemv:
+            _lib.call("moehip_grouped_gemv_multi", *args, self.items.data_ptr(), stream)
+        else:
+            _lib.call("moehip_grouped_gemm_multi", *args, stream)
         return out

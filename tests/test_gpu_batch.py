@@ -196,3 +196,48 @@ def test_grouped_layer_missing_copy_and_graph(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out2, eager), r
+
+
+def test_grouped_layer_routed_graph_replays(dev):
+    """The router-to-work-list launch (moehip_batch_route_decide) and the GEMVs captured in a HIP
+    graph: every replay equals the eager layer, and the eager layer equals the unfused steps."""
+    H, I, E, k, T = 2048, 512, 512, 10, 16
+    dtype = torch.bfloat16
+    st = _store(dev, ["int4"], H, I, E, 14)
+    lay = st.layouts["int4"]
+    g = torch.Generator().manual_seed(15)
+    sh_blob = torch.zeros(lay["record_bytes"], dtype=torch.uint8, device=dev)
+    encode_record_(lay, sh_blob, (torch.randn(2 * I, H, generator=g) * 0.02).to(dev),
+                   (torch.randn(H, I, generator=g) * 0.02).to(dev))
+    gate = (torch.randn(H, generator=g) * 0.05).to(dtype).to(dev)
+    Wr = (torch.randn(E, H, generator=g) * 0.02).to(dtype).to(dev)
+    shared = [{"gate": gate, "rec": {"int4": sh_blob}}]
+    x = torch.randn(T, H, generator=g).to(dtype).to(dev)
+    fused = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype, router_weights=[Wr], renorm=True, shared=shared)
+    steps = GroupedLayer(st, k, T, PrecisionPolicy("hi"), dtype, router_weights=[Wr], renorm=True, shared=shared,
+                         fused_decide=False)
+    eager = torch.zeros(T, H, dtype=dtype, device=dev)
+    ref = torch.zeros_like(eager)
+    fused.layer(0, x, eager)
+    steps.layer(0, x, ref)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.idx[:T], steps.idx[:T]) and torch.equal(fused.w32[:T], steps.w32[:T])
+    assert torch.equal(fused.info[0], steps.info[0])
+    # the same products and combine order; the gate dot product may round differently by one ulp
+    assert (eager.float() - ref.float()).abs().max().item() <= 2e-2
+    out2 = torch.zeros_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fused.layer(0, x, out2)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        fused.layer(0, x, out2)
+    for r in range(3):
+        out2.zero_()
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out2, eager), r
