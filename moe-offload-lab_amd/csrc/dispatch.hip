@@ -326,8 +326,9 @@ extern "C" int moehip_batch_route_decide(const void *logits, int dtype, int T, i
     MOEHIP_REQUIRE(!shared || (x && idx_ext && w_ext && shared_rec && H % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
                                ((uintptr_t)gate % 16) == 0),
                    "batch_route_decide: shared expert needs x, aligned gate, idx_ext, w_ext and records");
-    MOEHIP_REQUIRE(items == nullptr || (long)T * ks <= 256L * GV_TOKENS * EA,
-                   "batch_route_decide: work list limits (256 items per expert)");
+    MOEHIP_REQUIRE(items == nullptr || T <= 256 * GV_TOKENS,
+                   "batch_route_decide: %d tokens (an expert's work items are numbered in 8 bits: <= %d)", T,
+                   256 * GV_TOKENS);
     for (int i = 0; i < 3; ++i) MOEHIP_REQUIRE(lv2p[i] >= 0 && lv2p[i] < P, "batch_route_decide: lv2p[%d]=%d", i, lv2p[i]);
     SharedRecs sr = {{0, 0, 0, 0}};
     if (shared)

@@ -1000,7 +1000,8 @@ extern "C" int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t 
                                          const int32_t *sorted_pos, const int32_t *rank, const float *w, void *out,
                                          const void *add, int accumulate, void *ws, size_t ws_bytes,
                                          const int32_t *items, void *stream) {
-    MOEHIP_REQUIRE((long)T * k <= 256L * GV_TOKENS * E, "grouped_gemv: work list limits (256 items per expert)");
+    MOEHIP_REQUIRE(T <= 256 * GV_TOKENS, "grouped_gemv: %d tokens (an expert's work items are numbered in 8 bits: <= %d)",
+                   T, 256 * GV_TOKENS);
     return gg_run(P, precs, tabs, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
                   ws_bytes, stream, 0, 1, items);
 }
