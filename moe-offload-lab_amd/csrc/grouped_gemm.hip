@@ -273,10 +273,12 @@ __device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2],
         for (int u = 0; u < RING; ++u) {
             const int c = c0 + u;
             const int b = c & 1;
-            if (c < nch) {
-                mma_chunk<PREC, NM>(wr[u], s_a + b * ABUF, dk, d);
-                if (c + 1 < nch) xs_store<CK>(xv, s_a + (b ^ 1) * ABUF);
-            }
+            if (c < nch) mma_chunk<PREC, NM>(wr[u], s_a + b * ABUF, dk, d);
+            // unconditional: under a branch the compiler sinks the activation load of the previous
+            // step down to this store, and waiting for it then waits for every weight load too.
+            // The other buffer was last read before the previous barrier; a store past the last
+            // chunk is overwritten by the same thread in the next pass's prologue.
+            xs_store<CK>(xv, s_a + (b ^ 1) * ABUF);
             xs_load<CK>(srcrow, min(c + 2, cl), xv);
             load_chunk<PREC>(wr[u], qp, sp, min(c + RING, cl));
             if (c < nch) __syncthreads();
@@ -562,6 +564,11 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
 #pragma unroll
                     for (int q = 0; q < 4; ++q) xv[t][i][4 * b + q] = pack_h2(v[8 * b + q] * sc, v[8 * b + q + 4] * sc);
             }
+            // lanes past the row's chunks (G > C / CPL) load the clamped last chunk: a zero slice
+            // makes their products zero, so the weights need no select
+            if (cl + i * G >= C)
+#pragma unroll
+                for (int j = 0; j < ND; ++j) xv[t][i][j] = 0u;
         }
     auto compute = [&](int buf, int g) {
 #pragma unroll
@@ -573,11 +580,8 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                 for (int t = 0; t < GV_NT; ++t) acc[m][t] = 0.f;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) {
-                    // lanes past the row's chunks (G > C / CPL) use zero bytes and scale 0: nothing
-                    const bool ok = cl + i * G < C;
                     uint32_t wv[ND];
-                    gv_deq<PREC>(ok ? q[buf][p][m][i] : make_uint4(0u, 0u, 0u, 0u), ok ? sr[buf][p][m][i] : 0u, dk,
-                                 wv);
+                    gv_deq<PREC>(q[buf][p][m][i], sr[buf][p][m][i], dk, wv);
 #pragma unroll
                     for (int t = 0; t < GV_NT; ++t) {
                         if (t < nt) {
@@ -610,13 +614,21 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
             }
         }
     };
-    for (int g = 0; g < NG; g += 2) {
-        if (g + 1 < NG) load(1, g + 1);
+    // steady state with unconditional loads (a load under a branch makes the wait for the other
+    // buffer a wait for every load), then the last one or two groups
+    int g = 0;
+    for (; g + 2 < NG; g += 2) {
+        load(1, g + 1);
         compute(0, g);
-        if (g + 1 < NG) {
-            if (g + 2 < NG) load(0, g + 2);
-            compute(1, g + 1);
-        }
+        load(0, g + 2);
+        compute(1, g + 1);
+    }
+    if (g + 1 < NG) {
+        load(1, g + 1);
+        compute(0, g);
+        compute(1, g + 1);
+    } else {
+        compute(0, g);
     }
     // the outputs, written once the weight stream is done (a store makes every later wait for
     // a load also wait for the store's acknowledgement)
@@ -673,6 +685,7 @@ __global__ __launch_bounds__(256) void k_gemv_up(const uint16_t *__restrict__ x,
     gu8 *qb = record_ptr(tab[4 * e + 0]);
     if (ne <= 0 || qb == nullptr) return;
     const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
+    if (r0 >= I) return;  // a row block of the padding to a multiple of 8
     gv_rows<PREC, CPL, P, true>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 1]), lg, r0, NG,
                                 nullptr, hb, I, dk);
 }
@@ -690,6 +703,7 @@ __global__ __launch_bounds__(256) void k_gemv_down(const float *__restrict__ hb,
     gu8 *qb = record_ptr(tab[4 * e + 2]);
     if (ne <= 0 || qb == nullptr) return;
     const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
+    if (r0 >= H) return;  // a row block of the padding to a multiple of 8
     gv_rows<PREC, CPL, P, false>(hb, nullptr, I, H, 0, 1, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 3]), lg, r0, NG,
                                  w, y, H, dk);
 }
@@ -848,6 +862,12 @@ static GvGeo gv_geo(int prec, int K) {
     return g;
 }
 
+#ifndef GV_WG_BYTES
+#define GV_WG_BYTES (128 << 10)
+#endif
+#ifndef GV_MIN_WGS
+#define GV_MIN_WGS 2048
+#endif
 template <int PREC, int CPL>
 static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
                           int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
@@ -857,10 +877,20 @@ static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const
     // (an upper bound of the work items) still give about two workgroups per CU slot
     const int groups = (rows + g.rows_per_block - 1) / g.rows_per_block;
     const int row_bytes = (up ? 2 : 1) * (up ? H : I) * (PREC == MOEHIP_PREC_INT4 ? 1 : (PREC == MOEHIP_PREC_INT8 || PREC == MOEHIP_PREC_FP8 ? 2 : 4)) / 2;
-    int ng = max(1, min(groups, (128 << 10) / max(1, g.rows_per_block * row_bytes)));
+    int ng = max(1, min(groups, GV_WG_BYTES / max(1, g.rows_per_block * row_bytes)));
     ng = max(1, min(ng, GV_MAXROWS / g.rows_per_block));
-    ng = max(1, min(ng, groups * NP / 2048));
-    const dim3 grid((groups + ng - 1) / ng, NP);
+    ng = max(1, min(ng, groups * NP / GV_MIN_WGS));
+    // row blocks per item a multiple of the 8 XCDs: workgroups are dealt to the XCDs round robin,
+    // so row block b of every item (the items of one expert, one per token, are adjacent) then
+    // runs on XCD b % 8 and the re-reads of its rows hit that XCD's L2
+    int gx = (groups + ng - 1) / ng;
+#ifndef GV_NO_XCD
+    gx = (gx + 7) & ~7;
+    ng = (groups + gx - 1) / gx;
+    gx = (groups + ng - 1) / ng;
+    gx = (gx + 7) & ~7;
+#endif
+    const dim3 grid(gx, NP);
     if (up)
         hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act), ae,
                            H, I, k, items, NP, offsets,
