@@ -1241,14 +1241,27 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
         }
         __syncthreads();  // s_part is rewritten by the next chunk
     }
+    // the optional terms: each one's loads issued together under a uniform branch (clamped rows
+    // of this workgroup's own range), so they cost one round trip, not one per row
+    if (a.accumulate) {
+        float v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) v[u] = ld_act<XDT>(a.out, min(r0 + min(tid + 256 * u, rows - 1), a.H - 1));
+#pragma unroll
+        for (int u = 0; u < PER; ++u) acc[u] += v[u];
+    }
+    if (a.add != nullptr) {
+        float v[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) v[u] = ld_act<XDT>(a.add, min(r0 + min(tid + 256 * u, rows - 1), a.H - 1));
+#pragma unroll
+        for (int u = 0; u < PER; ++u) acc[u] += v[u];
+    }
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
         const int rr = tid + 256 * u, r = r0 + rr;
         if (rr >= rows || r >= a.H) continue;
-        float s = acc[u];
-        if (a.accumulate) s += ld_act<XDT>(a.out, r);
-        if (a.add != nullptr) s += ld_act<XDT>(a.add, r);
-        st_act<XDT>(a.out, r, s);
+        st_act<XDT>(a.out, r, acc[u]);
     }
     stamp(st, 5);
     __syncthreads();  // sh.h is reused by the next item

@@ -193,7 +193,8 @@ class MoEDecoder:
                   self.P, st.E, self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tab.data_ptr(),
                   self.wtab.data_ptr(), self.info[layer].data_ptr(), self.miss.data_ptr(), _lib.stream_of(idx.device))
 
-    def experts(self, x: torch.Tensor, out: torch.Tensor, cpu_part: torch.Tensor | None = None) -> None:
+    def experts(self, x: torch.Tensor, out: torch.Tensor, cpu_part: torch.Tensor | None = None,
+                accumulate: bool = False) -> None:
         first = True
         for pi, plan in self.plans.items():
             plan.up(self.k, self.tab[pi], self.wtab[pi], x, self.h[pi], self.acc, zero=first)
@@ -202,16 +203,20 @@ class MoEDecoder:
             self.acc.zero_()
         for pi, plan in self.plans.items():
             plan.down(self.k, self.tab[pi], self.wtab[pi], self.h[pi], self.acc)
-        _combine(self.acc, out, cpu_part, accumulate=False)
+        _combine(self.acc, out, cpu_part, accumulate=accumulate)
 
     def layer(self, layer: int, x: torch.Tensor, out: torch.Tensor, idx: torch.Tensor | None = None,
-              w32: torch.Tensor | None = None, cpu_part: torch.Tensor | None = None) -> torch.Tensor:
-        """out (1, H) = MoE layer `layer` applied to x (1, H). With idx/w32 given, the router is skipped."""
+              w32: torch.Tensor | None = None, cpu_part: torch.Tensor | None = None,
+              accumulate: bool = False) -> torch.Tensor:
+        """out (1, H) = MoE layer `layer` applied to x (1, H) (+ out if accumulate) (+ cpu_part, the
+        partial of experts run elsewhere), summed in fp32 in that order. With idx/w32 given, the
+        router is skipped."""
         if self.fused:
             st = self.store
             Wr = None if idx is not None else self.router_weights[layer]
             _lib.call("moehip_decode_layer", ctypes.byref(self._descs[layer]), x.data_ptr(), _lib.ptr(Wr),
-                      _lib.ptr(idx), _lib.ptr(w32), st.rtab[layer].data_ptr(), out.data_ptr(), _lib.ptr(cpu_part), 0,
+                      _lib.ptr(idx), _lib.ptr(w32), st.rtab[layer].data_ptr(), out.data_ptr(), _lib.ptr(cpu_part),
+                      1 if accumulate else 0,
                       self.logits.data_ptr(), self.idx.data_ptr() if idx is None else None,
                       self.w.data_ptr() if idx is None else None, self.w32.data_ptr() if idx is None else None,
                       self.info[layer].data_ptr(), self.miss.data_ptr(), self.ws.data_ptr(), self.ws.numel(),
@@ -221,7 +226,7 @@ class MoEDecoder:
             self.route(layer, x)
             idx, w32 = self.idx, self.w32
         self.decide(layer, idx, w32)
-        self.experts(x, out, cpu_part)
+        self.experts(x, out, cpu_part, accumulate)
         return out
 
 

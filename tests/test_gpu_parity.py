@@ -478,6 +478,33 @@ def test_fused_repeated_launches_and_graph_replays(dev):
     dec.check_error()
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_layer_add_and_accumulate(dev, fused):
+    """The optional output terms: out = layer(x) (+ out if accumulate) (+ cpu_part, the partial of
+    experts run elsewhere: the offload path's CPU experts), summed in fp32 in that order."""
+    H, I, E, k = 1024, 512, 32, 4
+    dtype = torch.float16
+    S = _Stack(dev, H, I, E, 1, ["int4"], 11)
+    dec = MoEDecoder(S.store, k, PrecisionPolicy("lo"), dtype, router_weights=[w.to(dev) for w in S.Wr],
+                     fused=fused)
+    x = torch.randn(1, H, generator=S.g).to(dtype)
+    ref = S.reference(0, x, k, False, O.Policy("lo"))[3]
+    scale = float(np.abs(ref).max())
+    add = (torch.randn(1, H, generator=S.g) * scale).to(dtype)
+    o0 = (torch.randn(1, H, generator=S.g) * scale).to(dtype)
+    for acc_flag, with_add in [(False, True), (True, False), (True, True)]:
+        out = o0.to(dev) if acc_flag else torch.zeros(1, H, dtype=dtype, device=dev)
+        dec.layer(0, x.to(dev), out, cpu_part=add.to(dev) if with_add else None, accumulate=acc_flag)
+        torch.cuda.synchronize()
+        exp = ref.astype(np.float64)
+        if acc_flag:
+            exp = exp + o0.double().numpy()
+        if with_add:
+            exp = exp + add.double().numpy()
+        assert_layer_close(out.float().cpu().numpy(), exp, dtype)
+    dec.check_error()
+
+
 def test_fused_external_routing(dev):
     """Router skipped: idx / w32 given (the experts-module call of moelab/runtime.py:1108)."""
     H, I, E, k = 512, 256, 16, 4
