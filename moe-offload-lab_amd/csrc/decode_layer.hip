@@ -249,14 +249,9 @@ __device__ __forceinline__ int block_of(const int (&base)[4], int P, int u) {
 //   int8: per 4 values (v0,v2) (v1,v3);                 corr = -1152 * sum
 //   fp16: natural pairs;                                corr = 0
 // ---------------------------------------------------------------------------------------
-constexpr uint32_t H2_M1032 = 0xE408E408u;  // (-1032, -1032)
-constexpr uint32_t H2_M72 = 0xD480D480u;    // (-72, -72)
-constexpr uint32_t H2_M1152 = 0xE480E480u;  // (-1152, -1152)
-
 // pairs of one chunk from 32-bit words w[0 .. VPC/2) (each word = 2 consecutive fp16 values)
 template <int PREC>
 __device__ __forceinline__ void pair_chunk(const uint32_t *w, uint32_t *xp, float &corr) {
-    float c = 0.f;
     if constexpr (PREC == MOEHIP_PREC_INT4) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -265,10 +260,6 @@ __device__ __forceinline__ void pair_chunk(const uint32_t *w, uint32_t *xp, floa
             xp[4 * j + 1] = hi_hi(d0, d2);
             xp[4 * j + 2] = lo_lo(d1, d3);
             xp[4 * j + 3] = hi_hi(d1, d3);
-            c = dot2h(H2_M1032, xp[4 * j + 0], c);
-            c = dot2h(H2_M72, xp[4 * j + 1], c);
-            c = dot2h(H2_M1032, xp[4 * j + 2], c);
-            c = dot2h(H2_M72, xp[4 * j + 3], c);
         }
     } else if constexpr (PREC == MOEHIP_PREC_INT8) {
 #pragma unroll
@@ -276,14 +267,12 @@ __device__ __forceinline__ void pair_chunk(const uint32_t *w, uint32_t *xp, floa
             const uint32_t d0 = w[2 * j + 0], d1 = w[2 * j + 1];
             xp[2 * j + 0] = lo_lo(d0, d1);
             xp[2 * j + 1] = hi_hi(d0, d1);
-            c = dot2h(H2_M1152, xp[2 * j + 0], c);
-            c = dot2h(H2_M1152, xp[2 * j + 1], c);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xp[j] = w[j];
     }
-    corr = c;
+    corr = chunk_corr<PREC>(xp);
 }
 
 // fp32 values -> fp16 words scaled by 2^-e (e from the chunk's largest magnitude, so that it
@@ -299,38 +288,6 @@ __device__ __forceinline__ float scale_to_h(const float *v, uint32_t *w) {
 #pragma unroll
     for (int i = 0; i < VPC / 2; ++i) w[i] = pack_h2(v[2 * i] * down, v[2 * i + 1] * down);
     return ldexpf(1.0f, e);
-}
-
-// chunk dot products sum(weight * v) for the dot2 formats (before the group scale)
-template <int PREC>
-__device__ __forceinline__ float dot2_chunk(const uint4 q, const uint32_t *xp, float corr) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    if constexpr (PREC == MOEHIP_PREC_INT4) {
-        float ae = corr, ao = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t t = d[j] >> 8;
-            ae = dot2h(and_or(d[j], 0x000F000Fu, 0x64006400u), xp[4 * j + 0], ae);
-            ao = dot2h(and_or(d[j], 0x00F000F0u, 0x64006400u), xp[4 * j + 1], ao);
-            ae = dot2h(and_or(t, 0x000F000Fu, 0x64006400u), xp[4 * j + 2], ae);
-            ao = dot2h(and_or(t, 0x00F000F0u, 0x64006400u), xp[4 * j + 3], ao);
-        }
-        return fmaf(ao, 0.0625f, ae);
-    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
-        float a0 = corr, a1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t b = d[j] ^ 0x80808080u, t = b >> 8;
-            a0 = dot2h(and_or(b, 0x00FF00FFu, 0x64006400u), xp[2 * j + 0], a0);
-            a1 = dot2h(and_or(t, 0x00FF00FFu, 0x64006400u), xp[2 * j + 1], a1);
-        }
-        return a0 + a1;
-    } else {
-        float a = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a = dot2h(d[j], xp[j], a);
-        return a;
-    }
 }
 
 // vector registers of one lane for one item format

@@ -156,4 +156,66 @@ __device__ __forceinline__ float weight_at(const uint8_t *qb, const uint8_t *sb,
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// dot2 chunk products of the integer records against fp16 activation pairs in operand order
+// (per 8 values (v0,v4) (v1,v5) (v2,v6) (v3,v7) for int4, (v0,v2) (v1,v3) per 4 for int8).
+// The weights enter as fp16 1024 + n (int4 low nibble), 1024 + 16 n (int4 high nibble, the sum
+// scaled by 1/16) or 1024 + q + 128 (int8), each from one v_and_or_b32; the offsets are taken
+// out by a per-chunk correction that depends on the activations only:
+//   int4: corr = -1032 * sum(even pairs) - 72 * sum(odd pairs);  int8: corr = -1152 * sum.
+// The result is sum(q * v) before the group scale (fp32 accumulation).
+// ---------------------------------------------------------------------------------------
+constexpr uint32_t H2_M1032 = 0xE408E408u;  // (-1032, -1032)
+constexpr uint32_t H2_M72 = 0xD480D480u;    // (-72, -72)
+constexpr uint32_t H2_M1152 = 0xE480E480u;  // (-1152, -1152)
+
+template <int PREC>
+__device__ __forceinline__ float chunk_corr(const uint32_t *xp) {
+    float c = 0.f;
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c = dot2h(H2_M1032, xp[4 * j + 0], c);
+            c = dot2h(H2_M72, xp[4 * j + 1], c);
+            c = dot2h(H2_M1032, xp[4 * j + 2], c);
+            c = dot2h(H2_M72, xp[4 * j + 3], c);
+        }
+    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c = dot2h(H2_M1152, xp[j], c);
+    }
+    return c;
+}
+
+template <int PREC>
+__device__ __forceinline__ float dot2_chunk(const uint4 q, const uint32_t *xp, float corr) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    if constexpr (PREC == MOEHIP_PREC_INT4) {
+        float ae = corr, ao = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t t = d[j] >> 8;
+            ae = dot2h(and_or(d[j], 0x000F000Fu, 0x64006400u), xp[4 * j + 0], ae);
+            ao = dot2h(and_or(d[j], 0x00F000F0u, 0x64006400u), xp[4 * j + 1], ao);
+            ae = dot2h(and_or(t, 0x000F000Fu, 0x64006400u), xp[4 * j + 2], ae);
+            ao = dot2h(and_or(t, 0x00F000F0u, 0x64006400u), xp[4 * j + 3], ao);
+        }
+        return fmaf(ao, 0.0625f, ae);
+    } else if constexpr (PREC == MOEHIP_PREC_INT8) {
+        float a0 = corr, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t b = d[j] ^ 0x80808080u, t = b >> 8;
+            a0 = dot2h(and_or(b, 0x00FF00FFu, 0x64006400u), xp[2 * j + 0], a0);
+            a1 = dot2h(and_or(t, 0x00FF00FFu, 0x64006400u), xp[2 * j + 1], a1);
+        }
+        return a0 + a1;
+    } else {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = dot2h(d[j], xp[j], a);
+        return a;
+    }
+}
+
 }  // namespace moehip

@@ -472,15 +472,24 @@ __device__ __forceinline__ void gv_slice_load(const uint16_t *row, int c, uint4 
 #pragma unroll
     for (int b = 0; b < VPC / 8; ++b) raw[b] = p[b];
 }
-template <int VPC>
+// (int8 records: the pairs of the integer dot instead, (v0,v2) (v1,v3) per 4 values)
+template <int VPC, bool I8 = false>
 __device__ __forceinline__ void gv_slice_perm(const uint4 *raw, uint32_t *xv) {
 #pragma unroll
     for (int b = 0; b < VPC / 8; ++b) {
         const uint4 u = raw[b];
-        xv[4 * b] = lo_lo(u.x, u.z), xv[4 * b + 1] = hi_hi(u.x, u.z);
-        xv[4 * b + 2] = lo_lo(u.y, u.w), xv[4 * b + 3] = hi_hi(u.y, u.w);
+        if constexpr (I8) {
+            xv[4 * b] = lo_lo(u.x, u.y), xv[4 * b + 1] = hi_hi(u.x, u.y);
+            xv[4 * b + 2] = lo_lo(u.z, u.w), xv[4 * b + 3] = hi_hi(u.z, u.w);
+        } else {
+            xv[4 * b] = lo_lo(u.x, u.z), xv[4 * b + 1] = hi_hi(u.x, u.z);
+            xv[4 * b + 2] = lo_lo(u.y, u.w), xv[4 * b + 3] = hi_hi(u.y, u.w);
+        }
     }
 }
+// the first value of pair q of 8 (the second is 4 further, or 2 further for the int8 pairs)
+template <bool I8>
+__device__ __forceinline__ constexpr int gv_pair_first(int q) { return I8 ? 4 * (q >> 1) + (q & 1) : q; }
 
 // NG row groups of 4 P RPW rows from r0 (gate and up rows for UP) of one expert, against up to
 // GV_NT of its tokens; UP: h[pair, r] = silu(gate . x) * (up . x); else y[pair, r] = w 2^he (down . h).
@@ -544,12 +553,16 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
     load(0, 0);
     uint32_t xv[GV_NT][CPL][ND];
     float fe[GV_NT][CPL];
+    // int4 / int8: the weights' integers straight into dot2 (offsets removed by the per-chunk
+    // correction, the group scale applied to the chunk sum in fp32)
+    constexpr bool IDOT = PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8;
+    float corr[GV_NT][CPL];
 #pragma unroll
     for (int t = 0; t < GV_NT; ++t)
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             if constexpr (UP) {
-                gv_slice_perm<VPC>(xr[t][i], xv[t][i]);
+                gv_slice_perm<VPC, PREC == MOEHIP_PREC_INT8>(xr[t][i], xv[t][i]);
                 fe[t][i] = 1.0f;
             } else {
                 const float *v = reinterpret_cast<const float *>(xr[t][i]);
@@ -562,13 +575,18 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
 #pragma unroll
                 for (int b = 0; b < VPC / 8; ++b)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) xv[t][i][4 * b + q] = pack_h2(v[8 * b + q] * sc, v[8 * b + q + 4] * sc);
+                    for (int q = 0; q < 4; ++q) {
+                        constexpr bool I8 = PREC == MOEHIP_PREC_INT8;
+                        const int f = 8 * b + gv_pair_first<I8>(q);
+                        xv[t][i][4 * b + q] = pack_h2(v[f] * sc, v[f + (I8 ? 2 : 4)] * sc);
+                    }
             }
             // lanes past the row's chunks (G > C / CPL) load the clamped last chunk: a zero slice
             // makes their products zero, so the weights need no select
             if (cl + i * G >= C)
 #pragma unroll
                 for (int j = 0; j < ND; ++j) xv[t][i][j] = 0u;
+            if constexpr (IDOT) corr[t][i] = chunk_corr<PREC>(xv[t][i]);
         }
     auto compute = [&](int buf, int g) {
 #pragma unroll
@@ -580,6 +598,16 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                 for (int t = 0; t < GV_NT; ++t) acc[m][t] = 0.f;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) {
+                    if constexpr (IDOT) {
+                        const float sc = f16_to_f32(sr[buf][p][m][i] & 0xffffu);
+#pragma unroll
+                        for (int t = 0; t < GV_NT; ++t) {
+                            if (t < nt) {
+                                const float cd = dot2_chunk<PREC>(q[buf][p][m][i], xv[t][i], corr[t][i]);
+                                acc[m][t] = fmaf(cd, UP ? sc : sc * fe[t][i], acc[m][t]);
+                            }
+                        }
+                    } else {
                     uint32_t wv[ND];
                     gv_deq<PREC>(q[buf][p][m][i], sr[buf][p][m][i], dk, wv);
 #pragma unroll
@@ -595,6 +623,7 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                                 acc[m][t] = fmaf(pc, fe[t][i], acc[m][t]);
                             }
                         }
+                    }
                     }
                 }
             }
