@@ -287,13 +287,26 @@ int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_
  * moehip_batch_levels + moehip_dispatch + moehip_batch_vote in one launch (one workgroup; the same
  * arguments and results): w32 / idx are (T, ks) with the shared expert (id E) as the last slot
  * when has_shared. T * ks <= 65536, E + has_shared <= 1025. For batched decode, where each of
- * those steps is a few microseconds of launch latency.
+ * those steps is a few microseconds of launch latency. items (T * ks + 1 int32, or NULL): also
+ * the work list of moehip_grouped_gemv_multi (T <= 256).
  */
 int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int ks, const moehip_policy *pol,
                         int32_t *levels, uint8_t *skip, int E, int has_shared, int32_t *counts, int32_t *offsets,
                         int32_t *sorted_pos, int32_t *rank, double hi_vote, const int *lv2p, const int64_t *rtab,
                         const int64_t *shared_rec, int P, const int64_t *offs, const int *planned, int64_t *tabs,
-                        float *info, float *miss, void *stream);
+                        float *info, float *miss, int32_t *items, void *stream);
+
+/*
+ * The per-token part of moehip_batch_route_decide over many workgroups (one wave per token): softmax
+ * top-k of the logits (as moehip_router_topk: idx (T, k) int64, w_out (T, k) in dtype or NULL,
+ * w32 (T, k) fp32 holding dtype values) and, when gate != NULL, the shared expert as slot k (as
+ * moehip_shared_slot: idx_ext / w_ext (T, k + 1); x (T, H), gate (H) 16-byte aligned). For batches
+ * too large for the single-workgroup launch; moehip_batch_decide takes it from there.
+ * logits (T, E) fp16 / bf16, E <= 1024, k <= 32.
+ */
+int moehip_route_tokens(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
+                        const void *gate, int H, int64_t *idx, void *w_out, float *w32, int64_t *idx_ext, float *w_ext,
+                        void *stream);
 
 /*
  * The logits part of moehip_router_topk alone: logits (T, E) = x Wr^T rounded to dtype (the gate's

@@ -132,6 +132,67 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ i
     dispatch_wg(idx, skip, NP, E, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
 }
 
+// softmax top-k of token t (one wave) and, when gate != nullptr, the shared expert as slot k:
+// idx / w_out / w32 (T, k) and idx_ext / w_ext (T, k + 1) (the same results as moehip_router_topk's
+// top-k part and moehip_shared_slot). s_p: 64 floats of this wave's LDS.
+template <int DT>
+__device__ __forceinline__ void route_token(const void *logits, int E, int k, int renorm, const void *x,
+                                            const void *gate, int H, int t, int64_t *idx, void *wout, float *w32,
+                                            int64_t *idx_ext, float *w_ext, float *s_p) {
+    const int lane = threadIdx.x & 63;
+    const bool shared = gate != nullptr;
+    const int ks = k + (shared ? 1 : 0);
+    int myc;
+    float p;
+    topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_p, myc, p);
+    const float r = rnd_act<DT>(p);
+    if (lane < k) {
+        idx[(size_t)t * k + lane] = myc;
+        if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
+        w32[(size_t)t * k + lane] = r;
+        if (shared) {
+            idx_ext[(size_t)t * ks + lane] = myc;
+            w_ext[(size_t)t * ks + lane] = r;
+        }
+    }
+    if (shared) {
+        const float l = rnd_act<DT>(gate_dot_wave<DT>(x, gate, t, H));
+        if (lane == k) {
+            idx_ext[(size_t)t * ks + k] = E;
+            w_ext[(size_t)t * ks + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
+        }
+    }
+}
+
+// the work list of the batched GEMVs (whole workgroup of 1024): one item (e << 8 | z) per
+// GV_TOKENS pairs of every expert, in expert order (exclusive scan of ceil(n_e / GV_TOKENS));
+// items[np] = their number. offsets must be visible to the workgroup (its own writes + barrier).
+__device__ __forceinline__ void write_items(const int32_t *offsets, int EA, int np, int32_t *items, int *s_wtot) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int base = 0;
+    for (int e0 = 0; e0 < EA; e0 += 1024) {
+        const int e = e0 + tid;
+        const int n = e < EA ? offsets[e + 1] - offsets[e] : 0;
+        const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
+        int incl = nz;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        if (lane == 63) s_wtot[wave] = incl;
+        __syncthreads();
+        int wb = base, tot = base;
+        for (int w = 0; w < DP_WAVES; ++w) {
+            if (w < wave) wb += s_wtot[w];
+            tot += s_wtot[w];
+        }
+        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
+        base = tot;
+        __syncthreads();
+    }
+    if (tid == 0) items[np] = base;
+}
+
 // The whole T > 1 decision in one workgroup (batched decode, where every step is latency-bound):
 // levels per (token, slot) (one wave per token, slot_level), the dispatch of the kept pairs over
 // the E + has_shared experts, and the vote / copy / tables per expert (vote_expert); the same
@@ -145,7 +206,7 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
                                                        int lv2, const int64_t *__restrict__ rtab, SharedRecs srec, int P,
                                                        const int64_t *__restrict__ offs, const int *__restrict__ planned,
                                                        int64_t *__restrict__ tabs, float *__restrict__ info,
-                                                       float *__restrict__ miss) {
+                                                       float *__restrict__ miss, int32_t *__restrict__ items) {
     extern __shared__ int s_cnt[];
     __shared__ int s_wtot[DP_WAVES];
     __shared__ float s_w[DP_WAVES][64], s_sorted[DP_WAVES][64], s_total[DP_WAVES];
@@ -171,11 +232,28 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     for (int e = tid; e < EA; e += 1024)
         vote_expert(e, levels, E, has_shared, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec, P,
                     offs, planned, tabs, rank, info, miss);
+    if (items == nullptr) return;
+    __syncthreads();  // the offsets are this workgroup's own writes
+    write_items(offsets, EA, T * ks, items, s_wtot);
 }
 
 }  // namespace moehip
 
 using namespace moehip;
+
+// per-token routing of moehip_batch_route_decide on its own, over many workgroups (one wave per
+// token): for batches whose tokens would queue behind each other in the single-workgroup launch
+template <int DT>
+__global__ __launch_bounds__(256) void k_route_tokens(const void *__restrict__ logits, int E, int k, int renorm,
+                                                      const void *__restrict__ x, const void *__restrict__ gate, int H,
+                                                      int T, int64_t *__restrict__ idx, void *__restrict__ wout,
+                                                      float *__restrict__ w32, int64_t *__restrict__ idx_ext,
+                                                      float *__restrict__ w_ext) {
+    __shared__ float s_p[4][64];
+    const int wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
+    if (t >= T) return;
+    route_token<DT>(logits, E, k, renorm, x, gate, H, t, idx, wout, w32, idx_ext, w_ext, s_p[wave]);
+}
 
 // Batched decode, everything between the router logits and the expert products in one workgroup:
 // softmax top-k per token (one wave per token, topk_wave), the shared expert as slot k (its gate
@@ -202,28 +280,8 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     int64_t *pidx = shared ? idx_ext : idx;
     float *pw = shared ? w_ext : w32;
     // routing of every token
-    for (int t = wave; t < T; t += DP_WAVES) {
-        int myc;
-        float p;
-        topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_w[wave], myc, p);
-        const float r = rnd_act<DT>(p);
-        if (lane < k) {
-            idx[(size_t)t * k + lane] = myc;
-            if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
-            w32[(size_t)t * k + lane] = r;
-            if (shared) {
-                idx_ext[(size_t)t * ks + lane] = myc;
-                w_ext[(size_t)t * ks + lane] = r;
-            }
-        }
-        if (shared) {
-            const float l = rnd_act<DT>(gate_dot_wave<DT>(x, gate, t, H));
-            if (lane == k) {
-                idx_ext[(size_t)t * ks + k] = E;
-                w_ext[(size_t)t * ks + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
-            }
-        }
-    }
+    for (int t = wave; t < T; t += DP_WAVES)
+        route_token<DT>(logits, E, k, renorm, x, gate, H, t, idx, wout, w32, idx_ext, w_ext, s_w[wave]);
     __syncthreads();
     // levels
     for (int t = wave; t < T; t += DP_WAVES) {
@@ -247,31 +305,8 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
         vote_expert(e, levels, E, shared ? 1 : 0, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec,
                     P, offs, planned, tabs, rank, info, miss);
     if (items == nullptr) return;
-    // the work list: exclusive scan of ceil(n_e / GV_TOKENS) over the experts (the offsets are
-    // this workgroup's own writes, ordered by the barrier)
-    __syncthreads();
-    int base = 0;
-    for (int e0 = 0; e0 < EA; e0 += 1024) {
-        const int e = e0 + tid;
-        const int n = e < EA ? offsets[e + 1] - offsets[e] : 0;
-        const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
-        int incl = nz;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
-        }
-        if (lane == 63) s_wtot[wave] = incl;
-        __syncthreads();
-        int wb = base, tot = base;
-        for (int w = 0; w < DP_WAVES; ++w) {
-            if (w < wave) wb += s_wtot[w];
-            tot += s_wtot[w];
-        }
-        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
-        base = tot;
-        __syncthreads();
-    }
-    if (tid == 0) items[T * ks] = base;
+    __syncthreads();  // the offsets are this workgroup's own writes
+    write_items(offsets, EA, T * ks, items, s_wtot);
 }
 
 static bool enable_big_lds(const void *fn, size_t lds) {
@@ -284,10 +319,13 @@ extern "C" int moehip_batch_decide(const float *w32, const int64_t *idx, int T, 
                                    int32_t *offsets, int32_t *sorted_pos, int32_t *rank, double hi_vote,
                                    const int *lv2p, const int64_t *rtab, const int64_t *shared_rec, int P,
                                    const int64_t *offs, const int *planned, int64_t *tabs, float *info, float *miss,
-                                   void *stream) {
+                                   int32_t *items, void *stream) {
     MOEHIP_REQUIRE(w32 && idx && pol && levels && skip && counts && offsets && sorted_pos && rank && lv2p && rtab &&
                        offs && planned && tabs,
                    "batch_decide: null pointer");
+    MOEHIP_REQUIRE(items == nullptr || T <= 256 * GV_TOKENS,
+                   "batch_decide: %d tokens (an expert's work items are numbered in 8 bits: <= %d)", T,
+                   256 * GV_TOKENS);
     const int EA = E + (has_shared ? 1 : 0);
     MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 64 && ks >= k && ks <= 64 && (long)T * ks <= 65536 && E > 0 && EA <= 1025 &&
                        P > 0 && P <= 4,
@@ -304,7 +342,7 @@ extern "C" int moehip_batch_decide(const float *w32, const int64_t *idx, int T, 
                    "batch_decide: cannot enable %zu bytes of LDS", lds);
     hipLaunchKernelGGL(k_batch_decide, dim3(1), dim3(1024), lds, as_stream(stream), w32, idx, T, k, ks, *pol, levels,
                        skip, E, has_shared ? 1 : 0, ebits, counts, offsets, sorted_pos, rank, hi_vote, lv2p[0], lv2p[1],
-                       lv2p[2], rtab, sr, P, offs, planned, tabs, info, miss);
+                       lv2p[2], rtab, sr, P, offs, planned, tabs, info, miss, items);
     return check_launch("batch_decide");
 }
 
@@ -353,6 +391,26 @@ extern "C" int moehip_batch_route_decide(const void *logits, int dtype, int T, i
                            miss, items);
     }
     return check_launch("batch_route_decide");
+}
+
+extern "C" int moehip_route_tokens(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
+                                   const void *gate, int H, int64_t *idx, void *w_out, float *w32, int64_t *idx_ext,
+                                   float *w_ext, void *stream) {
+    MOEHIP_REQUIRE(logits && idx && w32, "route_tokens: null pointer");
+    MOEHIP_REQUIRE(dtype == MOEHIP_DT_F16 || dtype == MOEHIP_DT_BF16, "route_tokens: logits dtype %d", dtype);
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 32 && k <= E && E <= 1024, "route_tokens: bad sizes T=%d E=%d k=%d", T, E,
+                   k);
+    MOEHIP_REQUIRE(gate == nullptr || (x && idx_ext && w_ext && H % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
+                                       ((uintptr_t)gate % 16) == 0),
+                   "route_tokens: shared expert needs x, aligned gate, idx_ext and w_ext");
+    const dim3 grid((T + 3) / 4);
+    if (dtype == MOEHIP_DT_F16)
+        hipLaunchKernelGGL((k_route_tokens<MOEHIP_DT_F16>), grid, dim3(256), 0, as_stream(stream), logits, E, k, renorm,
+                           x, gate, H, T, idx, w_out, w32, idx_ext, w_ext);
+    else
+        hipLaunchKernelGGL((k_route_tokens<MOEHIP_DT_BF16>), grid, dim3(256), 0, as_stream(stream), logits, E, k,
+                           renorm, x, gate, H, T, idx, w_out, w32, idx_ext, w_ext);
+    return check_launch("route_tokens");
 }
 
 extern "C" int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E, int32_t *counts,

@@ -81,7 +81,8 @@ _SIGS = {
     "moehip_batch_vote": ([_vp, _i, _i, _vp, _vp, ctypes.c_double, ctypes.POINTER(Policy), _vp, _vp, _vp, _i, _vp,
                            _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_batch_decide": ([_vp, _vp, _i, _i, _i, ctypes.POINTER(Policy), _vp, _vp, _i, _i, _vp, _vp, _vp, _vp,
-                             ctypes.c_double, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+                             ctypes.c_double, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+    "moehip_route_tokens": ([_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_shared_slot": ([_vp, _vp, _i, _i, _i, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
     "moehip_stage_records": ([ctypes.POINTER(Copy), _i, _i, _vp], _i),
     "moehip_table_set": ([_vp, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64), _i,

@@ -206,8 +206,7 @@ class GroupedLayer:
             raise RuntimeError("GroupedLayer.layer: out must be a contiguous tensor like x")
         stream = _lib.stream_of(self.device)
         srec = self._srec[layer]
-        if idx is None and self.fused_decide and x.dtype in (torch.float16, torch.bfloat16) \
-                and T <= self.route_fused_tokens:
+        if idx is None and self.fused_decide and x.dtype in (torch.float16, torch.bfloat16):
             return self._layer_routed(layer, x, out, add, srec, stream)
         if idx is None:
             Wr = self.router_weights[layer]
@@ -225,13 +224,11 @@ class GroupedLayer:
             pidx, pw, ks, EA = self.idx_ext, self.w_ext, k + 1, self.E + 1
         else:
             pidx, pw, ks, EA = idx, w32, k, self.E
+        gemv = T <= self.gemv_tokens
+        items = None
         if self.fused_decide:
-            _lib.call("moehip_batch_decide", pw.data_ptr(), pidx.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
-                      self.levels.data_ptr(), self.skip.data_ptr(), self.E, 1 if srec is not None else 0,
-                      self.counts.data_ptr(), self.offsets.data_ptr(), self.sorted_pos.data_ptr(),
-                      self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p, st.rtab[layer].data_ptr(), srec,
-                      self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(), self.tabs.data_ptr(),
-                      self.info[layer].data_ptr(), self.miss.data_ptr(), stream)
+            items = self.items.data_ptr() if gemv else None
+            self._decide(layer, pw, pidx, T, ks, srec, items, stream)
         else:
             _lib.call("moehip_batch_levels", pw.data_ptr(), T, k, ks, ctypes.byref(self._pols[layer]),
                       self.levels.data_ptr(), self.skip.data_ptr(), stream)
@@ -245,15 +242,25 @@ class GroupedLayer:
         args = (self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(), _lib.dt_code(x.dtype), T, self.H,
                 self.I, ks, EA, 64, self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(),
                 pw.data_ptr(), out.data_ptr(), _lib.ptr(add), 0, self.ws.data_ptr(), self.ws.numel())
-        if T <= self.gemv_tokens:
-            _lib.call("moehip_grouped_gemv_multi", *args, None, stream)  # the work list is built there
+        if gemv:  # without a work list from the decision it is built there
+            _lib.call("moehip_grouped_gemv_multi", *args, items, stream)
         else:
             _lib.call("moehip_grouped_gemm_multi", *args, stream)
         return out
 
+    def _decide(self, layer, pw, pidx, T, ks, srec, items, stream):
+        _lib.call("moehip_batch_decide", pw.data_ptr(), pidx.data_ptr(), T, self.k, ks,
+                  ctypes.byref(self._pols[layer]), self.levels.data_ptr(), self.skip.data_ptr(), self.E,
+                  1 if srec is not None else 0, self.counts.data_ptr(), self.offsets.data_ptr(),
+                  self.sorted_pos.data_ptr(), self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p,
+                  self.store.rtab[layer].data_ptr(), srec, self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(),
+                  self.tabs.data_ptr(), self.info[layer].data_ptr(), self.miss.data_ptr(), items, stream)
+
     def _layer_routed(self, layer, x, out, add, srec, stream):
         """The layer with the router run here: logits, then one launch from the logits to the work
-        list of the GEMVs (moehip_batch_route_decide), then the expert products."""
+        list of the GEMVs (moehip_batch_route_decide) for up to route_fused_tokens tokens, else the
+        per-token routing over many workgroups (moehip_route_tokens) and the decision with the work
+        list (moehip_batch_decide); then the expert products."""
         T, k, st = x.shape[0], self.k, self.store
         shared = srec is not None
         ks, EA = (k + 1, self.E + 1) if shared else (k, self.E)
@@ -263,14 +270,21 @@ class GroupedLayer:
                   stream)
         g = self.shared[layer]["gate"] if shared else None
         gemv = T <= self.gemv_tokens
-        _lib.call("moehip_batch_route_decide", self.logits.data_ptr(), dt, T, self.E, k, 1 if self.renorm else 0,
-                  x.data_ptr(), _lib.ptr(g), self.H, self.idx.data_ptr(), self.w.data_ptr(), self.w32.data_ptr(),
-                  self.idx_ext.data_ptr(), self.w_ext.data_ptr(), ctypes.byref(self._pols[layer]),
-                  self.levels.data_ptr(), self.skip.data_ptr(), self.counts.data_ptr(), self.offsets.data_ptr(),
-                  self.sorted_pos.data_ptr(), self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p,
-                  st.rtab[layer].data_ptr(), srec, self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(),
-                  self.tabs.data_ptr(), self.info[layer].data_ptr(), self.miss.data_ptr(),
-                  self.items.data_ptr() if gemv else None, stream)
+        if T > self.route_fused_tokens:
+            _lib.call("moehip_route_tokens", self.logits.data_ptr(), dt, T, self.E, k, 1 if self.renorm else 0,
+                      x.data_ptr(), _lib.ptr(g), self.H, self.idx.data_ptr(), self.w.data_ptr(), self.w32.data_ptr(),
+                      self.idx_ext.data_ptr(), self.w_ext.data_ptr(), stream)
+            pidx, pw = (self.idx_ext, self.w_ext) if shared else (self.idx, self.w32)
+            self._decide(layer, pw, pidx, T, ks, srec, self.items.data_ptr() if gemv else None, stream)
+        else:
+            _lib.call("moehip_batch_route_decide", self.logits.data_ptr(), dt, T, self.E, k, 1 if self.renorm else 0,
+                      x.data_ptr(), _lib.ptr(g), self.H, self.idx.data_ptr(), self.w.data_ptr(), self.w32.data_ptr(),
+                      self.idx_ext.data_ptr(), self.w_ext.data_ptr(), ctypes.byref(self._pols[layer]),
+                      self.levels.data_ptr(), self.skip.data_ptr(), self.counts.data_ptr(), self.offsets.data_ptr(),
+                      self.sorted_pos.data_ptr(), self.rank.data_ptr(), float(self.policy.hi_vote), self.lv2p,
+                      st.rtab[layer].data_ptr(), srec, self.P, self.offs.data_ptr(), self.planned_dev.data_ptr(),
+                      self.tabs.data_ptr(), self.info[layer].data_ptr(), self.miss.data_ptr(),
+                      self.items.data_ptr() if gemv else None, stream)
         pw = self.w_ext if shared else self.w32
         args = (self.P, self.precs_arr, self.tabs.data_ptr(), x.data_ptr(), dt, T, self.H, self.I, ks, EA, 64,
                 self.offsets.data_ptr(), self.sorted_pos.data_ptr(), self.rank.data_ptr(), pw.data_ptr(),

@@ -198,10 +198,12 @@ def test_grouped_layer_missing_copy_and_graph(dev):
         assert torch.equal(out2, eager), r
 
 
-def test_grouped_layer_routed_graph_replays(dev):
-    """The router-to-work-list launch (moehip_batch_route_decide) and the GEMVs captured in a HIP
-    graph: every replay equals the eager layer, and the eager layer equals the unfused steps."""
-    H, I, E, k, T = 2048, 512, 512, 10, 16
+@pytest.mark.parametrize("T", [16, 40])
+def test_grouped_layer_routed_graph_replays(dev, T):
+    """The router-to-work-list launch (moehip_batch_route_decide; above 16 tokens moehip_route_tokens
+    + moehip_batch_decide with the work list) and the GEMVs captured in a HIP graph: every replay
+    equals the eager layer, and the eager layer equals the unfused steps."""
+    H, I, E, k = 2048, 512, 512, 10
     dtype = torch.bfloat16
     st = _store(dev, ["int4"], H, I, E, 14)
     lay = st.layouts["int4"]
