@@ -486,8 +486,8 @@ def batch_line(args, name):
         "layer_us": round(layer_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole layer: router + levels + dispatch + vote + k_gemm_up/down per precision "
-                               "+ combine (HIP graph per step)",
+                     "kernel": "whole layer: router logits + top-k / shared slot + levels, dispatch, vote and "
+                               "work list + k_gemv_up/down per precision + combine (HIP graph per step)",
                      "bytes_per_launch": int(alg)},
         "cpu_baseline": None,
     }
