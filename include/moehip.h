@@ -286,7 +286,7 @@ int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_
 /*
  * moehip_batch_levels + moehip_dispatch + moehip_batch_vote in one launch (one workgroup; the same
  * arguments and results): w32 / idx are (T, ks) with the shared expert (id E) as the last slot
- * when has_shared. T * ks <= 65536, E + has_shared <= 1025. For batched decode, where each of
+ * when has_shared. T * ks <= 65536, E + has_shared <= 1024. For batched decode, where each of
  * those steps is a few microseconds of launch latency. items (T * ks + 1 int32, or NULL): also
  * the work list of moehip_grouped_gemv_multi (T <= 256).
  */
@@ -320,7 +320,7 @@ int moehip_router_logits(const void *x, const void *Wr, int T, int H, int E, int
  * w32 (T, k) fp32 holding dtype values), the shared expert as slot k when gate != NULL (as
  * moehip_shared_slot: idx_ext / w_ext (T, k + 1); x (T, H) and gate (H) 16-byte aligned), then
  * moehip_batch_decide, and the work list of moehip_grouped_gemv_multi (items, T * ks + 1 int32, or
- * NULL). logits (T, E) fp16 / bf16, E <= 1024, k <= 32.
+ * NULL). logits (T, E) fp16 / bf16, E + (gate != NULL) <= 1024, k <= 32.
  */
 int moehip_batch_route_decide(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
                               const void *gate, int H, int64_t *idx, void *w_out, float *w32, int64_t *idx_ext,

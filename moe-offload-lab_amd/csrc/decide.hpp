@@ -69,21 +69,14 @@ struct SharedRecs {
 // resident copy (as k_decide_table), the table row of that precision (all other precisions' rows
 // 0); an expert with no usable copy gets rank -1 on its pairs (they contribute nothing) and counts
 // them in miss. info[e] = chosen precision, -1 = missing, -2 = no pairs.
-__device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E, int has_shared, const int32_t *offsets,
-                                            const int32_t *sorted_pos, double hi_vote, int upgrade, int lv0, int lv1,
-                                            int lv2, const int64_t *rtab, const SharedRecs &srec, int P,
-                                            const int64_t *offs, const int *planned, int64_t *tabs, int32_t *rank,
-                                            float *info, float *miss) {
+__device__ __forceinline__ void vote_apply(int e, int n, int c0, int c1, const int32_t *offsets, int E, int has_shared,
+                                           const int32_t *sorted_pos, double hi_vote, int upgrade, int lv0, int lv1,
+                                           int lv2, const int64_t *rtab, const SharedRecs &srec, int P,
+                                           const int64_t *offs, const int *planned, int64_t *tabs, int32_t *rank,
+                                           float *info, float *miss) {
     const int EA = E + (has_shared ? 1 : 0);
-    const int p0 = offsets[e], n = offsets[e + 1] - p0;
     int chosen = -1;
     if (n > 0) {
-        int c0 = 0, c1 = 0;
-        for (int i = 0; i < n; ++i) {
-            const int l = levels[sorted_pos[p0 + i]];
-            c0 += l <= 0;
-            c1 += l <= 1;
-        }
         const double need = (hi_vote - 1e-9) * (double)n;
         const int level = (double)c0 >= need ? 0 : ((double)c1 >= need ? 1 : 2);
         const int req = level == 0 ? lv0 : (level == 1 ? lv1 : lv2);
@@ -99,10 +92,43 @@ __device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E,
         for (int f = 0; f < 4; ++f) tabs[((size_t)pi * EA + e) * 4 + f] = sel ? base + offs[pi * 4 + f] : 0;
     }
     if (n > 0 && chosen < 0) {
+        const int p0 = offsets[e];
         for (int i = 0; i < n; ++i) rank[sorted_pos[p0 + i]] = -1;
         if (miss != nullptr) atomicAdd(miss, (float)n);
     }
     if (info != nullptr) info[e] = n == 0 ? -2.f : (float)chosen;
+}
+
+// the vote of expert e from the levels of its dispatched pairs (global memory)
+__device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E, int has_shared, const int32_t *offsets,
+                                            const int32_t *sorted_pos, double hi_vote, int upgrade, int lv0, int lv1,
+                                            int lv2, const int64_t *rtab, const SharedRecs &srec, int P,
+                                            const int64_t *offs, const int *planned, int64_t *tabs, int32_t *rank,
+                                            float *info, float *miss) {
+    const int p0 = offsets[e], n = offsets[e + 1] - p0;
+    int c0 = 0, c1 = 0;
+    for (int i = 0; i < n; ++i) {
+        const int l = levels[sorted_pos[p0 + i]];
+        c0 += l <= 0;
+        c1 += l <= 1;
+    }
+    vote_apply(e, n, c0, c1, offsets, E, has_shared, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, rtab, srec, P, offs,
+               planned, tabs, rank, info, miss);
+}
+
+// per-expert tallies of the kept pairs for the vote, gathered while the levels are made (LDS
+// atomics, so the vote needs no walk over each expert's pairs): n, #(level <= 0), #(level <= 1)
+constexpr int VT_MAX = 1024;
+struct VoteTally {
+    int n[VT_MAX], c0[VT_MAX], c1[VT_MAX];
+};
+__device__ __forceinline__ void tally_clear(VoteTally &vt, int EA) {
+    for (int e = threadIdx.x; e < EA; e += blockDim.x) vt.n[e] = 0, vt.c0[e] = 0, vt.c1[e] = 0;
+}
+__device__ __forceinline__ void tally_add(VoteTally &vt, int e, int lvl) {
+    atomicAdd(&vt.n[e], 1);
+    if (lvl <= 0) atomicAdd(&vt.c0[e], 1);
+    if (lvl <= 1) atomicAdd(&vt.c1[e], 1);
 }
 
 

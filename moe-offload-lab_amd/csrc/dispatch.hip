@@ -164,6 +164,27 @@ __device__ __forceinline__ void route_token(const void *logits, int E, int k, in
     }
 }
 
+// levels and skip of token t's ks slots (one wave; slot k, when ks > k, is the shared expert:
+// level 0, never skipped), and the vote tallies of its kept pairs (expert id in [0, EA), not
+// skipped: the pairs the dispatch keeps)
+__device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const float *w, const int64_t *idx,
+                                             const moehip_policy &pol, int32_t *levels, uint8_t *skip, float *s_w,
+                                             float *s_sorted, float *s_total, VoteTally &vt) {
+    const int lane = threadIdx.x & 63;
+    const float wj = lane < k ? w[(size_t)t * ks + lane] : 0.f;
+    const int64_t e = lane < ks ? idx[(size_t)t * ks + lane] : -1;
+    int lvl;
+    bool sk;
+    slot_level(lane, k, wj, pol, s_w, s_sorted, s_total, lvl, sk);
+    if (lane >= k) lvl = 0, sk = false;  // the shared expert
+    if (lane < ks) {
+        levels[(size_t)t * ks + lane] = lvl;
+        skip[(size_t)t * ks + lane] = sk ? 1 : 0;
+        if (!sk && e >= 0 && e < EA) tally_add(vt, (int)e, lvl);
+    }
+    wave_sync();  // the wave's LDS is reused for its next token
+}
+
 // the work list of the batched GEMVs (whole workgroup of 1024): one item (e << 8 | z) per
 // GV_TOKENS pairs of every expert, in expert order (exclusive scan of ceil(n_e / GV_TOKENS));
 // items[np] = their number. offsets must be visible to the workgroup (its own writes + barrier).
@@ -210,28 +231,19 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     extern __shared__ int s_cnt[];
     __shared__ int s_wtot[DP_WAVES];
     __shared__ float s_w[DP_WAVES][64], s_sorted[DP_WAVES][64], s_total[DP_WAVES];
+    __shared__ VoteTally s_vt;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int EA = E + (has_shared ? 1 : 0);
-    for (int t = wave; t < T; t += DP_WAVES) {
-        const float wj = lane < k ? w[(size_t)t * ks + lane] : 0.f;
-        int lvl;
-        bool sk;
-        slot_level(lane, k, wj, pol, s_w[wave], s_sorted[wave], &s_total[wave], lvl, sk);
-        if (lane < k) {
-            levels[(size_t)t * ks + lane] = lvl;
-            skip[(size_t)t * ks + lane] = sk ? 1 : 0;
-        } else if (lane < ks) {  // the shared expert: level 0, never skipped
-            levels[(size_t)t * ks + lane] = 0;
-            skip[(size_t)t * ks + lane] = 0;
-        }
-        wave_sync();  // the wave's LDS is reused for its next token
-    }
+    tally_clear(s_vt, EA);
+    __syncthreads();
+    for (int t = wave; t < T; t += DP_WAVES)
+        token_levels(t, k, ks, EA, w, idx, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt);
     __syncthreads();
     dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
     for (int e = tid; e < EA; e += 1024)
-        vote_expert(e, levels, E, has_shared, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec, P,
-                    offs, planned, tabs, rank, info, miss);
+        vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, has_shared, sorted_pos, hi_vote, pol.upgrade, lv0,
+                   lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
     write_items(offsets, EA, T * ks, items, s_wtot);
@@ -279,38 +291,29 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     const int ks = k + (shared ? 1 : 0), EA = E + (shared ? 1 : 0);
     int64_t *pidx = shared ? idx_ext : idx;
     float *pw = shared ? w_ext : w32;
+    __shared__ VoteTally s_vt;
+    tally_clear(s_vt, EA);  // ordered before the levels by the barrier after the routing
     // routing of every token
     for (int t = wave; t < T; t += DP_WAVES)
         route_token<DT>(logits, E, k, renorm, x, gate, H, t, idx, wout, w32, idx_ext, w_ext, s_w[wave]);
     __syncthreads();
     // levels
-    for (int t = wave; t < T; t += DP_WAVES) {
-        const float wj = lane < k ? pw[(size_t)t * ks + lane] : 0.f;
-        int lvl;
-        bool sk;
-        slot_level(lane, k, wj, pol, s_w[wave], s_sorted[wave], &s_total[wave], lvl, sk);
-        if (lane < k) {
-            levels[(size_t)t * ks + lane] = lvl;
-            skip[(size_t)t * ks + lane] = sk ? 1 : 0;
-        } else if (lane < ks) {  // the shared expert: level 0, never skipped
-            levels[(size_t)t * ks + lane] = 0;
-            skip[(size_t)t * ks + lane] = 0;
-        }
-        wave_sync();
-    }
+    for (int t = wave; t < T; t += DP_WAVES)
+        token_levels(t, k, ks, EA, pw, pidx, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt);
     __syncthreads();
     dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
     for (int e = tid; e < EA; e += 1024)
-        vote_expert(e, levels, E, shared ? 1 : 0, offsets, sorted_pos, hi_vote, pol.upgrade, lv0, lv1, lv2, rtab, srec,
-                    P, offs, planned, tabs, rank, info, miss);
+        vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, shared ? 1 : 0, sorted_pos, hi_vote, pol.upgrade,
+                   lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
     write_items(offsets, EA, T * ks, items, s_wtot);
 }
 
+// more than 64 KiB of LDS per workgroup (dynamic + the kernels' static ~21 KiB) must be enabled
 static bool enable_big_lds(const void *fn, size_t lds) {
-    if (lds <= 60 * 1024) return true;
+    if (lds + 24 * 1024 <= 64 * 1024) return true;
     return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
 }
 
@@ -327,7 +330,7 @@ extern "C" int moehip_batch_decide(const float *w32, const int64_t *idx, int T, 
                    "batch_decide: %d tokens (an expert's work items are numbered in 8 bits: <= %d)", T,
                    256 * GV_TOKENS);
     const int EA = E + (has_shared ? 1 : 0);
-    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 64 && ks >= k && ks <= 64 && (long)T * ks <= 65536 && E > 0 && EA <= 1025 &&
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 64 && ks >= k && ks <= 64 && (long)T * ks <= 65536 && E > 0 && EA <= 1024 &&
                        P > 0 && P <= 4,
                    "batch_decide: bad sizes T=%d k=%d ks=%d E=%d P=%d", T, k, ks, E, P);
     MOEHIP_REQUIRE(!has_shared || shared_rec != nullptr, "batch_decide: shared expert without records");
@@ -359,7 +362,7 @@ extern "C" int moehip_batch_route_decide(const void *logits, int dtype, int T, i
     MOEHIP_REQUIRE(dtype == MOEHIP_DT_F16 || dtype == MOEHIP_DT_BF16, "batch_route_decide: logits dtype %d", dtype);
     const bool shared = gate != nullptr;
     const int ks = k + (shared ? 1 : 0), EA = E + (shared ? 1 : 0);
-    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 32 && k <= E && E <= 1024 && (long)T * ks <= 65536 && P > 0 && P <= 4,
+    MOEHIP_REQUIRE(T > 0 && k > 0 && k <= 32 && k <= E && EA <= 1024 && (long)T * ks <= 65536 && P > 0 && P <= 4,
                    "batch_route_decide: bad sizes T=%d E=%d k=%d P=%d", T, E, k, P);
     MOEHIP_REQUIRE(!shared || (x && idx_ext && w_ext && shared_rec && H % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
                                ((uintptr_t)gate % 16) == 0),

@@ -243,3 +243,70 @@ def test_grouped_layer_routed_graph_replays(dev, T):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(out2, eager), r
+
+
+@pytest.mark.parametrize("E,shared", [(64, False), (512, True), (800, False), (1023, True)])
+@pytest.mark.parametrize("mode", ["hobbit", "weight"])
+def test_batch_decide_matches_steps(dev, E, shared, mode):
+    """moehip_batch_decide (one launch: levels, dispatch, vote from per-expert tallies, work list)
+    against moehip_batch_levels + moehip_dispatch + moehip_batch_vote: every output bit-exact, up to
+    1023 experts + the shared one (the largest LDS), with skipped pairs (HOBBIT t2) and experts
+    without a resident copy (their pairs ranked -1 and counted in miss); the work list against the
+    offsets."""
+    import ctypes
+    from moelab_hip import _lib
+    T, k, P = 40, 8, 2
+    ks, EA = (k + 1, E + 1) if shared else (k, E)
+    g = np.random.default_rng(E + (7 if shared else 0))
+    idx = np.stack([g.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+    w = (g.random((T, k)) ** 2 + 0.01).astype(np.float32)
+    if shared:  # the shared expert (id E) as slot k with its own weight
+        idx = np.concatenate([idx, np.full((T, 1), E, np.int64)], 1)
+        w = np.concatenate([w, g.random((T, 1)).astype(np.float32)], 1)
+    pol = PrecisionPolicy("hobbit", t1=0.5, t2=0.85) if mode == "hobbit" else PrecisionPolicy("weight", t1=0.3)
+    cpol = pol.device_policy(0)
+    resident = g.random((P, E)) < 0.8
+    rtab = torch.from_numpy(np.where(resident, (np.arange(P * E).reshape(P, E) + 1) * 4096, 0).astype(np.int64)).to(dev)
+    srec = (ctypes.c_int64 * P)(*[(1 << 40) + 4096 * p for p in range(P)])
+    offs = torch.tensor([[0, 8, 16, 24], [0, 64, 128, 192]], dtype=torch.int64, device=dev)
+    planned = torch.tensor([1, 1], dtype=torch.int32, device=dev)
+    lv2p = (ctypes.c_int * 3)(0, 1, 1)
+    idx_d, w_d = torch.from_numpy(idx).to(dev), torch.from_numpy(w).to(dev)
+    st = _lib.stream_of(dev)
+
+    def bufs():
+        return dict(levels=torch.full((T * ks,), -7, dtype=torch.int32, device=dev),
+                    skip=torch.full((T * ks,), 9, dtype=torch.uint8, device=dev),
+                    counts=torch.full((EA,), -7, dtype=torch.int32, device=dev),
+                    offsets=torch.full((EA + 1,), -7, dtype=torch.int32, device=dev),
+                    sorted_pos=torch.full((T * ks,), -7, dtype=torch.int32, device=dev),
+                    rank=torch.full((T * ks,), -7, dtype=torch.int32, device=dev),
+                    tabs=torch.full((P, EA, 4), -7, dtype=torch.int64, device=dev),
+                    info=torch.full((EA,), -7.0, device=dev), miss=torch.zeros(1, device=dev))
+
+    a, b = bufs(), bufs()
+    items = torch.full((T * ks + 1,), -7, dtype=torch.int32, device=dev)
+    print(f"batch decide E={E} shared={shared} {mode}", flush=True)
+    _lib.call("moehip_batch_decide", w_d.data_ptr(), idx_d.data_ptr(), T, k, ks, ctypes.byref(cpol),
+              a["levels"].data_ptr(), a["skip"].data_ptr(), E, 1 if shared else 0, a["counts"].data_ptr(),
+              a["offsets"].data_ptr(), a["sorted_pos"].data_ptr(), a["rank"].data_ptr(), float(pol.hi_vote), lv2p,
+              rtab.data_ptr(), srec, P, offs.data_ptr(), planned.data_ptr(), a["tabs"].data_ptr(),
+              a["info"].data_ptr(), a["miss"].data_ptr(), items.data_ptr(), st)
+    _lib.call("moehip_batch_levels", w_d.data_ptr(), T, k, ks, ctypes.byref(cpol), b["levels"].data_ptr(),
+              b["skip"].data_ptr(), st)
+    _lib.call("moehip_dispatch", idx_d.data_ptr(), b["skip"].data_ptr(), T, ks, EA, b["counts"].data_ptr(),
+              b["offsets"].data_ptr(), b["sorted_pos"].data_ptr(), b["rank"].data_ptr(), st)
+    _lib.call("moehip_batch_vote", b["levels"].data_ptr(), E, 1 if shared else 0, b["offsets"].data_ptr(),
+              b["sorted_pos"].data_ptr(), float(pol.hi_vote), ctypes.byref(cpol), lv2p, rtab.data_ptr(), srec, P,
+              offs.data_ptr(), planned.data_ptr(), b["tabs"].data_ptr(), b["rank"].data_ptr(), b["info"].data_ptr(),
+              b["miss"].data_ptr(), st)
+    torch.cuda.synchronize()
+    for name in a:
+        assert torch.equal(a[name], b[name]), name
+    sk = a["skip"].cpu().numpy()
+    assert (sk == 1).any() == (mode == "hobbit")
+    assert a["miss"].item() > 0  # some chosen experts have no copy
+    off = a["offsets"].cpu().numpy()
+    exp = [(e << 8) | z for e in range(EA) for z in range(off[e + 1] - off[e])]
+    it = items.cpu().numpy()
+    assert it[T * ks] == len(exp) and it[:len(exp)].tolist() == exp
