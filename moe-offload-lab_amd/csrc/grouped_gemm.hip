@@ -598,7 +598,30 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                 for (int t = 0; t < GV_NT; ++t) acc[m][t] = 0.f;
 #pragma unroll
                 for (int i = 0; i < CPL; ++i) {
-                    if constexpr (IDOT) {
+                    if constexpr (PREC == MOEHIP_PREC_FP8) {
+                        // the exact fp16 pairs of value * 2^-8, the block scale * 2^8 on the sum
+                        const float sc = __uint_as_float(sr[buf][p][m][i]) * 256.0f;
+                        const uint4 qq = q[buf][p][m][i];
+                        const uint32_t d[4] = {qq.x, qq.y, qq.z, qq.w};
+                        uint32_t wv[8];
+#pragma unroll
+                        for (int b = 0; b < 2; ++b)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const uint32_t sel = 0x000C000Cu | ((uint32_t)(4 + j) << 24) | ((uint32_t)j << 8);
+                                const uint32_t v = __builtin_amdgcn_perm(d[2 * b + 1], d[2 * b], sel);
+                                wv[4 * b + j] = and_or(v >> 1, 0x3F803F80u, v & 0x80008000u);
+                            }
+#pragma unroll
+                        for (int t = 0; t < GV_NT; ++t) {
+                            if (t < nt) {
+                                float pc = 0.f;
+#pragma unroll
+                                for (int j = 0; j < 8; ++j) pc = dot2h(wv[j], xv[t][i][j], pc);
+                                acc[m][t] = fmaf(pc, UP ? sc : sc * fe[t][i], acc[m][t]);
+                            }
+                        }
+                    } else if constexpr (IDOT) {
                         const float sc = f16_to_f32(sr[buf][p][m][i] & 0xffffu);
 #pragma unroll
                         for (int t = 0; t < GV_NT; ++t) {
