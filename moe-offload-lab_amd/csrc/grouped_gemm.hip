@@ -494,7 +494,7 @@ __device__ __forceinline__ constexpr int gv_pair_first(int q) { return I8 ? 4 * 
 // NG row groups of 4 P RPW rows from r0 (gate and up rows for UP) of one expert, against up to
 // GV_NT of its tokens; UP: h[pair, r] = silu(gate . x) * (up . x); else y[pair, r] = w 2^he (down . h).
 // The loads of group g + 1 are issued before group g is computed (two register buffers).
-template <int PREC, int CPL, int P, bool UP>
+template <int PREC, int CPL, int P, bool UP, bool XBF = false>
 __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, int rows, int I, int k, int p0,
                                         int nt, const int32_t *sorted_pos, gu8 *qb, gu8 *sb, int lg, int r0, int NG,
                                         const float *w, float *out, int ostride, DeqK dk) {
@@ -556,16 +556,29 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
     // int4 / int8: the weights' integers straight into dot2 (offsets removed by the per-chunk
     // correction, the group scale applied to the chunk sum in fp32)
     constexpr bool IDOT = PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8;
+    constexpr bool XS = !UP || XBF;  // activation slices scaled per chunk (fe), not per token
     float corr[GV_NT][CPL];
 #pragma unroll
     for (int t = 0; t < GV_NT; ++t)
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            if constexpr (UP) {
+            if constexpr (UP && !XBF) {
                 gv_slice_perm<VPC, PREC == MOEHIP_PREC_INT8>(xr[t][i], xv[t][i]);
                 fe[t][i] = 1.0f;
             } else {
-                const float *v = reinterpret_cast<const float *>(xr[t][i]);
+                // fp32 h (down) or bf16 x (XBF: up without the activation preparation pass)
+                float v[VPC];
+                if constexpr (UP) {
+                    const uint32_t *wd = reinterpret_cast<const uint32_t *>(xr[t][i]);
+#pragma unroll
+                    for (int q = 0; q < VPC / 2; ++q) {
+                        v[2 * q] = __uint_as_float(wd[q] << 16);
+                        v[2 * q + 1] = __uint_as_float(wd[q] & 0xffff0000u);
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < VPC; ++q) v[q] = reinterpret_cast<const float *>(xr[t][i])[q];
+                }
                 float m = 0.f;
 #pragma unroll
                 for (int q = 0; q < VPC; ++q) m = fmaxf(m, fabsf(v[q]));
@@ -618,7 +631,7 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                                 float pc = 0.f;
 #pragma unroll
                                 for (int j = 0; j < 8; ++j) pc = dot2h(wv[j], xv[t][i][j], pc);
-                                acc[m][t] = fmaf(pc, UP ? sc : sc * fe[t][i], acc[m][t]);
+                                acc[m][t] = fmaf(pc, XS ? sc * fe[t][i] : sc, acc[m][t]);
                             }
                         }
                     } else if constexpr (IDOT) {
@@ -627,7 +640,7 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
                         for (int t = 0; t < GV_NT; ++t) {
                             if (t < nt) {
                                 const float cd = dot2_chunk<PREC>(q[buf][p][m][i], xv[t][i], corr[t][i]);
-                                acc[m][t] = fmaf(cd, UP ? sc : sc * fe[t][i], acc[m][t]);
+                                acc[m][t] = fmaf(cd, XS ? sc * fe[t][i] : sc, acc[m][t]);
                             }
                         }
                     } else {
@@ -636,7 +649,7 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
 #pragma unroll
                     for (int t = 0; t < GV_NT; ++t) {
                         if (t < nt) {
-                            if constexpr (UP) {
+                            if constexpr (!XS) {
 #pragma unroll
                                 for (int j = 0; j < ND; ++j) acc[m][t] = dot2h(wv[j], xv[t][i][j], acc[m][t]);
                             } else {
@@ -724,7 +737,7 @@ __global__ __launch_bounds__(1024) void k_gv_items(const int32_t *__restrict__ o
 
 // grid (row blocks, NP): block (b, i) covers rows [b * NG * 4 P RPW, ...) of work item i (expert e,
 // its tokens [z * GV_TG, (z + 1) * GV_TG)) when i < items[NP]
-template <int PREC, int CPL, int P>
+template <int PREC, int CPL, int P, bool XBF>
 __global__ __launch_bounds__(256) void k_gemv_up(const uint16_t *__restrict__ x, const int *__restrict__ xe, int H,
                                                  int I, int k, const int32_t *__restrict__ items, int NP,
                                                  const int32_t *__restrict__ offsets,
@@ -738,7 +751,7 @@ __global__ __launch_bounds__(256) void k_gemv_up(const uint16_t *__restrict__ x,
     if (ne <= 0 || qb == nullptr) return;
     const int r0 = blockIdx.x * NG * 4 * P * (64 >> lg);
     if (r0 >= I) return;  // a row block of the padding to a multiple of 8
-    gv_rows<PREC, CPL, P, true>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 1]), lg, r0, NG,
+    gv_rows<PREC, CPL, P, true, XBF>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, record_ptr(tab[4 * e + 1]), lg, r0, NG,
                                 nullptr, hb, I, dk);
 }
 
@@ -914,17 +927,14 @@ static GvGeo gv_geo(int prec, int K) {
     return g;
 }
 
-#ifndef GV_WG_BYTES
-#define GV_WG_BYTES (128 << 10)
-#endif
-#ifndef GV_MIN_WGS
-#define GV_MIN_WGS 2048
-#endif
+constexpr int GV_WG_BYTES = 128 << 10;  // weight bytes per workgroup at most
+constexpr int GV_MIN_WGS = 2048;        // workgroups per launch at least (about two per CU slot)
 template <int PREC, int CPL>
-static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
+static void launch_gv_cpl(int mode, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
                           int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
                           float *out, const float *w, DeqK dk) {
     constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
+    const bool up = mode != 0;
     // row groups per workgroup: up to 128 KiB of weights and GV_MAXROWS rows, while the pairs
     // (an upper bound of the work items) still give about two workgroups per CU slot
     const int groups = (rows + g.rows_per_block - 1) / g.rows_per_block;
@@ -936,15 +946,16 @@ static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const
     // so row block b of every item (the items of one expert, one per token, are adjacent) then
     // runs on XCD b % 8 and the re-reads of its rows hit that XCD's L2
     int gx = (groups + ng - 1) / ng;
-#ifndef GV_NO_XCD
     gx = (gx + 7) & ~7;
     ng = (groups + gx - 1) / gx;
     gx = (groups + ng - 1) / ng;
     gx = (gx + 7) & ~7;
-#endif
     const dim3 grid(gx, NP);
-    if (up)
-        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act), ae,
+    if (mode == 2)  // bf16 activations, scaled into fp16 per chunk by the kernel
+        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P, true>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act),
+                           nullptr, H, I, k, items, NP, offsets, sorted_pos, tab, out, dk, g.lg, ng);
+    else if (mode == 1)
+        hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P, false>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act), ae,
                            H, I, k, items, NP, offsets,
                            sorted_pos, tab, out, dk, g.lg, ng);
     else
@@ -954,30 +965,30 @@ static void launch_gv_cpl(bool up, int rows, const int32_t *items, int NP, const
 }
 
 template <int PREC>
-static void launch_gv(bool up, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I, int k,
+static void launch_gv(int mode, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I, int k,
                       const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
                       const float *w, DeqK dk) {
-    const GvGeo g = gv_geo(PREC, up ? H : I);
-    const int rows = up ? I : H;
+    const GvGeo g = gv_geo(PREC, mode != 0 ? H : I);
+    const int rows = mode != 0 ? I : H;
     if (g.rows_per_block > GV_MAXROWS) return;  // unreachable for K >= 128 (checked by the caller)
     switch (g.cpl) {
-        case 1: launch_gv_cpl<PREC, 1>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        case 2: launch_gv_cpl<PREC, 2>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case 1: launch_gv_cpl<PREC, 1>(mode, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case 2: launch_gv_cpl<PREC, 2>(mode, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
         case 3:
-        case 4: launch_gv_cpl<PREC, 4>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        default: launch_gv_cpl<PREC, 8>(up, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case 4: launch_gv_cpl<PREC, 4>(mode, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        default: launch_gv_cpl<PREC, 8>(mode, rows, items, NP, g, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
     }
 }
 
-static void launch_gv_prec(int prec, bool up, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I,
+static void launch_gv_prec(int prec, int mode, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I,
                            int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
                            const float *w, DeqK dk) {
     switch (prec) {
-        case MOEHIP_PREC_INT4: launch_gv<MOEHIP_PREC_INT4>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        case MOEHIP_PREC_INT8: launch_gv<MOEHIP_PREC_INT8>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        case MOEHIP_PREC_FP8: launch_gv<MOEHIP_PREC_FP8>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        case MOEHIP_PREC_F16: launch_gv<MOEHIP_PREC_F16>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
-        default: launch_gv<MOEHIP_PREC_BF16>(up, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_INT4: launch_gv<MOEHIP_PREC_INT4>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_INT8: launch_gv<MOEHIP_PREC_INT8>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_FP8: launch_gv<MOEHIP_PREC_FP8>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        case MOEHIP_PREC_F16: launch_gv<MOEHIP_PREC_F16>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
+        default: launch_gv<MOEHIP_PREC_BF16>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
     }
 }
 
@@ -1016,13 +1027,15 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     const bool bf = xdtype == MOEHIP_DT_BF16;
     const uint16_t *xa = bf ? x16 : xs;
     const int *xea = bf ? xe : nullptr;
-    if (bf) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
+    // bf16 activations: fp16 with a per-token power of two for the MFMA tiles; the GEMVs read
+    // the bf16 rows themselves and scale each chunk
+    if (bf && !gemv) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
     // the work list: the caller's (written by moehip_batch_route_decide) or built here
     int32_t *items = reinterpret_cast<int32_t *>(wsb + L.items);
     if (gemv && items_in == nullptr) hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, items);
     if (items_in != nullptr) items = const_cast<int32_t *>(items_in);
     for (int p = 0; p < P && gemv; ++p)
-        launch_gv_prec(precs[p], true, items, NP, st, xa, xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
+        launch_gv_prec(precs[p], bf ? 2 : 1, items, NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
     for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
@@ -1039,7 +1052,7 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     // the MFMA down kernels read h as fp16 with a per-pair power of two; the GEMVs read the fp32 rows
     if (!gemv) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
     for (int p = 0; p < P && gemv; ++p)
-        launch_gv_prec(precs[p], false, items, NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
+        launch_gv_prec(precs[p], 0, items, NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
                        y, w, dk);
     for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
