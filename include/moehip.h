@@ -250,8 +250,8 @@ int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, cons
  * tiles (for few tokens per expert: batched decode): weight rows streamed whole with 16-byte
  * loads and read once per launch however many tokens the expert has, v_dot2_f32_f16 products
  * against each token's activations; same arguments, workspace and results up to fp32 summation
- * order. items: the work list written by moehip_batch_route_decide (T * k + 1 int32), or NULL to
- * build it here. Replaces the same reference code as moehip_grouped_gemm_multi.
+ * order. items: the work lists written by moehip_batch_decide / moehip_batch_route_decide (P lists
+ * of T * k + 1 int32, one per record table), or NULL to build them here. Replaces the same reference code as moehip_grouped_gemm_multi.
  */
 int moehip_grouped_gemv_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H,
                               int I, int k, int E, int gs, const int32_t *offsets, const int32_t *sorted_pos,
@@ -287,8 +287,8 @@ int moehip_batch_vote(const int32_t *levels, int E, int has_shared, const int32_
  * moehip_batch_levels + moehip_dispatch + moehip_batch_vote in one launch (one workgroup; the same
  * arguments and results): w32 / idx are (T, ks) with the shared expert (id E) as the last slot
  * when has_shared. T * ks <= 65536, E + has_shared <= 1024. For batched decode, where each of
- * those steps is a few microseconds of launch latency. items (T * ks + 1 int32, or NULL): also
- * the work list of moehip_grouped_gemv_multi (T <= 256).
+ * those steps is a few microseconds of launch latency. items (P * (T * ks + 1) int32, or NULL):
+ * also the work lists of moehip_grouped_gemv_multi, one per record precision (T <= 256).
  */
 int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int ks, const moehip_policy *pol,
                         int32_t *levels, uint8_t *skip, int E, int has_shared, int32_t *counts, int32_t *offsets,
@@ -319,8 +319,8 @@ int moehip_router_logits(const void *x, const void *Wr, int T, int H, int E, int
  * softmax top-k per token (as moehip_router_topk: idx (T, k) int64, w_out (T, k) in dtype or NULL,
  * w32 (T, k) fp32 holding dtype values), the shared expert as slot k when gate != NULL (as
  * moehip_shared_slot: idx_ext / w_ext (T, k + 1); x (T, H) and gate (H) 16-byte aligned), then
- * moehip_batch_decide, and the work list of moehip_grouped_gemv_multi (items, T * ks + 1 int32, or
- * NULL). logits (T, E) fp16 / bf16, E + (gate != NULL) <= 1024, k <= 32.
+ * moehip_batch_decide, and the work lists of moehip_grouped_gemv_multi (items, P * (T * ks + 1)
+ * int32, or NULL). logits (T, E) fp16 / bf16, E + (gate != NULL) <= 1024, k <= 32.
  */
 int moehip_batch_route_decide(const void *logits, int dtype, int T, int E, int k, int renorm, const void *x,
                               const void *gate, int H, int64_t *idx, void *w_out, float *w32, int64_t *idx_ext,

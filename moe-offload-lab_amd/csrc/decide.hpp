@@ -69,7 +69,7 @@ struct SharedRecs {
 // resident copy (as k_decide_table), the table row of that precision (all other precisions' rows
 // 0); an expert with no usable copy gets rank -1 on its pairs (they contribute nothing) and counts
 // them in miss. info[e] = chosen precision, -1 = missing, -2 = no pairs.
-__device__ __forceinline__ void vote_apply(int e, int n, int c0, int c1, const int32_t *offsets, int E, int has_shared,
+__device__ __forceinline__ int vote_apply(int e, int n, int c0, int c1, const int32_t *offsets, int E, int has_shared,
                                            const int32_t *sorted_pos, double hi_vote, int upgrade, int lv0, int lv1,
                                            int lv2, const int64_t *rtab, const SharedRecs &srec, int P,
                                            const int64_t *offs, const int *planned, int64_t *tabs, int32_t *rank,
@@ -97,6 +97,7 @@ __device__ __forceinline__ void vote_apply(int e, int n, int c0, int c1, const i
         if (miss != nullptr) atomicAdd(miss, (float)n);
     }
     if (info != nullptr) info[e] = n == 0 ? -2.f : (float)chosen;
+    return n == 0 ? -1 : chosen;
 }
 
 // the vote of expert e from the levels of its dispatched pairs (global memory)
@@ -112,7 +113,7 @@ __device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E,
         c0 += l <= 0;
         c1 += l <= 1;
     }
-    vote_apply(e, n, c0, c1, offsets, E, has_shared, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, rtab, srec, P, offs,
+    (void)vote_apply(e, n, c0, c1, offsets, E, has_shared, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, rtab, srec, P, offs,
                planned, tabs, rank, info, miss);
 }
 
@@ -132,9 +133,10 @@ __device__ __forceinline__ void tally_add(VoteTally &vt, int e, int lvl) {
 }
 
 
-// tokens per batched-GEMV work item (the work list written by the decision kernels and read by
-// the GEMV kernels)
+// tokens per batched-GEMV work item (the work lists written by the decision kernels and read by
+// the GEMV kernels: one list of T * ks + 1 ints per record precision, at most GV_MAXP)
 constexpr int GV_TOKENS = 1;
+constexpr int GV_MAXP = 4;
 
 // order-preserving 32-bit key of a 16-bit logit (bits16) at index c < 1024: the logit bits above
 // 1023 - c, so the largest logit wins and equal logits go to the lowest index; -0 == +0

@@ -185,33 +185,38 @@ __device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const
     wave_sync();  // the wave's LDS is reused for its next token
 }
 
-// the work list of the batched GEMVs (whole workgroup of 1024): one item (e << 8 | z) per
-// GV_TOKENS pairs of every expert, in expert order (exclusive scan of ceil(n_e / GV_TOKENS));
-// items[np] = their number. offsets must be visible to the workgroup (its own writes + barrier).
-__device__ __forceinline__ void write_items(const int32_t *offsets, int EA, int np, int32_t *items, int *s_wtot) {
+// the work lists of the batched GEMVs (whole workgroup of 1024), one per record precision p < P
+// at items + p * (np + 1): one item (e << 8 | z) per GV_TOKENS pairs of every expert voted to p
+// (s_ch[e], LDS), in expert order (exclusive scan of ceil(n_e / GV_TOKENS)); [np] = their number.
+// offsets must be visible to the workgroup (its own writes + barrier).
+__device__ __forceinline__ void write_items(const int32_t *offsets, int EA, int np, int P, const int *s_ch,
+                                            int32_t *items, int *s_wtot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int base = 0;
-    for (int e0 = 0; e0 < EA; e0 += 1024) {
-        const int e = e0 + tid;
-        const int n = e < EA ? offsets[e + 1] - offsets[e] : 0;
-        const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
-        int incl = nz;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
+    for (int p = 0; p < P; ++p) {
+        int32_t *it = items + (size_t)p * (np + 1);
+        int base = 0;
+        for (int e0 = 0; e0 < EA; e0 += 1024) {
+            const int e = e0 + tid;
+            const int n = (e < EA && s_ch[e] == p) ? offsets[e + 1] - offsets[e] : 0;
+            const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
+            int incl = nz;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            if (lane == 63) s_wtot[wave] = incl;
+            __syncthreads();
+            int wb = base, tot = base;
+            for (int w = 0; w < DP_WAVES; ++w) {
+                if (w < wave) wb += s_wtot[w];
+                tot += s_wtot[w];
+            }
+            for (int z = 0; z < nz; ++z) it[wb + incl - nz + z] = (e << 8) | z;
+            base = tot;
+            __syncthreads();
         }
-        if (lane == 63) s_wtot[wave] = incl;
-        __syncthreads();
-        int wb = base, tot = base;
-        for (int w = 0; w < DP_WAVES; ++w) {
-            if (w < wave) wb += s_wtot[w];
-            tot += s_wtot[w];
-        }
-        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
-        base = tot;
-        __syncthreads();
+        if (tid == 0) it[np] = base;
     }
-    if (tid == 0) items[np] = base;
 }
 
 // The whole T > 1 decision in one workgroup (batched decode, where every step is latency-bound):
@@ -241,12 +246,13 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     __syncthreads();
     dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
+    __shared__ int s_ch[VT_MAX];
     for (int e = tid; e < EA; e += 1024)
-        vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, has_shared, sorted_pos, hi_vote, pol.upgrade, lv0,
-                   lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
+        s_ch[e] = vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, has_shared, sorted_pos, hi_vote,
+                             pol.upgrade, lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
-    write_items(offsets, EA, T * ks, items, s_wtot);
+    write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
 }
 
 }  // namespace moehip
@@ -303,17 +309,18 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     __syncthreads();
     dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
+    __shared__ int s_ch[VT_MAX];
     for (int e = tid; e < EA; e += 1024)
-        vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, shared ? 1 : 0, sorted_pos, hi_vote, pol.upgrade,
-                   lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
+        s_ch[e] = vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, shared ? 1 : 0, sorted_pos, hi_vote,
+                             pol.upgrade, lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
-    write_items(offsets, EA, T * ks, items, s_wtot);
+    write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
 }
 
-// more than 64 KiB of LDS per workgroup (dynamic + the kernels' static ~21 KiB) must be enabled
+// more than 64 KiB of LDS per workgroup (dynamic + the kernels' static ~25 KiB) must be enabled
 static bool enable_big_lds(const void *fn, size_t lds) {
-    if (lds + 24 * 1024 <= 64 * 1024) return true;
+    if (lds + 28 * 1024 <= 64 * 1024) return true;
     return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
 }
 

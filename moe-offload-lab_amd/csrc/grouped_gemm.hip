@@ -705,34 +705,39 @@ __device__ __forceinline__ void gv_rows(const void *act, const int *ae, int K, i
     }
 }
 
-// work items of the batched GEMVs: (expert, token group of GV_TG) for every expert with pairs, in
-// expert order (one workgroup, exclusive scan of ceil(n_e / GV_TG)); items[NP] = their number
+// work lists of the batched GEMVs when the decision did not write them: one per record precision
+// p < P at items + p * (NP + 1), the (expert, token group of GV_TG) items of every expert whose
+// table row of precision p is set, in expert order (one workgroup, exclusive scan of
+// ceil(n_e / GV_TG)); [NP] = their number
 __global__ __launch_bounds__(1024) void k_gv_items(const int32_t *__restrict__ offsets, int E, int NP,
-                                                   int32_t *__restrict__ items) {
+                                                   const int64_t *__restrict__ tabs, int P, int32_t *__restrict__ items) {
     __shared__ int s_w[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int base = 0;
-    for (int e0 = 0; e0 < E; e0 += 1024) {
-        const int e = e0 + tid;
-        const int n = e < E ? offsets[e + 1] - offsets[e] : 0;
-        const int nz = (n + GV_TG - 1) / GV_TG;
-        int incl = nz;
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
+    for (int p = 0; p < P; ++p) {
+        int32_t *it = items + (size_t)p * (NP + 1);
+        int base = 0;
+        for (int e0 = 0; e0 < E; e0 += 1024) {
+            const int e = e0 + tid;
+            const int n = (e < E && tabs[((size_t)p * E + e) * 4] != 0) ? offsets[e + 1] - offsets[e] : 0;
+            const int nz = (n + GV_TG - 1) / GV_TG;
+            int incl = nz;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            if (lane == 63) s_w[wave] = incl;
+            __syncthreads();
+            int wb = base, tot = base;
+            for (int w = 0; w < 16; ++w) {
+                if (w < wave) wb += s_w[w];
+                tot += s_w[w];
+            }
+            for (int z = 0; z < nz; ++z) it[wb + incl - nz + z] = (e << 8) | z;
+            base = tot;
+            __syncthreads();
         }
-        if (lane == 63) s_w[wave] = incl;
-        __syncthreads();
-        int wb = base, tot = base;
-        for (int w = 0; w < 16; ++w) {
-            if (w < wave) wb += s_w[w];
-            tot += s_w[w];
-        }
-        for (int z = 0; z < nz; ++z) items[wb + incl - nz + z] = (e << 8) | z;
-        base = tot;
-        __syncthreads();
+        if (tid == 0) it[NP] = base;
     }
-    if (tid == 0) items[NP] = base;
 }
 
 // grid (row blocks, NP): block (b, i) covers rows [b * NG * 4 P RPW, ...) of work item i (expert e,
@@ -881,8 +886,8 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     off = al(off + NP * 4);
     L.y = off;
     off = al(off + NP * H * 4);
-    L.items = off;
-    off = al(off + (NP + 1) * 4);
+    L.items = off;  // one work list per record precision
+    off = al(off + (size_t)GV_MAXP * (NP + 1) * 4);
     L.total = off;
     return L;
 }
@@ -1032,10 +1037,11 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     if (bf && !gemv) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
     // the work list: the caller's (written by moehip_batch_route_decide) or built here
     int32_t *items = reinterpret_cast<int32_t *>(wsb + L.items);
-    if (gemv && items_in == nullptr) hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, items);
+    if (gemv && items_in == nullptr)
+        hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, tabs, P, items);
     if (items_in != nullptr) items = const_cast<int32_t *>(items_in);
     for (int p = 0; p < P && gemv; ++p)
-        launch_gv_prec(precs[p], bf ? 2 : 1, items, NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
+        launch_gv_prec(precs[p], bf ? 2 : 1, items + (size_t)p * (NP + 1), NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
     for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
@@ -1052,7 +1058,7 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     // the MFMA down kernels read h as fp16 with a per-pair power of two; the GEMVs read the fp32 rows
     if (!gemv) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
     for (int p = 0; p < P && gemv; ++p)
-        launch_gv_prec(precs[p], 0, items, NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
+        launch_gv_prec(precs[p], 0, items + (size_t)p * (NP + 1), NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
                        y, w, dk);
     for (int p = 0; p < P && !gemv; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;

@@ -171,7 +171,7 @@ class GroupedLayer:
         self.sorted_pos = torch.empty(n * ks, dtype=torch.int32, device=d)
         self.rank = torch.empty(n * ks, dtype=torch.int32, device=d)
         self.tabs = torch.zeros(self.P, EA, 4, dtype=torch.int64, device=d)
-        self.items = torch.empty(n * ks + 1, dtype=torch.int32, device=d)
+        self.items = torch.empty(self.P * (n * ks + 1), dtype=torch.int32, device=d)  # a work list per precision
         self.info = torch.zeros(store.L, EA, dtype=torch.float32, device=d)
         self.miss = torch.zeros(1, dtype=torch.float32, device=d)
         self.offs = torch.tensor([field_offsets(store.layouts[p]) for p in precs], dtype=torch.int64, device=d)

@@ -285,7 +285,7 @@ def test_batch_decide_matches_steps(dev, E, shared, mode):
                     info=torch.full((EA,), -7.0, device=dev), miss=torch.zeros(1, device=dev))
 
     a, b = bufs(), bufs()
-    items = torch.full((T * ks + 1,), -7, dtype=torch.int32, device=dev)
+    items = torch.full((P * (T * ks + 1),), -7, dtype=torch.int32, device=dev)
     print(f"batch decide E={E} shared={shared} {mode}", flush=True)
     _lib.call("moehip_batch_decide", w_d.data_ptr(), idx_d.data_ptr(), T, k, ks, ctypes.byref(cpol),
               a["levels"].data_ptr(), a["skip"].data_ptr(), E, 1 if shared else 0, a["counts"].data_ptr(),
@@ -307,6 +307,9 @@ def test_batch_decide_matches_steps(dev, E, shared, mode):
     assert (sk == 1).any() == (mode == "hobbit")
     assert a["miss"].item() > 0  # some chosen experts have no copy
     off = a["offsets"].cpu().numpy()
-    exp = [(e << 8) | z for e in range(EA) for z in range(off[e + 1] - off[e])]
-    it = items.cpu().numpy()
-    assert it[T * ks] == len(exp) and it[:len(exp)].tolist() == exp
+    ch = a["info"].cpu().numpy()
+    it = items.cpu().numpy().reshape(P, T * ks + 1)
+    for p in range(P):  # one work list per record precision: the experts voted to it
+        exp = [(e << 8) | z for e in range(EA) if ch[e] == p for z in range(off[e + 1] - off[e])]
+        assert it[p, T * ks] == len(exp) and it[p, :len(exp)].tolist() == exp, p
+    assert (ch == 0).any() and (ch == 1).any()
