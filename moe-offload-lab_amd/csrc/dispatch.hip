@@ -136,11 +136,10 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ i
 // idx / w_out / w32 (T, k) and idx_ext / w_ext (T, k + 1) (the same results as moehip_router_topk's
 // top-k part and moehip_shared_slot). s_p: 64 floats of this wave's LDS.
 template <int DT>
-__device__ __forceinline__ void route_token(const void *logits, int E, int k, int renorm, const void *x,
-                                            const void *gate, int H, int t, int64_t *idx, void *wout, float *w32,
-                                            int64_t *idx_ext, float *w_ext, float *s_p) {
+__device__ __forceinline__ void route_topk_part(const void *logits, int E, int k, int renorm, bool shared, int t,
+                                                int64_t *idx, void *wout, float *w32, int64_t *idx_ext, float *w_ext,
+                                                float *s_p) {
     const int lane = threadIdx.x & 63;
-    const bool shared = gate != nullptr;
     const int ks = k + (shared ? 1 : 0);
     int myc;
     float p;
@@ -155,13 +154,23 @@ __device__ __forceinline__ void route_token(const void *logits, int E, int k, in
             w_ext[(size_t)t * ks + lane] = r;
         }
     }
-    if (shared) {
-        const float l = rnd_act<DT>(gate_dot_wave<DT>(x, gate, t, H));
-        if (lane == k) {
-            idx_ext[(size_t)t * ks + k] = E;
-            w_ext[(size_t)t * ks + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
-        }
+}
+template <int DT>
+__device__ __forceinline__ void route_shared_part(const void *x, const void *gate, int H, int E, int k, int t,
+                                                  int64_t *idx_ext, float *w_ext) {
+    const int lane = threadIdx.x & 63;
+    const float l = rnd_act<DT>(gate_dot_wave<DT>(x, gate, t, H));
+    if (lane == 0) {
+        idx_ext[(size_t)t * (k + 1) + k] = E;
+        w_ext[(size_t)t * (k + 1) + k] = rnd_act<DT>(1.0f / (1.0f + expf(-l)));
     }
+}
+template <int DT>
+__device__ __forceinline__ void route_token(const void *logits, int E, int k, int renorm, const void *x,
+                                            const void *gate, int H, int t, int64_t *idx, void *wout, float *w32,
+                                            int64_t *idx_ext, float *w_ext, float *s_p) {
+    route_topk_part<DT>(logits, E, k, renorm, gate != nullptr, t, idx, wout, w32, idx_ext, w_ext, s_p);
+    if (gate != nullptr) route_shared_part<DT>(x, gate, H, E, k, t, idx_ext, w_ext);
 }
 
 // levels and skip of token t's ks slots (one wave; slot k, when ks > k, is the shared expert:
@@ -259,8 +268,10 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
 
 using namespace moehip;
 
-// per-token routing of moehip_batch_route_decide on its own, over many workgroups (one wave per
-// token): for batches whose tokens would queue behind each other in the single-workgroup launch
+// per-token routing of moehip_batch_route_decide on its own, over many workgroups: for batches
+// whose tokens would queue behind each other in the single-workgroup launch. Two waves per token:
+// the top-k (and the copy of the routed slots into idx_ext / w_ext) on one, the shared expert's
+// gate on the other (their outputs are disjoint, so the two latency chains overlap)
 template <int DT>
 __global__ __launch_bounds__(256) void k_route_tokens(const void *__restrict__ logits, int E, int k, int renorm,
                                                       const void *__restrict__ x, const void *__restrict__ gate, int H,
@@ -268,9 +279,12 @@ __global__ __launch_bounds__(256) void k_route_tokens(const void *__restrict__ l
                                                       float *__restrict__ w32, int64_t *__restrict__ idx_ext,
                                                       float *__restrict__ w_ext) {
     __shared__ float s_p[4][64];
-    const int wave = threadIdx.x >> 6, t = blockIdx.x * 4 + wave;
+    const int wave = threadIdx.x >> 6, t = blockIdx.x * 2 + (wave >> 1);
     if (t >= T) return;
-    route_token<DT>(logits, E, k, renorm, x, gate, H, t, idx, wout, w32, idx_ext, w_ext, s_p[wave]);
+    if ((wave & 1) == 0)
+        route_topk_part<DT>(logits, E, k, renorm, gate != nullptr, t, idx, wout, w32, idx_ext, w_ext, s_p[wave]);
+    else if (gate != nullptr)
+        route_shared_part<DT>(x, gate, H, E, k, t, idx_ext, w_ext);
 }
 
 // Batched decode, everything between the router logits and the expert products in one workgroup:
@@ -413,7 +427,7 @@ extern "C" int moehip_route_tokens(const void *logits, int dtype, int T, int E, 
     MOEHIP_REQUIRE(gate == nullptr || (x && idx_ext && w_ext && H % 8 == 0 && ((uintptr_t)x % 16) == 0 &&
                                        ((uintptr_t)gate % 16) == 0),
                    "route_tokens: shared expert needs x, aligned gate, idx_ext and w_ext");
-    const dim3 grid((T + 3) / 4);
+    const dim3 grid((T + 1) / 2);
     if (dtype == MOEHIP_DT_F16)
         hipLaunchKernelGGL((k_route_tokens<MOEHIP_DT_F16>), grid, dim3(256), 0, as_stream(stream), logits, E, k, renorm,
                            x, gate, H, T, idx, w_out, w32, idx_ext, w_ext);
