@@ -297,7 +297,7 @@ int moehip_batch_decide(const float *w32, const int64_t *idx, int T, int k, int 
                         float *info, float *miss, int32_t *items, void *stream);
 
 /*
- * The per-token part of moehip_batch_route_decide over many workgroups (one wave per token): softmax
+ * The per-token part of moehip_batch_route_decide over many workgroups (two waves per token): softmax
  * top-k of the logits (as moehip_router_topk: idx (T, k) int64, w_out (T, k) in dtype or NULL,
  * w32 (T, k) fp32 holding dtype values) and, when gate != NULL, the shared expert as slot k (as
  * moehip_shared_slot: idx_ext / w_ext (T, k + 1); x (T, H), gate (H) 16-byte aligned). For batches
