@@ -663,40 +663,20 @@ def offload_line(args):
 
 
 def cpu_baseline(seconds: float):
-    """The oracle's CPU expert path (moelab/runtime.py:646-702) on a bounded sample."""
-    import numpy as np
-
+    """moelab's CPU expert branch (runtime.py:646-702: fp32 dequantize, F.linear, silu, add_ with
+    alpha = w) restated in torch (oracle/cpu_path.py), on one OLMoE layer of 8 int4 records, all
+    the cores this process may use (torch.set_num_threads), timed as hw.py:45-55 times it."""
     sys.path.insert(0, str(ROOT))
-    import oracle as O
+    from oracle import cpu_path
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([t.get("num_threads", 1) for t in threadpool_info()] or [1])
-    except Exception:  # noqa: BLE001
-        threads = 1
-    rng = np.random.default_rng(0)
-    lay = O.record_layout("int4", H, I, 64, scale="absmax")
-    n_rec = 8
-    t0 = time.time()
-    blobs = [O.encode_record(lay, (rng.standard_normal((2 * I, H)) * 0.02).astype(np.float32),
-                             (rng.standard_normal((H, I)) * 0.02).astype(np.float32), "absmax") for _ in range(n_rec)]
-    log(f"[bench] cpu baseline: {n_rec} records encoded in {time.time() - t0:.1f} s")
-    x = rng.standard_normal((1, H)).astype(np.float16).astype(np.float32)
-    ents = [("int4", blobs[j], 0.125) for j in range(K_TOP)]
-    O.cpu_expert_path(x, ents[:1], {"int4": lay})  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.cpu_expert_path(x, ents, {"int4": lay})
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
-            break
-    per_layer = el / n
-    return {"value": 1.0 / per_layer, "unit": "layer-tok/s", "cores": int(threads), "kind": "port",
-            "sample": f"{n} token-layers (OLMoE layer, 8 int4 experts each) in {el:.1f} s; "
-                      f"{K_TOP * lay['record_bytes'] * n / el / 1e9:.3f} GB/s of records; stack tok/s = "
-                      f"{1.0 / per_layer / L:.3f}"}
+    r = cpu_path.time_olmoe_layer(seconds, H, I, K_TOP)
+    log(f"[bench] cpu baseline: {r['n']} layers in {r['seconds']:.1f} s on {r['threads']} threads ({r['cpu_model']})")
+    return {"value": 1.0 / r["layer_s"], "unit": "layer-tok/s", "cores": r["threads"], "kind": "port",
+            "host_cpus": r["host_cpus"], "cpu_model": r["cpu_model"],
+            "sample": f"{r['n']} token-layers (OLMoE layer, 8 int4 gs64 records, torch fp32 dequantize + F.linear "
+                      f"on {r['threads']} threads) in {r['seconds']:.1f} s; "
+                      f"{r['k'] * r['record_bytes'] * r['n'] / r['seconds'] / 1e9:.3f} GB/s of records; "
+                      f"16-layer stack tok/s = {1.0 / r['layer_s'] / L:.3f}"}
 
 
 def main():

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MOEHIP_ABI_VERSION 2
+#define MOEHIP_ABI_VERSION 3
 
 /* error codes */
 #define MOEHIP_OK 0
@@ -123,6 +123,18 @@ typedef struct moehip_policy {
     float t2;    /* t2 + 1e-6, or < 0 */
     int protect; /* 1 if the layer is protected (level 0) */
     int upgrade; /* allow_upgrade: a more precise resident copy may serve the request */
+    /* f64 = 1: the one-token rule of moelab's default decode path instead (PrecisionPolicy
+     * .levels_one, policy.py:89-98 + 125-137, called by runtime.py:494-517): the weights' total,
+     * the running sum of weight / total and the comparisons in float64, against the float64
+     * thresholds below (t + 1e-6 as Python computes it; < 0 = None). f64 = 0 is the tensor rule
+     * (`levels` / `gpu_levels`, policy.py:110-123, fullgraph.py:101-114) that the T > 1 path and
+     * the whole-token graph use. The two differ only when s lies within float32 rounding of a
+     * threshold. Batched (T > 1) entry points ignore f64: moelab's T > 1 path is the tensor rule. */
+    int f64;
+    int reserved;
+    double t1_64;
+    double t_mid_64;
+    double t2_64;
 } moehip_policy;
 
 /*
@@ -206,6 +218,19 @@ int moehip_decode_layer(const moehip_layer_desc *desc, const void *x, const void
                         void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info, float *miss,
                         void *ws, size_t ws_bytes, int grid, uint64_t *trace, void *stream);
 size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H, int I);
+/*
+ * The same layer kernel on explicit table rows, with no routing and no decision: row j of
+ * precision p runs record rows_b[p * k + j] (a base address; 0 = unused row) with weight
+ * rows_w[p * k + j] (fp32), and out = sum over the rows in table order (+ add) (+ out if
+ * accumulate), cast to the activation dtype. desc gives P, prec, group sizes, offs, H, I, dtype
+ * and k = rows per precision (E, lv2p, pol, planned are ignored; no shared_gate: a shared expert
+ * is one more row). ws: moehip_decode_rows_workspace_bytes(P, k, H, I) bytes, as for
+ * moehip_decode_layer. Replaces the kernel sequence of moelab/kernels.py:909-984 (`GroupedGraph`:
+ * kernels A and B per precision, then out = acc + cpu_part) in one launch.
+ */
+int moehip_decode_rows(const moehip_layer_desc *desc, const void *x, const int64_t *rows_b, const float *rows_w,
+                       void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream);
+size_t moehip_decode_rows_workspace_bytes(int P, int k, int H, int I);
 /* Number of work items (tickets) of one moehip_decode_layer launch for this description, with
  * (with_router = 1) or without the router rows; -1 for a bad description. A grid larger than
  * this is clamped to it; the per-item trace needs 3 * (items + 3) + 8 * items uint64. */

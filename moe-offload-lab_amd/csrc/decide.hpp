@@ -18,13 +18,15 @@ __device__ __forceinline__ void wave_sync() {
 // HOBBIT level and skip of slot j (< k <= 64) of one token, computed by one wave (lane j; lanes
 // j >= k pass wj = 0 and get a meaningless level) in the wave's own LDS (s_w[64], s_sorted[64],
 // s_total[1]). policy.py:77-123 (unimportance over the normalised weights, stable descending
-// rank), the fixed modes (hi / lo / protected layer) and the weight threshold.
+// rank), the fixed modes (hi / lo / protected layer) and the weight threshold. With one64 and
+// pol.f64 set, the one-token float64 rule of levels_one (policy.py:89-98, 125-137) instead.
 __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_policy &pol, float *s_w, float *s_sorted,
-                                           float *s_total, int &lvl, bool &skip) {
+                                           float *s_total, int &lvl, bool &skip, bool one64 = false) {
     const bool act = j < k;
     s_w[j] = wj;
     wave_sync();
-    if (j == 0) {
+    const bool f64 = one64 && pol.f64 != 0 && pol.mode == 0 && !pol.protect;
+    if (j == 0 && !f64) {
         float tot = 0.f;
         for (int i = 0; i < k; ++i) tot += s_w[i];
         s_total[0] = fmaxf(tot, 1e-12f);
@@ -37,6 +39,26 @@ __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_
         lvl = 2;
     } else if (pol.mode == 3) {
         lvl = wj >= pol.t1 ? 0 : 2;  // weight threshold: the expert's own routed weight
+    } else if (f64) {
+        // levels_one: total = sum(weights) left to right in float64 ("or 1e-12" when it is 0),
+        // s_j = running sum of weight / total over the better-ranked slots (stable descending
+        // order of the raw weights), thresholds t + 1e-6 in float64
+        double tot = 0.0;
+        for (int i = 0; i < k; ++i) tot += (double)s_w[i];
+        if (tot == 0.0) tot = 1e-12;
+        int rank = 0;
+        for (int i = 0; i < k; ++i) {
+            const float o = s_w[i];
+            rank += (o > wj) || (o == wj && i < j);
+        }
+        if (act) s_sorted[rank] = wj;
+        wave_sync();
+        double s = 0.0;
+        for (int r = 0; r < rank && r < k; ++r) s += (double)s_sorted[r] / tot;
+        lvl = 2;
+        if (pol.t_mid_64 >= 0.0 && s <= pol.t_mid_64) lvl = 1;
+        if (s <= pol.t1_64) lvl = 0;
+        skip = pol.t2_64 >= 0.0 && s > pol.t2_64 && lvl != 0;
     } else {
         // unimportance (policy.py:77-87): stable descending rank, s = cumsum(sorted) - own weight
         const float wn = wj / s_total[0];
@@ -79,10 +101,13 @@ __device__ __forceinline__ int vote_apply(int e, int n, int c0, int c1, const in
     if (n > 0) {
         const double need = (hi_vote - 1e-9) * (double)n;
         const int level = (double)c0 >= need ? 0 : ((double)c1 >= need ? 1 : 2);
-        const int req = level == 0 ? lv0 : (level == 1 ? lv1 : lv2);
+        // the shared expert runs from its most precise present copy, as in the one-token kernels
+        const bool shared_row = e >= E;
+        const int req = shared_row ? P - 1 : (level == 0 ? lv0 : (level == 1 ? lv1 : lv2));
+        const bool up = shared_row || upgrade;
         for (int pi = P - 1; pi >= 0; --pi) {
             const int64_t base = e < E ? rtab[(size_t)pi * E + e] : srec.r[pi];
-            if (base != 0 && (upgrade ? req >= pi : req == pi)) chosen = pi;
+            if (base != 0 && (up ? req >= pi : req == pi)) chosen = pi;
         }
         if (chosen >= 0 && !planned[chosen]) chosen = -1;
     }

@@ -10,8 +10,9 @@
 //   becomes, resident (other kernels' workgroups drain), and the smallest unfinished item always
 //   belongs to a resident workgroup whose earlier items are done: the launch always drains, with
 //   no shared counter to take items from. Every wait is also bounded (WAIT_SPINS polls); on expiry
-//   the workgroup records an error in the workspace, treats the missing data as absent and moves
-//   on, so no launch can hang.
+//   the workgroup records an error in the workspace and writes NaN where the missing data would
+//   have gone (routed weights, partial rows, output rows), so no launch can hang and none returns
+//   a plausible wrong answer.
 //
 // Routing is computed by EVERY workgroup that runs an up or down item, from the logits: wave 0
 // polls the E logits, ranks them, applies softmax / renorm / HOBBIT and picks each table row's
@@ -48,6 +49,7 @@
 
 #include <limits.h>
 
+#include "decide.hpp"
 #include "gemv_core.hpp"
 
 namespace moehip {
@@ -75,6 +77,8 @@ struct LayerArgs {
     const void *Wr;         // (E, H) router weights, or null when idx_in/w32_in are given
     const int64_t *idx_in;  // (k) routed experts (router skipped) or null
     const float *w32_in;    // (k)
+    const int64_t *rows_b;  // (P, k) explicit table rows (record bases, 0 = unused) or null:
+    const float *rows_w;    //        routing and decision skipped (moehip_decode_rows)
     const int64_t *rtab;    // (P, E) base addresses of this layer's resident records, 0 = absent
     int64_t offs[DL_MAXP][4];
     int prec[DL_MAXP];
@@ -580,9 +584,11 @@ __device__ __forceinline__ uint32_t logit_key(float v, int c) {
 struct DlShared {
     uint32_t tag;
     int routed;
+    int poison;
     int idx[64];
     float w[64];
     float sorted[64];
+    float tot;
     float gl;                      // shared-expert gate logit
     float rw[DL_MAXP * 32];        // table rows: weight (0 = nothing to run)
     uint64_t rb[DL_MAXP * 32];     //             record address
@@ -599,6 +605,17 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
     const int tid = threadIdx.x, rwave = (tid >> 6) - (int)(blockIdx.x & 3u), lane = tid & 63;
     const int k = a.k, E = a.E, ks = a.ks, P = a.P;
     const bool has_sh = a.sgate != nullptr;
+    if (a.rows_b != nullptr) {  // explicit rows: read, nothing to decide
+        for (int j = tid; j < P * ks; j += blockDim.x) {
+            const int64_t b = a.rows_b[j];
+            const float w = a.rows_w[j];
+            sh.rb[j] = (uint64_t)b;
+            sh.rw[j] = b != 0 ? w : 0.f;
+        }
+        if (tid == 0) sh.routed = 1;
+        __syncthreads();
+        return;
+    }
     const bool pre = P * E <= RT_LDS;
     const int epl = (E + 63) >> 6;
     float *s_lv = sh.h;
@@ -651,7 +668,10 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                         s_key[lane + 64 * i] = 0u;
                     }
                 }
-            if (need >> 31) sh.gl = -INFINITY;  // gate weight 0
+            if (need >> 31) sh.gl = __uint_as_float(0x7fc00000u);  // gate weight NaN
+            // an expired wait must not give a plausible answer: every routed weight becomes NaN,
+            // so the output of this launch is NaN (and the workspace error flag is set)
+            if (lane == 0) sh.poison = __ballot(need != 0) != 0ull ? 1 : 0;
             if (a.Wr != nullptr && E <= 64)
                 for (int c = E + lane; c < 64 + 3; c += 64) s_key[c] = 0u;  // pad to whole quads
         }
@@ -757,7 +777,7 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
             const float tot = a.renorm ? wave_sum(p) : 1.f;
             if (lane < k) {
                 myp = a.renorm ? p / tot : p;
-                myw = rnd_act<XDT>(myp);
+                myw = sh.poison ? __uint_as_float(0x7fc00000u) : rnd_act<XDT>(myp);
             }
         } else if (lane < k) {
             myc = (int)a.idx_in[lane];
@@ -773,7 +793,7 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
             // dtype like the gate's output (modeling_qwen3_next.py:793-796), record from srec
             const float l = sh.gl;
             myc = -1;
-            myw = l == -INFINITY ? 0.f : rnd_act<XDT>(1.0f / (1.0f + expf(-l)));
+            myw = l == -INFINITY ? 0.f : (l != l ? l : rnd_act<XDT>(1.0f / (1.0f + expf(-l))));
 #pragma unroll
             for (int pi = 0; pi < DL_MAXP; ++pi) rt[pi] = pi < P ? a.srec[pi] : 0;
         }
@@ -784,41 +804,11 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
         const bool shr = has_sh && j == k;       // the shared row: level 0, never skipped
         const bool row = act || shr;
         const int e = act ? myc : 0;
-        if (act) {
-            sh.idx[j] = e;
-            sh.w[j] = myw;
-        }
-        __builtin_amdgcn_wave_barrier();
+        if (act) sh.idx[j] = e;
         const float wj = act ? myw : 0.f;
-        float tot = 0.f;
-        for (int i = 0; i < k; ++i) tot += sh.w[i];
-        tot = fmaxf(tot, 1e-12f);
         int lvl;
-        bool skip = false;
-        const moehip_policy pol = a.pol;
-        if (pol.mode == 1 || pol.protect) {
-            lvl = 0;
-        } else if (pol.mode == 2) {
-            lvl = 2;
-        } else if (pol.mode == 3) {
-            lvl = wj >= pol.t1 ? 0 : 2;  // weight threshold: the expert's own routed weight
-        } else {
-            const float wn = wj / tot;
-            int rank = 0;
-            for (int i = 0; i < k; ++i) {
-                const float o = sh.w[i] / tot;
-                rank += (o > wn) || (o == wn && i < j);
-            }
-            if (act) sh.sorted[rank] = wn;
-            __builtin_amdgcn_wave_barrier();
-            float cs = 0.f;
-            for (int r = 0; r <= rank && r < k; ++r) cs += sh.sorted[r];
-            const float s = cs - wn;
-            lvl = 2;
-            if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
-            if (s <= pol.t1) lvl = 0;
-            skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
-        }
+        bool skip;
+        slot_level(j, k, wj, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true);
         if (shr) {
             lvl = 0;
             skip = false;
@@ -827,7 +817,7 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
         const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
         // the shared row takes its most precise present copy
         const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
-        const bool upg = shr || pol.upgrade;
+        const bool upg = shr || a.pol.upgrade;
         int chosen = -1;
 #pragma unroll
         for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
@@ -946,6 +936,7 @@ __device__ __forceinline__ void route_fetch(const LayerArgs &a, uint32_t tag, Dl
             if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
         }
         if (lane < ks) sh.idx[lane] = (int)(need ? 0u : pay);
+        if (lane == 0 && __ballot(need) != 0ull) sh.poison = 1;  // the output will be NaN
         if (ist != nullptr && lane == 0) stamp_buf()[6] = __builtin_amdgcn_s_memrealtime();
     }
     __syncthreads();
@@ -1139,6 +1130,10 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
             load_h<PREC, XDT>(sh.h, lane & (G - 1), G, a.I / DlFmt<PREC>::VPC, lv);
             down_rows<PREC, XDT>(d, lv, row0, a.H, lg, rt0.w, part + (size_t)jj * a.H, tag);
             stamp(st, 4);
+        } else {  // h never arrived: this row's partials are NaN, so the output cannot look valid
+            const int rows = per_wave * 4;
+            for (int i = tid; i < rows; i += 256)
+                if (b * rows + i < a.H) st_tag(part + (size_t)jj * a.H + b * rows + i, 0x7fc00000u, tag);
         }
         __syncthreads();  // sh.h is reused below and by the next item
     }
@@ -1182,11 +1177,11 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
             }
             if (!__syncthreads_or(need != 0)) break;
             backoff(nap, 2);
-            if (it == WAIT_SPINS - 1) {  // give up: the missing partials count as 0
+            if (it == WAIT_SPINS - 1) {  // give up: the missing partials make the output NaN
                 flag_error(err);
 #pragma unroll
                 for (int m = 0; m < PER; ++m)
-                    if (need & (1u << m)) s_part[tid + 256 * m] = 0.f;
+                    if (need & (1u << m)) s_part[tid + 256 * m] = __uint_as_float(0x7fc00000u);
                 __syncthreads();
             }
         }
@@ -1197,6 +1192,10 @@ __device__ __forceinline__ void down_item(const LayerArgs &a, uint32_t tag, int 
                 for (int qq = 0; qq < nq; ++qq) acc[u] += s_part[qq * rows + rr];
         }
         __syncthreads();  // s_part is rewritten by the next chunk
+    }
+    if (sh.poison) {  // this workgroup's routing wait expired: no plausible output
+#pragma unroll
+        for (int u = 0; u < PER; ++u) acc[u] = __uint_as_float(0x7fc00000u);
     }
     // the optional terms: each one's loads issued together under a uniform branch (clamped rows
     // of this workgroup's own range), so they cost one round trip, not one per row
@@ -1252,6 +1251,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
     if (tid == 0) {
         sh.tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
         sh.routed = 0;
+        sh.poison = 0;
     }
     __syncthreads();
     const uint32_t tag = uni((int)sh.tag);
@@ -1349,6 +1349,7 @@ __global__ __launch_bounds__(256) void k_decode_tok(LayerArgs) {
         if (tid == 0) {
             sh.tag = ld_co32(a.ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
             sh.routed = 0;
+            sh.poison = 0;
         }
     }
     __syncthreads();
@@ -1537,7 +1538,7 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
                    "decode_layer: x, Wr and the shared gate must be 16-byte aligned");
     MOEHIP_REQUIRE(d->P * ks <= DL_MAXP * 32, "decode_layer: %d precisions x %d rows exceed %d table rows", d->P, ks,
                    DL_MAXP * 32);
-    LayerArgs a;
+    LayerArgs a{};
     a.x = x;
     a.Wr = Wr;
     a.idx_in = idx_in;
@@ -1589,7 +1590,9 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     // items fit on the GPU at once; otherwise the item loop over at most that many workgroups
     DlKernel kern = nullptr;
     int cap = 0;
-    if (d->P == 1 && (grid <= 0 || grid >= total)) {
+    // (external routing runs the item-loop kernel: every workgroup reads the fp32 weights itself,
+    // where the one-item kernel's routing record carries them in 16 bits)
+    if (d->P == 1 && Wr != nullptr && (grid <= 0 || grid >= total)) {
         kern = dl_kernel(d->dtype, true, d->prec[0]);
         if (kern == nullptr || dl_capacity(kern, &cap) != 0 || cap < total) kern = nullptr;
     }
@@ -1605,6 +1608,76 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
     }
     hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, as_stream(stream), a);
     return check_launch("decode_layer");
+}
+
+extern "C" int moehip_decode_rows(const moehip_layer_desc *d, const void *x, const int64_t *rows_b, const float *rows_w,
+                                  void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream) {
+    MOEHIP_REQUIRE(d && x && rows_b && rows_w && out && ws, "decode_rows: null pointer");
+    MOEHIP_REQUIRE(d->shared_gate == nullptr, "decode_rows: a shared expert is one of the explicit rows here");
+    MOEHIP_REQUIRE(d->P > 0 && d->P <= DL_MAXP, "decode_rows: P=%d (1..%d)", d->P, DL_MAXP);
+    MOEHIP_REQUIRE(d->k > 0 && d->k <= 32, "decode_rows: k=%d (1..32 rows per precision)", d->k);
+    MOEHIP_REQUIRE(d->H > 0 && d->H <= DL_MAXROW && d->H % 32 == 0 && d->I > 0 && d->I <= DL_MAXROW && d->I % 32 == 0,
+                   "decode_rows: H=%d I=%d (multiples of 32, <= %d)", d->H, d->I, DL_MAXROW);
+    MOEHIP_REQUIRE(d->dtype >= MOEHIP_DT_F16 && d->dtype <= MOEHIP_DT_F32, "decode_rows: dtype %d", d->dtype);
+    for (int p = 0; p < d->P; ++p) {
+        const int pr = d->prec[p];
+        MOEHIP_REQUIRE(pr >= MOEHIP_PREC_INT4 && pr <= MOEHIP_PREC_FP8 && pr != MOEHIP_PREC_F32,
+                       "decode_rows: precision %d (fp32 records use the grouped kernels)", pr);
+        if (pr == MOEHIP_PREC_INT4 || pr == MOEHIP_PREC_INT8) {
+            const int vpc = vpc_of(pr);
+            MOEHIP_REQUIRE(d->gs_up[p] > 0 && d->gs_up[p] % vpc == 0 && d->H % d->gs_up[p] == 0 && d->gs_dn[p] > 0 &&
+                               d->gs_dn[p] % vpc == 0 && d->I % d->gs_dn[p] == 0,
+                           "decode_rows: group sizes %d/%d need multiples of %d dividing H/I", d->gs_up[p],
+                           d->gs_dn[p], vpc);
+        }
+    }
+    const DlLayout L = dl_layout(d->P, d->k, 1, d->H, d->I);
+    MOEHIP_REQUIRE(ws_bytes >= L.total, "decode_rows: workspace %zu bytes < %u", ws_bytes, L.total);
+    MOEHIP_REQUIRE(((uintptr_t)ws % 256) == 0 && ((uintptr_t)x % 16) == 0,
+                   "decode_rows: workspace 256-byte and x 16-byte aligned");
+    moehip_layer_desc dd = *d;
+    dd.E = 1;
+    for (int p = 0; p < DL_MAXP; ++p) dd.planned[p] = p < d->P ? 1 : 0;
+    LayerArgs a{};
+    a.x = x;
+    a.rows_b = rows_b;
+    a.rows_w = rows_w;
+    for (int p = 0; p < DL_MAXP; ++p) {
+        const bool on = p < d->P;
+        for (int f = 0; f < 4; ++f) a.offs[p][f] = on ? d->offs[p][f] : 0;
+        a.prec[p] = on ? d->prec[p] : 0;
+        a.gs_up[p] = on ? d->gs_up[p] : 0;
+        a.gs_dn[p] = on ? d->gs_dn[p] : 0;
+        a.planned[p] = on ? 1 : 0;
+    }
+    const int total = dl_plan(&dd, 0, &a);
+    a.P = d->P;
+    a.E = 1;
+    a.k = d->k;
+    a.ks = d->k;
+    a.H = d->H;
+    a.I = d->I;
+    a.accumulate = accumulate;
+    a.out = out;
+    a.add = add;
+    a.ws = reinterpret_cast<uint32_t *>(ws);
+    a.off_rec = L.rec;
+    a.off_logits = L.logits;
+    a.off_h = L.h;
+    a.off_part = L.part;
+    DlKernel kern = dl_kernel(d->dtype, false, 0);
+    int cap = 0;
+    if (dl_capacity(kern, &cap) != 0 || cap <= 0) {
+        set_error("decode_rows: occupancy query failed");
+        return MOEHIP_ELAUNCH;
+    }
+    hipLaunchKernelGGL(kern, dim3(total < cap ? total : cap), dim3(256), 0, as_stream(stream), a);
+    return check_launch("decode_rows");
+}
+
+extern "C" size_t moehip_decode_rows_workspace_bytes(int P, int k, int H, int I) {
+    if (P <= 0 || k <= 0 || H <= 0 || I <= 0) return 0;
+    return dl_layout(P, k, 1, H, I).total;
 }
 
 extern "C" int moehip_decode_layer_work_items(const moehip_layer_desc *d, int with_router) {

@@ -234,7 +234,7 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
     __shared__ float s_w[64], s_sorted[64], s_total[1];
     int lvl;
     bool skip;
-    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, skip);
+    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, skip, true);
     const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
     int chosen = -1;
     for (int pi = P - 1; pi >= 0; --pi) {

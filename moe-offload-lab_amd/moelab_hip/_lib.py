@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(os.environ.get("MOEHIP_LIB", Path(__file__).resolve().parent / "libmoehip.so"))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 PREC_CODES = {"int4": 0, "int8": 1, "fp16": 2, "bf16": 3, "fp32": 4, "fp8": 5}
 DT_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -27,7 +27,9 @@ _f = ctypes.c_float
 class Policy(ctypes.Structure):
     """moehip_policy: HOBBIT parameters for one layer (thresholds include the +1e-6 of policy.py:120-122)."""
 
-    _fields_ = [("mode", _i), ("t1", _f), ("t_mid", _f), ("t2", _f), ("protect", _i), ("upgrade", _i)]
+    _fields_ = [("mode", _i), ("t1", _f), ("t_mid", _f), ("t2", _f), ("protect", _i), ("upgrade", _i),
+                ("f64", _i), ("reserved", _i), ("t1_64", ctypes.c_double), ("t_mid_64", ctypes.c_double),
+                ("t2_64", ctypes.c_double)]
 
 
 class LayerDesc(ctypes.Structure):
@@ -65,6 +67,8 @@ _SIGS = {
                              _vp, _vp, _vp, ctypes.c_size_t, _i, _vp, _vp], _i),
     "moehip_decode_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
     "moehip_decode_layer_work_items": ([ctypes.POINTER(LayerDesc), _i], _i),
+    "moehip_decode_rows": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp], _i),
+    "moehip_decode_rows_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
     "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
     "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                              ctypes.c_size_t, _vp], _i),

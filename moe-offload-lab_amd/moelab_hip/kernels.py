@@ -25,6 +25,8 @@ Differences, all deliberate:
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -101,51 +103,17 @@ def expert_ffn_int4(x_row: torch.Tensor, v: dict, groups: dict, act_fn) -> torch
 # ---------------------------------------------------------------------------------------
 # tables
 # ---------------------------------------------------------------------------------------
-class _Staging:
-    """Pinned host ring for table uploads without a host sync (kernels.py:195-224)."""
-
-    def __init__(self, slots: int = 32, nbytes: int = 4096):
-        self.nbytes = nbytes
-        self.bufs = [torch.empty(nbytes, dtype=torch.uint8, pin_memory=True) for _ in range(slots)]
-        self.events: list = [None] * slots
-        self.i = 0
-
-    def send(self, host: torch.Tensor, device) -> torch.Tensor:
-        n = host.numel()
-        if n > self.nbytes:
-            return host.to(device)
-        i = self.i
-        self.i = (i + 1) % len(self.bufs)
-        if self.events[i] is not None:
-            self.events[i].synchronize()
-        buf = self.bufs[i][:n]
-        buf.copy_(host)
-        dev = torch.empty(n, dtype=torch.uint8, device=device)
-        dev.copy_(buf, non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self.events[i] = ev
-        return dev
-
-
-_staging: _Staging | None = None
-
-
 def _table(entries, keys, device) -> tuple[torch.Tensor, torch.Tensor]:
-    """Address table (n, 4) int64 + weights (n,) fp32 on `device`, one async upload (kernels.py:230-244)."""
-    global _staging
+    """Address table (n, 4) int64 + weights (n,) fp32 of [(views, weight)] on `device`
+    (kernels.py:230-244): one host buffer from torch's pinned-memory cache, one asynchronous copy
+    (the cache keeps the buffer until the copy has run, so nothing waits here)."""
     n = len(entries)
-    buf = torch.empty(n * 36, dtype=torch.uint8)
-    buf[: n * 32].view(torch.int64).copy_(
-        torch.tensor([[v[k].data_ptr() for k in keys] for v, _ in entries], dtype=torch.int64).reshape(-1))
-    buf[n * 32:].view(torch.float32).copy_(torch.tensor([float(w) for _, w in entries], dtype=torch.float32))
-    if torch.device(device).type == "cuda":
-        if _staging is None:
-            _staging = _Staging()
-        dev = _staging.send(buf, device)
-    else:
-        dev = buf.to(device)
-    return dev[: n * 32].view(torch.int64).view(n, 4), dev[n * 32:].view(torch.float32)
+    dev = torch.device(device)
+    host = torch.empty(n * 36, dtype=torch.uint8, pin_memory=dev.type == "cuda")
+    host[: n * 32].view(torch.int64).numpy().reshape(n, 4)[:] = [[v[key].data_ptr() for key in keys] for v, _ in entries]
+    host[n * 32:].view(torch.float32).numpy()[:] = [float(w) for _, w in entries]
+    out = host.to(dev, non_blocking=True)
+    return out[: n * 32].view(torch.int64).view(n, 4), out[n * 32:].view(torch.float32)
 
 
 # ---------------------------------------------------------------------------------------
@@ -259,103 +227,176 @@ def grouped_ffn_fp8(x_row: torch.Tensor, entries: list, out: torch.Tensor) -> No
 # ---------------------------------------------------------------------------------------
 # per-layer graph (kernels.py:909-984)
 # ---------------------------------------------------------------------------------------
+def _fused_ok(layouts: dict, dtype) -> bool:
+    """The layouts the one-launch layer kernel takes (16-bit or fp32 activations, no fp32 records,
+    d_model and d_ff <= 2048 and multiples of 32)."""
+    for lay in layouts.values():
+        H, I = dims(lay)
+        if lay["precision"] == "fp32" or H > 2048 or I > 2048 or H % 32 or I % 32:
+            return False
+    return dtype in _lib.DT_CODES
+
+
 class GroupedGraph:
-    """The grouped computation of one MoE layer replayed as one HIP graph: pinned host table ->
-    device table copy, kernels A then B for each precision, out = acc + cpu_part. Per token the
-    host writes k addresses and k weights per precision and replays (one launch)."""
+    """One MoE layer's grouped expert computation for one decode token, replayed as a HIP graph
+    (interface of kernels.py:909-984: GroupedGraph(layouts, x, out, k, version, capture),
+    .run(items, cpu_out), .supports(prec); attributes graph / runs / replays / out / x / k /
+    version).
+
+    Per token the host writes one request block: for every precision p (layouts' order) k rows of
+    (record base address int64, router weight fp32), 12 bytes a row, unused rows 0 (the field
+    offsets are static and applied on the device). The block travels in ONE host-to-device copy,
+    then ONE launch of the layer kernel on explicit rows (moehip_decode_rows) runs every row's
+    gate/up and down products and writes out = sum of the rows in table order + cpu_part. Two
+    request blocks alternate, each with its own graph and the event of its last copy: the host
+    waits on that event before rewriting a block, so it never overwrites a block whose copy is
+    still queued. Layouts the layer kernel does not take (fp32 records, d_model or d_ff above
+    2048) run kernels A and B per precision instead, from the same request block."""
+
+    NBLOCKS = 2
 
     def __init__(self, layouts: dict, x: torch.Tensor, out: torch.Tensor, k: int, version: int = 2,
                  capture: bool = True):
         self.dev = x.device
         self.x, self.out, self.k, self.version = x.reshape(-1), out, k, version
+        self.precs = list(layouts)
+        self.layouts = dict(layouts)
         self.plans: dict[str, _Plan] = {p: _Plan(lay, version) for p, lay in layouts.items()}
-        H = out.shape[-1]
-        pin = self.dev.type == "cuda"
-        self.tabs = {}
-        for p, plan in self.plans.items():
-            host = torch.zeros(k * 36, dtype=torch.uint8, pin_memory=pin)
-            dev = torch.empty_like(host, device=self.dev)
-            self.tabs[p] = {
-                "host": host, "dev": dev,
-                "tab_np": host[: k * 32].view(torch.int64).numpy(), "w_np": host[k * 32:].view(torch.float32).numpy(),
-                "tab": dev[: k * 32].view(torch.int64), "w": dev[k * 32:].view(torch.float32),
-                "h": torch.empty(k, plan.I, dtype=torch.float32, device=self.dev),
-            }
-            plan.partial(k, self.dev)
-        self.acc = torch.empty(H, dtype=torch.float32, device=self.dev)
+        P = len(self.precs)
+        cuda = self.dev.type == "cuda"
+        self.blocks = []
+        for _ in range(self.NBLOCKS):
+            host = torch.zeros(P * k * 12, dtype=torch.uint8, pin_memory=cuda)
+            devb = torch.zeros_like(host, device=self.dev)
+            self.blocks.append({
+                "host": host, "dev": devb, "event": None, "graph": None,
+                "bases": host[: P * k * 8].view(torch.int64).numpy().reshape(P, k),
+                "weights": host[P * k * 8:].view(torch.float32).numpy().reshape(P, k),
+                "dev_bases": devb[: P * k * 8].view(torch.int64), "dev_weights": devb[P * k * 8:].view(torch.float32),
+            })
         self.cpu_part = torch.zeros_like(out)
         self.cpu_dirty = False
-        self.capture = capture and self.dev.type == "cuda"
-        self.graph = None
+        self.fused = cuda and _fused_ok(self.layouts, self.x.dtype) and self.out.is_contiguous()
+        if self.fused:
+            self.desc = self._desc()
+            n = _lib.load().moehip_decode_rows_workspace_bytes(P, k, self.desc.H, self.desc.I)
+            self.ws = torch.zeros(n, dtype=torch.uint8, device=self.dev)
+        else:
+            H = out.shape[-1]
+            self.offs = torch.tensor([field_offsets(self.layouts[p]) for p in self.precs], dtype=torch.int64,
+                                     device=self.dev)
+            self.h = {p: torch.empty(k, plan.I, dtype=torch.float32, device=self.dev) for p, plan in self.plans.items()}
+            self.acc = torch.empty(H, dtype=torch.float32, device=self.dev)
+            self.tabs = torch.zeros(P, k, 4, dtype=torch.int64, device=self.dev)
+            for plan in self.plans.values():
+                plan.partial(k, self.dev)
+        self.capture = capture and cuda
         self.replays = 0
         self.runs = 0
+        self._last = None
+
+    @property
+    def graph(self):
+        """The graph of the block the last run used (None before the first capture)."""
+        return None if self._last is None else self._last["graph"]
 
     def supports(self, prec: str) -> bool:
         return prec in self.plans
 
-    def _sequence(self) -> None:
-        for t in self.tabs.values():
-            t["dev"].copy_(t["host"], non_blocking=True)
-        first = True
-        for p, plan in self.plans.items():
-            t = self.tabs[p]
-            plan.up(self.k, t["tab"], t["w"], self.x, t["h"], self.acc, zero=first)
-            first = False
-        for p, plan in self.plans.items():
-            t = self.tabs[p]
-            plan.down(self.k, t["tab"], t["w"], t["h"], self.acc)
+    def _desc(self) -> _lib.LayerDesc:
+        d = _lib.LayerDesc()
+        d.P, d.E, d.k = len(self.precs), 1, self.k
+        d.H, d.I = self.plans[self.precs[0]].H, self.plans[self.precs[0]].I
+        d.dtype = _lib.dt_code(self.x.dtype)
+        for pi, p in enumerate(self.precs):
+            plan = self.plans[p]
+            if (plan.H, plan.I) != (d.H, d.I):
+                raise ValueError("GroupedGraph: every layout must have the same d_model and d_ff")
+            d.prec[pi] = plan.code
+            d.gs_up[pi], d.gs_dn[pi] = plan.g_up, plan.g_dn
+            d.planned[pi] = 1
+            for f, o in enumerate(plan.offs):
+                d.offs[pi][f] = o
+        return d
+
+    def _launches(self, blk: dict) -> None:
+        """What one replay enqueues: the request copy, then the layer."""
+        blk["dev"].copy_(blk["host"], non_blocking=True)
+        stream = _lib.stream_of(self.dev)
+        if self.fused:
+            _lib.call("moehip_decode_rows", ctypes.byref(self.desc), self.x.data_ptr(), blk["dev_bases"].data_ptr(),
+                      blk["dev_weights"].data_ptr(), self.out.data_ptr(), self.cpu_part.data_ptr(), 0,
+                      self.ws.data_ptr(), self.ws.numel(), stream)
+            return
+        bases = blk["dev_bases"].view(len(self.precs), self.k, 1)
+        torch.mul(bases + self.offs.view(-1, 1, 4), (bases != 0).to(torch.int64), out=self.tabs)
+        w = blk["dev_weights"].view(len(self.precs), self.k)
+        for pi, p in enumerate(self.precs):
+            self.plans[p].up(self.k, self.tabs[pi], w[pi], self.x, self.h[p], self.acc, zero=pi == 0)
+        for pi, p in enumerate(self.precs):
+            self.plans[p].down(self.k, self.tabs[pi], w[pi], self.h[p], self.acc)
         _combine(self.acc, self.out, self.cpu_part, accumulate=False)
 
     def run(self, items: dict, cpu_out: torch.Tensor | None = None) -> None:
-        """items: {precision: [(record on the GPU, weight), ...]}; cpu_out: sum of the CPU-computed experts."""
+        """items: {precision: [(record on the GPU, weight), ...]} (at most k per precision);
+        cpu_out: the sum of the experts computed on the CPU, added to the result."""
         self.runs += 1
-        for p, t in self.tabs.items():
-            tab, w = t["tab_np"], t["w_np"]
-            tab[:] = 0
-            w[:] = 0.0
-            offs = self.plans[p].offs
-            rows = items.get(p, ())
+        blk = self.blocks[self.runs % self.NBLOCKS]
+        if blk["event"] is not None:
+            blk["event"].synchronize()  # that block's previous copy has run (long ago, in practice)
+        bases, weights = blk["bases"], blk["weights"]
+        bases[:] = 0
+        weights[:] = 0.0
+        for p, rows in items.items():
+            if p not in self.plans:
+                raise ValueError(f"GroupedGraph: no layout for precision {p}")
             if len(rows) > self.k:
                 raise ValueError(f"{len(rows)} {p} experts for a table of {self.k} rows")
+            pi = self.precs.index(p)
             for j, (blob, wt) in enumerate(rows):
-                base = blob.data_ptr()
-                tab[4 * j: 4 * j + 4] = [base + o for o in offs]
-                w[j] = wt
+                bases[pi, j] = blob.data_ptr()
+                weights[pi, j] = wt
         if cpu_out is not None:
             self.cpu_part.copy_(cpu_out)
             self.cpu_dirty = True
         elif self.cpu_dirty:
             self.cpu_part.zero_()
             self.cpu_dirty = False
+        self._last = blk
         if not self.capture:
-            self._sequence()
-            return
-        if self.graph is not None:
-            self.graph.replay()
+            self._launches(blk)
+        elif blk["graph"] is not None:
+            blk["graph"].replay()
             self.replays += 1
-            return
-        self._sequence()
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self._sequence()
-        self.graph = g
-        torch.cuda.synchronize()
+        else:  # first token: run it, then capture every block's launches for the later tokens
+            self._launches(blk)
+            torch.cuda.synchronize(self.dev)
+            for b in self.blocks:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._launches(b)
+                b["graph"] = g
+        if self.dev.type == "cuda":
+            ev = torch.cuda.Event()
+            ev.record()
+            blk["event"] = ev
 
 
 def grouped_graph_gpu_ms(layout: dict, x, out, k: int, version: int, items: dict, repeat: int = 50) -> float:
-    """GPU time of one grouped computation (k experts) replayed as a graph (kernels.py:590-602)."""
+    """GPU milliseconds of one grouped computation of k experts as a graph replay (kernels.py:
+    590-602): both request blocks are captured, then `repeat` replays alternate between them."""
     gg = GroupedGraph({layout["precision"]: layout}, x, out, k, version=version)
-    gg.run(items)
-    gg.run(items)
+    for _ in range(GroupedGraph.NBLOCKS):  # both request blocks hold the same rows
+        gg.run(items)
+    graphs = [b["graph"] for b in gg.blocks]
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(repeat):
-        gg.graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / repeat
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(repeat):
+        graphs[i % len(graphs)].replay()
+    t1.record()
+    t1.synchronize()
+    return t0.elapsed_time(t1) / repeat
 
 
 AUTO_CANDIDATES = (2,)

@@ -87,9 +87,12 @@ class MoEDecoder:
 
     def __init__(self, store: ResidentStore, k: int, policy: PrecisionPolicy | None = None, dtype=torch.float16,
                  router_weights: list | None = None, renorm: bool = False, planned: list | None = None,
-                 fused: bool = True, grid: int = 0, shared: list | None = None):
+                 fused: bool = True, grid: int = 0, shared: list | None = None, one_token_rule: bool = False):
         """shared: per layer None or {"gate": (H,) tensor in dtype, "rec": {precision: record blob}}
-        for a Qwen3-Next shared expert (out += sigmoid(x . gate) * FFN_s(x)); fused path only."""
+        for a Qwen3-Next shared expert (out += sigmoid(x . gate) * FFN_s(x)); fused path only.
+        one_token_rule: HOBBIT levels by the float64 rule of PrecisionPolicy.levels_one (moelab's
+        default decode path, runtime.py:494-517) instead of the tensor rule of gpu_levels (the
+        whole-token graph, fullgraph.py:101-114)."""
         self.store = store
         self.shared = shared
         self.k = k
@@ -121,7 +124,7 @@ class MoEDecoder:
         self.w32 = torch.zeros(1, k, dtype=torch.float32, device=dev)
         self.info = torch.zeros(store.L, 3, k, dtype=torch.float32, device=dev)
         self.miss = torch.zeros(1, dtype=torch.float32, device=dev)
-        self._pols = [self.policy.device_policy(l) for l in range(store.L)]
+        self._pols = [self.policy.device_policy(l, one_token=one_token_rule) for l in range(store.L)]
         self.grid = grid
         self.trace = None  # optional int64 device tensor of 3 * (items + 3) + 8 * items: per-item stamps
         self.fused = fused and all(store.layouts[p]["precision"] != "fp32" for p in precs) and H <= 2048 \

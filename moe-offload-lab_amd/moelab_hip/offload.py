@@ -5,10 +5,12 @@ copy stream before its experts run, next-layer predictions in the background.
 
 The host-side objects keep the names, arguments and semantics of moelab's offload runtime, so
 code written against those objects works on these:
-  HostPool     moelab/hostpool.py:52-185   pinned slabs carved into exact record slots
-  TierCache    moelab/cache.py:78-311      LRFU (Lee et al. 2001) with heap victims
+  HostPool     moelab/hostpool.py:52-185   (tiers.py) page extents of pinned arenas
+  TierCache    moelab/cache.py:78-311      (tiers.py) LRFU (Lee et al. 2001), indexed victim heap
   Stager       moelab/runtime.py:186 (copy_stream), 310-326 (`_to_fast`), 328-333 (`_ready`)
   DeviceTable  moelab/fullgraph.py:43-98   TierCache listener keeping the device record table
+Stager takes any pinned uint8 record buffer, so the reference's own HostPool slots and TierCache
+entries can drive it unchanged.
 What changes is the device side: a layer's records are staged by ONE moehip_stage_records call
 (a gather kernel reading pinned host memory directly, or SDMA copies) into slots of a fixed
 device pool (no allocator traffic), and table entries are written on the copy stream after
@@ -23,10 +25,6 @@ of `OffloadDecoder.layer` (the host must know which experts to stage).
 from __future__ import annotations
 
 import ctypes
-import heapq
-import math
-import threading
-from dataclasses import dataclass
 from types import SimpleNamespace
 
 import torch
@@ -34,415 +32,12 @@ import torch
 from . import _lib
 from .layer import MoEDecoder
 from .policy import PrecisionPolicy, level_to_precision
+from .tiers import HostPool, TierCache  # noqa: F401  (re-exported: the runtime imports them from here)
 
 SLAB_BYTES = 256 << 20
 STAGE_MAX = 32   # records per moehip_stage_records call
 TABLE_MAX = 64   # entries per moehip_table_set call
 STAGE_MODES = {"kernel": 0, "sdma": 1}
-
-
-def _pow2_ceil(n: int) -> int:
-    return 1 << (max(n, 1) - 1).bit_length()
-
-
-def _pow2_floor(n: int) -> int:
-    return 1 << (max(n, 1).bit_length() - 1)
-
-
-# ---------------------------------------------------------------------------------------------
-# Host tier
-# ---------------------------------------------------------------------------------------------
-class HostPool:
-    """Bounded pool of host record buffers (moelab/hostpool.py:52-185): slabs of a power-of-two
-    size (<= 256 MiB, ~16 records) each cut into exact slots of one precision; a released slot
-    waits in quarantine until its event has passed AND `advance()` was called (the next layer);
-    a slab whose slots are all free is re-cut for a precision that ran out; past `cap` bytes (or
-    when the system refuses to pin more) `acquire` hands out an ordinary buffer and counts it."""
-
-    def __init__(self, record_bytes: dict, cap_bytes: int, pin: bool, log=print):
-        self.record_bytes = dict(record_bytes)
-        self.cap = int(cap_bytes)
-        self.pin = pin
-        self.log = log
-        self.lock = threading.Lock()
-        self.slabs: list[torch.Tensor] = []
-        self.slab_prec: list[str] = []
-        self.slab_slots: list[list[torch.Tensor]] = []
-        self.allocated = 0
-        self.free: dict[str, list[torch.Tensor]] = {p: [] for p in self.record_bytes}
-        self.quarantine: list[tuple] = []  # (slot, precision, event, epoch)
-        self.owner: dict[int, str] = {}
-        self.in_use: set[int] = set()
-        self.epoch = 0
-        self.exhausted = False
-        self.fallbacks = 0
-        self.reclaims = 0
-
-    def _alloc(self, size: int) -> torch.Tensor:
-        if self.pin:
-            return torch.empty(size, dtype=torch.uint8, pin_memory=True)
-        raw = torch.empty(size + 4096, dtype=torch.uint8)
-        off = (-raw.data_ptr()) % 4096
-        return raw[off:off + size]
-
-    def _grow(self, prec: str) -> bool:
-        rb = self.record_bytes[prec]
-        size = max(_pow2_ceil(rb), min(SLAB_BYTES, _pow2_ceil(16 * rb)))
-        room = self.cap - self.allocated
-        if size > room:
-            size = _pow2_floor(room) if room >= rb else 0
-            if size < rb:
-                return False
-        try:
-            slab = self._alloc(size)
-        except RuntimeError as exc:
-            self.exhausted = True
-            self.log(f"host pool: pinning refused after {self.allocated / 2**30:.2f} GiB ({type(exc).__name__}); "
-                     "ordinary buffers from now on")
-            return False
-        self.slabs.append(slab)
-        self.slab_prec.append(prec)
-        self.slab_slots.append([])
-        self.allocated += size
-        self._cut(len(self.slabs) - 1, prec)
-        return True
-
-    def _cut(self, i: int, prec: str) -> None:
-        slab, rb = self.slabs[i], self.record_bytes[prec]
-        slots = [slab[j * rb:(j + 1) * rb] for j in range(slab.numel() // rb)]
-        for s in slots:
-            self.owner[s.data_ptr()] = prec
-        self.free[prec].extend(slots)
-        self.slab_prec[i] = prec
-        self.slab_slots[i] = slots
-
-    def _recut(self, prec: str) -> bool:
-        rb = self.record_bytes[prec]
-        for i, other in enumerate(self.slab_prec):
-            if other == prec or self.slabs[i].numel() < rb:
-                continue
-            ptrs = {s.data_ptr() for s in self.slab_slots[i]}
-            if not ptrs <= {s.data_ptr() for s in self.free[other]}:
-                continue
-            self.free[other] = [s for s in self.free[other] if s.data_ptr() not in ptrs]
-            for p in ptrs:
-                self.owner.pop(p, None)
-            self._cut(i, prec)
-            self.reclaims += 1
-            return True
-        return False
-
-    def _sweep(self) -> None:
-        waiting = []
-        for slot, prec, ev, epoch in self.quarantine:
-            if epoch < self.epoch and (ev is None or ev.query()):
-                self.free[prec].append(slot)
-            else:
-                waiting.append((slot, prec, ev, epoch))
-        self.quarantine = waiting
-
-    def acquire(self, prec: str) -> torch.Tensor:
-        """A buffer of exactly one `prec` record (thread-safe)."""
-        with self.lock:
-            if not self.free[prec]:
-                self._sweep()
-            if not self.free[prec] and not self.exhausted:
-                self._grow(prec)
-            if not self.free[prec]:
-                self._sweep()
-                self._recut(prec)
-            if self.free[prec]:
-                slot = self.free[prec].pop()
-                self.in_use.add(slot.data_ptr())
-                return slot
-            self.fallbacks += 1
-        return torch.empty(self.record_bytes[prec], dtype=torch.uint8)
-
-    def release(self, blob: torch.Tensor, event=None) -> None:
-        """Give a buffer back (ignored for ordinary buffers and double releases)."""
-        p = blob.data_ptr()
-        with self.lock:
-            prec = self.owner.get(p)
-            if prec is None or p not in self.in_use:
-                return
-            self.in_use.discard(p)
-            self.quarantine.append((blob, prec, event, self.epoch))
-
-    def advance(self) -> None:
-        """Start of a layer: slots released before it may be reused once their event passed."""
-        with self.lock:
-            self.epoch += 1
-
-    def is_pooled(self, blob: torch.Tensor) -> bool:
-        return blob.data_ptr() in self.owner
-
-    def describe(self) -> str:
-        n_free = sum(len(v) for v in self.free.values())
-        s = (f"host pool ({'pinned' if self.pin else 'pageable'}): {self.allocated / 2**30:.2f}/"
-             f"{self.cap / 2**30:.2f} GiB, {n_free} free slots")
-        if self.fallbacks:
-            s += f", {self.fallbacks} buffers outside the pool"
-        if self.reclaims:
-            s += f", {self.reclaims} slabs re-cut"
-        return s
-
-    def close(self) -> None:
-        with self.lock:
-            self.slabs.clear()
-            self.slab_prec.clear()
-            self.slab_slots.clear()
-            self.free = {p: [] for p in self.record_bytes}
-            self.quarantine.clear()
-            self.owner.clear()
-            self.in_use.clear()
-            self.allocated = 0
-
-
-# ---------------------------------------------------------------------------------------------
-# LRFU cache
-# ---------------------------------------------------------------------------------------------
-@dataclass
-class Entry:
-    key: tuple
-    blob: torch.Tensor
-    nbytes: int
-    f: float = 0.0
-    t: int = 0
-    pinned: bool = False
-    event: object = None       # copy to this tier still in flight
-    prefetched: bool = False   # staged ahead and not used yet
-    ver: int = 0
-
-
-@dataclass
-class TierStats:
-    hits: int = 0
-    misses: int = 0
-    inserts: int = 0
-    evictions: int = 0
-    rejected: int = 0
-    bytes_in: int = 0
-
-
-class TierCache:
-    """One memory tier's expert cache (moelab/cache.py:78-311). Key (layer, expert, precision).
-
-    LRFU score f * gamma^(clock - t), gamma = 0.5^(1/half_life); a touch sets f <- score + 1,
-    t <- clock. Since the clock is common to every entry, the victim order is the order of the
-    fixed key log f - t log gamma, kept in a heap with lazy invalidation (an entry's `ver` moves
-    on every touch). eviction="stale" evicts entries last touched before the current pass first.
-    Pinned entries are never evicted on demand; `repin` swaps cold pinned entries for hot
-    unpinned ones (25 % hysteresis, at most 4 swaps per call)."""
-
-    def __init__(self, name: str, device, budget_bytes: int, rank_of, half_life: float = 32.0,
-                 pin_fraction: float = 0.5, on_evict=None, eviction: str = "lrfu"):
-        if eviction not in ("lrfu", "stale"):
-            raise ValueError(f"unknown eviction policy {eviction} (lrfu or stale)")
-        self.eviction = eviction
-        self.listener = None
-        self.name = name
-        self.on_evict = on_evict
-        self.device = torch.device(device)
-        self.budget = int(budget_bytes)
-        self.rank_of = rank_of
-        self.gamma = 0.5 ** (1.0 / half_life)
-        self._lg = math.log(self.gamma)
-        self.pin_budget = int(self.budget * pin_fraction)
-        self.entries: dict[tuple, Entry] = {}
-        self.by_expert: dict[tuple, set] = {}
-        self.used = 0
-        self.pinned_bytes = 0
-        self.clock = 0
-        self.stats = TierStats()
-        self._heap: list = []
-        self._seq = 0
-
-    def _order_key(self, e: Entry) -> float:
-        return math.log(e.f) - e.t * self._lg
-
-    def _push(self, e: Entry) -> None:
-        e.ver += 1
-        if e.pinned:
-            return
-        self._seq += 1
-        heapq.heappush(self._heap, (self._order_key(e), self._seq, e.ver, e.key))
-        if len(self._heap) > 4 * len(self.entries) + 64:
-            self._heap = [(self._order_key(x), i, x.ver, x.key) for i, x in enumerate(self.entries.values())
-                          if not x.pinned]
-            heapq.heapify(self._heap)
-
-    def score(self, e: Entry) -> float:
-        return e.f * self.gamma ** (self.clock - e.t)
-
-    def touch(self, e: Entry) -> None:
-        e.f = self.score(e) + 1.0
-        e.t = self.clock
-        if e.key in self.entries:
-            self._push(e)
-
-    def tick(self, n: int = 1) -> None:
-        self.clock += n
-
-    def lookup(self, layer: int, expert: int, need: str, exact: bool = False, count: bool = True) -> Entry | None:
-        """Best entry of (layer, expert) at least as precise as `need` (only `need` if exact);
-        count=False: a check that counts neither hit nor miss."""
-        precs = self.by_expert.get((layer, expert))
-        best = None
-        if precs:
-            if exact:
-                best = need if need in precs else None
-            else:
-                ok = [p for p in precs if self.rank_of(p) <= self.rank_of(need)]
-                best = min(ok, key=self.rank_of) if ok else None
-        if best is None:
-            self.stats.misses += count
-            return None
-        self.stats.hits += count
-        return self.entries[(layer, expert, best)]
-
-    def contains(self, key) -> bool:
-        return key in self.entries
-
-    def insert(self, key, blob: torch.Tensor, pinned: bool = False, protect: frozenset = frozenset(),
-               event=None) -> Entry | None:
-        """Add an entry, evicting unpinned, unprotected entries of lowest score as needed;
-        None if the room cannot be made. An existing key is touched and returned."""
-        if key in self.entries:
-            e = self.entries[key]
-            self.touch(e)
-            return e
-        need = blob.numel() * blob.element_size()
-        if pinned and self.pinned_bytes + need > self.pin_budget:
-            pinned = False
-        if need > self.budget - self.pinned_bytes:
-            self.stats.rejected += 1
-            return None
-        if self.used + need > self.budget:
-            chosen = self._victims(need, protect)
-            if chosen is None:
-                self.stats.rejected += 1
-                return None
-            for v in chosen:
-                self.evict(v.key)
-        e = Entry(key, blob, need, pinned=pinned, event=event)
-        self.touch(e)
-        self.entries[key] = e
-        self._push(e)
-        self.by_expert.setdefault(key[:2], set()).add(key[2])
-        self.used += need
-        if pinned:
-            self.pinned_bytes += need
-        self.stats.inserts += 1
-        self.stats.bytes_in += need
-        if self.listener is not None:
-            self.listener.added(e)
-        return e
-
-    def _victims(self, need: int, protect) -> list[Entry] | None:
-        chosen, freed = [], 0
-        if self.eviction == "stale":
-            order = sorted((e for e in self.entries.values() if not e.pinned and e.key not in protect),
-                           key=lambda e: (e.t >= self.clock, self.score(e)))
-            for v in order:
-                if self.used - freed + need <= self.budget:
-                    break
-                chosen.append(v)
-                freed += v.nbytes
-        else:
-            held, seen = [], set()
-            while self.used - freed + need > self.budget and self._heap:
-                item = heapq.heappop(self._heap)
-                key, ver = item[3], item[2]
-                e = self.entries.get(key)
-                if e is None or e.ver != ver or e.pinned or key in seen:
-                    continue  # stale heap item
-                if key in protect:
-                    held.append(item)
-                    continue
-                seen.add(key)
-                chosen.append(e)
-                freed += e.nbytes
-            for item in held:
-                heapq.heappush(self._heap, item)
-        if self.used - freed + need > self.budget:
-            for e in chosen:
-                self._push(e)
-            return None
-        return chosen
-
-    def evict(self, key) -> None:
-        e = self.entries.pop(key)
-        if e.event is not None and self.device.type == "cuda":
-            torch.cuda.current_stream(self.device).wait_event(e.event)  # a copy into it may be in flight
-        precs = self.by_expert[key[:2]]
-        precs.discard(key[2])
-        if not precs:
-            del self.by_expert[key[:2]]
-        self.used -= e.nbytes
-        if e.pinned:
-            self.pinned_bytes -= e.nbytes
-        self.stats.evictions += 1
-        if self.listener is not None:
-            self.listener.removed(e)
-        if self.on_evict is not None:
-            self.on_evict(e.blob)
-
-    def clear(self) -> None:
-        for k in list(self.entries):
-            self.evict(k)
-        self._heap = []
-        self.stats = TierStats()
-
-    def pin(self, key) -> bool:
-        e = self.entries.get(key)
-        if e is None or e.pinned:
-            return e is not None
-        if self.pinned_bytes + e.nbytes > self.pin_budget:
-            return False
-        e.pinned = True
-        self.pinned_bytes += e.nbytes
-        return True
-
-    def unpin(self, key) -> None:
-        e = self.entries.get(key)
-        if e is not None and e.pinned:
-            e.pinned = False
-            self.pinned_bytes -= e.nbytes
-            self._push(e)
-
-    def repin(self, hysteresis: float = 0.25, max_swaps: int = 4) -> list:
-        """Pin hot unpinned entries, swapping out colder pinned ones only when the candidate beats
-        the victim by `hysteresis`; at most `max_swaps`. Returns [(candidate, victim or None)]."""
-        swaps = []
-        cands = sorted((e for e in self.entries.values() if not e.pinned), key=self.score, reverse=True)
-        victims = sorted((e for e in self.entries.values() if e.pinned), key=self.score)
-        vi = 0
-        for c in cands:
-            if len(swaps) >= max_swaps:
-                break
-            if self.pinned_bytes + c.nbytes <= self.pin_budget:
-                self.pin(c.key)
-                swaps.append((c.key, None))
-                continue
-            while vi < len(victims) and not victims[vi].pinned:
-                vi += 1
-            if vi >= len(victims):
-                break
-            v = victims[vi]
-            if self.score(c) <= self.score(v) * (1.0 + hysteresis):
-                break
-            self.unpin(v.key)
-            if self.pin(c.key):
-                swaps.append((c.key, v.key))
-                vi += 1
-            else:
-                self.pin(v.key)
-                break
-        return swaps
-
-    def describe(self) -> str:
-        return (f"{self.name}: {self.used / 2**20:.0f}/{self.budget / 2**20:.0f} MiB, {len(self.entries)} entries "
-                f"({self.pinned_bytes / 2**20:.0f} MiB pinned)")
 
 
 # ---------------------------------------------------------------------------------------------
@@ -658,7 +253,9 @@ class OffloadDecoder:
         self.stager = Stager(self.device, self.pool, self.table, mode)
         view = SimpleNamespace(device=self.device, precisions=self.precisions, layouts=self.layouts, L=num_layers,
                                E=num_experts, rtab=self.table.dev)
-        self.dec = MoEDecoder(view, k, self.policy, dtype, router_weights=router_weights, renorm=renorm)
+        # the host decides what to stage with levels_one, so the kernel uses the same float64 rule
+        self.dec = MoEDecoder(view, k, self.policy, dtype, router_weights=router_weights, renorm=renorm,
+                              one_token_rule=True)
         self._blob_prec: dict[int, str] = {}
         self.rb = (torch.empty(2, k, dtype=torch.float32, pin_memory=True))
         self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0}

@@ -123,18 +123,24 @@ class PrecisionPolicy:
         """policy.py:176-185."""
         return self.upgrade and self.mode != "lo"
 
-    def device_policy(self, layer: int) -> Policy:
-        """Parameters of moehip_decide_table for `layer`."""
+    def device_policy(self, layer: int, one_token: bool = False) -> Policy:
+        """Parameters of the decision kernels for `layer`. one_token=True selects, for the
+        one-token kernels, the float64 rule of `levels_one` (moelab's default decode path,
+        runtime.py:494-517); otherwise the tensor rule of `levels` / `gpu_levels` (the T > 1 path
+        and the whole-token graph, fullgraph.py:101-114). Both threshold forms are packed."""
         mode = {"hobbit": 0, "hi": 1, "lo": 2, "weight": 3}[self.mode]
         f32 = lambda v: float(torch.tensor(v, dtype=torch.float32))  # noqa: E731
+        prot = 1 if layer in self.protect_layers else 0
+        upg = 1 if self.allow_upgrade else 0
         if self.mode == "weight":
-            return Policy(mode=mode, t1=f32(self.t1), t_mid=-1.0, t2=-1.0,
-                          protect=1 if layer in self.protect_layers else 0, upgrade=1 if self.allow_upgrade else 0)
-        return Policy(mode=mode, t1=f32(self.t1_for(layer) + 1e-6),
-                      t_mid=-1.0 if self.t_mid is None else f32(self.t_mid + 1e-6),
-                      t2=-1.0 if self.t2 is None else f32(self.t2 + 1e-6),
-                      protect=1 if layer in self.protect_layers else 0,
-                      upgrade=1 if self.allow_upgrade else 0)
+            return Policy(mode=mode, t1=f32(self.t1), t_mid=-1.0, t2=-1.0, protect=prot, upgrade=upg,
+                          f64=0, t1_64=-1.0, t_mid_64=-1.0, t2_64=-1.0)
+        t1 = self.t1_for(layer) + 1e-6
+        tm = None if self.t_mid is None else self.t_mid + 1e-6
+        t2 = None if self.t2 is None else self.t2 + 1e-6
+        return Policy(mode=mode, t1=f32(t1), t_mid=-1.0 if tm is None else f32(tm), t2=-1.0 if t2 is None else f32(t2),
+                      protect=prot, upgrade=upg, f64=1 if one_token else 0, t1_64=t1,
+                      t_mid_64=-1.0 if tm is None else tm, t2_64=-1.0 if t2 is None else t2)
 
 
 def level_to_precision(level: int, precisions: list) -> str:

@@ -15,6 +15,9 @@ reference's files, each function citing the file:line it follows:
 - router        transformers' OlmoeTopKRouter / Qwen3MoeTopKRouter / Qwen3NextTopKRouter
 - runtime.py    dispatch (_decide_general), expert_ffn, combine, the CPU expert branch
 
+`oracle/cpu_path.py` restates the CPU expert branch (runtime.py:646-702) in torch for bench.py's
+reported CPU baseline; tests/test_oracle.py checks it against moe_ref.
+
 Pinning (what fixes each function independently of this restatement) is listed in
 `oracle/moe_ref.py`'s module docstring.
 """

@@ -405,6 +405,31 @@ class Policy:
         skip = (s > np.float32(self.t2 + 1e-6)) & (lvl != 0) if self.t2 is not None else none
         return lvl, skip
 
+    def levels_one(self, layer, weights):
+        """policy.py:89-98 + 125-137: the same rule for ONE token in float64 Python arithmetic
+        (moelab's default decode path, runtime.py:494-517): total = sum of the weights, s = the
+        exclusive running sum of weight / total in stable descending order, thresholds t + 1e-6 in
+        float64. Returns (levels list, skip list, s list)."""
+        ws = [float(v) for v in np.asarray(weights, np.float32).reshape(-1)]
+        k = len(ws)
+        fixed = self._fixed(layer)
+        if fixed is not None:
+            return [fixed] * k, [False] * k, [0.0] * k
+        if self.mode == "weight":
+            return [0 if np.float32(v) >= np.float32(self.t1) else 2 for v in ws], [False] * k, [0.0] * k
+        total = sum(ws) or 1e-12
+        s = [0.0] * k
+        acc = 0.0
+        for j in sorted(range(k), key=lambda j: -ws[j]):
+            s[j] = acc
+            acc += ws[j] / total
+        t1 = self.t1_for(layer) + 1e-6
+        tm = None if self.t_mid is None else self.t_mid + 1e-6
+        lvl = [0 if v <= t1 else (1 if tm is not None and v <= tm else 2) for v in s]
+        if self.t2 is None:
+            return lvl, [False] * k, s
+        return lvl, [v > self.t2 + 1e-6 and lv != 0 for v, lv in zip(s, lvl)], s
+
     def expert_level(self, token_levels) -> int:
         """policy.py:148-154: most precise level requested by >= hi_vote of the expert's tokens."""
         tl = np.asarray(token_levels)

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.moehip_abi_version() == 2
+    assert lib.moehip_abi_version() == _lib.ABI_VERSION == 3
     assert lib.moehip_layer_desc_bytes() == ctypes.sizeof(_lib.LayerDesc)
 
 
@@ -51,7 +51,7 @@ def test_argument_validation_without_gpu():
 
 
 def test_policy_struct_layout():
-    assert ctypes.sizeof(_lib.Policy) == 24
+    assert ctypes.sizeof(_lib.Policy) == 56
 
 
 @pytest.mark.parametrize("prec", ["fp32", "fp16", "bf16", "int8", "int4", "fp8"])
@@ -91,4 +91,6 @@ def test_device_policy_thresholds():
     assert d.t_mid == -1.0 and d.protect == 0 and d.upgrade == 1
     assert p.device_policy(5).protect == 1
     assert PrecisionPolicy("lo").device_policy(0).upgrade == 0
+    assert d.f64 == 0 and d.t1_64 == 0.2 + 1e-6 and d.t2_64 == 0.9 + 1e-6 and d.t_mid_64 == -1.0
+    assert p.device_policy(3, one_token=True).f64 == 1
     assert [level_to_precision(v, ["fp16", "int4"]) for v in (0, 1, 2)] == ["fp16", "int4", "int4"]

@@ -230,6 +230,52 @@ def test_decide_general_vote_by_hand():
     assert O.decide_general(pol, 0, idx, w, ["fp16", "int4"])[1][5] == (2, "int4")
 
 
+def test_mse_planted_negative_scale_group():
+    """The known answer of tests/test_requant.py:35-42 scaled by 1/16 inside random rows: the
+    group's mse scale is -1/16 (the largest weight on -8), the negated group's is +1/16, and both
+    dequantise exactly; the GPU parity tests plant the same groups in their mse records."""
+    rng = np.random.default_rng(0)
+    gu = (rng.standard_normal((256, 128)) * 0.05).astype(np.float32)
+    dn = (rng.standard_normal((128, 128)) * 0.05).astype(np.float32)
+    grp = np.zeros(64, np.float32)
+    grp[:5] = np.array([8.0, 1.0, 2.0, 3.0, -4.0], np.float32) / 16
+    gu[0, :64], dn[3, 64:128] = grp, -grp
+    lay = O.record_layout("int4", 128, 128, 64, scale="mse")
+    blob = O.encode_record(lay, gu, dn, method="mse")
+    v = O.views(lay, blob)
+    assert float(v["gate_up.s"][0, 0]) == -0.0625 and float(v["down.s"][3, 1]) == 0.0625
+    g2, d2 = O.materialize(lay, blob)
+    assert np.array_equal(g2[0, :64], gu[0, :64]) and np.array_equal(d2[3, 64:128], dn[3, 64:128])
+
+
+def test_levels_one_known_answers():
+    """The one-token float64 rule gives the reference's known answers too (tests/test_units.py:
+    168-176, 364-373: levels_one == levels there; tests/test_optim.py:129-136 per-layer t1)."""
+    w = [0.1345, 0.1063, 0.0921, 0.0855, 0.0829, 0.0705, 0.0682, 0.0214]
+    lvl, skip, s = O.Policy("hobbit", t1=0.6, t2=0.9).levels_one(0, w)
+    assert np.allclose(s, [0.0, 0.2034, 0.3641, 0.5034, 0.6327, 0.7580, 0.8646, 0.9677], atol=2e-4)
+    assert [v == 0 for v in lvl] == [True] * 4 + [False] * 4 and skip == [False] * 7 + [True]
+    pol = O.Policy("hobbit", t1=0.6, t1_layers={1: 0.0})
+    assert pol.levels_one(1, [0.5, 0.3, 0.2])[0] == [0, 2, 2]
+    assert pol.levels_one(0, [0.5, 0.3, 0.2])[0] == [0, 0, 2]
+    assert O.Policy("hobbit", t1=0.3, t_mid=0.85, t2=0.9).levels_one(0, [0.5, 0.3, 0.15, 0.05])[:2] == \
+        ([0, 1, 1, 2], [False, False, False, True])
+
+
+def test_levels_one_differs_from_levels_at_a_threshold():
+    """Weights that are exact binary fractions give s = [0, 0.5, 0.75] exactly in both rules. With
+    t1 = 0.5 - 1e-6 - 1e-9 the float64 threshold t1 + 1e-6 = 0.499999999 lies below s = 0.5, but
+    rounded to float32 (the tensor rule compares fp32 s against fp32(t1 + 1e-6)) it is 0.5: the
+    tensor rule serves slot 1 at level 0 and the float64 rule at level 2."""
+    t1 = 0.5 - 1e-6 - 1e-9
+    assert np.float32(t1 + 1e-6) == np.float32(0.5) and t1 + 1e-6 < 0.5
+    pol = O.Policy("hobbit", t1=t1)
+    w = np.array([[0.5, 0.25, 0.25]], np.float32)
+    assert pol.levels(0, w)[0][0].tolist() == [0, 0, 2]
+    lvl, _, s = pol.levels_one(0, w[0])
+    assert s == [0.0, 0.5, 0.75] and lvl == [0, 2, 2]
+
+
 def test_t_mid_levels():
     w = np.array([[0.5, 0.3, 0.15, 0.05]], np.float32)  # s = 0, .5, .8, .95
     lvl, skip = O.Policy("hobbit", t1=0.3, t_mid=0.85, t2=0.9).levels(0, w)
@@ -445,3 +491,29 @@ def test_weight_threshold_rule():
     assert l1 == lvl[0].tolist() and not any(s1)
     dp = pol.device_policy(3)
     assert dp.mode == 3 and dp.t1 == float(np.float32(0.15)) and dp.t2 < 0
+
+
+# -- the CPU baseline's torch restatement (oracle/cpu_path.py) -------------------------------
+def test_cpu_path_matches_the_oracle():
+    """The torch restatement of the CPU expert branch dequantises byte-identically to the oracle
+    and gives the oracle's layer output (fp32 vs float64 accumulation)."""
+    import torch
+
+    from oracle import cpu_path as C
+
+    rng = np.random.default_rng(3)
+    for prec in ("int4", "int8", "fp16"):
+        lay = O.record_layout(prec, 256, 128, 64, scale="absmax" if prec != "fp16" else None)
+        blobs, mats = [], []
+        for _ in range(3):
+            b = O.encode_record(lay, (rng.standard_normal((256, 256)) * 0.02).astype(np.float32),
+                                (rng.standard_normal((256, 128)) * 0.02).astype(np.float32))
+            blobs.append(b)
+            mats.append(O.materialize(lay, b))
+            g, d = C.materialize(lay, torch.from_numpy(b))
+            assert np.array_equal(g.numpy(), mats[-1][0]) and np.array_equal(d.numpy(), mats[-1][1])
+        x = rng.standard_normal((1, 256)).astype(np.float16)
+        w = [0.5, 0.3, 0.2]
+        got = C.cpu_layer(torch.from_numpy(x), [(prec, torch.from_numpy(b), wi) for b, wi in zip(blobs, w)], {prec: lay})
+        ref = O.moe_layer(x.astype(np.float32), np.array([[0, 1, 2]]), np.array([w]), lambda e: mats[e])
+        assert np.abs(got.numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
