@@ -311,3 +311,154 @@ def test_shared_expert_only_less_precise_copy(dev, path):
     gs = O.round_to((1.0 / (1.0 + np.exp(-logit.astype(np.float64)))).astype(np.float32), "bfloat16")
     ref = ref + gs.astype(np.float64)[:, None] * O.expert_ffn(xf, *O.materialize(lay4, sh_blob.cpu().numpy()))
     assert_layer_close(out.float().cpu().numpy(), ref, dtype)
+
+
+# ---------------------------------------------------------------------------------------
+# the fast paths behind moelab's layer signatures (adapters.py)
+# ---------------------------------------------------------------------------------------
+def _olmoe_block(dev, H, I, E, k, dtype, precs, seed):
+    """A transformers OlmoeSparseMoeBlock (its router on the GPU, in `dtype`) and a ResidentStore
+    holding its experts in every precision of `precs` (records built from the block's weights)."""
+    from transformers import OlmoeConfig
+    from transformers.models.olmoe.modeling_olmoe import OlmoeSparseMoeBlock
+
+    torch.manual_seed(seed)
+    cfg = OlmoeConfig(hidden_size=H, intermediate_size=I, num_experts=E, num_experts_per_tok=k, norm_topk_prob=False)
+    blk = OlmoeSparseMoeBlock(cfg)
+    with torch.no_grad():
+        blk.gate.weight.normal_(0, 0.05)
+        blk.experts.gate_up_proj.normal_(0, 0.02)
+        blk.experts.down_proj.normal_(0, 0.02)
+    st = ResidentStore({p: record_layout(p, H, I, 64, scale="absmax") for p in precs}, 1, E, dev)
+    for e in range(E):
+        for p in precs:
+            st.encode(p, 0, e, blk.experts.gate_up_proj[e].detach().to(dev), blk.experts.down_proj[e].detach().to(dev))
+    return blk.to(dev, dtype), st
+
+
+@pytest.mark.parametrize("T", [1, 5, 70])
+def test_experts_module_signature(dev, T):
+    """transformers' OLMoE MoE block with its `experts` module swapped for ResidentExperts (the call
+    moelab's OffloadedExperts.forward receives, runtime.py:1108-1112): bf16 hidden states, the
+    block's own router, fp16 + int4 records and HOBBIT t1 = 0.5 (upgrade off). T = 1 takes the
+    decode kernel (float64 one-token rule), T = 5 the batched GEMVs, T = 70 the MFMA tiles (tensor
+    rule, per-expert vote); each checked against the oracle on the float view of the records."""
+    from moelab_hip.adapters import HipMoE, ResidentExperts
+
+    H, I, E, k = 512, 256, 16, 4
+    dtype = torch.bfloat16
+    precs = ["fp16", "int4"]
+    blk, st = _olmoe_block(dev, H, I, E, k, dtype, precs, 71)
+    pol = PrecisionPolicy("hobbit", t1=0.5, upgrade=False)
+    moe = HipMoE(st, k, pol, dtype, max_tokens=128)
+    seen = {}
+    blk.experts = ResidentExperts(moe, 0, blk.experts.act_fn, E)
+    blk.experts.register_forward_pre_hook(lambda m, a: seen.__setitem__("args", tuple(t.clone() for t in a)))
+    x = torch.randn(1, T, H, generator=torch.Generator().manual_seed(72)).to(dev, dtype)
+    print(f"experts-module binding T={T}", flush=True)
+    with torch.no_grad():
+        got = blk(x)
+    torch.cuda.synchronize()
+    hs, idx, w = (t.cpu() for t in seen["args"])
+    assert got.shape == x.shape and got.dtype == dtype
+    w32 = w.float().numpy()
+    opol = O.Policy("hobbit", t1=0.5)
+    mats = lambda p, e: O.materialize(st.layouts[p], st.blob(p, 0, e).cpu().numpy())  # noqa: E731
+    xf = hs.float().numpy()
+    if T == 1:
+        lvl = opol.levels_one(0, w32[0])[0]
+        prec_of = {int(e): precs[0] if v == 0 else precs[1] for e, v in zip(idx[0].tolist(), lvl)}
+        ref = O.moe_layer(xf, idx.numpy(), w32.astype(np.float64), lambda e: mats(prec_of[e], e))
+    else:
+        skip, decs = O.decide_general(opol, 0, idx.numpy(), w32, precs)
+        ref = O.moe_layer(xf, idx.numpy(), w32.astype(np.float64), lambda e: mats(decs[e][1], e), skip=skip)
+    assert_layer_close(got.reshape(T, H).float().cpu().numpy(), ref, dtype)
+    assert moe.miss == 0
+
+
+def test_run_layer_refuses_other_activations(dev):
+    from moelab_hip.adapters import HipMoE
+
+    st = ResidentStore({"int4": record_layout("int4", 512, 256, 64, scale="absmax")}, 1, 8, dev)
+    moe = HipMoE(st, 2, dtype=torch.float16, max_tokens=8)
+    x = torch.zeros(1, 512, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="silu"):
+        moe.run_layer(0, x, torch.zeros(1, 2, dtype=torch.int64, device=dev), torch.zeros(1, 2, device=dev),
+                      torch.nn.GELU())
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_fullmoe_layer_signature(dev, graph):
+    """FullMoE.layer(layer, x, idx, w, call) (fullgraph.py:149-188) on FullMoEHip: eagerly, and
+    captured in a HIP graph with `call` launching inside the capture, replayed on new routing;
+    readout() = [missing] + info, HOBBIT by the tensor rule."""
+    from moelab_hip.adapters import FullMoEHip
+
+    H, I, E, k, L = 512, 256, 16, 4, 2
+    dtype = torch.float16
+    S = _Stack(dev, H, I, E, L, ["fp16", "int4"], 81)
+    x = torch.zeros(1, H, dtype=dtype, device=dev)
+    idx = torch.zeros(1, k, dtype=torch.int64, device=dev)
+    w = torch.zeros(1, k, dtype=dtype, device=dev)
+    fm = FullMoEHip(S.store, k, x, PrecisionPolicy("hobbit", t1=0.6, upgrade=False))
+    outs = []
+
+    def token():
+        outs.clear()
+        for l in range(L):
+            outs.append(fm.layer(l, x, idx, w, lambda fn: fn()))
+
+    g = None
+    if graph:
+        token()  # eager warm-up, then capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            token()
+    rng = np.random.default_rng(82)
+    for step in range(3):
+        xi = torch.randn(1, H, generator=S.g).to(dtype)
+        ii = torch.from_numpy(rng.choice(E, k, replace=False)).view(1, k)
+        wi = torch.from_numpy(rng.random((1, k)).astype(np.float32)).to(dtype)
+        x.copy_(xi.to(dev))
+        idx.copy_(ii.to(dev))
+        w.copy_(wi.to(dev))
+        print(f"fullmoe binding graph={graph} step {step}", flush=True)
+        if graph:
+            g.replay()
+        else:
+            token()
+        torch.cuda.synchronize()
+        ro = fm.readout()
+        assert ro[0] == 0.0
+        info = np.array(ro[1:]).reshape(L, 3, k)
+        w32 = wi.float().numpy()
+        lvl = O.Policy("hobbit", t1=0.6).levels(0, w32)[0][0]
+        for l in range(L):
+            prec_of = {int(e): "fp16" if v == 0 else "int4" for e, v in zip(ii[0].tolist(), lvl)}
+            ref = O.moe_layer(xi.float().numpy(), ii.numpy(), w32.astype(np.float64),
+                              lambda e: S.mats(l, e, prec_of[e]))
+            assert_layer_close(outs[l].float().cpu().numpy(), ref, dtype)
+            assert info[l, 0].tolist() == ii[0].float().tolist() and info[l, 2].tolist() == lvl.astype(float).tolist()
+
+
+def test_grouped_graph_fp32_records(dev):
+    """GroupedGraph on fp32 records (outside the one-launch kernel): kernels A and B per precision
+    from the same request block, replayed."""
+    H, I, k = 256, 128, 3
+    from test_gpu_parity import make_records, to_dev
+    lay32, b32, m32 = make_records("fp32", H, I, 5, 91)
+    r32 = to_dev(b32, dev)
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(92)).to(dev)
+    out = torch.zeros(1, H, device=dev)
+    gg = K.GroupedGraph({"fp32": lay32}, x, out, k)
+    assert not gg.fused
+    rng = np.random.default_rng(93)
+    for step in range(4):
+        e = rng.choice(5, k, replace=False)
+        wv = rng.random(k).astype(np.float32)
+        gg.run({"fp32": [(r32[i], float(v)) for i, v in zip(e, wv)]})
+        torch.cuda.synchronize()
+        ref = O.moe_layer(x.cpu().numpy(), np.array([list(e)]), np.array([wv]), lambda i: m32[i])
+        assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 1e-4
+    assert gg.replays == 3
