@@ -205,11 +205,17 @@ typedef struct moehip_layer_desc {
  * moehip_decide_table. rtab (P, E) holds the base address of each resident record of this layer.
  * `ws` is caller-owned scratch of moehip_decode_layer_workspace_bytes() bytes, 256-B aligned and
  * zeroed once before its first use; every launch leaves it ready for the next. Launches sharing a
- * workspace must not overlap (one workspace per stream). grid = number of workgroups (0 = one per
- * work item), clamped to the number the device holds at once (occupancy x CUs). trace (optional, NULL in production): 3 uint64 per work item = (start, end,
- * workgroup) in the GPU's constant real-time clock, 9 route stamps, then 8 stage stamps per item,
- * for profiling (tracing adds waits inside the items). H, I multiples of 32 and
- * <= 2048, E <= 1024, k <= 32; x and Wr 16-byte aligned; fp32 records are not supported here.
+ * workspace must not overlap (one workspace per stream).
+ * Kernels: with one record precision and 16-bit activations, on a device whose workgroups are
+ * dispatched to XCD b % 8 (checked by moehip_device_check), the XCD-local kernel (routing and the h
+ * exchange inside each XCD, one exchange of partial rows between XCDs); otherwise the item kernels.
+ * grid: 0 = automatic; > 0 = the item kernels with at most that many workgroups (clamped to what
+ * the device holds at once); -1 = the XCD-local kernel when it applies, with its trace format.
+ * trace (optional, NULL in production): for the item kernels 3 uint64 per work item = (start, end,
+ * workgroup) in the GPU's constant real-time clock, 9 route stamps, then 8 stage stamps per item
+ * (tracing adds waits inside the items); for the XCD-local kernel (grid = -1) 8 real-time stamps
+ * per workgroup. H, I multiples of 32 and <= 2048, E <= 1024, k <= 32; x and Wr 16-byte aligned;
+ * fp32 records are not supported here.
  * Replaces, for decode, the whole moelab/runtime.py:523-770 `run_layer` GPU path when every
  * expert is resident (the A5 whole-token path, moelab/fullgraph.py:149-188 + graphs.py:351-426).
  */

@@ -44,5 +44,6 @@ extern "C" int moehip_device_check(int dev) {
         moehip::set_error("device %d is %s, this library is built for gfx950", dev, prop.gcnArchName);
         return MOEHIP_ENODEV;
     }
+    moehip::xcd_probe(dev);  // whether the XCD-local decode kernel may run on this device
     return MOEHIP_OK;
 }

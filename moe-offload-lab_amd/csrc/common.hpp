@@ -24,6 +24,16 @@ int check_launch(const char *what);
 
 static inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
+// the XCD-local one-token layer kernel (decode_xcd.hip): the dispatch check of a device (run once
+// by moehip_device_check), its workspace size (0 = the layer does not fit it) and its launch
+// (*used = 0 when the layer does not fit it or the device was not confirmed)
+int xcd_probe(int dev);
+size_t xcd_workspace_bytes(int prec, int ks, int E, int H, int I);
+int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in, const float *w32_in,
+               const int64_t *rows_b, const float *rows_w, const int64_t *rtab, void *out, const void *add,
+               int accumulate, void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info,
+               float *miss, void *ws, size_t ws_bytes, uint64_t *trace, void *stream, int *used);
+
 // ---------------------------------------------------------------------------------------
 // scalar conversions
 // ---------------------------------------------------------------------------------------
