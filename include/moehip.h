@@ -213,7 +213,7 @@ typedef struct moehip_layer_desc {
  * the device holds at once); -1 = the XCD-local kernel when it applies, with its trace format.
  * trace (optional, NULL in production): for the item kernels 3 uint64 per work item = (start, end,
  * workgroup) in the GPU's constant real-time clock, 9 route stamps, then 8 stage stamps per item
- * (tracing adds waits inside the items); for the XCD-local kernel (grid = -1) 8 real-time stamps
+ * (tracing adds waits inside the items); for the XCD-local kernel (grid = -1) 16 real-time stamps
  * per workgroup. H, I multiples of 32 and <= 2048, E <= 1024, k <= 32; x and Wr 16-byte aligned;
  * fp32 records are not supported here.
  * Replaces, for decode, the whole moelab/runtime.py:523-770 `run_layer` GPU path when every

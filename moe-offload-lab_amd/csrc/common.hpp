@@ -231,5 +231,11 @@ __device__ __forceinline__ uint32_t gld4(gbyte *p) { return *(const __attribute_
 __device__ __forceinline__ uint32_t gld2(gbyte *p) { return *(const __attribute__((address_space(1))) uint16_t *)p; }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+// the same from the hardware's exp2 and reciprocal (about 1 ulp each): 6 instructions instead of ~30,
+// for kernels whose every lane evaluates it (exp2(+large) = inf gives g * 0 = -0, as g / inf)
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
 
 }  // namespace moehip

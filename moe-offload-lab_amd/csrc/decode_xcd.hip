@@ -9,15 +9,18 @@
 //
 //   1. routing, replicated per XCD: the workgroups of an XCD compute the E router logits (and the
 //      Qwen3-Next shared gate) between them, each into its XCD's copy, and every workgroup reads
-//      all of them back and ranks them itself (softmax, top-k, renorm, HOBBIT, the record of each
-//      table row);
+//      all of them back and ranks them itself (top-k and the record of each table row; the
+//      weights, renorm and HOBBIT decision follow while the expert weights load);
 //   2. the table rows' h values (k routed + shared, I each, flattened row after row) are cut into
-//      8 contiguous segments, one per XCD; the XCD's up items produce its segment's
-//      h = w * silu(gate x) * (up x) into the XCD's h area (w = the row's routed weight);
-//   3. the XCD's down items each hold DR output rows and multiply the down columns of the segment
-//      with h: a partial output of the whole layer restricted to the segment;
+//      8 contiguous segments, one per XCD; workgroup q of an XCD holds up part q (hpi h values
+//      of its segment: h = w * silu(gate x) * (up x), w = the row's routed weight, into the XCD's
+//      h area) and down part q (output rows [q * DR, q * DR + DR) times the segment's down
+//      columns: a partial output of the layer restricted to the segment). Every wave requests the
+//      weights of its up part, then those of its down part, as soon as the rows are ranked: the
+//      whole layer's expert bytes are in flight at once, up part first;
+//   3. once the XCD's h values are in (polled from the XCD's L2), the down part's products;
 //   4. the one exchange between XCDs: the partial rows of the 8 XCDs, summed in XCD order by the
-//      down item of XCD d % 8 for its row block d, plus add / accumulate, cast to the output dtype.
+//      workgroup of XCD q % 8 for row block q, plus add / accumulate, cast to the output dtype.
 //
 // Cross-workgroup words are tagged ((launch tag << 32) | payload): inside an XCD written with
 // plain stores and polled with non-temporal loads (which do not allocate in the CU's L1, so each
@@ -28,7 +31,7 @@
 // the missing data would have gone (routed weights, partial rows, output rows), so a launch never
 // hangs and never returns a plausible wrong answer.
 //
-// Co-residency: the grid (8 x items per XCD) never exceeds what the GPU holds at once.
+// Co-residency: the grid (8 x workgroups per XCD) never exceeds what the GPU holds at once.
 
 #include "decide.hpp"
 #include "lanevec.hpp"
@@ -44,6 +47,7 @@ constexpr int XC_MAXE = 1024;
 constexpr int XC_MAXKS = 33;
 constexpr int XC_LDS_H = 8192;     // h values of one XCD's segment staged in LDS (fp32)
 constexpr int XC_MAXDR = 512;      // output rows of one down item
+constexpr int XC_NST = 16;         // trace stamps per workgroup
 
 struct XcArgs {
     const void *x;            // (H) activation dtype, 16-byte aligned
@@ -66,21 +70,19 @@ struct XcArgs {
     float *info;
     float *miss;
     uint32_t *ws;
-    uint64_t *trace;          // 8 stamps per workgroup or null
+    uint64_t *trace;          // XC_NST stamps per workgroup or null
     uint32_t off_lg, off_h, off_part;  // byte offsets of the tagged areas in ws
     uint32_t lg_stride, h_stride;      // 64-bit words between two XCDs' copies
-    uint32_t defer;           // real-time ticks (10 ns) the down items wait before loading
     int E, k, ks, H, I, gs_up, gs_dn, renorm, accumulate, planned;
     int unit, units;          // h values per segment unit, units over all table rows
     int nu, nd;               // up / down items per XCD
     int hpi;                  // h values per up item
     int lg_up, lg_dn;         // log2 lanes per gate/up row and per down row
     int dr;                   // output rows per down item
+    uint32_t defer;           // real-time ticks (10 ns) the down items wait before loading
 };
 
 struct XcShared {
-    uint32_t tag;
-    int poison;
     int idx[64];
     float w[64];
     float sorted[64];
@@ -89,9 +91,9 @@ struct XcShared {
     int64_t rb[64];           //             record base
     int lvl[64];
     int chosen[64];
-    uint64_t st[8];           // trace stamps of this workgroup
+    uint64_t st[XC_NST];      // trace stamps of this workgroup
     float part[XC_MAXDR];     // a combiner's own partial rows
-    union {
+    union {  // (up items use the routing arrays to the end: the report; down items stage h here)
         struct {
             int64_t rt[XC_MAXE];
             float lv[XC_MAXE + 64];
@@ -101,8 +103,17 @@ struct XcShared {
     } u;
 };
 
+// down rows per lane group and wave pass
+template <int PREC> struct XcFmt {
+    static constexpr int NPD = DlFmt<PREC>::NPD;
+};
+
 __device__ __forceinline__ void xc_stamp(const XcArgs &a, XcShared &sh, int i) {
     if (a.trace != nullptr && threadIdx.x == 0) sh.st[i] = __builtin_amdgcn_s_memrealtime();
+}
+// (inside the routing, by the routing wave's first lane)
+__device__ __forceinline__ void xc_stamp_r(const XcArgs &a, XcShared &sh, int i) {
+    if (a.trace != nullptr && (threadIdx.x & 63) == 0) sh.st[i] = __builtin_amdgcn_s_memrealtime();
 }
 
 // XCD-local words: plain stores (through to the XCD's L2), non-temporal polls (L1 not allocated).
@@ -118,12 +129,19 @@ __device__ __forceinline__ uint64_t ld_local(const uint64_t *p) {
 
 __device__ __forceinline__ int xc_seg_begin(int x, int units) { return (x * units) / XC_N; }
 
+// the launch tag from the generation word as loaded: computed at the point of use (the opaque
+// step keeps the compiler from computing it, and so waiting for the load, any earlier)
+__device__ __forceinline__ uint32_t xc_tag_of(uint32_t gen) {
+    asm volatile("" : "+v"(gen));
+    return gen + 1u;
+}
+
 // ---------------------------------------------------------------------------------------
 // generation: count this workgroup as having read the tag; workgroups 0..15 drain the counters
 // and the last one advances the generation (bounded, advanced all the same on expiry)
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void xc_gen_read(uint32_t *ws) {
-    if (threadIdx.x == 64)
+    if (threadIdx.x == 0)
         __hip_atomic_fetch_add(ws + XC_READ + 32 * (blockIdx.x % XC_NSUB), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void xc_gen_manage(uint32_t *ws, uint32_t tag) {
@@ -151,25 +169,30 @@ __device__ __forceinline__ void xc_gen_manage(uint32_t *ws, uint32_t tag) {
 // rounded to the activation dtype (the gate's F.linear output) and stored in the XCD's copy.
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int first, int nrows, uint64_t *lg, uint32_t tag) {
+__device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int first, int nrows, uint64_t *lg, uint32_t gen) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c0 = lane * 32;
     const bool on = c0 < a.H;
-    uint4 xv[4];
+    // the first row's weights are requested before x is used (both loads in flight together)
+    auto row_ptr = [&](int id) {
+        const int r = first + id;  // logit index: Wr row r < E, the shared gate at E
+        return r < a.E ? reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)r * a.H + c0) * 2)
+                       : reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.sgate) + (size_t)c0 * 2);
+    };
+    int id = q + NQ * wave;
+    if (id >= nrows) return;
+    uint4 wv[4], xv[4];
     if (on) {
+        const uint4 *wp = row_ptr(id);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[i] = wp[i];
         const uint4 *xp = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.x) + (size_t)c0 * 2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) xv[i] = xp[i];
     }
-    for (int id = q + NQ * wave; id < nrows; id += 4 * NQ) {
-        const int r = first + id;  // logit index: Wr row r < E, the shared gate at E
+    while (true) {
         float acc = 0.f;
         if (on) {
-            const uint8_t *wp = r < a.E ? reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)r * a.H + c0) * 2
-                                        : reinterpret_cast<const uint8_t *>(a.sgate) + (size_t)c0 * 2;
-            uint4 wv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) wv[i] = reinterpret_cast<const uint4 *>(wp)[i];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
@@ -187,22 +210,35 @@ __device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int fi
             }
         }
         acc = wave_sum(acc);
-        if (lane == 0) st_local(lg + r, __float_as_uint(rnd_act<XDT>(acc)), tag);
+        if (lane == 0) st_local(lg + first + id, __float_as_uint(rnd_act<XDT>(acc)), xc_tag_of(gen));
+        id += 4 * NQ;
+        if (id >= nrows) break;
+        if (on) {
+            const uint4 *wp = row_ptr(id);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wv[i] = wp[i];
+        }
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// routing of this launch, computed by wave 0 of every workgroup into LDS: sh.rw / sh.rb for the
-// ks table rows (k routed + the shared row), and for the report: idx, w, levels, choices.
+// routing, part 1, by wave 0 of every workgroup: the k routed experts in rank order (lanes < k:
+// expert myc, logit myv) and the record base of every table row (k routed + the shared row) in
+// sh.rb. The rows' weight loads start from these; the weights and the HOBBIT decision (part 2)
+// follow while they are in flight. A row with no resident copy (or an unplanned layer) has
+// base 0 and never runs; a row that part 2 skips runs with weight 0.
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void xc_route(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag,
-                                         int64_t idx_pre, float w_pre) {
+__device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag,
+                                        int64_t idx_pre, int &myc, float &myv, bool &poisoned) {
     const int lane = threadIdx.x & 63;
     const int k = a.k, E = a.E, ks = a.ks;
     const bool has_sh = a.sgate != nullptr;
     const bool routed = a.Wr != nullptr;
-    if (a.rows_b != nullptr) {  // explicit rows
+    myc = 0;
+    myv = 0.f;
+    poisoned = false;
+    if (a.rows_b != nullptr) {  // explicit rows: bases and weights as given
         if (lane < ks) {
             const int64_t b = a.rows_b[lane];
             sh.rb[lane] = b;
@@ -214,7 +250,6 @@ __device__ __forceinline__ void xc_route(const XcArgs &a, XcShared &sh, const ui
     uint32_t *s_key = sh.u.r.key;
     const int nlog = (routed ? E : 0) + (has_sh ? 1 : 0);
     const int first = routed ? 0 : E;  // the shared gate alone sits at index E
-    bool poisoned = false;
     if (nlog > 0) {
         const int epl = (nlog + 63) >> 6;
         uint32_t need = 0;
@@ -254,32 +289,19 @@ __device__ __forceinline__ void xc_route(const XcArgs &a, XcShared &sh, const ui
         if (routed)
             for (int c = E + lane; c < ((E + 63) & ~63) + 64; c += 64) s_key[c] = 0u;
     }
+    xc_stamp_r(a, sh, 2);
     __builtin_amdgcn_wave_barrier();
-    int myc = 0;
-    float myw = 0.f, myp = 0.f;
     if (routed) {
-        float myv = 0.f;
         if (E <= 64) {
-            // one logit per lane; its rank is the number of larger keys (16-bit keys are distinct)
-            const uint32_t key = lane < E ? s_key[lane] : 0u;
-            const float lvv = lane < E ? s_lv[lane] : -INFINITY;
-            int rank = 0;
-#pragma unroll
-            for (int q0 = 0; q0 < 64; q0 += 4) {
-                const uint4 o = *reinterpret_cast<const uint4 *>(s_key + q0);
-                rank += (o.x > key) + (o.y > key) + (o.z > key) + (o.w > key);
+            // one key per lane: k rounds of a wave maximum, the winner's key cleared after each
+            // (keys are distinct: the expert index is part of the key)
+            uint32_t key = lane < E ? s_key[lane] : 0u;
+            for (int r = 0; r < k; ++r) {
+                const uint32_t M = wave_max_u32(key);
+                const int c = min(1023 - (int)(M & 1023u), E - 1);
+                if (lane == c) key = 0u;
+                if (lane == r) myc = c;
             }
-            __builtin_amdgcn_wave_barrier();
-            if (lane < E && rank < k) {
-                s_key[XC_MAXE + rank] = (uint32_t)lane;
-                sh.sorted[rank] = lvv;
-            }
-            __builtin_amdgcn_wave_barrier();
-            if (lane < k) {
-                myc = (int)s_key[XC_MAXE + lane];
-                myv = sh.sorted[lane];
-            }
-            __builtin_amdgcn_wave_barrier();
         } else {
             const int epl = (E + 63) >> 6;
             for (int r = 0; r < k; ++r) {
@@ -291,17 +313,42 @@ __device__ __forceinline__ void xc_route(const XcArgs &a, XcShared &sh, const ui
                 }
                 const uint32_t M = wave_max_u32(lb);
                 const int c = min(1023 - (int)(M & 1023u), E - 1);
-                const float v = s_lv[c];
                 __builtin_amdgcn_wave_barrier();
                 if (lane == (c & 63)) s_key[c] = 0u;
                 __builtin_amdgcn_wave_barrier();
-                if (lane == r) {
-                    myc = c;
-                    myv = v;
-                }
+                if (lane == r) myc = c;
             }
         }
-        // softmax over the E logits (fp32), the top-k weights, renormalised when asked
+        if (lane < k) myv = s_lv[myc];
+    } else if (lane < k) {
+        myc = (int)idx_pre;
+    }
+    xc_stamp_r(a, sh, 3);
+    const bool act = lane < k, shr = has_sh && lane == k;
+    int64_t base = 0;
+    if (act && myc >= 0 && myc < E) base = sh.u.r.rt[myc];
+    if (shr) base = a.srec;
+    if (lane < ks) {
+        sh.rb[lane] = a.planned ? base : 0;
+        sh.idx[lane] = myc;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// routing, part 2, by wave 0 of the up items while their weights load: softmax over the E logits
+// (fp32), the top-k weights (renormalised when asked), the HOBBIT levels and skips (the shared
+// row: level 0, never skipped, weight sigmoid(shared gate logit)); sh.rw[j] = the weight of table
+// row j, 0 for a row that does not run; the report's indices, weights, levels and choices.
+// ---------------------------------------------------------------------------------------
+template <int XDT>
+__device__ __forceinline__ void xc_weigh(const XcArgs &a, XcShared &sh, int myc, float myv, bool poisoned, float w_pre) {
+    if (a.rows_b != nullptr) return;
+    const int lane = threadIdx.x & 63;
+    const int k = a.k, E = a.E, ks = a.ks;
+    const bool has_sh = a.sgate != nullptr;
+    const float *s_lv = sh.u.r.lv;
+    float myw = 0.f, myp = 0.f;
+    if (a.Wr != nullptr) {
         const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(myv), 0));
         float sum = 0.f;
         for (int c = lane; c < E; c += 64) sum += expf(s_lv[c] - m);
@@ -313,31 +360,23 @@ __device__ __forceinline__ void xc_route(const XcArgs &a, XcShared &sh, const ui
             myw = poisoned ? __uint_as_float(0x7fc00000u) : rnd_act<XDT>(myp);
         }
     } else if (lane < k) {
-        myc = (int)idx_pre;
         myw = w_pre;
     }
-    // HOBBIT levels and skip of the routed rows; the shared row is level 0, never skipped
+    xc_stamp_r(a, sh, 4);
     const bool act = lane < k, shr = has_sh && lane == k;
     int lvl;
     bool skip;
     slot_level(lane, k, act ? myw : 0.f, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true);
     if (shr) lvl = 0, skip = false;
-    int64_t base = 0;
-    float wt = 0.f;
-    if (act && myc >= 0 && myc < E) base = sh.u.r.rt[myc];
+    xc_stamp_r(a, sh, 5);
+    float wt = myw;
     if (shr) {
-        base = a.srec;
         const float l = s_lv[E];
         wt = l != l ? l : rnd_act<XDT>(1.0f / (1.0f + expf(-l)));
-    } else {
-        wt = myw;
     }
-    const bool usable = base != 0 && a.planned;
-    const bool sel = (act || shr) && !skip && usable;
     if (lane < ks) {
-        sh.rb[lane] = sel ? base : 0;
-        sh.rw[lane] = sel ? wt : 0.f;
-        sh.idx[lane] = myc;
+        const bool usable = sh.rb[lane] != 0;
+        sh.rw[lane] = (act || shr) && !skip && usable ? wt : 0.f;
         sh.w[lane] = myp;  // (slot_level is done with sh.w)
         sh.lvl[lane] = lvl;
         sh.chosen[lane] = skip ? -2 : (usable ? 0 : -1);
@@ -376,72 +415,132 @@ __device__ __forceinline__ void xc_report(const XcArgs &a, XcShared &sh) {
 
 // ---------------------------------------------------------------------------------------
 // up item: h values [f0, f0 + hpi) of the flattened table rows (one row j), written weighted by
-// the row's routed weight into the XCD's h area at local index f - seg0
+// the row's routed weight into the XCD's h area at local index f - seg0. Two steps: the loads
+// (x raw, every weight and scale: no load waits on another one's result), issued as soon as the
+// row's record is known, then, once routing part 2 has weighed the row, the dot products.
 // ---------------------------------------------------------------------------------------
+template <int PREC>
+struct XcX {
+    uint4 r[DlFmt<PREC>::CPL][DlFmt<PREC>::VPC / 8 > 0 ? DlFmt<PREC>::VPC / 8 : 1];
+};
+template <int PREC>
+struct XcUp {
+    uint4 qg[DlFmt<PREC>::NPU][DlFmt<PREC>::CPL], qu[DlFmt<PREC>::NPU][DlFmt<PREC>::CPL];
+    uint32_t sg[DlFmt<PREC>::NPU][DlFmt<PREC>::CPL], su[DlFmt<PREC>::NPU][DlFmt<PREC>::CPL];
+    uint32_t okm;  // chunk (p, i) inside the row: bit p * CPL + i
+};
+
+// the item's h values as zeros (a row that does not run), so the down items never wait
+template <int PREC>
+__device__ __forceinline__ void xc_up_zero(const XcArgs &a, int f0, int seg0, uint64_t *hx, uint32_t tag) {
+    constexpr int NPU = DlFmt<PREC>::NPU;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lg = a.lg_up, G = 1 << lg, RPW = 64 >> lg;
+    const int slot = lane >> lg, cl = lane & (G - 1);
+    const int I = a.I, j = f0 / I, i0 = f0 % I;
+    const int pair0 = i0 + wave * NPU * RPW;
+    if (cl == G - 1)
+#pragma unroll
+        for (int p = 0; p < NPU; ++p) {
+            const int r = pair0 + p * RPW + slot;
+            if (r < i0 + a.hpi) st_local(hx + (j * I + r - seg0), 0u, tag);
+        }
+}
+
+// the lane's x chunks of a gate/up row (raw), loaded at the start of the launch with the router's
+template <int PREC>
+__device__ __forceinline__ void xc_up_x(const XcArgs &a, XcX<PREC> &xr) {
+    constexpr int CPL = DlFmt<PREC>::CPL, VPC = DlFmt<PREC>::VPC;
+    const int lane = threadIdx.x & 63;
+    const int G = 1 << a.lg_up, cl = lane & (G - 1);
+    const int C = a.H / VPC;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+        const int c = min(cl + i * G, C - 1);
+        const uint4 *src = reinterpret_cast<const uint4 *>(a.x) + (size_t)c * (VPC / 8);
+#pragma unroll
+        for (int m = 0; m < VPC / 8; ++m) xr.r[i][m] = src[m];
+    }
+}
+
+// step 1: false (after writing the zeros) when row j has no record
 template <int PREC, int XDT>
-__device__ __forceinline__ void xc_up(const XcArgs &a, XcShared &sh, int f0, int seg0, uint64_t *hx, uint32_t tag) {
+__device__ __forceinline__ bool xc_up_issue(const XcArgs &a, const XcShared &sh, int f0, int seg0, uint64_t *hx,
+                                            uint32_t tag, XcUp<PREC> &u) {
     constexpr int CPL = DlFmt<PREC>::CPL, NPU = DlFmt<PREC>::NPU, VPC = DlFmt<PREC>::VPC;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lg = a.lg_up, G = 1 << lg, RPW = 64 >> lg;
     const int slot = lane >> lg, cl = lane & (G - 1);
     const int I = a.I, H = a.H;
     const int j = f0 / I, i0 = f0 % I;
-    const int per_wave = NPU * RPW;
-    const int pair0 = i0 + wave * per_wave;
-    const float wj = sh.rw[j];
-    const int64_t base = sh.rb[j];
-    if (base == 0 || wj == 0.f) {  // a row that does not run: zeros, so the down items never wait
-        if (cl == G - 1)
-#pragma unroll
-            for (int p = 0; p < NPU; ++p) {
-                const int r = pair0 + p * RPW + slot;
-                if (r < i0 + a.hpi) st_local(hx + (j * I + r - seg0), 0u, tag);
-            }
-        return;
+    const int pair0 = i0 + wave * NPU * RPW;
+    const int64_t base = uni64(sh.rb[j]);  // (j is the same for the whole workgroup)
+    if (base == 0) {
+        xc_up_zero<PREC>(a, f0, seg0, hx, tag);
+        return false;
     }
+    // uniform bases, 32-bit lane offsets stepped row by row (no 64-bit products per load)
     gbyte *qb = gbytes(base + a.off_gq);
     gbyte *sb = gbytes(base + a.off_gs);
     const int C = H / VPC;
-    const size_t RB = (size_t)C * 16;
-    // x first (raw), then every weight and scale load, and only then the lane vector: no load
-    // waits on another one's result before all of them are in flight
-    uint4 xr[CPL][VPC / 8 > 0 ? VPC / 8 : 1];
+    const uint32_t RB = (uint32_t)C * 16;
+    const uint32_t step = (uint32_t)RPW * RB, upo = (uint32_t)I * RB;
+    const int ng = sc_cols<PREC>(H, a.gs_up);
+    const int r0 = pair0 + slot;  // row of pass 0 (within the item: hpi divides the unit)
+    u.okm = 0;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-        const int c = min(cl + i * G, C - 1);
-        const uint4 *src = reinterpret_cast<const uint4 *>(a.x) + (size_t)c * (VPC / 8);
+        const int c0 = cl + i * G;
+        const int c = min(c0, C - 1);
+        const uint32_t qo = __umul24(r0, RB) + (uint32_t)c * 16;
+        const int cg = sc_col<PREC>(c, a.gs_up);
 #pragma unroll
-        for (int m = 0; m < VPC / 8; ++m) xr[i][m] = src[m];
-    }
-    uint4 qg[NPU][CPL], qu[NPU][CPL];
-    uint32_t sg[NPU][CPL], su[NPU][CPL];
-    uint32_t okm = 0;  // chunk (p, i) inside the row: bit p * CPL + i
-#pragma unroll
-    for (int p = 0; p < NPU; ++p) {
-        const int r = pair0 + p * RPW + slot;  // within the item (hpi divides the unit)
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int c0 = cl + i * G;
-            const int c = min(c0, C - 1);
-            okm |= (c0 < C ? 1u : 0u) << (p * CPL + i);
-            qg[p][i] = gld16_nt(qb + (size_t)r * RB + (size_t)c * 16);
-            qu[p][i] = gld16_nt(qb + (size_t)(r + I) * RB + (size_t)c * 16);
-            sg[p][i] = scale_bits<PREC>(sb, r, c, H, a.gs_up);
-            su[p][i] = scale_bits<PREC>(sb, r + I, c, H, a.gs_up);
+        for (int p = 0; p < NPU; ++p) {
+            u.okm |= (c0 < C ? 1u : 0u) << (p * CPL + i);
+            u.qg[p][i] = gld16_nt(qb + (qo + p * step));
+            u.qu[p][i] = gld16_nt(qb + (qo + upo + p * step));
+            u.sg[p][i] = sc_load<PREC>(sb, sc_off<PREC>(r0 + p * RPW, cg, ng));
+            u.su[p][i] = sc_load<PREC>(sb, sc_off<PREC>(r0 + p * RPW + I, cg, ng));
         }
     }
+    return true;
+}
+
+// step 2: h = w * silu(gate x) * (up x); zeros when routing part 2 gave the row weight 0 (skipped)
+template <int PREC, int XDT>
+__device__ __forceinline__ void xc_up_finish(const XcArgs &a, XcShared &sh, int f0, int seg0, uint64_t *hx,
+                                             uint32_t tag, const XcUp<PREC> &u, const XcX<PREC> &xr) {
+    constexpr int CPL = DlFmt<PREC>::CPL, NPU = DlFmt<PREC>::NPU;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lg = a.lg_up, G = 1 << lg, RPW = 64 >> lg;
+    const int slot = lane >> lg, cl = lane & (G - 1);
+    const int I = a.I, j = f0 / I, i0 = f0 % I;
+    const int pair0 = i0 + wave * NPU * RPW;
+    const float wj = sh.rw[j];
+    if (wj == 0.f) {
+        xc_up_zero<PREC>(a, f0, seg0, hx, tag);
+        return;
+    }
+    // the loaded scales pass through opaque steps here, so that no conversion of them is moved
+    // before routing part 2 (which would wait for the loads there)
+    XcUp<PREC> w = u;
+#pragma unroll
+    for (int p = 0; p < NPU; ++p)
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) asm volatile("" : "+v"(w.sg[p][i]), "+v"(w.su[p][i]));
     LaneVec<PREC, XDT> lv;
-    prep_x<PREC, XDT>(xr, lv);
+    prep_x<PREC, XDT>(xr.r, lv);
+    xc_stamp(a, sh, 8);
     float v[2 * NPU];
 #pragma unroll
     for (int p = 0; p < NPU; ++p) {
         float pg = 0.f, pu = 0.f;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            const bool ok = (okm >> (p * CPL + i)) & 1u;
-            const float s0 = ok ? scale_val<PREC>(sg[p][i]) : 0.f, s1 = ok ? scale_val<PREC>(su[p][i]) : 0.f;
-            pg = fmaf(s0 * lv.p2e[i], lane_dot<PREC, XDT>(qg[p][i], lv, i), pg);
-            pu = fmaf(s1 * lv.p2e[i], lane_dot<PREC, XDT>(qu[p][i], lv, i), pu);
+            const bool ok = (w.okm >> (p * CPL + i)) & 1u;
+            const float s0 = ok ? scale_val<PREC>(w.sg[p][i]) : 0.f, s1 = ok ? scale_val<PREC>(w.su[p][i]) : 0.f;
+            pg = fmaf(s0 * lv.p2e[i], lane_dot<PREC, XDT>(w.qg[p][i], lv, i), pg);
+            pu = fmaf(s1 * lv.p2e[i], lane_dot<PREC, XDT>(w.qu[p][i], lv, i), pu);
         }
         v[2 * p] = pg;
         v[2 * p + 1] = pu;
@@ -451,7 +550,7 @@ __device__ __forceinline__ void xc_up(const XcArgs &a, XcShared &sh, int f0, int
 #pragma unroll
         for (int p = 0; p < NPU; ++p) {
             const int r = pair0 + p * RPW + slot;
-            st_local(hx + (j * I + r - seg0), __float_as_uint(wj * silu_mul(v[2 * p], v[2 * p + 1])), tag);
+            st_local(hx + (j * I + r - seg0), __float_as_uint(wj * silu_mul_fast(v[2 * p], v[2 * p + 1])), tag);
         }
     }
 }
@@ -462,39 +561,43 @@ __device__ __forceinline__ void xc_up(const XcArgs &a, XcShared &sh, int f0, int
 // ---------------------------------------------------------------------------------------
 template <int PREC>
 struct XcDown {
-    uint4 q[DlFmt<PREC>::NPD][DlFmt<PREC>::CPL];
-    uint32_t s[DlFmt<PREC>::NPD][DlFmt<PREC>::CPL];
+    uint4 q[XcFmt<PREC>::NPD][DlFmt<PREC>::CPL];
+    uint32_t s[XcFmt<PREC>::NPD][DlFmt<PREC>::CPL];
     uint32_t ok;  // bit p * CPL + i: chunk (p, i) counts (the others multiply by scale 0)
 };
 
 template <int PREC>
 __device__ __forceinline__ void xc_down_load(const XcArgs &a, const XcShared &sh, int row0, int seg0, int nch,
-                                             XcDown<PREC> &d) {
-    constexpr int CPL = DlFmt<PREC>::CPL, NPD = DlFmt<PREC>::NPD, VPC = DlFmt<PREC>::VPC;
+                                             bool on, XcDown<PREC> &d) {
+    constexpr int CPL = DlFmt<PREC>::CPL, NPD = XcFmt<PREC>::NPD, VPC = DlFmt<PREC>::VPC;
     const int lane = threadIdx.x & 63;
     const int lg = a.lg_dn, G = 1 << lg, RPW = 64 >> lg;
     const int slot = lane >> lg, cl = lane & (G - 1);
     const int I = a.I, H = a.H;
-    const size_t RB = (size_t)(I / VPC) * 16;  // bytes of one down row
+    const uint32_t RB = (uint32_t)(I / VPC) * 16;  // bytes of one down row
+    const int ng = sc_cols<PREC>(I, a.gs_dn);
     d.ok = 0;
 #pragma unroll
-    for (int p = 0; p < NPD; ++p) {
-        const int r0 = row0 + p * RPW + slot;
-        const int r = min(r0, H - 1);
+    for (int i = 0; i < CPL; ++i) {
+        // the chunk's table row j and column: one base per chunk, 32-bit offsets row by row
+        const int c0 = cl + i * G;
+        const int c = min(c0, max(nch - 1, 0));
+        const int f = seg0 + c * VPC;  // flattened h index of the chunk's first value
+        const int j = min(f / I, a.ks - 1), col = f - j * I;
+        const int64_t base = nch > 0 && on ? sh.rb[j] : 0;
+        // rows without a record (and a workgroup without a down part) read the activation vector
+        // (in bounds) at offset 0, scale 0
+        gbyte *qb = base != 0 ? gbytes(base + a.off_dq) : gbytes(a.x);
+        gbyte *sb = base != 0 ? gbytes(base + a.off_ds) : gbytes(a.x);
+        const uint32_t co = base != 0 ? (uint32_t)(col / VPC) * 16 : 0u;
+        const int cg = sc_col<PREC>(col / VPC, a.gs_dn);
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-            const int c0 = cl + i * G;
-            const int c = min(c0, max(nch - 1, 0));
-            const int f = seg0 + c * VPC;  // flattened h index of the chunk's first value
-            const int j = min(f / I, a.ks - 1), col = f - j * I;
-            const int64_t base = nch > 0 ? sh.rb[j] : 0;
+        for (int p = 0; p < NPD; ++p) {
+            const int r0 = row0 + p * RPW + slot;
+            const int r = min(r0, H - 1);
             const bool ok = c0 < nch && r0 < H && base != 0;
-            // rows without a record read the activation vector instead (in bounds) at scale 0
-            gbyte *qp = base != 0 ? gbytes(base + a.off_dq) + (size_t)r * RB + (size_t)(col / VPC) * 16 : gbytes(a.x);
-            d.q[p][i] = gld16_nt(qp);
-            // (the scale of a row without a record is read from x too; the bit drops it)
-            d.s[p][i] = scale_bits<PREC>(base != 0 ? gbytes(base + a.off_ds) : gbytes(a.x), base != 0 ? r : 0,
-                                         base != 0 ? col / VPC : 0, I, a.gs_dn);
+            d.q[p][i] = gld16_nt(qb + (base != 0 ? __umul24(r, RB) + co : 0u));
+            d.s[p][i] = sc_load<PREC>(sb, base != 0 ? sc_off<PREC>(r, cg, ng) : 0u);
             d.ok |= (ok ? 1u : 0u) << (p * CPL + i);
         }
     }
@@ -503,8 +606,8 @@ __device__ __forceinline__ void xc_down_load(const XcArgs &a, const XcShared &sh
 // the down rows' partial sums (valid in the last lane of each lane group)
 template <int PREC, int XDT>
 __device__ __forceinline__ void xc_down_rows(const XcArgs &a, const XcDown<PREC> &d, const LaneVec<PREC, XDT> &lv,
-                                             float (&v)[DlFmt<PREC>::NPD]) {
-    constexpr int CPL = DlFmt<PREC>::CPL, NPD = DlFmt<PREC>::NPD;
+                                             float (&v)[XcFmt<PREC>::NPD]) {
+    constexpr int CPL = DlFmt<PREC>::CPL, NPD = XcFmt<PREC>::NPD;
 #pragma unroll
     for (int p = 0; p < NPD; ++p) {
         float acc = 0.f;
@@ -524,76 +627,99 @@ __device__ __forceinline__ void xc_down_rows(const XcArgs &a, const XcDown<PREC>
 template <int XDT, int PREC>
 __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     __shared__ XcShared sh;
-    constexpr int VPC = DlFmt<PREC>::VPC, NPD = DlFmt<PREC>::NPD;
+    constexpr int VPC = DlFmt<PREC>::VPC, NPD = XcFmt<PREC>::NPD;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int b = blockIdx.x, x = b % XC_N, q = b / XC_N, NQ = gridDim.x / XC_N;
     uint8_t *wsb = reinterpret_cast<uint8_t *>(a.ws);
     uint64_t *lg = reinterpret_cast<uint64_t *>(wsb + a.off_lg) + (size_t)x * a.lg_stride;
     uint64_t *hx = reinterpret_cast<uint64_t *>(wsb + a.off_h) + (size_t)x * a.h_stride;
     uint64_t *part = reinterpret_cast<uint64_t *>(wsb + a.off_part);
+    if (a.trace != nullptr && tid == 0)
+        for (int i = 0; i < XC_NST; ++i) sh.st[i] = 0;
     xc_stamp(a, sh, 0);
-    // the launch tag, read by every wave (one of 16 copies; never 0), used from the first store on
-    const uint32_t tag = (uint32_t)uni((int)(ld_co32(a.ws + XC_GEN + 256 * (b % XC_NGEN)) + 1u));
-    if (tid == 0) sh.poison = 0;
-    // the record table into LDS (the k chosen records are looked up after the routing)
-    const bool routed = a.Wr != nullptr;
-    if (a.rows_b == nullptr)
-        for (int e = tid; e < a.E; e += 256) sh.u.r.rt[e] = a.rtab[e];
+    // every independent load first: the launch tag (one of 16 copies; never 0), the layer's record
+    // table, the given routing, x for the up part; the router rows' x and weights follow; nothing
+    // waits before these are all in flight
+    const uint32_t gen = ld_co32(a.ws + XC_GEN + 256 * (b % XC_NGEN));
+    const bool routed = a.Wr != nullptr, tab = a.rows_b == nullptr;
+    int64_t rtv[XC_MAXE / 256];
+#pragma unroll
+    for (int i = 0; i < XC_MAXE / 256; ++i) {
+        const int e = tid + 256 * i;
+        rtv[i] = tab && e < a.E ? a.rtab[e] : 0;
+    }
+    const bool is_up = q < a.nu;
+    XcX<PREC> xr;
+    if (is_up) xc_up_x<PREC>(a, xr);
     int64_t idx_pre = 0;
     float w_pre = 0.f;
-    if (!routed && a.rows_b == nullptr && tid < a.k) {
-        idx_pre = a.idx_in[tid];
-        w_pre = a.w32_in[tid];
+    if (!routed && tab && lane < a.k) {  // (lane: any wave may be the routing wave)
+        idx_pre = a.idx_in[lane];
+        w_pre = a.w32_in[lane];
     }
-    // 1. router rows of this XCD (logits, shared gate), then the routing (wave 0)
-    const int nrows = a.rows_b != nullptr ? 0 : (routed ? a.E : 0) + (a.sgate != nullptr ? 1 : 0);
-    if (nrows > 0) xc_router<XDT>(a, q, NQ, routed ? 0 : a.E, nrows, lg, tag);
-    if (tag != 0u) xc_gen_read(a.ws);  // (after the tag has arrived)
+    // 1. router rows of this XCD (logits, shared gate), then the routing, by one wave chosen by
+    //    workgroup: the workgroups q, q + 32, q + 64 of an XCD usually share a CU, and route on
+    //    different SIMDs
+    const int nrows = tab ? (routed ? a.E : 0) + (a.sgate != nullptr ? 1 : 0) : 0;
+    if (nrows > 0) xc_router<XDT>(a, q, NQ, routed ? 0 : a.E, nrows, lg, gen);
+#pragma unroll
+    for (int i = 0; i < XC_MAXE / 256; ++i) {
+        const int e = tid + 256 * i;
+        if (tab && e < a.E) sh.u.r.rt[e] = rtv[i];
+    }
+    const uint32_t tag = (uint32_t)uni((int)xc_tag_of(gen));
     xc_stamp(a, sh, 1);
     const int seg0u = xc_seg_begin(x, a.units), seg1u = xc_seg_begin(x + 1, a.units);
     const int seg0 = seg0u * a.unit, seg_len = (seg1u - seg0u) * a.unit;
-    const bool is_up = q < a.nu;
     const int f0 = seg0 + q * a.hpi;
     const bool up_work = is_up && q * a.hpi < seg_len;
-    xc_stamp(a, sh, 2);
+    const int rwave = (q ^ (q >> 5)) & 3;
     __syncthreads();  // the record table is in LDS
-    if (wave == 0) xc_route<XDT>(a, sh, lg, tag, idx_pre, w_pre);
+    int myc = 0;
+    float myv = 0.f;
+    bool poisoned = false;
+    if (wave == rwave) xc_rank<XDT>(a, sh, lg, tag, idx_pre, myc, myv, poisoned);
     __syncthreads();
-    xc_stamp(a, sh, 3);
+    xc_stamp(a, sh, 6);
     if (is_up) {
-        // 2. h of this item's rows (x is requested with the weights: it arrives no later)
-        if (up_work) xc_up<PREC, XDT>(a, sh, f0, seg0, hx, tag);
-        xc_stamp(a, sh, 5);
+        // 2. h of this item's rows: the loads, routing part 2 meanwhile, then the products
+        XcUp<PREC> u;
+        const bool run = up_work && xc_up_issue<PREC, XDT>(a, sh, f0, seg0, hx, tag, u);
+        xc_stamp(a, sh, 7);
+        if (wave == rwave) xc_weigh<XDT>(a, sh, myc, myv, poisoned, w_pre);
+        __syncthreads();
+        if (run) xc_up_finish<PREC, XDT>(a, sh, f0, seg0, hx, tag, u, xr);
+        if (tag != 0u) xc_gen_read(a.ws);  // (counted once this item's loads are all used)
+        xc_stamp(a, sh, 9);
     } else {
-        // 3. the down rows over the segment
+        // 3. the down rows over the segment: their weights (after the gate/up weights' head start),
+        //    the segment's h -> LDS (piece-major: piece m of chunk c at (m * C + c) * 4), the products
         const int d = q - a.nu;
         const int lgd = a.lg_dn, G = 1 << lgd, RPW = 64 >> lgd;
-        const int per_wave = NPD * RPW;
-        const int row0 = d * a.dr + wave * per_wave;
+        const int row0 = d * a.dr + wave * NPD * RPW;
         const int nch = seg_len / VPC;
-        {  // the gate/up weights first: they are needed before these can be used
+        if (a.defer != 0u) {
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             const uint32_t defer = (uint32_t)uni((int)a.defer);
             while (__builtin_amdgcn_s_memrealtime() - t0 < defer) __builtin_amdgcn_s_sleep(8);
         }
         XcDown<PREC> dd;
-        xc_down_load<PREC>(a, sh, row0, seg0, nch, dd);
-        xc_stamp(a, sh, 4);
-        // h of the segment -> LDS (piece-major: piece m of chunk c at (m * C + c) * 4)
+        xc_down_load<PREC>(a, sh, row0, seg0, nch, true, dd);
+        if (tag != 0u) xc_gen_read(a.ws);
+        xc_stamp(a, sh, 8);
         float *s_h = sh.u.h;
         const int C = nch > 0 ? nch : 1;
         bool h_ok = true;
         for (int w0 = 0; w0 < seg_len; w0 += 256 * 8) {
+            // two rounds of 8 words in flight (every round loads all 8, at clamped indices, so the
+            // wait for the older round is exact)
             uint32_t need = 0;
 #pragma unroll
             for (int m = 0; m < 8; ++m)
                 if (w0 + tid + 256 * m < seg_len) need |= 1u << m;
-            int nap = 1;
-            for (int it = 0; it < XC_SPIN; ++it) {
-                uint64_t v[8];
-#pragma unroll
-                for (int m = 0; m < 8; ++m)
-                    if (need & (1u << m)) v[m] = ld_local(hx + w0 + tid + 256 * m);
+            const uint64_t *hs = hx + w0 + tid;
+            const int lim = seg_len - 1 - w0 - tid;  // (index of the last word, relative)
+            auto take = [&](const uint64_t (&v)[8]) {
 #pragma unroll
                 for (int m = 0; m < 8; ++m) {
                     if ((need & (1u << m)) && tag_ok(v[m], tag)) {
@@ -603,14 +729,28 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
                         need &= ~(1u << m);
                     }
                 }
+            };
+            uint64_t va[8], vb[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+            int it = 0;
+            for (; it < XC_SPIN; it += 2) {
+#pragma unroll
+                for (int m = 0; m < 8; ++m) vb[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+                take(va);
                 if (!__syncthreads_or(need != 0)) break;
-                backoff(nap, 2);
-                if (it == XC_SPIN - 1) {
-                    h_ok = false;
-                    if (tid == 0) flag_error(a.ws + XC_ERR);
-                }
+#pragma unroll
+                for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+                take(vb);
+                if (!__syncthreads_or(need != 0)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (it >= XC_SPIN) {
+                h_ok = false;
+                if (tid == 0) flag_error(a.ws + XC_ERR);
             }
         }
+        xc_stamp(a, sh, 10);
         LaneVec<PREC, XDT> lh;
         load_h<PREC, XDT>(s_h, lane & (G - 1), G, C, lh);
         float v[NPD];
@@ -618,7 +758,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
         if (!h_ok)
 #pragma unroll
             for (int p = 0; p < NPD; ++p) v[p] = __uint_as_float(0x7fc00000u);
-        xc_stamp(a, sh, 5);
+        xc_stamp(a, sh, 11);
         // 4. the partial rows: the combiner of this row block keeps its own, the others send theirs
         const bool combiner = (d % XC_N) == x;
         const int cl = lane & (G - 1), slot = lane >> lgd;
@@ -636,26 +776,37 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
             __syncthreads();
             const int r0 = d * a.dr, nrow = min(a.dr, a.H - r0);
             for (int rr = tid; rr < nrow; rr += 256) {
+                // two rounds of the 8 words in flight at once (each round loads all 8, so the
+                // compiler's wait for the older round is exact): a new round every poll, not every
+                // round trip
+                const uint64_t *src = part + r0 + rr;
                 float val[XC_N];
-                uint32_t need = 0;
+                uint32_t need = 0xFFu & ~(1u << x);
+                val[x] = sh.part[rr];
+                uint64_t wa[XC_N], wb[XC_N];
 #pragma unroll
-                for (int xx = 0; xx < XC_N; ++xx) {
-                    if (xx == x) val[xx] = sh.part[rr];
-                    else need |= 1u << xx;
-                }
-                int nap = 1;
-                for (int it = 0; it < XC_SPIN && need != 0; ++it) {
-                    uint64_t w8[XC_N];
+                for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
+                for (int it = 0; it < XC_SPIN; it += 2) {
 #pragma unroll
-                    for (int xx = 0; xx < XC_N; ++xx)
-                        if (need & (1u << xx)) w8[xx] = ld_tag(part + (size_t)xx * a.H + r0 + rr);
+                    for (int xx = 0; xx < XC_N; ++xx) wb[xx] = ld_tag(src + (size_t)xx * a.H);
 #pragma unroll
                     for (int xx = 0; xx < XC_N; ++xx)
-                        if ((need & (1u << xx)) && tag_ok(w8[xx], tag)) {
-                            val[xx] = __uint_as_float((uint32_t)w8[xx]);
+                        if ((need & (1u << xx)) && tag_ok(wa[xx], tag)) {
+                            val[xx] = __uint_as_float((uint32_t)wa[xx]);
                             need &= ~(1u << xx);
                         }
-                    if (need != 0) backoff(nap, 2);
+                    if (need == 0) break;
+                    __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                    for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
+#pragma unroll
+                    for (int xx = 0; xx < XC_N; ++xx)
+                        if ((need & (1u << xx)) && tag_ok(wb[xx], tag)) {
+                            val[xx] = __uint_as_float((uint32_t)wb[xx]);
+                            need &= ~(1u << xx);
+                        }
+                    if (need == 0) break;
+                    __builtin_amdgcn_s_sleep(2);
                 }
                 float acc = 0.f;
 #pragma unroll
@@ -666,8 +817,9 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
                 st_act<XDT>(a.out, r0 + rr, acc);
             }
         }
-        xc_stamp(a, sh, 6);
+        xc_stamp(a, sh, 12);
     }
+    xc_stamp(a, sh, 13);
     if (b == 0) {
         __syncthreads();
         xc_report<XDT>(a, sh);
@@ -676,8 +828,8 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     if (a.trace != nullptr) {
         __syncthreads();
         if (tid == 0) {
-            sh.st[7] = __builtin_amdgcn_s_memrealtime();
-            for (int i = 0; i < 8; ++i) a.trace[(size_t)b * 8 + i] = sh.st[i];
+            sh.st[14] = __builtin_amdgcn_s_memrealtime();
+            for (int i = 0; i < XC_NST; ++i) a.trace[(size_t)b * XC_NST + i] = sh.st[i];
         }
     }
 }
@@ -726,7 +878,7 @@ static XcPlan xc_plan(int prec, int ks, int E, int H, int I) {
     XcPlan p{};
     const int vpc = xc_vpc(prec), cpl = xc_cpl(prec);
     if (vpc == 0 || prec == MOEHIP_PREC_F32 || H > 2048 || H % 32 || I % 32 || E > XC_MAXE || ks > XC_MAXKS) return p;
-    const int npu = 4 / cpl, npd = 8 / cpl;
+    const int npu = 4 / cpl, npd = 8 / cpl;  // (XcFmt::NPD)
     p.lg_up = xc_lg(H / vpc, prec);
     p.hpi = npu * (64 >> p.lg_up) * 4;
     p.unit = p.hpi > 32 ? p.hpi : 32;
@@ -739,7 +891,7 @@ static XcPlan xc_plan(int prec, int ks, int E, int H, int I) {
     p.dr = npd * (64 >> p.lg_dn) * 4;
     if (p.dr > XC_MAXDR) return p;
     p.nd = (H + p.dr - 1) / p.dr;
-    p.grid = XC_N * (p.nu + p.nd);
+    p.grid = XC_N * (p.nu + p.nd);  // workgroup q: up item q < nu, else down item q - nu
     // workspace: header, 8 logit copies, 8 h segments, 8 partial rows
     p.lg_stride = (uint32_t)(((size_t)(E + 1) * 8 + 255) / 256 * 32 + 32);
     p.h_stride = (uint32_t)(((size_t)seg_max * 8 + 255) / 256 * 32);
@@ -848,9 +1000,6 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     a.off_part = p.off_part;
     a.lg_stride = p.lg_stride;
     a.h_stride = p.h_stride;
-    // the time the HBM needs for the ks gate/up blocks (q + scales) at 8 TB/s, in 10 ns ticks
-    const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
-    a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8);
     a.E = d->E;
     a.k = d->k;
     a.ks = ks;
@@ -869,6 +1018,11 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     a.lg_up = p.lg_up;
     a.lg_dn = p.lg_dn;
     a.dr = p.dr;
+    // the time the HBM needs for the ks gate/up blocks (q + scales) at 8 TB/s, in 10 ns ticks: the
+    // down items request theirs after it (measured at the OLMoE int4 bs=1 shape: 14.7 us per layer
+    // with it, 15.1 without, 15.0 with half of it)
+    const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
+    a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8);
     hipLaunchKernelGGL(kern, dim3(p.grid), dim3(256), 0, as_stream(stream), a);
     *used = 1;
     return check_launch("decode_layer (xcd)");

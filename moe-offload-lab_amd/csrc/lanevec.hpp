@@ -318,6 +318,32 @@ __device__ __forceinline__ uint32_t scale_bits(gbyte *sb, int row, int c, int co
         return 0x3f800000u;
     }
 }
+// the same scale addressing in three parts, for kernels that step over rows: scale columns per
+// row-group (ng), the chunk's scale column (cg), and the byte offset of (row, cg) from the scale base
+template <int PREC>
+__device__ __forceinline__ int sc_cols(int cols, int gs) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return cols / gs;
+    else if constexpr (PREC == MOEHIP_PREC_FP8) return (cols + 127) >> 7;
+    else return 0;
+}
+template <int PREC>
+__device__ __forceinline__ int sc_col(int c, int gs) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return (c * Fmt<PREC>::VPC) / gs;
+    else if constexpr (PREC == MOEHIP_PREC_FP8) return (c * 16) >> 7;
+    else return 0;
+}
+template <int PREC>
+__device__ __forceinline__ uint32_t sc_off(int row, int cg, int ng) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return 2u * (__umul24(row, ng) + (uint32_t)cg);
+    else if constexpr (PREC == MOEHIP_PREC_FP8) return 4u * (__umul24(row >> 7, ng) + (uint32_t)cg);
+    else return 0u;
+}
+template <int PREC>
+__device__ __forceinline__ uint32_t sc_load(gbyte *sb, uint32_t off) {
+    if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return gld2(sb + off);
+    else if constexpr (PREC == MOEHIP_PREC_FP8) return gld4(sb + off);
+    else return 0x3f800000u;
+}
 template <int PREC>
 __device__ __forceinline__ float scale_val(uint32_t bits) {
     if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8) return f16_to_f32(bits);
