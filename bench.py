@@ -7,8 +7,8 @@ d_model 2048, 64 experts per layer, softmax router top-8 without renormalisation
 1024, router weights and expert weights N(0, 0.02) (experts quantised int4 gs64 absmax on the
 GPU with moelab's packing), fp16 hidden states N(0, 1), one seeded state per (token, layer).
 A step = one decode token through the 16 MoE layers: per layer ONE launch of the fused kernel
-(router -> HOBBIT table -> gate/up rows -> down rows -> ordered combine), replayed as one HIP
-graph per token. 16 x 64 int4
+(router -> routing and HOBBIT decision -> gate/up rows -> down rows -> combine; the XCD-local
+kernel k_decode_xcd), replayed as one HIP graph per token. 16 x 64 int4
 records = 3.42 GB, far above the 256 MB Infinity Cache, and each token routes differently.
 
 Roofline: the dominant (only) kernel is the fused decode-layer kernel, one launch per layer; its
@@ -18,7 +18,7 @@ live with HIP events on the stream it runs on, over launches that rotate through
 layers.
 
 HBM traffic per launch (roofline.traffic) is read from the committed rocprofv3 counter summary
-profiles/k_decode_tok_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
+profiles/k_decode_xcd_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
 same counters on a plain copy of known size, `--copy-calibration`); null when that file is absent.
 
 CPU baseline: the oracle's restatement of moelab's CPU expert branch (dequantise to fp32,
@@ -45,7 +45,7 @@ sys.path.insert(0, str(ROOT / "moe-offload-lab_amd"))
 
 H, I, E, K_TOP, L = 2048, 1024, 64, 8, 16
 HBM_PEAK_GBS = 8000.0
-PROFILE = ROOT / "profiles" / "k_decode_tok_olmoe_int4_bs1.md"
+PROFILE = ROOT / "profiles" / "k_decode_xcd_olmoe_int4_bs1.md"
 
 
 def measured_traffic():
@@ -746,7 +746,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "k_decode_tok<f16, int4> (router + HOBBIT table + 8 int4 experts + combine, one launch)",
+            "kernel": "k_decode_xcd<f16, int4> (router + routing + 8 int4 experts + combine, one launch)",
             "bytes_per_launch": r["kernel_bytes"],
         },
         "cpu_baseline": cpu,
