@@ -225,6 +225,19 @@ int moehip_decode_layer(const moehip_layer_desc *desc, const void *x, const void
                         void *ws, size_t ws_bytes, int grid, uint64_t *trace, void *stream);
 size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H, int I);
 /*
+ * moehip_decode_layer without a workspace argument and without any allocation: the workspace is a
+ * 2 MiB array inside this library, one copy per GPU (found and zero-filled by moehip_device_check,
+ * which must have been called for the current device first), with the automatic kernel choice and
+ * no trace. No counterpart in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, serving loops that forbid hipMalloc). A layer whose workspace
+ * (moehip_decode_layer_workspace_bytes) exceeds 2 MiB is refused with MOEHIP_EINVAL. All calls on
+ * one GPU share its array: calls that overlap on one GPU (two streams at once) race.
+ */
+int moehip_decode_layer_noalloc(const moehip_layer_desc *desc, const void *x, const void *Wr, const int64_t *idx_in,
+                                const float *w32_in, const int64_t *rtab, void *out, const void *add, int accumulate,
+                                void *logits_out, int64_t *idx_out, void *w_out, float *w32_out, float *info,
+                                float *miss, void *stream);
+/*
  * The same layer kernel on explicit table rows, with no routing and no decision: row j of
  * precision p runs record rows_b[p * k + j] (a base address; 0 = unused row) with weight
  * rows_w[p * k + j] (fp32), and out = sum over the rows in table order (+ add) (+ out if

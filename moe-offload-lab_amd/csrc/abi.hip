@@ -45,5 +45,5 @@ extern "C" int moehip_device_check(int dev) {
         return MOEHIP_ENODEV;
     }
     moehip::xcd_probe(dev);  // whether the XCD-local decode kernel may run on this device
-    return MOEHIP_OK;
+    return moehip::noalloc_init(dev);  // this device's copy of moehip_decode_layer_noalloc's scratch array
 }

@@ -28,6 +28,7 @@ static inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream
 // by moehip_device_check), its workspace size (0 = the layer does not fit it) and its launch
 // (*used = 0 when the layer does not fit it or the device was not confirmed)
 int xcd_probe(int dev);
+int noalloc_init(int dev);
 size_t xcd_workspace_bytes(int prec, int ks, int E, int H, int I);
 int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in, const float *w32_in,
                const int64_t *rows_b, const float *rows_w, const int64_t *rtab, void *out, const void *add,

@@ -66,6 +66,8 @@ _SIGS = {
     "moehip_decode_layer": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                              _vp, _vp, _vp, ctypes.c_size_t, _i, _vp, _vp], _i),
     "moehip_decode_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
+    "moehip_decode_layer_noalloc": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _vp], _i),
     "moehip_decode_layer_work_items": ([ctypes.POINTER(LayerDesc), _i], _i),
     "moehip_decode_rows": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp], _i),
     "moehip_decode_rows_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
