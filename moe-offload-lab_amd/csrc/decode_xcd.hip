@@ -42,7 +42,14 @@ constexpr int XC_N = 8;            // XCDs
 constexpr int XC_SPIN = 1 << 21;   // polls before a wait gives up (~1 s)
 constexpr int XC_NGEN = 16;        // header as in decode_layer.hip: reader counters, error flag,
 constexpr int XC_NSUB = 16;        // drained count, generation copies 1 KB apart
-enum { XC_READ = 0, XC_ERR = XC_NSUB * 32, XC_TOP = XC_NSUB * 32 + 32, XC_GEN = 1024, XC_HDR = XC_GEN + 256 * XC_NGEN };
+enum { XC_READ = 0, XC_ERR = XC_NSUB * 32, XC_TOP = XC_NSUB * 32 + 32, XC_TEST = XC_NSUB * 32 + 64, XC_GEN = 1024,
+       XC_HDR = XC_GEN + 256 * XC_NGEN };
+// XC_TEST: a word the library never writes (zero from the workspace's first zero-fill). When a test
+// sets it, the data waits of every later launch on that workspace give up after XC_TEST_SPIN polls and
+// the logits are polled for a tag that is never written: an expired wait, forced from the host, in a
+// launch whose every workgroup still exits normally (the generation's own counting keeps its full
+// bound, so the launch after the test word is cleared runs normally).
+constexpr int XC_TEST_SPIN = 8;
 constexpr int XC_MAXE = 1024;
 constexpr int XC_MAXKS = 33;
 constexpr int XC_LDS_H = 8192;     // h values of one XCD's segment staged in LDS (fp32)
@@ -229,7 +236,7 @@ __device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int fi
 // base 0 and never runs; a row that part 2 skips runs with weight 0.
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag,
+__device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag, int spin,
                                         int64_t idx_pre, int &myc, float &myv, bool &poisoned) {
     const int lane = threadIdx.x & 63;
     const int k = a.k, E = a.E, ks = a.ks;
@@ -256,7 +263,7 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
         for (int i = 0; i < epl; ++i)
             if (lane + 64 * i < nlog) need |= 1u << i;
         int nap = 1;
-        for (int it = 0; it < XC_SPIN && __ballot(need != 0) != 0ull; ++it) {
+        for (int it = 0; it < spin && __ballot(need != 0) != 0ull; ++it) {
             for (int i0 = 0; i0 < epl; i0 += 4) {  // up to 4 words per lane in flight at a time
                 uint64_t v[4];
 #pragma unroll
@@ -641,6 +648,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     // table, the given routing, x for the up part; the router rows' x and weights follow; nothing
     // waits before these are all in flight
     const uint32_t gen = ld_co32(a.ws + XC_GEN + 256 * (b % XC_NGEN));
+    uint32_t test = ld_co32(a.ws + XC_TEST);
     const bool routed = a.Wr != nullptr, tab = a.rows_b == nullptr;
     int64_t rtv[XC_MAXE / 256];
 #pragma unroll
@@ -678,7 +686,10 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     int myc = 0;
     float myv = 0.f;
     bool poisoned = false;
-    if (wave == rwave) xc_rank<XDT>(a, sh, lg, tag, idx_pre, myc, myv, poisoned);
+    asm volatile("" : "+v"(test));  // (read here, long after its load was issued)
+    const bool forced = uni((int)test) != 0;
+    const int spin = forced ? XC_TEST_SPIN : XC_SPIN;
+    if (wave == rwave) xc_rank<XDT>(a, sh, lg, forced ? tag + 0x40000000u : tag, spin, idx_pre, myc, myv, poisoned);
     __syncthreads();
     xc_stamp(a, sh, 6);
     if (is_up) {
@@ -734,7 +745,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
 #pragma unroll
             for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
             int it = 0;
-            for (; it < XC_SPIN; it += 2) {
+            for (; it < spin; it += 2) {
 #pragma unroll
                 for (int m = 0; m < 8; ++m) vb[m] = ld_local(hs + min(256 * m, max(lim, 0)));
                 take(va);
@@ -745,7 +756,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
                 if (!__syncthreads_or(need != 0)) break;
                 __builtin_amdgcn_s_sleep(1);
             }
-            if (it >= XC_SPIN) {
+            if (it >= spin) {
                 h_ok = false;
                 if (tid == 0) flag_error(a.ws + XC_ERR);
             }
@@ -786,7 +797,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
                 uint64_t wa[XC_N], wb[XC_N];
 #pragma unroll
                 for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
-                for (int it = 0; it < XC_SPIN; it += 2) {
+                for (int it = 0; it < spin; it += 2) {
 #pragma unroll
                     for (int xx = 0; xx < XC_N; ++xx) wb[xx] = ld_tag(src + (size_t)xx * a.H);
 #pragma unroll

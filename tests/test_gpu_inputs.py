@@ -462,3 +462,40 @@ def test_grouped_graph_fp32_records(dev):
         ref = O.moe_layer(x.cpu().numpy(), np.array([list(e)]), np.array([wv]), lambda i: m32[i])
         assert np.abs(out.cpu().numpy() - ref).max() / np.abs(ref).max() < 1e-4
     assert gg.replays == 3
+
+
+# ---------------------------------------------------------------------------------------
+# an expired bounded wait, forced from the host: NaN output and the error flag, every workgroup
+# exits, and the next launch on the same workspace is exact again
+# ---------------------------------------------------------------------------------------
+XC_TEST_WORD, ERR_WORD = 576, 512  # header words of the decode-layer workspace (uint32 index)
+
+
+def test_forced_expired_wait_poisons_output_and_sets_the_flag(dev):
+    H, I, E, k = 2048, 1024, 64, 8
+    S = _Stack(dev, H, I, E, 1, ["int4"], 31)
+    dec = MoEDecoder(S.store, k, PrecisionPolicy("lo"), torch.float16, router_weights=[S.Wr[0].to(dev)])
+    assert dec.fused
+    x = torch.randn(1, H, generator=torch.Generator().manual_seed(5)).half().to(dev)
+    ref = torch.zeros(1, H, dtype=torch.float16, device=dev)
+    dec.layer(0, x, ref)
+    torch.cuda.synchronize()
+    dec.check_error()
+    words = dec.ws.view(torch.int32)
+    print("forced expiry: test word set", flush=True)
+    words[XC_TEST_WORD] = 1
+    out = torch.zeros(1, H, dtype=torch.float16, device=dev)
+    dec.layer(0, x, out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
+    with pytest.raises(RuntimeError, match="bounded wait expired"):
+        dec.check_error()
+    print("forced expiry: cleared, normal launch", flush=True)
+    words[XC_TEST_WORD] = 0
+    words[ERR_WORD] = 0
+    out2 = torch.zeros(1, H, dtype=torch.float16, device=dev)
+    for _ in range(2):
+        dec.layer(0, x, out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref)
+    dec.check_error()
