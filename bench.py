@@ -29,6 +29,7 @@ F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workl
     python bench.py --workload qwen3-30b-prefill   # the grouped-GEMM path: one Qwen3-30B-shaped
                                                    # layer on a 512-token bf16 chunk (own JSON line)
     python bench.py --workload qwen3-next-offload  # offloaded decode, records in pinned host memory
+    python bench.py --workload dense-int8          # one-token int8 GEMVs of the dense part (LM head)
 """
 
 from __future__ import annotations
@@ -260,6 +261,72 @@ def prefill_line(args):
                      "bytes_per_launch": int(r["alg"])},
         "mfma": {"achieved": round(tfs, 1), "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFS, 4),
                  "flops_per_launch": r["flops"]},
+        "cpu_baseline": None,
+    }
+
+
+# The dense part in int8 (moelab/denseq.py), one token: the LM heads and an attention projection
+DENSE_SHAPES = {"olmoe-lm-head": (50304, 2048), "qwen3-next-lm-head": (151936, 2048), "attention-proj": (2048, 2048)}
+
+
+def dense_line(args):
+    """One-token int8 GEMVs at the dense part's shapes (moehip_dense_gemv_int8 behind QLinear), each
+    timed with HIP events around one HIP graph of back-to-back launches that rotate over enough
+    weight copies to exceed the 256 MB Infinity Cache; the headline is the OLMoE LM head."""
+    import torch
+
+    from moelab_hip import _lib
+    from moelab_hip import denseq as D
+
+    dev = torch.device("cuda:0")
+    _lib.check_device(dev)
+    st = torch.cuda.current_stream(dev)
+    res = {}
+    for name, (O_, K) in DENSE_SHAPES.items():
+        nb = O_ * K + O_ * (K // 64) * 2
+        copies = max(3, -(-768 * 2**20 // nb))
+        g = torch.Generator(device=dev).manual_seed(O_)
+        mats = []
+        for _ in range(copies):
+            q, s = D.quantize_int8(torch.randn(O_, K, device=dev, generator=g) * 0.02, 64)
+            mats.append((q, s))
+        x = torch.randn(K, device=dev, generator=g).bfloat16()
+        for i in range(2 * copies):
+            D.gemv_int8(*mats[i % copies], x, 64)
+        torch.cuda.synchronize()
+        # the launches replayed as one HIP graph (the host's per-call cost stays out of the figure)
+        n = max(4 * copies, args.kernel_launches // 4)
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for i in range(n):
+                D.gemv_int8(*mats[i % copies], x, 64)
+        gr.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st = torch.cuda.current_stream(dev)
+        a.record(st)
+        gr.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1000 / n
+        del gr
+        res[name] = {"O": O_, "K": K, "bytes": nb + 2 * K + 2 * O_, "us": round(us, 3),
+                     "gbs": round((nb + 2 * K + 2 * O_) / (us * 1e-6) / 1e9, 1), "copies": copies, "launches": n}
+        log(f"[bench] dense int8 GEMV {name} {O_}x{K}: {us:.2f} us, {res[name]['gbs']:.0f} GB/s")
+        del mats
+        torch.cuda.empty_cache()
+    h = res["olmoe-lm-head"]
+    return {
+        "metric": "dense-part int8 GEMV GB/s (one token), OLMoE LM head, 1 GPU",
+        "value": h["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": h["launches"], "warmup": 2 * h["copies"],
+        "ms_per_step": round(h["us"] / 1000, 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "one-token int8 gs64 GEMVs of the dense part (QLinear), bf16 activations",
+                   "shapes": {k: [v["O"], v["K"]] for k, v in res.items()}},
+        "roofline": {"bound": "hbm", "achieved": h["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv8<bf16> (moehip_dense_gemv_int8)", "bytes_per_launch": h["bytes"]},
+        "shapes": res,
         "cpu_baseline": None,
     }
 
@@ -689,7 +756,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
-    ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload",
+    ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload", "dense-int8",
                                            *DECODE_SPECS, *BATCH_SPECS],
                     default="olmoe-decode-bs1")
     ap.add_argument("--offload-layers", type=int, default=48)
@@ -711,6 +778,9 @@ def main():
         return
     if args.workload == "qwen3-next-offload":
         print(json.dumps(offload_line(args)), flush=True)
+        return
+    if args.workload == "dense-int8":
+        print(json.dumps(dense_line(args)), flush=True)
         return
     if args.workload in DECODE_SPECS:
         print(json.dumps(decode_line(args, args.workload)), flush=True)

@@ -64,6 +64,22 @@ int moehip_gemv_int4(const void *q, const void *s, const void *x, void *y, int O
                      void *stream);
 
 /*
+ * The dense part in int8 (attention projections, shared experts, LM head), one token:
+ * y (O,) = W x for W = (q (O, K) int8, s (O, K/gs) fp16 group scales), x (K,) and y in `dtype`,
+ * fp32 accumulation. K a multiple of 32, gs a multiple of 16 dividing K; q and x 16-byte aligned.
+ * Replaces moelab/denseq.py:32-56 (`_gemv8`, behind `gemv_int8`, denseq.py:59-66).
+ */
+int moehip_dense_gemv_int8(const void *q, const void *s, const void *x, void *y, int O, int K, int gs, int dtype,
+                           void *stream);
+/*
+ * The multi-token path's weights: w (rows, K) in `dtype` = q * s for rows of the same int8 matrix,
+ * the scale rounded to `dtype` first and the product rounded once (as moelab/quant.py:191-205
+ * `dequantize(q, s, 8, dtype)` computes it). K a multiple of 16; q 16-byte aligned.
+ * Replaces the row-block dequantisation of moelab/denseq.py:95-101 (QLinear.forward, n > 1).
+ */
+int moehip_dense_dequant_int8(const void *q, const void *s, int rows, int K, int gs, int dtype, void *w, void *stream);
+
+/*
  * Kernel A of the grouped expert FFN: for every table row e < n with w[e] != 0,
  *   h[e, r] = silu(gate_e[r] . x) * (up_e[r] . x),  r < I,
  * where gate_e / up_e are rows r and r+I of the record's gate_up matrix (2I, H), dequantised in

@@ -53,6 +53,8 @@ _SIGS = {
     "moehip_last_error": ([], ctypes.c_char_p),
     "moehip_device_check": ([_i], _i),
     "moehip_gemv_int4": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "moehip_dense_gemv_int8": ([_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp], _i),
+    "moehip_dense_dequant_int8": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp], _i),
     "moehip_grouped_up": ([_i, _vp, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp], _i),
     "moehip_grouped_down": ([_i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp], _i),
     "moehip_down_workspace_floats": ([_i, _i], ctypes.c_size_t),
