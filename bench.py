@@ -564,31 +564,37 @@ def batch_line(args, name):
 NH, NI, NE, NK = 2048, 512, 512, 10
 
 
-def zipf_routing(steps: int, L: int, E: int, k: int, s: float, reuse: float, seed: int):
-    """(steps, L, k) expert ids: per layer, expert ranks follow Zipf(s) under a random
-    permutation; each slot keeps the previous token's expert with probability `reuse`."""
-    import numpy as np
+def residual_stream(dev, steps: int, L: int, E: int, H: int, seed: int, rho: float = 0.6, alpha: float = 0.35,
+                    pop: float = 1.0):
+    """A synthetic decode: per layer a router (E, H) and per (token, layer) a hidden state, bf16.
+    Routers: N(0, 1/H) rows plus a popularity term pop * -log(rank + 1) (a random rank order per
+    layer) along a direction u that every hidden state carries, so the logits are a Zipf-like
+    per-expert bias plus N(0, 1) noise. Hidden states: x = u + z, z of unit variance per coordinate;
+    token t's first z is rho-correlated with token t-1's (experts recur from token to token), and
+    each layer adds alpha * N(0, 1) (a residual stream: the next layer's gate on this layer's
+    state predicts that layer's routing imperfectly)."""
+    import math
 
-    rng = np.random.default_rng(seed)
-    p = 1.0 / np.arange(1, E + 1) ** s
-    p /= p.sum()
-    perm = np.stack([rng.permutation(E) for _ in range(L)])
-    idx = np.zeros((steps, L, k), np.int64)
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    u = torch.randn(H, device=dev, generator=g)
+    u /= u.norm()
+    Ws = []
+    for _ in range(L):
+        rank = torch.randperm(E, device=dev, generator=g).float()
+        bias = -pop * torch.log(rank + 1.0)
+        W = torch.randn(E, H, device=dev, generator=g) / math.sqrt(H) + bias[:, None] * u[None, :]
+        Ws.append(W.bfloat16().contiguous())
+    xs = torch.empty(steps, L, 1, H, dtype=torch.bfloat16, device=dev)
+    z = torch.randn(H, device=dev, generator=g)
     for t in range(steps):
+        z = rho * z + math.sqrt(1.0 - rho * rho) * torch.randn(H, device=dev, generator=g)
+        zl = z.clone()
         for l in range(L):
-            row = []
-            for j in range(k):
-                if t > 0 and rng.random() < reuse and idx[t - 1, l, j] not in row:
-                    row.append(int(idx[t - 1, l, j]))
-                    continue
-                while True:
-                    e = int(perm[l, rng.choice(E, p=p)])
-                    if e not in row:
-                        row.append(e)
-                        break
-            idx[t, l] = row
-    w = rng.random((steps, L, k)) + 0.05
-    return idx, (w / w.sum(-1, keepdims=True)).astype(np.float32)
+            xs[t, l, 0] = (u + zl).bfloat16()
+            zl = zl + alpha * torch.randn(H, device=dev, generator=g)
+    return Ws, xs
 
 
 def staging_peak(dev, lay, mode: str, reps: int = 5):
@@ -660,71 +666,92 @@ def offload_bench(args):
         f"torch pinned copy {copy_peak:.1f} GB/s")
     mode = max(peaks, key=peaks.get) if args.stage_mode == "auto" else args.stage_mode
     steps, warm = args.offload_steps, args.offload_warmup
-    idx, w = zipf_routing(warm + steps, L, NE, NK, 1.1, 0.4, seed=1)
-    idx_d = torch.from_numpy(idx).to(dev)
-    w_d = torch.from_numpy(w).to(dev)
+    Wr, xs = residual_stream(dev, warm + steps, L, NE, NH, seed=1)
     budget = 16 * 10**9 * L // 48  # 16 GB for the 48-layer model: the same resident fraction (39 %)
     off = OffloadDecoder({"int4": lay}, L, NE, NK, lambda l, e, p: host[(l, e)], budget, dev, PrecisionPolicy("lo"),
-                         torch.bfloat16, renorm=True, mode=mode)
-    gx = torch.Generator(device=dev).manual_seed(2)
-    xs = torch.randn(8, L, 1, NH, device=dev, generator=gx).bfloat16()
+                         torch.bfloat16, router_weights=Wr, renorm=True, mode=mode, predictor="gate")
     out = torch.zeros(1, NH, dtype=torch.bfloat16, device=dev)
-
-    def token(t, prefetch):
+    # the routing every layer will get (the same router kernel on the same states), for the
+    # ground-truth predictor run only
+    truth = torch.zeros(warm + steps, L, NK, dtype=torch.int64, device=dev)
+    dec = off.dec
+    for t in range(warm + steps):
         for l in range(L):
-            nxt = {int(e): "int4" for e in idx[t, l + 1]} if (prefetch and l + 1 < L) else None
-            off.layer(l, xs[t % 8, l], out, idx=idx_d[t, l:l + 1], w32=w_d[t, l:l + 1], predict=nxt)
+            dec.route(l, xs[t, l])
+            truth[t, l] = dec.idx[0]
+    truth = truth.cpu().numpy()
+    distinct = float(np.mean([len(np.unique(truth[:, l])) for l in range(L)]))
+    reuse = float(np.mean([len(set(truth[t, l]) & set(truth[t - 1, l])) / NK
+                           for t in range(1, warm + steps) for l in range(L)]))
+    log(f"[bench] routing: {distinct:.0f} distinct experts per layer over {warm + steps} tokens, "
+        f"{reuse:.2f} of a token's experts also used by the previous token")
+
+    def token(t, how):
+        for l in range(L):
+            if how == "truth" and l + 1 < L:
+                off.layer(l, xs[t, l], out, predict={int(e): "int4" for e in truth[t, l + 1]})
+            else:
+                off.layer(l, xs[t, l], out)
         off.tick()
 
     res = {}
-    for prefetch in (True, False):
+    for how in ("gate", "truth", "none"):
+        off.predictor = "gate" if how == "gate" else "none"
         off.cache.clear()
         off.stats = {k: 0 for k in off.stats}
         for t in range(warm):
-            token(t, prefetch)
+            token(t, how)
         torch.cuda.synchronize()
         s0 = dict(off.stats)
         b0 = off.stager.bytes_h2d
         t0 = time.perf_counter()
         for t in range(warm, warm + steps):
-            token(t, prefetch)
+            token(t, how)
         torch.cuda.synchronize()
         dt = time.perf_counter() - t0
         ds = {k: off.stats[k] - s0[k] for k in s0}
         h2d = off.stager.bytes_h2d - b0
         hit = ds["hits"] / max(1, ds["hits"] + ds["misses"])
-        res[prefetch] = {"tok_s": steps / dt, "ms_per_token": dt * 1000 / steps, "hit_rate": hit,
-                         "h2d_gb_per_token": h2d / steps / 1e9, "h2d_gbs": h2d / dt / 1e9,
-                         "prefetch_hits": ds["prefetch_hits"], "prefetch_issued": ds["prefetch_issued"]}
+        res[how] = {"tok_s": steps / dt, "ms_per_token": dt * 1000 / steps, "hit_rate": hit,
+                    "h2d_gb_per_token": h2d / steps / 1e9, "h2d_gbs": h2d / dt / 1e9,
+                    "prefetch_hits": ds["prefetch_hits"], "prefetch_issued": ds["prefetch_issued"],
+                    "predictor_recall": ds["pred_hits"] / max(1, ds["pred_total"])}
         off.dec.check_error()
         if off.dec.miss.item() != 0:
             raise RuntimeError("offloaded decode ran an expert that was not resident")
-        log(f"[bench] offload prefetch={prefetch}: {res[prefetch]}")
+        log(f"[bench] offload predictor={how}: {res[how]}")
     return {"res": res, "peaks": peaks, "copy_peak": copy_peak, "mode": mode, "L": L, "steps": steps, "warm": warm,
-            "records_host_gb": L * NE * rb / 1e9, "budget_gb": budget / 1e9}
+            "records_host_gb": L * NE * rb / 1e9, "budget_gb": budget / 1e9, "distinct": distinct, "reuse": reuse}
 
 
 def offload_line(args):
     r = offload_bench(args)
-    p = r["res"][True]
+    p = r["res"]["gate"]
     peak = max(r["peaks"].values())
+    side = lambda d: {k: round(v, 4) if isinstance(v, float) else v for k, v in d.items()}  # noqa: E731
     return {
         "metric": "offloaded int4 MoE decode tok/s + H2D GB/s, Qwen3-Next shape, bs=1, 1 GPU",
         "value": round(p["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": r["steps"], "warmup": r["warm"],
         "ms_per_step": round(p["ms_per_token"], 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int4", "data": "synthetic",
         "config": {"workload": "Qwen3-Next-shaped offloaded decode, int4 gs64 records in pinned host memory, "
-                               "16 GB device budget, LRFU, Zipf(1.1) routing with 40% token reuse, bs=1",
+                               "16 GB device budget, LRFU, routing by each layer's router on a synthetic "
+                               "residual stream (Zipf-like expert popularity, token-to-token correlation), bs=1",
                    "d_model": NH, "experts": NE, "top_k": NK, "d_ff": NI, "layers": r["L"],
                    "records_host_gb": round(r["records_host_gb"], 1), "device_budget_gb": r["budget_gb"],
-                   "staging": r["mode"], "prefetch": "next layer's actual routing (a perfect next-layer predictor)",
+                   "staging": r["mode"],
+                   "prefetch": "the next layer's gate on the current hidden state, on the GPU (read back with "
+                               "the current routing)",
+                   "distinct_experts_per_layer": round(r["distinct"], 1), "token_reuse": round(r["reuse"], 3),
                    "shared_expert": "not included"},
-        "hit_rate": round(p["hit_rate"], 4), "h2d_gb_per_token": round(p["h2d_gb_per_token"], 4),
+        "hit_rate": round(p["hit_rate"], 4), "predictor_recall": round(p["predictor_recall"], 4),
+        "h2d_gb_per_token": round(p["h2d_gb_per_token"], 4),
         "roofline": {"bound": "host link", "achieved": round(p["h2d_gbs"], 2), "peak": round(peak, 2), "unit": "GB/s",
                      "frac": round(p["h2d_gbs"] / peak, 4), "traffic": None,
                      "peak_is": "best measured staging batch (32 records) over kernel and sdma modes"},
         "staging_gbs": {k: round(v, 2) for k, v in r["peaks"].items()}, "torch_pinned_copy_gbs": round(r["copy_peak"], 2),
-        "no_prefetch": {k: round(v, 4) if isinstance(v, float) else v for k, v in r["res"][False].items()},
+        "ground_truth_predictor": side(r["res"]["truth"]),
+        "no_prefetch": side(r["res"]["none"]),
         "cpu_baseline": None,
     }
 

@@ -234,7 +234,7 @@ class OffloadDecoder:
     def __init__(self, layouts: dict, num_layers: int, num_experts: int, k: int, host_record, fast_budget_bytes: int,
                  device, policy: PrecisionPolicy | None = None, dtype=torch.float16, router_weights: list | None = None,
                  renorm: bool = False, mode: str = "kernel", half_life: float = 32.0, eviction: str = "lrfu",
-                 margin_records: int | None = None):
+                 margin_records: int | None = None, predictor: str = "none"):
         self.device = torch.device(device)
         _lib.check_device(self.device)
         self.precisions = list(layouts)
@@ -257,8 +257,22 @@ class OffloadDecoder:
         self.dec = MoEDecoder(view, k, self.policy, dtype, router_weights=router_weights, renorm=renorm,
                               one_token_rule=True)
         self._blob_prec: dict[int, str] = {}
-        self.rb = (torch.empty(2, k, dtype=torch.float32, pin_memory=True))
-        self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0}
+        if predictor not in ("none", "gate"):
+            raise ValueError(f"predictor {predictor!r}: 'none' or 'gate'")
+        if predictor == "gate" and router_weights is None:
+            raise ValueError("the gate predictor needs the layers' router weights")
+        self.predictor = predictor
+        self.renorm = renorm
+        # the next layer's gate on the current state (moelab graphs.py:252-263): its own buffers
+        self.p_logits = torch.empty(1, num_experts, dtype=dtype, device=self.device)
+        self.p_idx = torch.zeros(1, k, dtype=torch.int64, device=self.device)
+        self.p_w = torch.zeros(1, k, dtype=dtype, device=self.device)
+        self.p_w32 = torch.zeros(1, k, dtype=torch.float32, device=self.device)
+        # one pinned readback per layer: the current routing and the prediction for the next layer
+        self.rb = torch.empty(4, k, dtype=torch.float32, pin_memory=True)
+        self._predicted: tuple[int, frozenset] | None = None
+        self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0,
+                      "pred_hits": 0, "pred_total": 0}
 
     def _evicted(self, blob: torch.Tensor) -> None:
         prec = self._blob_prec.pop(blob.data_ptr())
@@ -319,21 +333,46 @@ class OffloadDecoder:
             waits.append(tab_ev)
         return waits
 
+    def _gate_predict(self, layer: int, x: torch.Tensor) -> None:
+        """Layer `layer`'s router on x into the prediction buffers (the next layer's gate applied
+        to the current hidden state, moelab runtime.py:851-869 with prefetch_mass None)."""
+        Wr = self.dec.router_weights[layer]
+        _lib.call("moehip_router_topk", x.data_ptr(), Wr.data_ptr(), 1, x.shape[-1], self.E, self.k,
+                  1 if self.renorm else 0, _lib.dt_code(x.dtype), self.p_logits.data_ptr(), self.p_idx.data_ptr(),
+                  self.p_w.data_ptr(), self.p_w32.data_ptr(), _lib.stream_of(x.device))
+
     def layer(self, layer: int, x: torch.Tensor, out: torch.Tensor, idx: torch.Tensor | None = None,
               w32: torch.Tensor | None = None, predict: dict | None = None) -> torch.Tensor:
         """out (1, H) = MoE layer `layer` on x (1, H). idx/w32 (device, (1, k)) skip the router.
-        predict {expert: precision} for layer + 1 is staged in the background afterwards."""
+        predict {expert: precision} for layer + 1 is staged in the background afterwards; without
+        it, the gate predictor (predictor='gate') predicts layer + 1's experts from x with that
+        layer's router, read back with this layer's routing (one host wait per layer)."""
         cur = torch.cuda.current_stream(self.device)
         if idx is None:
             self.dec.route(layer, x)
             idx, w32 = self.dec.idx, self.dec.w32
+        gate = predict is None and self.predictor == "gate" and layer + 1 < self.L
+        if gate:
+            self._gate_predict(layer + 1, x)
         self.rb[0].copy_(idx.view(-1).float(), non_blocking=True)
         self.rb[1].copy_(w32.view(-1), non_blocking=True)
+        if gate:
+            self.rb[2].copy_(self.p_idx.view(-1).float(), non_blocking=True)
+            self.rb[3].copy_(self.p_w32.view(-1), non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(cur)
         ev.synchronize()
         ids = [int(v) for v in self.rb[0].tolist()]
         ws = self.rb[1].tolist()
+        if self._predicted is not None and self._predicted[0] == layer:
+            self.stats["pred_total"] += len(ids)
+            self.stats["pred_hits"] += sum(1 for e in ids if e in self._predicted[1])
+        self._predicted = None
+        if gate:
+            pids = [int(v) for v in self.rb[2].tolist()]
+            predict = self._wants(layer + 1, pids, self.rb[3].tolist())
+        if predict and layer + 1 < self.L:
+            self._predicted = (layer + 1, frozenset(predict))
         want = self._wants(layer, ids, ws)
         protect = frozenset((layer, e, p) for e, p in want.items())
         for wev in self._stage_missing(layer, want, protect, prefetch=False):

@@ -135,3 +135,35 @@ def test_offload_decoder_matches_resident(dev, mode, routed):
     # every slot handed out is either resident or free again
     n_slots = off.pool.allocated // ((rb + 4095) // 4096 * 4096)
     assert len(off.cache.entries) + len(off.pool.free["int4"]) == n_slots
+
+
+@pytest.mark.parametrize("mode", ["kernel", "sdma"])
+def test_offload_gate_predictor(dev, mode):
+    """The gate predictor (the next layer's router on the current state, on the GPU, read back with
+    the current routing) stages layer l + 1's predicted experts while layer l runs: outputs stay
+    identical to the resident decoder's, predictions are counted, and the states that repeat
+    (a layer's state fed to the next layer unchanged) are predicted exactly."""
+    H, I, E, L, k, T = 512, 256, 32, 4, 4, 8
+    lay, store, Wr, host_record = _setup(dev, H, I, E, L, k, 7)
+    rb = lay["record_bytes"]
+    ref_dec = MoEDecoder(store, k, PrecisionPolicy("lo"), torch.float16, router_weights=Wr)
+    off = OffloadDecoder({"int4": lay}, L, E, k, host_record, 3 * k * rb, dev, PrecisionPolicy("lo"), torch.float16,
+                         router_weights=Wr, mode=mode, predictor="gate")
+    g = torch.Generator().manual_seed(11)
+    xs = torch.randn(T, 1, 1, H, generator=g).half().repeat(1, L, 1, 1).to(dev)  # one state through every layer
+    got = torch.zeros(T, L, 1, H, dtype=torch.float16, device=dev)
+    ref = torch.zeros_like(got)
+    print(f"offload gate predictor mode {mode}", flush=True)
+    for t in range(T):
+        for l in range(L):
+            ref_dec.route(l, xs[t, l])
+            ref_dec.layer(l, xs[t, l], ref[t, l], idx=ref_dec.idx, w32=ref_dec.w32)
+            off.layer(l, xs[t, l], got[t, l])
+        off.tick()
+    torch.cuda.synchronize()
+    assert off.dec.miss.item() == 0
+    assert torch.equal(got, ref)
+    st = off.stats
+    assert st["pred_total"] == T * (L - 1) * k
+    assert st["pred_hits"] == st["pred_total"]  # the same state: the gate predicts exactly
+    assert st["prefetch_issued"] > 0 and st["prefetch_hits"] > 0
