@@ -167,6 +167,25 @@ def gpu_bench(args):
     kern_us = ea.elapsed_time(eb) * 1000 / (reps * nA)
     dec.check_error()
 
+    # the expert phase of the launch (first weight request to the last down product, per-workgroup
+    # real-time stamps of a traced launch), over a few (token, layer) launches
+    phases = []
+    tr = torch.zeros(16 * 4096, dtype=torch.int64, device=dev)
+    for j in range(min(nA, 12)):
+        dec.grid, dec.trace = -1, tr
+        tr.zero_()
+        dec.layer(j % L, xs[j // L, j % L], outs[j // L, j % L])
+        torch.cuda.synchronize()
+        dec.grid, dec.trace = 0, None
+        t = tr.view(-1, 16).cpu()
+        t = t[t[:, 0] > 0]
+        done = t[:, 11][t[:, 11] > 0]
+        if len(t) and len(done):
+            phases.append(float(done.max() - t[:, 6].min()) * 10 / 1000)
+    dec.check_error()
+    phases.sort()
+    expert_phase_us = phases[len(phases) // 2] if phases else None
+
     gu_bytes = 2 * I * (H // 2) + 2 * I * (H // 64) * 2  # gate_up.q + gate_up.s of one record
     dn_bytes = H * (I // 2) + H * (I // 64) * 2
     rec_bytes = gu_bytes + dn_bytes
@@ -181,6 +200,8 @@ def gpu_bench(args):
         "kernel_us": kern_us, "kernel_bytes": layer_alg,
         "kernel_gbs": layer_alg / (kern_us * 1e-6) / 1e9,
         "record_bytes": rec_bytes, "fused": dec.fused,
+        "expert_phase_us": expert_phase_us,
+        "expert_phase_gbs": (K_TOP * rec_bytes / (expert_phase_us * 1e-6) / 1e9) if expert_phase_us else None,
     }
 
 
@@ -840,6 +861,10 @@ def main():
         "expert_gbs_ref_definition": round(r["expert_gbs"], 1),
         "layer_alg_gbs": round(r["layer_alg_gbs"], 1),
         "kernel_us": round(r["kernel_us"], 3),
+        "expert_phase": {"us": r["expert_phase_us"] and round(r["expert_phase_us"], 3),
+                         "gbs": r["expert_phase_gbs"] and round(r["expert_phase_gbs"], 1),
+                         "is": "8 records' bytes over the time from the first weight request to the last down "
+                               "product inside a launch (per-workgroup stamps of traced launches)"},
         "roofline": {
             "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
