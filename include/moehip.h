@@ -292,6 +292,27 @@ int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, int xdtype,
 size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I);
 
 /*
+ * One MoE layer on a T-token chunk in four launches, int4 gs64 records, 16-bit activations:
+ * router logits (as moehip_router_topk), then one launch for the softmax top-k (renorm as given;
+ * idx (T*k) int64, w (T*k) in xdtype or null, w32 (T*k) fp32 as moehip_router_topk writes them),
+ * the expert buckets and, for bf16, the fp16 copy of x the MFMA tiles read, then the grouped
+ * GEMMs and the slot-order combine of moehip_grouped_gemm (out (T, H) in xdtype, + out if
+ * accumulate, + add). The pairs' order within an expert depends on scheduling; the output does
+ * not (every pair's products and every token's slot-order sum are independent of it). logits
+ * (T, E) in xdtype. H a multiple of 512, I of 128, E <= 1024, k <= 32, gs = 64. ws: at least
+ * moehip_prefill_layer_workspace_bytes(), 256-B aligned, ZEROED before its first use (the routing
+ * counters; every launch leaves them zero).
+ * Replaces, for a prefill chunk, the model's gate call (transformers Qwen3MoeTopKRouter /
+ * OlmoeTopKRouter.forward, called by moelab at runtime.py:909) followed by
+ * moelab/runtime.py:459-492 (expert sort) and :418-436, 352-353 (`_run_grouped_tokens`,
+ * `out.index_add_`).
+ */
+int moehip_prefill_layer(int prec, const int64_t *tab, const void *x, const void *Wr, int xdtype, int T, int H, int I,
+                         int k, int E, int gs, int renorm, void *logits, int64_t *idx, void *w, float *w32, void *out,
+                         const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream);
+size_t moehip_prefill_layer_workspace_bytes(int T, int k, int H, int I, int E);
+
+/*
  * moehip_grouped_gemm over P record tables, one per record precision precs[p] (MOEHIP_PREC_INT4 /
  * INT8 / FP8 / F16 / BF16): tabs (P, E, 4) int64, row (p, e) = the field addresses of expert e's
  * record when the expert runs at precision p (as written by moehip_batch_vote), else 0. Pairs of

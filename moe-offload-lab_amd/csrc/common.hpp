@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/moehip.h"
 
@@ -28,6 +29,10 @@ static inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream
 // by moehip_device_check), its workspace size (0 = the layer does not fit it) and its launch
 // (*used = 0 when the layer does not fit it or the device was not confirmed)
 int xcd_probe(int dev);
+// 1 once xcd_probe confirmed that workgroup b runs on XCD b % 8 on the current device
+int xcd_dispatch_ok();
+// logits (T, E) = x Wr^T in dtype (router.hip): MFMA tiles for 16-bit rows when the shape allows
+void launch_router_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits, hipStream_t st);
 int noalloc_init(int dev);
 size_t xcd_workspace_bytes(int prec, int ks, int E, int H, int I);
 int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in, const float *w32_in,

@@ -921,6 +921,11 @@ static XcPlan xc_plan(int prec, int ks, int E, int H, int I) {
 // 1 once moehip_device_check confirmed the round-robin XCD dispatch on a device (per device)
 static int g_xcd_ok[64];
 
+int xcd_dispatch_ok() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && g_xcd_ok[dev];
+}
+
 __global__ void k_xcd_probe(uint32_t *out) {
     if (threadIdx.x == 0) {
         uint32_t v;

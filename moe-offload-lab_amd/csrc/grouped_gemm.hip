@@ -29,8 +29,8 @@
 // bytes, permuted into operand order) one chunk ahead. Workgroups of one expert land on one XCD
 // (its L2 then serves the expert's activation rows to all of them).
 
-#include "gemv_core.hpp"
 #include "decide.hpp"
+#include "lanevec.hpp"
 
 namespace moehip {
 
@@ -839,13 +839,622 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Persistent expert FFN: the gate/up and down GEMMs of one record table in ONE launch.
+//
+// Work units: (expert e, pass m) = up to 64 of the expert's pairs. Unit u (numbered in expert
+// order over the experts with pairs) belongs to XCD u % 8. Its tiles: NBU = I / 128 up tiles
+// (128 h columns each) and NBD = H / 256 down tiles (256 output rows each). k_ffn_plan writes
+// one queue per XCD (a unit's down tiles about a round of up tiles after its up tiles). The
+// grid is what the GPU holds at once (or less); workgroup b takes tickets from the queue of XCD
+// b % 8 (the XCD it runs on: the MI355X deals workgroups to XCDs round robin, checked once per
+// device), so an expert's activation rows and h rows are re-read from that XCD's L2.
+//
+// An up tile writes h = silu(gate x) * (up x) as fp16 scaled by a power of two per (pair, up
+// tile) (2^-eb, eb from the largest |h| of the pair's 128 columns), the exponents beside, then
+// counts itself done on the unit (agent-scope counter, after its stores are acknowledged). A
+// down tile waits for its unit's NBU up tiles (bounded wait; on expiry its outputs are NaN and
+// the error word is set), rescales each h block to the pair's largest exponent while staging it
+// (2^(eb - Emax), exact for all but subnormal results) and writes y = w 2^Emax (down h). The
+// waits cannot deadlock: a down tile's up tiles were handed out earlier, to running workgroups,
+// and up tiles wait for nothing. Reads of h and its exponents bypass the CU's L1 (non-temporal
+// loads), which may hold lines fetched before a neighbouring pair's h was written.
+//
+// K loop: the activation (or h) chunk of a pass is loaded two chunks ahead into registers and
+// stored into LDS one chunk ahead (two LDS buffers, one barrier per chunk); the weights of RING
+// chunks are in flight in registers per wave.
+// ---------------------------------------------------------------------------------------
+constexpr int FP_TICK = 0;     // ticket counter of XCD x at FP_TICK + FP_TSTRIDE x (2 KB apart: no shared channel);
+constexpr int FP_TSTRIDE = 512; // those of the down phase of a two-phase run at FP_TICK + FP_TSTRIDE (8 + x)
+constexpr int FP_NALL = 8192;  // all tiles of XCD x
+constexpr int FP_NUP = 8208;   // up tiles of XCD x (the first ones of its queue when the lag covers every unit)
+constexpr int FP_ERR = 8200;   // error word: a bounded wait expired
+constexpr int FP_DONE = 8448;  // flag[u * NBU + nb]: up tile nb of unit u has stored its h
+constexpr int FF_SKIP = 1 << 30;  // entry flag: expert without a record (no tile to run)
+constexpr int FF_ZERO = 1 << 29;  // entry flag: down tile of an expert without a record: y = 0
+constexpr int FF_SPIN = 1 << 21;  // polls before a wait gives up (~1 s)
+constexpr int FF_DUMMY = 512;     // bytes of the workgroup's own line pair read past a pass's last chunk
+constexpr int FF_DUMMY_WGS = 4096; // workgroups with a line pair of their own (more share them)
+
+// units over every expert with pairs: at most NP (one per pair) plus one per 64 pairs
+__host__ __device__ inline int ffn_max_units(int NP) { return NP + (NP + 63) / 64 + 8; }
+// entries per XCD queue: up and down tiles of its units
+__host__ __device__ inline int ffn_lmax(int NP, int NBU, int NBD) { return (ffn_max_units(NP) + 7) / 8 * (NBU + NBD); }
+
+// One workgroup: unit numbers by an exclusive scan of the experts' pass counts (twice: the
+// first pass counts the units), then every expert writes the entries of its units (32 bytes:
+// {e, p0, pairs, nb | flags} {u}, bit 31 of the third word set for down tiles) and zeroes their
+// flags; per pair it writes the token's row of x, its exponent and the routed weight. Queue of
+// XCD x (its nu units, local index l = u / 8): the up tiles of units 0 .. L - 1, then per unit
+// l the up tiles of unit l + L and the down tiles of unit l, L = min(nu, lag): a unit's down
+// tiles are handed out about a round of up tiles (lag units: the workgroups of an XCD over its
+// NBU up tiles per unit, plus one) after its own up tiles, when those have mostly finished.
+__global__ __launch_bounds__(1024) void k_ffn_plan(const int32_t *__restrict__ offsets, const int64_t *__restrict__ tab,
+                                                   int E, int NBU, int NBD, int lmax, int zero_missing, int lag,
+                                                   int *__restrict__ plan, int4 *__restrict__ list,
+                                                   const int32_t *__restrict__ sorted_pos, int k,
+                                                   const float *__restrict__ w, const int *__restrict__ xe,
+                                                   int *__restrict__ xrow, float *__restrict__ wp,
+                                                   int *__restrict__ xep) {
+    __shared__ int s_w[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int U = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        int base = 0;  // units of the experts before this chunk (the same in every thread)
+        for (int e0 = 0; e0 < E; e0 += 1024) {
+            const int e = e0 + tid;
+            const int ne = e < E ? offsets[e + 1] - offsets[e] : 0;
+            const int np = (ne + 63) >> 6;
+            int incl = np;
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            // the wave's total written by every lane (no lane-divergent branch next to the barriers)
+            s_w[wave] = __builtin_amdgcn_readlane(incl, 63);
+            __syncthreads();
+            int ub = base, tot = base;
+            for (int w = 0; w < 16; ++w) {
+                if (w < wave) ub += s_w[w];
+                tot += s_w[w];
+            }
+            ub += incl - np;
+            if (pass == 1 && np > 0) {
+                const bool res = tab[4 * (size_t)e] != 0;
+                const int fu = res ? 0 : FF_SKIP;
+                const int fd = (int)(1u << 31) | (res ? 0 : (zero_missing ? FF_ZERO : FF_SKIP));
+                for (int m = 0; m < np; ++m) {
+                    const int u = ub + m, x = u & 7, l = u >> 3;
+                    const int nu = (U - x + 7) >> 3, L = min(nu, lag);
+                    // start of block b: the up tiles of unit b + L (if any), then the down tiles of unit b
+                    auto blk = [&](int b) { return L * NBU + b * NBD + NBU * min(b, nu - L); };
+                    const int up0 = l < L ? l * NBU : blk(l - L);
+                    const int dn0 = blk(l) + (l + L < nu ? NBU : 0);
+                    for (int nb = 0; nb < NBU; ++nb) plan[FP_DONE + u * NBU + nb] = 0;
+                    int4 *q = list + (size_t)x * lmax * 2;
+                    const int p0 = offsets[e] + m * GG_TOK, mn = min(GG_TOK, ne - m * GG_TOK);
+                    for (int nb = 0; nb < NBU; ++nb) {
+                        q[2 * (up0 + nb)] = make_int4(e, p0, mn, nb | fu);
+                        q[2 * (up0 + nb) + 1] = make_int4(u, 0, 0, 0);
+                    }
+                    for (int nb = 0; nb < NBD; ++nb) {
+                        q[2 * (dn0 + nb)] = make_int4(e, p0, mn, nb | fd);
+                        q[2 * (dn0 + nb) + 1] = make_int4(u, 0, 0, 0);
+                    }
+                }
+            }
+            __syncthreads();  // s_w of the next chunk
+            base = tot;
+        }
+        U = base;
+    }
+    // per pair (expert-sorted order): its token's row of x, that row's exponent, its routed weight
+    const int np_all = offsets[E];
+    for (int p = tid; p < np_all; p += 1024) {
+        const int sp = sorted_pos[p], r = sp / k;
+        xrow[p] = r;
+        xep[p] = xe != nullptr ? xe[r] : 0;
+        wp[p] = w[sp];
+    }
+    if (tid < 8) {
+        const int nu = U > tid ? (U - tid + 7) >> 3 : 0;  // units u < U with u % 8 == tid
+        plan[FP_TICK + FP_TSTRIDE * tid] = 0;
+        plan[FP_TICK + FP_TSTRIDE * (8 + tid)] = nu * NBU;
+        plan[FP_NALL + tid] = nu * (NBU + NBD);
+        plan[FP_NUP + tid] = nu * NBU;
+    }
+    if (tid == 0) plan[FP_ERR] = 0;
+}
+
+struct FfnArgs {
+    const uint16_t *x;  // fp16 activations (the caller's, or x16 of bf16 input)
+    const int *xe;      // per-token exponents of x16, or null
+    int H, I, k, NBU, NBD, lmax;
+    const int32_t *offsets, *sorted_pos;
+    const int64_t *tab;
+    const float *w;     // routed weight of pair-slot t * k + j
+    uint16_t *h16;      // (pairs, I) fp16 h, scaled by 2^-eb per (pair, up tile)
+    int *hbe;           // (pairs, NBU) those exponents
+    float *y;           // (pairs, H) fp32 expert outputs times the routed weight
+    int *plan;
+    const int4 *list;   // 2 int4 per entry
+    const int *xrow;    // per pair: the token's row of x
+    const int *xep;     // per pair: that row's exponent (0 without)
+    const float *wp;    // per pair: the routed weight
+    gu8 *dummy;         // FF_DUMMY bytes per workgroup, read by the loads past a pass's last chunk
+    int phase;          // -1: the whole queue; 0: its up tiles; 1: its down tiles (after a phase-0 launch)
+    DeqK dk;
+};
+
+__device__ __forceinline__ uint4 ld16_nt(const void *p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// fp16 bits of 2^d for d <= 0 (subnormal below 2^-14, 0 below 2^-24)
+__device__ __forceinline__ uint32_t pow2_h(int d) {
+    return d >= -14 ? (uint32_t)(d + 15) << 10 : (d >= -24 ? 1u << (d + 24) : 0u);
+}
+
+// activation staging of one pass: NT tokens (64, or 32 for a single 32-token M tile) over the
+// 256 threads, TPT threads per token, VPT values each (NV 16-byte loads)
+template <int CK, int NT> struct Stg {
+    static constexpr int TPT = 256 / NT;
+    static constexpr int VPT = CK / TPT;
+    static constexpr int NV = VPT / 8;
+};
+// tokens staged for NMT M tiles of 16 (32 when that covers them and still gives 16 bytes per load)
+template <int CK, int NMT> struct StgOf {
+    static constexpr int NT = (NMT <= 2 && CK >= 64) ? 32 : 64;
+};
+
+// one activation chunk of a thread in registers (and, for h, its block exponent)
+template <int CK, int NT> struct XStage {
+    uint4 v[Stg<CK, NT>::NV];
+    int eb;
+};
+
+template <int CK, int NT, bool DOWN>
+__device__ __forceinline__ void stage_load(const uint16_t *row, const int *ebrow, int c, XStage<CK, NT> &s) {
+    const uint16_t *p = row + (size_t)c * CK + (threadIdx.x % Stg<CK, NT>::TPT) * Stg<CK, NT>::VPT;
+#pragma unroll
+    for (int m = 0; m < Stg<CK, NT>::NV; ++m) s.v[m] = DOWN ? ld16_nt(p + 8 * m) : reinterpret_cast<const uint4 *>(p)[m];
+    if constexpr (DOWN) s.eb = __builtin_nontemporal_load(ebrow + (c * CK) / 128);
+}
+
+template <int CK, int NT, bool DOWN>
+__device__ __forceinline__ void stage_store(const XStage<CK, NT> &s, int emax, uint16_t *s_a) {
+    const int tok = threadIdx.x / Stg<CK, NT>::TPT, part = threadIdx.x % Stg<CK, NT>::TPT;
+    uint4 *dst = reinterpret_cast<uint4 *>(s_a + tok * GgChunk<CK>::LDA + part * Stg<CK, NT>::VPT);
+    half2_t f2;
+    if constexpr (DOWN) {
+        const uint32_t fb = pow2_h(s.eb - emax);
+        f2 = __builtin_bit_cast(half2_t, fb | (fb << 16));
+    }
+#pragma unroll
+    for (int m = 0; m < Stg<CK, NT>::NV; ++m) {
+        uint4 u = s.v[m];
+        if constexpr (DOWN) {
+            u.x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, u.x) * f2);
+            u.y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, u.y) * f2);
+            u.z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, u.z) * f2);
+            u.w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, u.w) * f2);
+        }
+        dst[m] = make_uint4(lo_lo(u.x, u.z), hi_hi(u.x, u.z), lo_lo(u.y, u.w), hi_hi(u.y, u.w));
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// v_mfma_f32_16x16x32_f16 tiles: A = 16 tokens x 32 K (lane l: token l % 16, K 8 (l / 16) + e),
+// B = 32 K x 16 weight rows (lane l: row l % 16, K 8 (l / 16) + e), D = 16 x 16 fp32 (lane l:
+// tokens 4 (l / 16) + r, row l % 16). A wave holds 64 weight rows as 4 subtiles of 16. Per
+// 64-byte chunk of a row, lane l loads bytes 16 (l / 16) .. + 15 (the four lanes of a row read
+// its 64 bytes: one load instruction covers 16 rows x 64 contiguous bytes); step s of the
+// chunk's CK / 32 MFMA steps takes the lane's s-th group of 8 values, i.e. K positions
+// (CK / 4) (l / 16) + 8 s + (c0 c4 c1 c5 c2 c6 c3 c7), which is LDS block (CK / 32) (l / 16) + s
+// of the staged activation rows (the same layout as the 32 x 32 tiles').
+// ---------------------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// byte offsets (32-bit, from the field bases) of the lane's row data (bytes 16 q16 .. of each
+// chunk) and of its scale, for `row` of K values
+template <int PREC>
+__device__ __forceinline__ void rows16(int row, int K, int q16, uint32_t &qo, uint32_t &so) {
+    qo = (uint32_t)row * (uint32_t)(K * GgPrec<PREC>::BITS / 8) + 16u * q16;
+    if constexpr (PREC == MOEHIP_PREC_INT4) so = (uint32_t)row * (K / GG_KG) * 2 + 2u * (q16 >> 1);
+    else if constexpr (PREC == MOEHIP_PREC_INT8) so = (uint32_t)row * (K / GG_KG) * 2;
+    else if constexpr (PREC == MOEHIP_PREC_FP8) so = (uint32_t)(row >> 7) * (K >> 7) * 4;
+    else so = 0u;
+}
+
+struct WChunk16 {
+    uint4 q[4];
+    uint32_t s[4];
+};
+
+// chunk c at uniform field bases (qb, sb) + the lane's offsets; `live` false: the same loads at
+// `dum` with offset 0 (the workgroup's own dummy lines)
+template <int PREC>
+__device__ __forceinline__ void load_chunk16(WChunk16 &w, gu8 *qb, gu8 *sb, const uint32_t (&qo)[4],
+                                             const uint32_t (&so)[4], int c, bool live, gu8 *dum) {
+    gu8 *qbase = live ? qb : dum;
+    gu8 *sbase = live ? sb : dum;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t q = live ? qo[t] + (uint32_t)c * 64u : 0u;
+        w.q[t] = gld16(qbase + q);
+        uint32_t so2 = 0u;
+        if constexpr (PREC == MOEHIP_PREC_INT4) so2 = so[t] + (uint32_t)c * 4u;
+        else if constexpr (PREC == MOEHIP_PREC_INT8) so2 = so[t] + (uint32_t)c * 2u;
+        else if constexpr (PREC == MOEHIP_PREC_FP8) so2 = so[t] + (uint32_t)(c >> 1) * 4u;
+        so2 = live ? so2 : 0u;
+        if constexpr (PREC == MOEHIP_PREC_INT4 || PREC == MOEHIP_PREC_INT8)
+            w.s[t] = *(const __attribute__((address_space(1))) uint16_t *)(sbase + so2);
+        else if constexpr (PREC == MOEHIP_PREC_FP8)
+            w.s[t] = *(const __attribute__((address_space(1))) uint32_t *)(sbase + so2);
+        else
+            w.s[t] = 0u;
+    }
+}
+
+// one chunk of MFMAs for a wave: CK / 32 steps x NMT token tiles x 4 subtiles. A step reads its
+// A operands from LDS first, converts the 4 subtiles' weights while they arrive, then issues its
+// MFMAs; the scheduler is kept from moving work across steps (which would hold more registers).
+template <int PREC, int NMT>
+__device__ __forceinline__ void mma_chunk16(const WChunk16 &w, const uint16_t *s_a, DeqK dk, f32x4 (&d)[4][4]) {
+    constexpr int CK = GgPrec<PREC>::CK, S = CK / 32;
+    const int lane = threadIdx.x & 63;
+    const uint16_t *ap = s_a + (lane & 15) * GgChunk<CK>::LDA + 8 * S * (lane >> 4);
+#pragma unroll
+    for (int M = 0; M < S; ++M) {
+        f16x8 a[4];
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt) a[mt] = *reinterpret_cast<const f16x8 *>(ap + mt * 16 * GgChunk<CK>::LDA + 8 * M);
+        f16x8 b[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint4 qq[2] = {w.q[t], w.q[t]};
+            switch (M) {  // b_operand takes the step as a template argument
+                case 0: b[t] = b_operand<PREC, 0>(qq, w.s[t], dk); break;
+                case 1: b[t] = b_operand<PREC, (S > 1 ? 1 : 0)>(qq, w.s[t], dk); break;
+                case 2: b[t] = b_operand<PREC, (S > 2 ? 2 : 0)>(qq, w.s[t], dk); break;
+                default: b[t] = b_operand<PREC, (S > 3 ? 3 : 0)>(qq, w.s[t], dk); break;
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) d[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], b[t], d[mt][t], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Single-thread work of the persistent kernel (tickets, flags, waits) is done by wave 0 under a
+// branch on the wave index made uniform by v_readfirstlane. A branch on threadIdx.x == 0 is
+// lane-divergent: the compiler may then thread the other lanes of wave 0 past a later
+// thread-0 block straight into the next barrier, splitting the wave around the ticket loop.
+__device__ __forceinline__ bool ffn_wave0() { return uni((int)(threadIdx.x >> 6)) == 0; }
+
+// An up tile's flag: a plain store once every store of the workgroup so far is acknowledged (the
+// waiting down tiles run on the same XCD and poll its L2). Every lane of wave 0 writes the same
+// word: one write, no lane-divergent branch.
+__device__ __forceinline__ void ffn_flag(int *plan, int f) {
+    if (ffn_wave0()) *reinterpret_cast<volatile int *>(plan + FP_DONE + f) = 1;
+}
+__device__ __forceinline__ void ffn_release_now(int *plan, int f) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    ffn_flag(plan, f);
+}
+
+// The K loop of one pass (RING = 2). Queue order: X0 W0 X1 W1 | X2 | per chunk c: X(c + 3),
+// W(c + 2). Chunk c is in LDS buffer c % 2; X(c + 1) is stored during chunk c from the register
+// set it was loaded into two chunks earlier. Every load is issued (the compiler can then count
+// them); those past the last chunk read the workgroup's own lines at `dummy` (no weight or
+// activation traffic). `rel` >= 0: the flag of the previous tile, set once the prologue has
+// waited for its first activation chunk (every store issued before it by this workgroup is then
+// acknowledged).
+template <int PREC, int NMT, bool DOWN>
+__device__ __forceinline__ void k_loop16(gu8 *qb, gu8 *sb, const uint32_t (&qo)[4], const uint32_t (&so)[4], int nch,
+                                         const uint16_t *srcrow,
+                                         const int *ebrow, int emax, uint16_t *s_a, DeqK dk, f32x4 (&d)[4][4],
+                                         int *plan, int rel, gu8 *dummy) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    constexpr int NT = StgOf<CK, NMT>::NT;
+    constexpr int ABUF = GG_TOK * GgChunk<CK>::LDA;
+    WChunk16 wr[2];
+    XStage<CK, NT> xs[2];
+    // this workgroup's own lines: a line shared by every workgroup would be a hot spot
+    dummy += (size_t)(blockIdx.x % FF_DUMMY_WGS) * FF_DUMMY;
+    const uint16_t *xdum = (const uint16_t *)(uintptr_t)dummy;
+    const int *edum = (const int *)(uintptr_t)dummy;
+    // chunk c of the weights / activations, or the dummy lines past the last chunk
+    auto wload = [&](WChunk16 &w, int c) { load_chunk16<PREC>(w, qb, sb, qo, so, c, c < nch, dummy); };
+    auto xload = [&](XStage<CK, NT> &x, int c) {
+        const bool live = c < nch;
+        stage_load<CK, NT, DOWN>(live ? srcrow : xdum, live ? ebrow : edum, live ? c : 0, x);
+    };
+    xload(xs[0], 0);
+    wload(wr[0], 0);
+    xload(xs[1], 1);
+    wload(wr[1], 1);
+    stage_store<CK, NT, DOWN>(xs[0], emax, s_a);
+    xload(xs[0], 2);
+    __syncthreads();
+    if (rel >= 0) ffn_flag(plan, rel);
+#pragma unroll 1
+    for (int c0 = 0; c0 < nch; c0 += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int c = c0 + u;
+            if (c < nch) mma_chunk16<PREC, NMT>(wr[u], s_a + u * ABUF, dk, d);
+            // the buffer of chunk c + 1 was last read before the previous barrier
+            stage_store<CK, NT, DOWN>(xs[(u + 1) & 1], emax, s_a + ((u + 1) & 1) * ABUF);
+            xload(xs[(u + 1) & 1], c + 3);
+            wload(wr[u], c + 2);
+            if (c < nch) __syncthreads();
+        }
+    }
+}
+
+// the 4 subtiles' K loop for NMT = ceil(tokens / 16) token tiles (a uniform switch)
+template <int PREC, bool DOWN>
+__device__ __forceinline__ void k_loop16_n(int nmt, gu8 *qb, gu8 *sb, const uint32_t (&qo)[4], const uint32_t (&so)[4],
+                                           int nch,
+                                           const uint16_t *src32, const int *eb32, int emax32,
+                                           const uint16_t *src64, const int *eb64, int emax64, uint16_t *s_a, DeqK dk,
+                                           f32x4 (&d)[4][4], int *plan, int rel, gu8 *dummy) {
+    constexpr int CK = GgPrec<PREC>::CK;
+#define FF_LOOP(N)                                                                                         \
+    k_loop16<PREC, N, DOWN>(qb, sb, qo, so, nch, StgOf<CK, N>::NT == 32 ? src32 : src64,                   \
+                            StgOf<CK, N>::NT == 32 ? eb32 : eb64, StgOf<CK, N>::NT == 32 ? emax32 : emax64, \
+                            s_a, dk, d, plan, rel, dummy)
+    if (nmt == 1) FF_LOOP(1);
+    else if (nmt == 2) FF_LOOP(2);
+    else if (nmt == 3) FF_LOOP(3);
+    else FF_LOOP(4);
+#undef FF_LOOP
+}
+
+// largest value over each aligned row of 16 lanes, in every lane of the row (v >= 0)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+
+template <int PREC>
+struct FfnShared {
+    uint16_t a[2 * GG_TOK * GgChunk<GgPrec<PREC>::CK>::LDA];
+    float f[GG_TOK];
+    int i[GG_TOK];
+    float mx[4][GG_TOK];
+    int t, ok;
+};
+
+// up tile: h columns nb * 128 + 32 w + 16 t + (lane % 16), t = 0, 1, of unit (e, m); subtiles
+// 0, 1 = their gate rows, 2, 3 = their up rows. Its stores are released later (the caller passes
+// its flag on as `rel`).
+// the next tile's entry, read once the ticket taken at this tile's start is published (wave 0
+// holds it in tn); the caller's loop ends at t >= nall
+struct FfnNext {
+    int t;
+    int4 e0, e1;
+};
+template <int PREC>
+__device__ __forceinline__ void ffn_next_publish(FfnShared<PREC> &sh, int tn) {
+    if (ffn_wave0()) sh.t = uni(tn);
+}
+__device__ __forceinline__ void ffn_next_read(const FfnArgs &a, int t, int nall, int vx, FfnNext &nx) {
+    nx.t = t;
+    const int tc = t < nall ? t : 0;
+    const int4 *q = a.list + ((size_t)vx * a.lmax + tc) * 2;
+    nx.e0 = q[0];
+    nx.e1 = q[1];
+}
+
+template <int PREC>
+__device__ __forceinline__ void ffn_up(const FfnArgs &a, int4 en, int u, FfnShared<PREC> &sh, int rel, int tn,
+                                       int nall, int vx, FfnNext &nx) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    const int e = en.x, p0 = en.y, mn = en.z, nb = en.w & 0xffff;
+    const int nmt = (mn + 15) >> 4;
+    gu8 *qb = record_ptr(uni64(a.tab[4 * e + 0]));
+    gu8 *sb = record_ptr(uni64(a.tab[4 * e + 1]));
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    const int col0 = nb * 128 + 32 * wave;
+    uint32_t qo[4], so[4];
+    rows16<PREC>(col0 + j, a.H, g, qo[0], so[0]);
+    rows16<PREC>(col0 + 16 + j, a.H, g, qo[1], so[1]);
+    rows16<PREC>(a.I + col0 + j, a.H, g, qo[2], so[2]);
+    rows16<PREC>(a.I + col0 + 16 + j, a.H, g, qo[3], so[3]);
+    // the token of this thread for 64-token staging (tid / 4: also its exponent slot) and 32-token
+    const int s64 = tid >> 2, s32 = tid >> 3;
+    const int x64 = a.xrow[p0 + (s64 < mn ? s64 : 0)];
+    const int x32 = a.xrow[p0 + (s32 < mn ? s32 : 0)];
+    if ((tid & 3) == 0) sh.i[s64] = s64 < mn ? a.xep[p0 + s64] : 0;
+    f32x4 d[4][4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) d[p][q] = f32x4{};
+    k_loop16_n<PREC, false>(nmt, qb, sb, qo, so, a.H / CK, a.x + (size_t)x32 * a.H, nullptr, 0, a.x + (size_t)x64 * a.H,
+                            nullptr, 0, sh.a, a.dk, d, a.plan, rel, a.dummy);
+    ffn_next_publish(sh, tn);
+    // h = silu(gate) * up with the token's 2^xe, then the largest |h| per token over the tile
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        if (mt >= nmt) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * mt + 4 * g + r;
+            const float f = ldexpf(1.0f, sh.i[tok]);
+            const float h0 = silu_mul(d[mt][0][r] * f, d[mt][2][r] * f);
+            const float h1 = silu_mul(d[mt][1][r] * f, d[mt][3][r] * f);
+            d[mt][0][r] = h0;
+            d[mt][1][r] = h1;
+            const float mx = row16_max(fmaxf(fabsf(h0), fabsf(h1)));
+            if (j == 0) sh.mx[wave][tok] = mx;
+        }
+    }
+    __syncthreads();
+    ffn_next_read(a, uni(sh.t), nall, vx, nx);
+    if (ffn_wave0()) {  // tid < GG_TOK
+        const float mx = fmaxf(fmaxf(sh.mx[0][tid], sh.mx[1][tid]), fmaxf(sh.mx[2][tid], sh.mx[3][tid]));
+        const int eb = row_exp(mx);
+        sh.i[tid] = eb;
+        if (tid < mn) a.hbe[(size_t)(p0 + tid) * a.NBU + nb] = eb;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        if (mt >= nmt) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * mt + 4 * g + r;
+            if (tok < mn) {
+                const float sc = ldexpf(1.0f, -sh.i[tok]);
+                uint16_t *hr = a.h16 + (size_t)(p0 + tok) * a.I + col0 + j;
+                hr[0] = f32_to_f16_rne(d[mt][0][r] * sc);
+                hr[16] = f32_to_f16_rne(d[mt][1][r] * sc);
+            }
+        }
+    }
+    // the tile's flag once its stores are acknowledged: the down tiles of the unit wait for it
+    ffn_release_now(a.plan, u * a.NBU + nb);
+}
+
+// down tile: output rows nb * 256 + 64 w + 16 t + (lane % 16), t = 0 .. 3, of unit (e, m)
+template <int PREC>
+__device__ __forceinline__ void ffn_down(const FfnArgs &a, int4 en, int u, FfnShared<PREC> &sh, int tn, int nall,
+                                         int vx, FfnNext &nx) {
+    constexpr int CK = GgPrec<PREC>::CK;
+    const int e = en.x, p0 = en.y, mn = en.z, nb = en.w & 0xffff;
+    const int nmt = (mn + 15) >> 4;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, g = lane >> 4;
+    if (en.w & FF_ZERO) {  // expert without a record: its pairs contribute nothing
+        for (int i = tid; i < mn * GG_ROWS; i += 256)
+            a.y[(size_t)(p0 + i / GG_ROWS) * a.H + nb * GG_ROWS + i % GG_ROWS] = 0.f;
+        ffn_next_publish(sh, tn);
+        __syncthreads();
+        ffn_next_read(a, uni(sh.t), nall, vx, nx);
+        return;
+    }
+    gu8 *qb = record_ptr(uni64(a.tab[4 * e + 2]));
+    gu8 *sb = record_ptr(uni64(a.tab[4 * e + 3]));
+    const int row0 = nb * GG_ROWS + 64 * wave;
+    uint32_t qo[4], so[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) rows16<PREC>(row0 + 16 * t + j, a.I, g, qo[t], so[t]);
+    if (ffn_wave0()) {  // lane nb polls the flag of up tile nb (non-temporal: through the XCD's L2)
+        const int *fl = a.plan + FP_DONE + u * a.NBU + min(lane, a.NBU - 1);
+        int ok = 0, nap = 1;
+        for (int it = 0; it < FF_SPIN; ++it) {
+            const int v = __builtin_nontemporal_load(fl);
+            asm volatile("" ::: "memory");
+            if (__builtin_amdgcn_ballot_w64(v != 1) == 0ull) {
+                ok = 1;
+                break;
+            }
+            backoff(nap, 2);
+        }
+        if (!ok) flag_error(reinterpret_cast<uint32_t *>(a.plan + FP_ERR));
+        sh.ok = ok;
+    }
+    __syncthreads();
+    const bool ok = sh.ok != 0;
+    // per token (tid / 4): the largest block exponent of its h and w * 2^that; a 32-token staging
+    // thread (tid / 8) reads the exponent of its token back from LDS
+    const int s64 = tid >> 2, s32 = tid >> 3;
+    const size_t pr = (size_t)(p0 + (s64 < mn ? s64 : 0));
+    int emax = -1000;
+    for (int c = 0; c < a.NBU; ++c) emax = max(emax, __builtin_nontemporal_load(a.hbe + pr * a.NBU + c));
+    if ((tid & 3) == 0) {
+        sh.i[s64] = emax;
+        sh.f[s64] = !ok ? __builtin_nanf("") : (s64 < mn ? a.wp[pr] * ldexpf(1.0f, emax) : 0.f);
+    }
+    __syncthreads();
+    const size_t p32 = (size_t)(p0 + (s32 < mn ? s32 : 0));
+    f32x4 d[4][4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) d[p][q] = f32x4{};
+    k_loop16_n<PREC, true>(nmt, qb, sb, qo, so, a.I / CK, a.h16 + p32 * a.I, a.hbe + p32 * a.NBU, sh.i[s32],
+                           a.h16 + pr * a.I, a.hbe + pr * a.NBU, emax, sh.a, a.dk, d, a.plan, -1, a.dummy);
+    ffn_next_publish(sh, tn);
+    __syncthreads();
+    ffn_next_read(a, uni(sh.t), nall, vx, nx);
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        if (mt >= nmt) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 16 * mt + 4 * g + r;
+            if (tok >= mn) continue;
+            const float f = sh.f[tok];
+            float *yr = a.y + (size_t)(p0 + tok) * a.H + row0 + j;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) yr[16 * t] = f * d[mt][t][r];
+        }
+    }
+}
+
+// Tickets are taken one tile ahead: wave 0 requests the next one when a tile starts (the whole
+// wave runs the atomic, lane 0 adding 1) and passes it through LDS when the tile ends. No wait
+// can deadlock: a down tile's up tiles are earlier in the queue, and the waiting workgroup with
+// the earliest down tile waits only for tiles held (run or reserved) by workgroups whose current
+// tiles are earlier still, none of them waiting. An up tile's release is deferred into the next
+// tile's prologue; before a down tile (which may wait) or without a next K loop it is done at once.
+template <int PREC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_ffn(FfnArgs a) {
+    __shared__ __align__(16) FfnShared<PREC> sh;
+    const int vx = blockIdx.x & 7;
+    const int nall = a.phase == 0 ? a.plan[FP_NUP + vx] : a.plan[FP_NALL + vx];
+    uint32_t *ctr = reinterpret_cast<uint32_t *>(a.plan + FP_TICK + FP_TSTRIDE * (a.phase == 1 ? 8 + vx : vx));
+    const uint32_t one = (threadIdx.x & 63) == 0 ? 1u : 0u;
+    if (ffn_wave0()) sh.t = uni((int)add_co32(ctr, one));
+    __syncthreads();
+    FfnNext cur;
+    ffn_next_read(a, uni(sh.t), nall, vx, cur);
+    int pend = -1;  // flag of this workgroup's last up tile, not yet set
+    while (cur.t < nall) {
+        __syncthreads();  // every thread has read sh.t
+        int tn = 0;
+        if (ffn_wave0()) tn = (int)add_co32(ctr, one);
+        const int4 en = cur.e0;
+        const int u = cur.e1.x;
+        FfnNext nx;
+        if (en.w >= 0 && (en.w & FF_SKIP) == 0) {
+            ffn_up<PREC>(a, en, u, sh, -1, tn, nall, vx, nx);
+        } else {
+            if (pend >= 0) ffn_release_now(a.plan, pend);
+            pend = -1;
+            if ((en.w & FF_SKIP) == 0) {
+                ffn_down<PREC>(a, en, u, sh, tn, nall, vx, nx);
+            } else {
+                ffn_next_publish(sh, tn);
+                __syncthreads();
+                ffn_next_read(a, uni(sh.t), nall, vx, nx);
+            }
+        }
+        cur = nx;
+    }
+    if (pend >= 0) ffn_release_now(a.plan, pend);
+}
+
 // out[t] = sum over slots j (in order) of y[rank[t k + j]] (+ out if accumulate) (+ add):
 // one workgroup per token, 8 consecutive columns per thread
 template <int DT>
 __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__ y, const int32_t *__restrict__ rank,
                                                        int T, int k, int H, const void *__restrict__ add,
-                                                       void *__restrict__ out, int accumulate) {
+                                                       void *__restrict__ out, int accumulate, int *__restrict__ clear,
+                                                       int nclear, int cstride) {
     const int t = blockIdx.x;
+    // words left zero for the next launch (a prefill layer's routing counters, read before this one)
+    if (clear != nullptr && t == 0)
+        for (int i = threadIdx.x; i < nclear; i += 256) clear[(size_t)i * cstride] = 0;
     for (int c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
         float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         for (int jj = 0; jj < k; ++jj) {
@@ -866,8 +1475,143 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// Routing of a prefill chunk once its logits are in (16-bit activations, E <= 1024, k <= 32): one
+// wave per token takes the softmax top-k (renormalised or not) exactly as moehip_router_topk,
+// appends the token's slots to its experts' buckets (agent-scope counters: slot order within an
+// expert depends on scheduling, the results do not, since every pair's products and every
+// token's slot-order sum are independent of it), and for bf16 activations writes the fp16 copy
+// of the token's row scaled by its power of two (the MFMA tiles' operand, as k_prep). The next
+// launch (k_route_place) turns the buckets into the expert-sorted pair order of moehip_dispatch;
+// the combine at the end of the layer leaves the counters at zero again.
+// ---------------------------------------------------------------------------------------
+constexpr int RP_MAXE = 1024;   // experts at most
+constexpr int RP_STRIDE = 32;   // words between two experts' counters: a 128-byte line each (returning
+                                // atomics on counters sharing lines queue on one memory channel)
+constexpr int RP_DONE = RP_MAXE * RP_STRIDE;  // words of the counter area
+
+// exclusive scan of v over the 256 threads of a workgroup (s: 4 words of LDS), total in tot
+__device__ __forceinline__ int block_excl_scan256(int v, int *s, int &tot) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += o;
+    }
+    s[wave] = __builtin_amdgcn_readlane(incl, 63);
+    __syncthreads();
+    int base = 0;
+    tot = 0;
+    for (int w = 0; w < 4; ++w) {
+        if (w < wave) base += s[w];
+        tot += s[w];
+    }
+    __syncthreads();
+    return base + incl - v;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_route_post(const void *__restrict__ logits, const uint16_t *__restrict__ x,
+                                                    int T, int H, int E, int k, int renorm, int64_t *__restrict__ idx,
+                                                    void *__restrict__ wout, float *__restrict__ w32,
+                                                    int *__restrict__ cnt, int *__restrict__ bucket,
+                                                    int *__restrict__ xe, uint16_t *__restrict__ x16, int prep) {
+    __shared__ float s_p[4][32];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + wave;
+    if (t < T) {  // the whole wave
+        int myc;
+        float p;
+        topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_p[wave], myc, p);
+        if (lane < k) {
+            const size_t q = (size_t)t * k + lane;
+            idx[q] = myc;
+            if (wout != nullptr) st_act<DT>(wout, q, p);
+            w32[q] = rnd_act<DT>(p);
+            const int r = (int)add_co32(reinterpret_cast<uint32_t *>(cnt + myc * RP_STRIDE), 1u);
+            // r < T whenever the counters started at zero (each token takes an expert once); the
+            // test keeps a corrupted counter from writing past the bucket
+            if (r < T) bucket[(size_t)myc * T + r] = (int)q;
+        }
+        if (prep) {  // the token's row: fp16 with max |x| in [2^14, 2^15) (k_prep's rule)
+            const uint4 *src = reinterpret_cast<const uint4 *>(x + (size_t)t * H);
+            uint4 *dst = reinterpret_cast<uint4 *>(x16 + (size_t)t * H);
+            float m = 0.f;
+            for (int c = lane; c < H / 8; c += 64) {
+                const uint4 v = src[c];
+                const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf16_lo(wd[i])), fabsf(bf16_hi(wd[i]))));
+            }
+            m = wave_max(m);
+            const int e = row_exp(m);
+            const float sc = ldexpf(1.0f, -e);
+            for (int c = lane; c < H / 8; c += 64) {
+                const uint4 v = src[c];
+                dst[c] = make_uint4(pack_h2(bf16_lo(v.x) * sc, bf16_hi(v.x) * sc), pack_h2(bf16_lo(v.y) * sc, bf16_hi(v.y) * sc),
+                                    pack_h2(bf16_lo(v.z) * sc, bf16_hi(v.z) * sc), pack_h2(bf16_lo(v.w) * sc, bf16_hi(v.w) * sc));
+            }
+            if (lane == 0) xe[t] = e;
+        }
+    }
+}
+
+// the expert-sorted pair order of moehip_dispatch from the buckets (counts, offsets, sorted_pos,
+// rank): every workgroup scans the E counters (thread i holds experts 4 i .. 4 i + 3) and places
+// its 256 positions, q belonging to the expert e with offsets[e] <= q < offsets[e + 1]
+__global__ __launch_bounds__(256) void k_route_place(const int *__restrict__ cnt, const int *__restrict__ bucket,
+                                                     int T, int k, int E, int32_t *__restrict__ counts,
+                                                     int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
+                                                     int32_t *__restrict__ rank) {
+    __shared__ int s_off[RP_MAXE + 1];
+    __shared__ int s_scan[4];
+    int c4[4], loc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = 4 * threadIdx.x + i;
+        c4[i] = e < E ? min(cnt[e * RP_STRIDE], T) : 0;
+        loc += c4[i];
+    }
+    int total = 0;
+    int run = block_excl_scan256(loc, s_scan, total);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = 4 * threadIdx.x + i;
+        if (e < E) {
+            s_off[e] = run;
+            if (blockIdx.x == 0) {
+                offsets[e] = run;
+                counts[e] = c4[i];
+            }
+        }
+        run += c4[i];
+    }
+    if (threadIdx.x == 0) {
+        s_off[E] = total;
+        if (blockIdx.x == 0) offsets[E] = total;
+    }
+    __syncthreads();
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= T * k) return;
+    if (q >= total) {
+        sorted_pos[q] = -1;
+        return;
+    }
+    int lo = 0, hi = E;  // s_off[lo] <= q < s_off[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid] <= q) lo = mid;
+        else hi = mid;
+    }
+    const int pr = bucket[(size_t)lo * T + (q - s_off[lo])];
+    const bool ok = pr >= 0 && pr < T * k;
+    sorted_pos[q] = ok ? pr : -1;
+    if (ok) rank[pr] = q;
+}
+
 struct GgLayout {
-    size_t xe, x16, h, h16, he, y, items, total;
+    size_t xe, x16, h, h16, he, y, items, hbe, plan, list, pairs, dummy, total;
+    int lmax;
 };
 static GgLayout gg_layout(int T, int k, int H, int I) {
     auto al = [](size_t v) { return (v + 255) / 256 * 256; };
@@ -888,6 +1632,19 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     off = al(off + NP * H * 4);
     L.items = off;  // one work list per record precision
     off = al(off + (size_t)GV_MAXP * (NP + 1) * 4);
+    // the persistent FFN's block exponents of h, plan words and tile queues
+    const int NBU = I / 128, NBD = H / GG_ROWS;
+    L.lmax = ffn_lmax((int)NP, NBU, NBD);
+    L.hbe = off;
+    off = al(off + NP * NBU * 4);
+    L.plan = off;
+    off = al(off + (size_t)(FP_DONE + (size_t)ffn_max_units((int)NP) * max(NBU, 1)) * 4);
+    L.list = off;
+    off = al(off + (size_t)8 * L.lmax * 32);
+    L.pairs = off;  // xrow, xep, wp: NP words each
+    off = al(off + NP * 12);
+    L.dummy = off;
+    off = al(off + (size_t)FF_DUMMY_WGS * FF_DUMMY);
     L.total = off;
     return L;
 }
@@ -912,6 +1669,45 @@ static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *
                         DeqK dk, int zero_missing) {
     hipLaunchKernelGGL((k_gemm_down<PREC>), g, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk,
                        zero_missing);
+}
+
+// the persistent FFN of one record table: plan, then one workgroup per CU slot (at most)
+template <int PREC>
+static int ffn_grid() {
+    static int grid[64];  // per device, computed once
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (grid[dev] == 0) {
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(k_ffn<PREC>), 256, 0) !=
+                hipSuccess)
+            return 0;
+        grid[dev] = max(8, cus * per_cu / 8 * 8);
+    }
+    return grid[dev];
+}
+
+template <int PREC>
+static void launch_ffn(hipStream_t st, FfnArgs a, const int64_t *tab, int E, int zero_missing) {
+    a.tab = tab;
+    const int grid = ffn_grid<PREC>();
+    const bool one = getenv("MOEHIP_FFN_TWO_LAUNCHES") == nullptr;
+    // one launch: a unit's down tiles a round of up tiles after its own; two: every up tile first
+    int lag = one ? (grid / 8 + a.NBU - 1) / a.NBU + 1 : (1 << 30);
+    if (const char *lv = getenv("MOEHIP_FFN_LAG")) lag = atoi(lv);
+    hipLaunchKernelGGL(k_ffn_plan, dim3(1), dim3(1024), 0, st, a.offsets, tab, E, a.NBU, a.NBD, a.lmax, zero_missing,
+                       lag, a.plan, const_cast<int4 *>(a.list), a.sorted_pos, a.k, a.w, a.xe,
+                       const_cast<int *>(a.xrow), const_cast<float *>(a.wp), const_cast<int *>(a.xep));
+    if (one) {
+        a.phase = -1;
+        hipLaunchKernelGGL(k_ffn<PREC>, dim3(grid), dim3(256), 0, st, a);
+    } else {
+        a.phase = 0;
+        hipLaunchKernelGGL(k_ffn<PREC>, dim3(grid), dim3(256), 0, st, a);
+        a.phase = 1;
+        hipLaunchKernelGGL(k_ffn<PREC>, dim3(grid), dim3(256), 0, st, a);
+    }
 }
 
 // batched GEMV launch geometry for rows of K values: G = 2^lg lanes per row, CPL chunks per lane,
@@ -1006,7 +1802,8 @@ static bool gg_prec_ok(int prec) {
 static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T, int H, int I, int k,
                   int E, int gs, const int32_t *offsets, const int32_t *sorted_pos, const int32_t *rank, const float *w,
                   void *out, const void *add, int accumulate, void *ws, size_t ws_bytes, void *stream, int zero_missing,
-                  int gemv, const int32_t *items_in = nullptr) {
+                  int gemv, const int32_t *items_in = nullptr, bool x16_ready = false, int *clear = nullptr,
+                  int nclear = 0, int cstride = 1) {
     MOEHIP_REQUIRE(tabs && x && offsets && sorted_pos && rank && w && out && ws && precs, "grouped_gemm: null pointer");
     MOEHIP_REQUIRE(P >= 1 && P <= 4, "grouped_gemm: %d record tables (1..4)", P);
     for (int p = 0; p < P; ++p) MOEHIP_REQUIRE(gg_prec_ok(precs[p]), "grouped_gemm: record precision %d", precs[p]);
@@ -1034,7 +1831,45 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     const int *xea = bf ? xe : nullptr;
     // bf16 activations: fp16 with a per-token power of two for the MFMA tiles; the GEMVs read
     // the bf16 rows themselves and scale each chunk
-    if (bf && !gemv) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
+    if (bf && !gemv && !x16_ready) hipLaunchKernelGGL(k_prep, dim3((T + 3) / 4), dim3(256), 0, st, xs, T, H, xe, x16);
+    // MFMA tiles: the separate up / h / down launches below, or (MOEHIP_GEMM_FUSED set, where
+    // workgroups are dealt to the XCDs round robin) the persistent FFN, one launch per record table
+    const bool fused = !gemv && xcd_dispatch_ok() && getenv("MOEHIP_GEMM_FUSED") != nullptr;
+    if (fused) {
+        FfnArgs fa{};
+        fa.x = xa;
+        fa.xe = xea;
+        fa.H = H;
+        fa.I = I;
+        fa.k = k;
+        fa.NBU = I / 128;
+        fa.NBD = H / GG_ROWS;
+        fa.lmax = L.lmax;
+        fa.offsets = offsets;
+        fa.sorted_pos = sorted_pos;
+        fa.w = w;
+        fa.h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
+        fa.hbe = reinterpret_cast<int *>(wsb + L.hbe);
+        fa.y = y;
+        fa.plan = reinterpret_cast<int *>(wsb + L.plan);
+        fa.list = reinterpret_cast<const int4 *>(wsb + L.list);
+        fa.dummy = (gu8 *)(uintptr_t)(wsb + L.dummy);
+        fa.xrow = reinterpret_cast<const int *>(wsb + L.pairs);
+        fa.xep = reinterpret_cast<const int *>(wsb + L.pairs + (size_t)NP * 4);
+        fa.wp = reinterpret_cast<const float *>(wsb + L.pairs + (size_t)NP * 8);
+        fa.dk = dk;
+        for (int p = 0; p < P; ++p) {
+            const int64_t *tab = tabs + (size_t)p * E * 4;
+            const int zm = zero_missing && P == 1;
+            switch (precs[p]) {
+                case MOEHIP_PREC_INT4: launch_ffn<MOEHIP_PREC_INT4>(st, fa, tab, E, zm); break;
+                case MOEHIP_PREC_INT8: launch_ffn<MOEHIP_PREC_INT8>(st, fa, tab, E, zm); break;
+                case MOEHIP_PREC_FP8: launch_ffn<MOEHIP_PREC_FP8>(st, fa, tab, E, zm); break;
+                case MOEHIP_PREC_F16: launch_ffn<MOEHIP_PREC_F16>(st, fa, tab, E, zm); break;
+                default: launch_ffn<MOEHIP_PREC_BF16>(st, fa, tab, E, zm); break;
+            }
+        }
+    }
     // the work list: the caller's (written by moehip_batch_route_decide) or built here
     int32_t *items = reinterpret_cast<int32_t *>(wsb + L.items);
     if (gemv && items_in == nullptr)
@@ -1043,7 +1878,7 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     for (int p = 0; p < P && gemv; ++p)
         launch_gv_prec(precs[p], bf ? 2 : 1, items + (size_t)p * (NP + 1), NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
-    for (int p = 0; p < P && !gemv; ++p) {
+    for (int p = 0; p < P && !gemv && !fused; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         switch (precs[p]) {
             case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
@@ -1056,11 +1891,11 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
     int *he = reinterpret_cast<int *>(wsb + L.he);
     // the MFMA down kernels read h as fp16 with a per-pair power of two; the GEMVs read the fp32 rows
-    if (!gemv) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
+    if (!gemv && !fused) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
     for (int p = 0; p < P && gemv; ++p)
         launch_gv_prec(precs[p], 0, items + (size_t)p * (NP + 1), NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
                        y, w, dk);
-    for (int p = 0; p < P && !gemv; ++p) {
+    for (int p = 0; p < P && !gemv && !fused; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         const int zm = zero_missing && P == 1;
         switch (precs[p]) {
@@ -1073,10 +1908,10 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     }
     if (xdtype == MOEHIP_DT_F16)
         hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_F16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
-                           accumulate);
+                           accumulate, clear, nclear, cstride);
     else
         hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_BF16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
-                           accumulate);
+                           accumulate, clear, nclear, cstride);
     return check_launch("grouped_gemm");
 }
 
@@ -1086,6 +1921,82 @@ extern "C" int moehip_grouped_gemm(int prec, const int64_t *tab, const void *x, 
                                    void *ws, size_t ws_bytes, void *stream) {
     return gg_run(1, &prec, tab, x, xdtype, T, H, I, k, E, gs, offsets, sorted_pos, rank, w, out, add, accumulate, ws,
                   ws_bytes, stream, 1, 0);
+}
+
+// A prefill layer's workspace: the routing counters at offset 0 (zero at first use; every launch
+// leaves them zero; at a fixed place whatever the chunk's length), the buckets, counts, offsets,
+// sorted_pos and rank of the chunk, then the grouped GEMM's workspace
+struct RpLayout {
+    size_t cnt, bucket, counts, offsets, sorted, rank, gg, total;
+};
+static RpLayout rp_layout(int T, int k, int H, int I, int E) {
+    auto al = [](size_t v) { return (v + 255) / 256 * 256; };
+    RpLayout L;
+    size_t off = 0;
+    L.cnt = off;
+    off = al(off + (RP_DONE + 64) * 4);
+    L.bucket = off;
+    off = al(off + (size_t)E * T * 4);
+    L.counts = off;
+    off = al(off + (size_t)E * 4);
+    L.offsets = off;
+    off = al(off + (size_t)(E + 1) * 4);
+    L.sorted = off;
+    off = al(off + (size_t)T * k * 4);
+    L.rank = off;
+    off = al(off + (size_t)T * k * 4);
+    L.gg = off;
+    off = al(off + gg_layout(T, k, H, I).total);
+    L.total = off;
+    return L;
+}
+
+extern "C" size_t moehip_prefill_layer_workspace_bytes(int T, int k, int H, int I, int E) {
+    if (T <= 0 || k <= 0 || H <= 0 || I <= 0 || E <= 0) return 0;
+    return rp_layout(T, k, H, I, E).total;
+}
+
+extern "C" int moehip_prefill_layer(int prec, const int64_t *tab, const void *x, const void *Wr, int xdtype, int T,
+                                    int H, int I, int k, int E, int gs, int renorm, void *logits, int64_t *idx,
+                                    void *w, float *w32, void *out, const void *add, int accumulate, void *ws,
+                                    size_t ws_bytes, void *stream) {
+    MOEHIP_REQUIRE(tab && x && Wr && logits && idx && w32 && out && ws, "prefill_layer: null pointer");
+    MOEHIP_REQUIRE(xdtype == MOEHIP_DT_F16 || xdtype == MOEHIP_DT_BF16, "prefill_layer: activation dtype %d", xdtype);
+    MOEHIP_REQUIRE(T > 0 && E > 0 && E <= RP_MAXE && k > 0 && k <= 32 && k <= E && H % 512 == 0 && H % GG_ROWS == 0 &&
+                       I % 128 == 0,
+                   "prefill_layer: T=%d E=%d k=%d H=%d I=%d (E <= 1024, k <= 32, H a multiple of 512, I of 128)", T, E,
+                   k, H, I);
+    MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)Wr % 16) == 0, "prefill_layer: x and Wr must be 16-byte aligned");
+    const RpLayout R = rp_layout(T, k, H, I, E);
+    const GgLayout G = gg_layout(T, k, H, I);
+    MOEHIP_REQUIRE(ws_bytes >= R.total && ((uintptr_t)ws % 256) == 0, "prefill_layer: workspace %zu < %zu bytes (or unaligned)",
+                   ws_bytes, R.total);
+    hipStream_t st = as_stream(stream);
+    uint8_t *wsb = reinterpret_cast<uint8_t *>(ws);
+    uint8_t *wgg = wsb + R.gg;  // the grouped GEMM's workspace (its x16 / xe written by the routing launch)
+    launch_router_logits(x, Wr, T, H, E, xdtype, logits, st);
+    int *cnt = reinterpret_cast<int *>(wsb + R.cnt);
+    int *bucket = reinterpret_cast<int *>(wsb + R.bucket);
+    int32_t *counts = reinterpret_cast<int32_t *>(wsb + R.counts);
+    int32_t *offsets = reinterpret_cast<int32_t *>(wsb + R.offsets);
+    int32_t *sorted = reinterpret_cast<int32_t *>(wsb + R.sorted);
+    int32_t *rank = reinterpret_cast<int32_t *>(wsb + R.rank);
+    int *xe = reinterpret_cast<int *>(wgg + G.xe);
+    uint16_t *x16 = reinterpret_cast<uint16_t *>(wgg + G.x16);
+    const uint16_t *xs = reinterpret_cast<const uint16_t *>(x);
+    const int prep = xdtype == MOEHIP_DT_BF16;
+    const dim3 grid((T + 3) / 4);
+    if (xdtype == MOEHIP_DT_F16)
+        hipLaunchKernelGGL((k_route_post<MOEHIP_DT_F16>), grid, dim3(256), 0, st, logits, xs, T, H, E, k, renorm, idx, w,
+                           w32, cnt, bucket, xe, x16, prep);
+    else
+        hipLaunchKernelGGL((k_route_post<MOEHIP_DT_BF16>), grid, dim3(256), 0, st, logits, xs, T, H, E, k, renorm, idx, w,
+                           w32, cnt, bucket, xe, x16, prep);
+    hipLaunchKernelGGL(k_route_place, dim3((T * k + 255) / 256), dim3(256), 0, st, cnt, bucket, T, k, E, counts, offsets,
+                       sorted, rank);
+    // the combine (after every reader of the counters) leaves them zero
+    return gg_run(1, &prec, tab, x, xdtype, T, H, I, k, E, gs, offsets, sorted, rank, w32, out, add, accumulate, wgg,
+                  G.total, stream, 1, 0, nullptr, true, cnt, E, RP_STRIDE);
 }
 
 extern "C" int moehip_grouped_gemm_multi(int P, const int *precs, const int64_t *tabs, const void *x, int xdtype, int T,

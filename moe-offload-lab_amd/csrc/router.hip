@@ -333,7 +333,7 @@ using namespace moehip;
 
 // logits (T, E) = x Wr^T rounded to dtype: MFMA tiles from 4 tokens (16-bit, H a multiple of 512,
 // 16-byte aligned rows), VALU GEMVs otherwise
-static void launch_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits,
+void moehip::launch_router_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits,
                           hipStream_t st) {
     const int vec16 = (H % 8 == 0) && ((uintptr_t)Wr % 16) == 0 && ((uintptr_t)x % 16) == 0;
     const dim3 g1((E + 3) / 4, (T + ROUTER_TT - 1) / ROUTER_TT);
@@ -361,7 +361,7 @@ extern "C" int moehip_router_topk(const void *x, const void *Wr, int T, int H, i
     MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E,
                    "router_topk: bad sizes T=%d H=%d E=%d k=%d", T, H, E, k);
     hipStream_t st = as_stream(stream);
-    launch_logits(x, Wr, T, H, E, dtype, logits, st);
+    launch_router_logits(x, Wr, T, H, E, dtype, logits, st);
     switch (dtype) {
         case MOEHIP_DT_F16:
             hipLaunchKernelGGL((k_router_topk<MOEHIP_DT_F16>), dim3(T), dim3(64), 0, st, logits, T, E, k, renorm, idx, w, w32);
@@ -381,7 +381,7 @@ extern "C" int moehip_router_logits(const void *x, const void *Wr, int T, int H,
     MOEHIP_REQUIRE(x && Wr && logits, "router_logits: null pointer");
     MOEHIP_REQUIRE(dtype >= MOEHIP_DT_F16 && dtype <= MOEHIP_DT_F32, "router_logits: bad dtype %d", dtype);
     MOEHIP_REQUIRE(T > 0 && H > 0 && E > 0 && E <= 1024, "router_logits: bad sizes T=%d H=%d E=%d", T, H, E);
-    launch_logits(x, Wr, T, H, E, dtype, logits, as_stream(stream));
+    launch_router_logits(x, Wr, T, H, E, dtype, logits, as_stream(stream));
     return check_launch("router_logits");
 }
 

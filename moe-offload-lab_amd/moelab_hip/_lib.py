@@ -77,6 +77,9 @@ _SIGS = {
     "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                              ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemm_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
+    "moehip_prefill_layer": ([_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                              ctypes.c_size_t, _vp], _i),
+    "moehip_prefill_layer_workspace_bytes": ([_i, _i, _i, _i, _i], ctypes.c_size_t),
     "moehip_grouped_gemm_multi": ([_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
                                    _vp, ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemv_multi": ([_i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,

@@ -40,6 +40,9 @@ class GroupedTokens:
         self.rank = torch.empty(max_tokens * k, dtype=torch.int32, device=self.device)
         self.offs = torch.tensor(field_offsets(layout), dtype=torch.int64, device=self.device)
         self._route_bufs = None
+        # the one-call layer (moehip_prefill_layer): its own workspace, zeroed once (routing counters)
+        n = lib.moehip_prefill_layer_workspace_bytes(max_tokens, k, self.H, self.I, num_experts)
+        self.ws_layer = torch.zeros(n, dtype=torch.uint8, device=self.device)
 
     def route(self, x: torch.Tensor, Wr: torch.Tensor, renorm: bool):
         """Router for the T rows of x (moehip_router_topk): returns (logits, idx, w, w32) views of
@@ -60,10 +63,29 @@ class GroupedTokens:
         return logits, idx, w, w32
 
     def layer(self, x: torch.Tensor, Wr: torch.Tensor, renorm: bool, tab: torch.Tensor, out: torch.Tensor,
-              add: torch.Tensor | None = None) -> torch.Tensor:
-        """One MoE layer on a chunk: router, expert-sorted dispatch, grouped GEMMs, ordered combine."""
-        _, idx, _, w32 = self.route(x, Wr, renorm)
-        return self.run(x, idx, w32, tab, out, add=add)
+              add: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+        """One MoE layer on a chunk: router logits, top-k with the expert buckets (and the fp16 copy
+        of bf16 activations), grouped GEMMs, ordered combine (moehip_prefill_layer, four launches).
+        The routing it used is left in the route buffers (`route_out`)."""
+        T = x.shape[0]
+        if T > self.max_tokens or x.shape[1] != self.H or Wr.shape != (self.E, self.H) or Wr.dtype != x.dtype:
+            raise RuntimeError(f"GroupedTokens.layer: x {tuple(x.shape)} Wr {tuple(Wr.shape)} {Wr.dtype}")
+        for t, name in ((x, "x"), (Wr, "Wr"), (tab, "tab"), (out, "out")):
+            if not t.is_contiguous() or t.device != self.device:
+                raise RuntimeError(f"GroupedTokens.layer: {name} must be a contiguous tensor on {self.device}")
+        if tab.dtype != torch.int64 or out.dtype != x.dtype or out.shape != x.shape:
+            raise RuntimeError("GroupedTokens.layer: tab int64, out like x")
+        if self._route_bufs is None or self._route_bufs[0].dtype != x.dtype:
+            n, E, k, d = self.max_tokens, self.E, self.k, self.device
+            self._route_bufs = (torch.empty(n, E, dtype=x.dtype, device=d), torch.empty(n, k, dtype=torch.int64, device=d),
+                                torch.empty(n, k, dtype=x.dtype, device=d), torch.empty(n, k, dtype=torch.float32, device=d))
+        logits, idx, w, w32 = (b[:T] for b in self._route_bufs)
+        _lib.call("moehip_prefill_layer", _lib.prec_code("int4"), tab.data_ptr(), x.data_ptr(), Wr.data_ptr(),
+                  _lib.dt_code(x.dtype), T, self.H, self.I, self.k, self.E, 64, 1 if renorm else 0, logits.data_ptr(),
+                  idx.data_ptr(), w.data_ptr(), w32.data_ptr(), out.data_ptr(), _lib.ptr(add), 1 if accumulate else 0,
+                  self.ws_layer.data_ptr(), self.ws_layer.numel(), _lib.stream_of(self.device))
+        self.route_out = (logits, idx, w, w32)
+        return out
 
     def table(self, bases: torch.Tensor) -> torch.Tensor:
         """(E, 4) field-address table from the (E,) record base addresses (0 = not resident)."""

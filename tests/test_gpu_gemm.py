@@ -127,3 +127,66 @@ def test_grouped_gemm_qwen3_30b_prefill_shape(dev):
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(12)).to(dtype)
     got, ref = _run(dev, ex, x, idx, w, dtype)
     assert_layer_close(got, ref, dtype)
+
+
+def test_persistent_ffn_matches_the_separate_launches(dev, monkeypatch):
+    """The persistent up + down kernel (MOEHIP_GEMM_FUSED: per-XCD tile queues, 16 x 16 x 32 MFMA
+    tiles, fp16 h with a power of two per (pair, up tile), rescaled while staged) against the
+    default separate up / h / down launches (32 x 32 x 16 tiles), on a Qwen3-30B-shaped layer
+    with several passes for some experts and a missing expert: both within the oracle's bar, and
+    within one bf16 rounding of the output of each other (the two tile shapes sum a row's
+    products in different orders)."""
+    H, I, E, k, T = 2048, 768, 32, 8, 320
+    dtype = torch.bfloat16
+    ex = _Experts(dev, H, I, E, 13)
+    g = torch.Generator().manual_seed(14)
+    # skewed routing: experts 0..3 get most tokens (several 64-token passes each)
+    pref = torch.tensor([8.0] * 4 + [1.0] * (E - 4))
+    idx = torch.stack([torch.multinomial(pref, k, replacement=False, generator=g) for _ in range(T)])
+    w = torch.rand(T, k, generator=g).float() + 0.05
+    x = torch.randn(T, H, generator=g).to(dtype)
+    monkeypatch.setenv("MOEHIP_GEMM_FUSED", "1")
+    fused, ref = _run(dev, ex, x, idx, w, dtype, missing=(5,))
+    monkeypatch.delenv("MOEHIP_GEMM_FUSED")
+    sep, _ = _run(dev, ex, x, idx, w, dtype, missing=(5,))
+    assert_layer_close(fused, ref, dtype)
+    assert_layer_close(sep, ref, dtype)
+    scale = np.abs(ref).max(axis=1, keepdims=True)
+    assert (np.abs(fused - sep) / scale).max() < 2.0 ** -7
+
+
+@pytest.mark.parametrize("dtype,renorm", [(torch.bfloat16, True), (torch.float16, False)])
+def test_prefill_layer_one_call_matches_route_then_run(dev, dtype, renorm):
+    """moehip_prefill_layer (logits, one launch for top-k + expert buckets + fp16 copy of x,
+    grouped GEMMs, combine) against moehip_router_topk + moehip_dispatch + moehip_grouped_gemm
+    (GroupedTokens.route + run): the same routing bit for bit, the same output bit for bit (the
+    pairs' order within an expert differs, the products and sums do not), repeatably (the routing
+    counters are left at zero), for a full chunk and a shorter one in between; and the oracle's
+    layer on that routing."""
+    H, I, E, k, T = 2048, 768, 64, 8, 192
+    ex = _Experts(dev, H, I, E, 21)
+    gt = GroupedTokens(ex.store.layouts["int4"], E, k, T, dev)
+    tab = gt.table(ex.bases())
+    g = torch.Generator().manual_seed(22)
+    Wr = (torch.randn(E, H, generator=g) * 0.05).to(dtype).to(dev)
+    x = torch.randn(T, H, generator=g).to(dtype).to(dev)
+    outs = []
+    for T_ in (T, 37, T):
+        out = torch.zeros(T_, H, dtype=dtype, device=dev)
+        gt.layer(x[:T_].contiguous(), Wr, renorm, tab, out)
+        torch.cuda.synchronize()
+        if T_ == T:
+            outs.append((out.clone(), [b.clone() for b in gt.route_out]))
+    (o1, r1), (o2, r2) = outs
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+    _, idx, _, w32 = (b.clone() for b in gt.route(x, Wr, renorm))
+    for a, b in ((idx, r1[1]), (w32, r1[3])):
+        assert torch.equal(a, b)
+    ref_out = torch.zeros(T, H, dtype=dtype, device=dev)
+    gt.run(x, idx, w32, tab, ref_out)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.view(torch.int16), ref_out.view(torch.int16))
+    ref = O.moe_layer_grouped(x.float().cpu().numpy(), idx.cpu().numpy(), w32.cpu().numpy().astype(np.float64), ex.mats)
+    assert_layer_close(o1.float().cpu().numpy(), ref, dtype)
