@@ -20,6 +20,7 @@ layers.
 HBM traffic per launch (roofline.traffic) is read from the committed rocprofv3 counter summary
 profiles/k_decode_xcd_olmoe_int4_bs1.md (FETCH_SIZE + WRITE_SIZE of this kernel, scaled by the
 same counters on a plain copy of known size, `--copy-calibration`); null when that file is absent.
+The prefill layer's comes from profiles/k_gemm_qwen3_30b_prefill_t512.md the same way.
 
 CPU baseline: the oracle's restatement of moelab's CPU expert branch (dequantise to fp32,
 F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workload, host cores.
@@ -47,12 +48,14 @@ sys.path.insert(0, str(ROOT / "moe-offload-lab_amd"))
 H, I, E, K_TOP, L = 2048, 1024, 64, 8, 16
 HBM_PEAK_GBS = 8000.0
 PROFILE = ROOT / "profiles" / "k_decode_xcd_olmoe_int4_bs1.md"
+PREFILL_PROFILE = ROOT / "profiles" / "k_gemm_qwen3_30b_prefill_t512.md"
 
 
-def measured_traffic():
-    """HBM bytes per launch of the fused kernel from the committed counter summary, or None."""
+def measured_traffic(profile: Path = PROFILE):
+    """HBM bytes per launch from a committed counter summary (its `traffic_bytes_per_launch:`
+    line), or None."""
     try:
-        for line in PROFILE.read_text().splitlines():
+        for line in profile.read_text().splitlines():
             if line.strip().startswith("traffic_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1].split()[0]))
     except (OSError, ValueError):
@@ -211,9 +214,10 @@ MFMA_PEAK_TFS = 2500.0  # dense fp16/bf16 MFMA
 
 
 def prefill_bench(args):
-    """One Qwen3-30B-shaped MoE layer on a 512-token bf16 chunk: router -> dispatch -> grouped
-    GEMMs -> combine, rotating over QL layers of int4 records (8 x 128 x 2.5 MB = 2.6 GB, far
-    above the Infinity Cache)."""
+    """One Qwen3-30B-shaped MoE layer on a 512-token bf16 chunk in one moehip_prefill_layer call
+    (router logits -> top-k with expert buckets -> placement -> gate/up GEMM -> down GEMM ->
+    combine), rotating over QL layers of int4 records (8 x 128 x 2.5 MB = 2.6 GB, far above the
+    Infinity Cache)."""
     import torch
 
     from moelab_hip import _lib
@@ -277,8 +281,8 @@ def prefill_line(args):
                    "d_model": QH, "experts": QE, "top_k": QK, "d_ff": QI, "layers_rotated": QL, "tokens": QT,
                    "router": "softmax top-8, renormalised", "distinct_experts": r["distinct"]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole layer: router + dispatch + k_gemm_up + k_gemm_down + combine",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(PREFILL_PROFILE),
+                     "kernel": "whole layer: router logits + k_route_post + k_route_place + k_gemm_up + k_gemm_down + k_combine_pairs",
                      "bytes_per_launch": int(r["alg"])},
         "mfma": {"achieved": round(tfs, 1), "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFS, 4),
                  "flops_per_launch": r["flops"]},
@@ -573,7 +577,7 @@ def batch_line(args, name):
                    "distinct_experts_per_layer": round(distinct / (S * L_), 2)},
         "layer_us": round(layer_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(PREFILL_PROFILE),
                      "kernel": "whole layer: router logits + top-k / shared slot + levels, dispatch, vote and "
                                "work list + k_gemv_up/down per precision + combine (HIP graph per step)",
                      "bytes_per_launch": int(alg)},

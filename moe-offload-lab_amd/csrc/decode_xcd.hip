@@ -952,11 +952,11 @@ int xcd_probe(int dev) {
             for (int b = 0; b < NB; ++b) ok &= (int)(h[b] == (uint32_t)(b % XC_N));
         }
         free(h);
-        hipFree(d);
+        (void)hipFree(d);
     }
-    hipGetLastError();
+    (void)hipGetLastError();
     g_xcd_ok[dev] = ok;
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     return ok;
 }
 

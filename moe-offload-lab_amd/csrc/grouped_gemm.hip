@@ -245,6 +245,28 @@ __device__ __forceinline__ void mma_chunk(const WChunk &w, const uint16_t *s_a, 
     mma_steps<PREC, NM>(w, s_a + i * GgChunk<CK>::LDA + h * (CK / 2), dk, d);
 }
 
+// fp16 bits of 2^d for d <= 0 (subnormal below 2^-14, 0 below 2^-24)
+__device__ __forceinline__ uint32_t pow2_h(int d) {
+    return d >= -14 ? (uint32_t)(d + 15) << 10 : (d >= -24 ? 1u << (d + 24) : 0u);
+}
+
+// h chunks staged by the down tiles: h is fp16 scaled by 2^-eb per (pair, 32 columns) (the up
+// wave of those columns chose eb); a staging thread multiplies its part of a chunk (CK / 4
+// columns, within one block of 32) by 2^(eb - emax), emax the pair's largest eb (exact unless the
+// product is subnormal), so one power per pair remains
+template <int CK>
+__device__ __forceinline__ void xs_scale(uint4 (&v)[GgChunk<CK>::NV], int eb, int emax) {
+    const uint32_t fb = pow2_h(eb - emax);
+    const half2_t f2 = __builtin_bit_cast(half2_t, fb | (fb << 16));
+#pragma unroll
+    for (int m = 0; m < GgChunk<CK>::NV; ++m) {
+        v[m].x = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, v[m].x) * f2);
+        v[m].y = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, v[m].y) * f2);
+        v[m].z = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, v[m].z) * f2);
+        v[m].w = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, v[m].w) * f2);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // the K loop of one pass (nch chunks): queue order of the loads is X0, R0 .. R(RING-2), X1,
 // R(RING-1) | per chunk c: X(c + 2), R(c + RING): waiting for an activation chunk never waits
@@ -252,19 +274,29 @@ __device__ __forceinline__ void mma_chunk(const WChunk &w, const uint16_t *s_a, 
 // is issued unconditionally (chunk indices clamped to the last chunk: a few repeated loads at
 // the end hit L2): with loads under branches the compiler cannot count them and waits for all.
 // ---------------------------------------------------------------------------------------
-template <int PREC, int RING, int NM>
+template <int PREC, int RING, int NM, bool SC = false>
 __device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2], int nch, const uint16_t *srcrow,
-                                       uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2]) {
+                                       uint16_t *s_a, DeqK dk, f32x16 (&d)[2][2], const int *ebrow = nullptr,
+                                       int emax = 0) {
     constexpr int CK = GgPrec<PREC>::CK;
     constexpr int ABUF = GG_TOK * GgChunk<CK>::LDA;
     const int cl = nch - 1;
     WChunk wr[RING];
     uint4 xv[GgChunk<CK>::NV];
-    xs_load<CK>(srcrow, 0, xv);
+    int xeb = 0;  // SC: the block exponent of the chunk in xv
+    auto xload = [&](int c) {
+        xs_load<CK>(srcrow, c, xv);
+        if constexpr (SC) xeb = ebrow[(c * CK + (threadIdx.x & 3) * GgChunk<CK>::VPT) / 32];
+    };
+    auto xstore = [&](uint16_t *dst) {
+        if constexpr (SC) xs_scale<CK>(xv, xeb, emax);
+        xs_store<CK>(xv, dst);
+    };
+    xload(0);
 #pragma unroll
     for (int u = 0; u + 1 < RING; ++u) load_chunk<PREC>(wr[u], qp, sp, min(u, cl));
-    xs_store<CK>(xv, s_a);
-    xs_load<CK>(srcrow, min(1, cl), xv);
+    xstore(s_a);
+    xload(min(1, cl));
     load_chunk<PREC>(wr[RING - 1], qp, sp, min(RING - 1, cl));
     __syncthreads();
 #pragma unroll 1
@@ -278,8 +310,8 @@ __device__ __forceinline__ void k_loop(gu8 *const (&qp)[2], gu8 *const (&sp)[2],
             // step down to this store, and waiting for it then waits for every weight load too.
             // The other buffer was last read before the previous barrier; a store past the last
             // chunk is overwritten by the same thread in the next pass's prologue.
-            xs_store<CK>(xv, s_a + (b ^ 1) * ABUF);
-            xs_load<CK>(srcrow, min(c + 2, cl), xv);
+            xstore(s_a + (b ^ 1) * ABUF);
+            xload(min(c + 2, cl));
             load_chunk<PREC>(wr[u], qp, sp, min(c + RING, cl));
             if (c < nch) __syncthreads();
         }
@@ -297,7 +329,8 @@ __device__ __forceinline__ bool tile_of(int t, int E, int NB, int &e, int &nb) {
 
 // exponent e with max * 2^-e in [2^14, 2^15) (0 for 0, inf or nan)
 __device__ __forceinline__ int row_exp(float m) {
-    return (m > 0.f && m <= 3.0e38f) ? max(ilogbf(m) - 14, -100) : 0;
+    // ilogb(m) = frexp exponent - 1 (v_frexp_exp_i32_f32; subnormal m included)
+    return (m > 0.f && m <= 3.0e38f) ? max(__builtin_amdgcn_frexp_expf(m) - 15, -100) : 0;
 }
 
 // bf16 activations, one wave per row: xe[r] = row_exp(max |x[r]|) and x16[r] = fp16(x[r] * 2^-xe[r])
@@ -336,11 +369,25 @@ __global__ __launch_bounds__(256) void k_prep(const uint16_t *__restrict__ x, in
 // gate rows, subtile 1 = up rows. Writes h (pairs, I) fp32.
 // ---------------------------------------------------------------------------------------
 // x: fp16 activations (the caller's, or x16 with exponents xe for bf16 input; xe null = 0)
+// largest of a non-negative float over each 32-lane half of the wave, in every lane of the half
+// (every lane active), on the float's bits (their order is the values' for v >= 0; 0 is the
+// identity of the unsigned max, so each DPP move folds into its max): butterflies within rows of
+// 16, then lane i against lane i ^ 16 (ds_swizzle, bit-mask mode: and 0x1f, or 0, xor 0x10)
+__device__ __forceinline__ float half_max(float f) {
+    uint32_t v = __float_as_uint(f);
+    v = max(v, (uint32_t)dpp_i<0xB1>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x4E>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x141>((int)v));
+    v = max(v, (uint32_t)dpp_i<0x140>((int)v));
+    v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));
+    return __uint_as_float(v);
+}
+
 template <int PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_up(
     const uint16_t *__restrict__ x, const int *__restrict__ xe, int H, int I, int k, int E,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
-    float *__restrict__ hb, DeqK dk) {
+    uint16_t *__restrict__ h16, int *__restrict__ hbe, DeqK dk) {
     constexpr int CK = GgPrec<PREC>::CK;
     __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<CK>::LDA];
     __shared__ int s_e[GG_TOK];
@@ -371,7 +418,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
         if (nm == 2) k_loop<PREC, 2, 2>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
         else k_loop<PREC, 2, 1>(qp, sp, nch, x + (size_t)xr * H, s_a, dk, d);
-        // epilogue: h = silu(gate) * up (scaled back by the token's 2^e), stored fp32
+        // epilogue: h = silu(gate) * up (scaled back by the token's 2^e); per token the largest
+        // |h| of the wave's 32 columns (one half of the wave) sets the block exponent eb; h is
+        // stored fp16 times 2^-eb, eb beside it
+        // (branch-free first loop: the 16 lane reductions of a tile interleave)
+        const int NB32 = I / 32;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             if (mt >= nm) break;
@@ -380,32 +431,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const int tok = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 const float f = ldexpf(1.0f, s_e[tok]);
                 const float hv = silu_mul(d[mt][0][r] * f, d[mt][1][r] * f);
-                if (tok < mn) hb[(size_t)(p0 + m0 + tok) * I + col] = hv;
+                d[mt][0][r] = hv;
+                d[mt][1][r] = half_max(fabsf(hv));
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tok = mt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int eb = row_exp(d[mt][1][r]);
+                if (tok < mn) {
+                    const size_t p = (size_t)(p0 + m0 + tok);
+                    h16[p * I + col] = f32_to_f16_rne(d[mt][0][r] * ldexpf(1.0f, -eb));
+                    if (j == 0) hbe[p * NB32 + (col >> 5)] = eb;
+                }
             }
         }
         __syncthreads();  // s_e of the next pass
     }
-}
-
-// one wave per pair: he[p] = row_exp(max |h[p]|), h16[p] = fp16(h[p] * 2^-he[p])
-__global__ __launch_bounds__(256) void k_h16(const float *__restrict__ hb, int NP, int I, uint16_t *__restrict__ h16,
-                                             int *__restrict__ he) {
-    const int p = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (p >= NP) return;
-    const float4 *src = reinterpret_cast<const float4 *>(hb + (size_t)p * I);
-    float m = 0.f;
-    for (int c = lane; c < I / 4; c += 64) {
-        const float4 v = src[c];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    const int e = row_exp(wave_max(m));
-    const float sc = ldexpf(1.0f, -e);
-    uint2 *dst = reinterpret_cast<uint2 *>(h16 + (size_t)p * I);
-    for (int c = lane; c < I / 4; c += 64) {
-        const float4 v = src[c];
-        dst[c] = make_uint2(pack_h2(v.x * sc, v.y * sc), pack_h2(v.z * sc, v.w * sc));
-    }
-    if (lane == 0) he[p] = e;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -780,16 +821,17 @@ __global__ __launch_bounds__(256) void k_gemv_down(const float *__restrict__ hb,
 
 // ---------------------------------------------------------------------------------------
 // down: tiles (expert, 256 output rows); wave w: rows nb*256 + 64 w + 32 t + (lane % 32).
-// y[pair, row] = w[pair] * (down_row . h_pair)
+// y[pair, row] = w[pair] * (down_row . h_pair); h is read as the up tiles left it (fp16 times
+// 2^-eb per 32 columns) and rescaled to the pair's largest exponent Emax while staged
 // ---------------------------------------------------------------------------------------
 template <int PREC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_down(
-    const uint16_t *__restrict__ h16, const int *__restrict__ he, int H, int I, int E,
+    const uint16_t *__restrict__ h16, const int *__restrict__ hbe, int H, int I, int E,
     const int32_t *__restrict__ offsets, const int32_t *__restrict__ sorted_pos, const int64_t *__restrict__ tab,
     const float *__restrict__ w, float *__restrict__ y, DeqK dk, int zero_missing) {
     constexpr int CK = GgPrec<PREC>::CK;
     __shared__ __align__(16) uint16_t s_a[2 * GG_TOK * GgChunk<CK>::LDA];
-    __shared__ float s_f[GG_TOK];  // w[pair] * 2^e
+    __shared__ float s_f[GG_TOK];  // w[pair] * 2^Emax
     const int NB = H / GG_ROWS;
     int e, nb;
     if (!tile_of(blockIdx.x, E, NB, e, nb)) return;
@@ -814,14 +856,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int stok = tid >> 2;
         const bool sok = stok < mn;
         const size_t pr = (size_t)(p0 + m0 + (sok ? stok : 0));
-        if ((tid & 3) == 0) s_f[stok] = sok ? w[sorted_pos[pr]] * ldexpf(1.0f, he[pr]) : 0.f;
+        // the pair's largest block exponent: the 4 staging threads of the pair take every 4th
+        // block (independent loads, issued together), then the largest over the 4 (DPP)
+        const int NB32 = I / 32;
+        const int *ebrow = hbe + pr * NB32;
+        int emax = -1000;
+        for (int i0 = tid & 3; i0 < NB32; i0 += 32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (i0 + 4 * i < NB32) emax = max(emax, ebrow[i0 + 4 * i]);
+        }
+        emax = max(emax, dpp_i<0xB1>(emax));
+        emax = max(emax, dpp_i<0x4E>(emax));
+        if ((tid & 3) == 0) s_f[stok] = sok ? w[sorted_pos[pr]] * ldexpf(1.0f, emax) : 0.f;
         f32x16 d[2][2];
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int b = 0; b < 2; ++b) d[a][b] = f32x16{};
-        if (nm == 2) k_loop<PREC, 2, 2>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
-        else k_loop<PREC, 2, 1>(qp, sp, nch, h16 + pr * I, s_a, dk, d);
+        if (nm == 2) k_loop<PREC, 2, 2, true>(qp, sp, nch, h16 + pr * I, s_a, dk, d, ebrow, emax);
+        else k_loop<PREC, 2, 1, true>(qp, sp, nch, h16 + pr * I, s_a, dk, d, ebrow, emax);
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
             if (mt >= nm) break;
@@ -991,10 +1045,6 @@ __device__ __forceinline__ uint4 ld16_nt(const void *p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-// fp16 bits of 2^d for d <= 0 (subnormal below 2^-14, 0 below 2^-24)
-__device__ __forceinline__ uint32_t pow2_h(int d) {
-    return d >= -14 ? (uint32_t)(d + 15) << 10 : (d >= -24 ? 1u << (d + 24) : 0u);
-}
 
 // activation staging of one pass: NT tokens (64, or 32 for a single 32-token M tile) over the
 // 256 threads, TPT threads per token, VPT values each (NV 16-byte loads)
@@ -1610,7 +1660,7 @@ __global__ __launch_bounds__(256) void k_route_place(const int *__restrict__ cnt
 }
 
 struct GgLayout {
-    size_t xe, x16, h, h16, he, y, items, hbe, plan, list, pairs, dummy, total;
+    size_t xe, x16, h, h16, y, items, hbe, plan, list, pairs, dummy, total;
     int lmax;
 };
 static GgLayout gg_layout(int T, int k, int H, int I) {
@@ -1626,17 +1676,16 @@ static GgLayout gg_layout(int T, int k, int H, int I) {
     off = al(off + NP * I * 4);
     L.h16 = off;
     off = al(off + NP * I * 2);
-    L.he = off;
-    off = al(off + NP * 4);
     L.y = off;
     off = al(off + NP * H * 4);
     L.items = off;  // one work list per record precision
     off = al(off + (size_t)GV_MAXP * (NP + 1) * 4);
-    // the persistent FFN's block exponents of h, plan words and tile queues
+    // the block exponents of h (one per pair and 32 columns; the persistent FFN's one per 128),
+    // the persistent FFN's plan words and tile queues
     const int NBU = I / 128, NBD = H / GG_ROWS;
     L.lmax = ffn_lmax((int)NP, NBU, NBD);
     L.hbe = off;
-    off = al(off + NP * NBU * 4);
+    off = al(off + NP * (I / 32) * 4);
     L.plan = off;
     off = al(off + (size_t)(FP_DONE + (size_t)ffn_max_units((int)NP) * max(NBU, 1)) * 4);
     L.list = off;
@@ -1660,14 +1709,15 @@ extern "C" size_t moehip_grouped_gemm_workspace_bytes(int T, int k, int H, int I
 
 template <int PREC>
 static void launch_up(dim3 g, hipStream_t st, const uint16_t *x, const int *xe, int H, int I, int k, int E,
-                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *hb, DeqK dk) {
-    hipLaunchKernelGGL((k_gemm_up<PREC>), g, dim3(256), 0, st, x, xe, H, I, k, E, offsets, sorted_pos, tab, hb, dk);
+                      const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, uint16_t *h16, int *hbe,
+                      DeqK dk) {
+    hipLaunchKernelGGL((k_gemm_up<PREC>), g, dim3(256), 0, st, x, xe, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk);
 }
 template <int PREC>
-static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *he, int H, int I, int E,
+static void launch_down(dim3 g, hipStream_t st, const uint16_t *h16, const int *hbe, int H, int I, int E,
                         const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, const float *w, float *y,
                         DeqK dk, int zero_missing) {
-    hipLaunchKernelGGL((k_gemm_down<PREC>), g, dim3(256), 0, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk,
+    hipLaunchKernelGGL((k_gemm_down<PREC>), g, dim3(256), 0, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk,
                        zero_missing);
 }
 
@@ -1878,20 +1928,19 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     for (int p = 0; p < P && gemv; ++p)
         launch_gv_prec(precs[p], bf ? 2 : 1, items + (size_t)p * (NP + 1), NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
+    // the MFMA up tiles write h as fp16 with a power of two per (pair, 32 columns); the GEMVs fp32
+    uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
+    int *hbe = reinterpret_cast<int *>(wsb + L.hbe);
     for (int p = 0; p < P && !gemv && !fused; ++p) {
         const int64_t *tab = tabs + (size_t)p * E * 4;
         switch (precs[p]) {
-            case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
-            case MOEHIP_PREC_INT8: launch_up<MOEHIP_PREC_INT8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
-            case MOEHIP_PREC_FP8: launch_up<MOEHIP_PREC_FP8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
-            case MOEHIP_PREC_F16: launch_up<MOEHIP_PREC_F16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
-            default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, hb, dk); break;
+            case MOEHIP_PREC_INT4: launch_up<MOEHIP_PREC_INT4>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
+            case MOEHIP_PREC_INT8: launch_up<MOEHIP_PREC_INT8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
+            case MOEHIP_PREC_FP8: launch_up<MOEHIP_PREC_FP8>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
+            case MOEHIP_PREC_F16: launch_up<MOEHIP_PREC_F16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
+            default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
         }
     }
-    uint16_t *h16 = reinterpret_cast<uint16_t *>(wsb + L.h16);
-    int *he = reinterpret_cast<int *>(wsb + L.he);
-    // the MFMA down kernels read h as fp16 with a per-pair power of two; the GEMVs read the fp32 rows
-    if (!gemv && !fused) hipLaunchKernelGGL(k_h16, dim3((NP + 3) / 4), dim3(256), 0, st, hb, NP, I, h16, he);
     for (int p = 0; p < P && gemv; ++p)
         launch_gv_prec(precs[p], 0, items + (size_t)p * (NP + 1), NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
                        y, w, dk);
@@ -1899,11 +1948,11 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
         const int64_t *tab = tabs + (size_t)p * E * 4;
         const int zm = zero_missing && P == 1;
         switch (precs[p]) {
-            case MOEHIP_PREC_INT4: launch_down<MOEHIP_PREC_INT4>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
-            case MOEHIP_PREC_INT8: launch_down<MOEHIP_PREC_INT8>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
-            case MOEHIP_PREC_FP8: launch_down<MOEHIP_PREC_FP8>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
-            case MOEHIP_PREC_F16: launch_down<MOEHIP_PREC_F16>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
-            default: launch_down<MOEHIP_PREC_BF16>(gd, st, h16, he, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_INT4: launch_down<MOEHIP_PREC_INT4>(gd, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_INT8: launch_down<MOEHIP_PREC_INT8>(gd, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_FP8: launch_down<MOEHIP_PREC_FP8>(gd, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            case MOEHIP_PREC_F16: launch_down<MOEHIP_PREC_F16>(gd, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
+            default: launch_down<MOEHIP_PREC_BF16>(gd, st, h16, hbe, H, I, E, offsets, sorted_pos, tab, w, y, dk, zm); break;
         }
     }
     if (xdtype == MOEHIP_DT_F16)

@@ -54,7 +54,7 @@ int noalloc_init(int dev) {
             g_scratch[dev] = ptr;
         }
     }
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     return rc;
 }
 
