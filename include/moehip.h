@@ -188,6 +188,30 @@ int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E
  */
 int moehip_quantize(const float *w, int O, int I, int bits, int gs, void *q, void *s, void *stream);
 
+/*
+ * The same with the mse scale search (moelab/quant.py:64-93 with method="mse", the int4 store
+ * default, moelab/store.py:84-85): per group the fp16 scale of least squared error among
+ * (max|w| / qmax) x f and, for int4, (w at the first largest |w|) / -8 x f, f = 1.00, 0.98, ...,
+ * 0.70; the first of equal errors wins. Errors are float32 sums in numpy's pairwise order.
+ * Scales may be negative (int4). Same sizes and packing as moehip_quantize.
+ */
+int moehip_quantize_mse(const float *w, int O, int I, int bits, int gs, void *q, void *s, void *stream);
+
+/*
+ * GPTQ column sweep of one block (moelab/quant.py:172-186, inside gptq_quantize, quant.py:130-188):
+ * rows 0..O-1 of W (float32, row stride ldw), columns i1 .. i1 + nb - 1 (nb <= 128, i1 and nb
+ * multiples of gs = 32 or 64), against the block of Hinv (the upper Cholesky factor of H^-1, row
+ * stride ldh) at (i1, i1). Left to right: at a group's first column its fp16 scale is chosen from
+ * the corrected weights (method 0 absmax, 1 mse), q = rint(w / s) clamped, err = (w - q s) /
+ * Hinv[i][i], later columns of the block lose err * Hinv[i][j]. Writes q in the store's packing
+ * (int4: byte (i1 + i) / 2 of row stride ldq; int8: byte i1 + i), the block's scales into s (fp16,
+ * row stride lds, group (i1 + i) / gs) and the errors into E (float32, row stride lde, column i).
+ * W is read only: the caller applies W[:, i1 + nb:] -= E Hinv[i1 : i1 + nb, i1 + nb:] between
+ * blocks (a float32 matrix product), as the reference does.
+ */
+int moehip_gptq_block(const float *W, int ldw, const float *Hinv, int ldh, int O, int i1, int nb, int bits, int gs,
+                      int method, void *q, int ldq, void *s, int lds, float *E, int lde, void *stream);
+
 /* Static description of one MoE layer for the fused decode kernel. Precision index p follows
  * the store's order (most precise first, moelab/store.py `precisions`). */
 typedef struct moehip_layer_desc {

@@ -64,6 +64,8 @@ _SIGS = {
                              _vp, _vp], _i),
     "moehip_dispatch": ([_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_quantize": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
+    "moehip_quantize_mse": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
+    "moehip_gptq_block": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp], _i),
     "moehip_quantize_fp8_block": ([_vp, _i, _i, _vp, _vp, _vp], _i),
     "moehip_decode_layer": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,
                              _vp, _vp, _vp, ctypes.c_size_t, _i, _vp, _vp], _i),

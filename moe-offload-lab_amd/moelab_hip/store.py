@@ -10,7 +10,7 @@ This module adds one record kind the reference does not have: "fp8" (checkpoint-
 weights with fp32 128x128 block scales, the `weight_scale_inv` of moelab/quant.py:208-219),
 laid out with the same alignment rules.
 
-Encoding runs on the GPU (`encode_record_`): absmax int4/int8 through the moehip quantiser
+Encoding runs on the GPU (`encode_record_`): absmax or mse int4/int8 through the moehip quantisers
 (bit-exact with moelab/quant.py's absmax path), fp8 through the moehip block quantiser (amax/448 scales,
 round-to-nearest-even e4m3fn codes), float records by casting.
 """
@@ -132,9 +132,9 @@ def views(layout: dict, blob: torch.Tensor) -> dict[str, torch.Tensor]:
 
 def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor) -> torch.Tensor:
     """Write one record into `blob` (uint8 device tensor of record_bytes) from float weights on
-    the same device. int4/int8: absmax scales through the moehip quantiser (identical bytes to
-    moelab/store.py:122-150 with scale="absmax"); float: cast; fp8: per-128x128-block
-    amax/448 scales and round-to-nearest-even e4m3fn codes."""
+    the same device. int4/int8: the layout's scale method ("absmax" or "mse", moelab/quant.py:64-93)
+    through the moehip quantisers (identical bytes to moelab/store.py:122-150); float: cast; fp8:
+    per-128x128-block amax/448 scales and round-to-nearest-even e4m3fn codes."""
     prec = layout["precision"]
     spec = PRECISIONS[prec]
     if blob.numel() != layout["record_bytes"] or blob.dtype != torch.uint8:
@@ -157,10 +157,14 @@ def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down
                       v[f"{name}.s"].data_ptr(), _lib.stream_of(blob.device))
         return blob
     bits = spec["bits"]
+    method = layout.get("scale") or "absmax"
+    if method not in ("absmax", "mse"):
+        raise ValueError(f"unknown scale method {method!r} (absmax, mse)")
+    entry = "moehip_quantize_mse" if method == "mse" else "moehip_quantize"
     for name, w in mats.items():
         wf = w.float().contiguous()
         O, I = wf.shape
         gs = layout["group_sizes"][name]
-        _lib.call("moehip_quantize", wf.data_ptr(), O, I, bits, gs, v[f"{name}.q"].data_ptr(),
+        _lib.call(entry, wf.data_ptr(), O, I, bits, gs, v[f"{name}.q"].data_ptr(),
                   v[f"{name}.s"].data_ptr(), _lib.stream_of(blob.device))
     return blob

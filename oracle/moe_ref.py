@@ -16,6 +16,9 @@ How each part is pinned (tests/test_oracle.py):
 - absmax scales: closed form on hand-made groups (zero group -> fp16(1e-7), exact powers of two).
 - mse scales: known answer of tests/test_requant.py:35-42 (scale -1.0), and the invariant of
   tests/test_requant.py:21-33 (never worse than absmax, group by group).
+- GPTQ: the reference's property test (tests/test_requant.py:45-60: at least 15 % less output
+  error than mse on correlated inputs), a diagonal Hessian (no error to carry: exactly the mse
+  quantisation), dead columns (zero weights), and Hinv against its definition (U^T U = H^-1).
 - record layout: the record sizes computed independently for the three model shapes, 4096-B
   record alignment (tests/test_units.py:49-60), round trips at the reference tolerances.
 - FP8 e4m3fn decode: all 256 codes against torch.float8_e4m3fn (a library routine).
@@ -174,6 +177,83 @@ def quantize(w: np.ndarray, bits: int, group_size: int, method: str = "absmax"):
     s = choose_scales(wf, bits, method)
     q = np.clip(np.rint(wf / s.astype(np.float32)), QMIN[bits], QMAX[bits]).astype(np.int16)
     return pack(q.reshape(out_f, in_f), bits), np.ascontiguousarray(s.reshape(out_f, in_f // group_size))
+
+
+def gptq_hinv(hessian: np.ndarray, damp: float = 0.01):
+    """quant.py:151-166: dead columns (zero diagonal) get H[d, d] = 1, then damp * mean(diag) on
+    the diagonal (again on each failed factorisation, up to 6 tries); Hinv = the upper Cholesky
+    factor of H^-1, float32 throughout. Returns (Hinv, dead) or (None, dead) when every try
+    failed (the reference then falls back to plain `quantize`). The factorisations are LAPACK's
+    (numpy), so Hinv agrees with torch's to rounding, not bit for bit."""
+    H = np.array(hessian, dtype=np.float32, copy=True)
+    dead = np.diag(H) == 0
+    H[dead, dead] = 1.0
+    add = np.float32(damp) * np.float32(np.mean(np.diag(H), dtype=np.float32))
+    H[np.diag_indices_from(H)] += add
+    for _ in range(6):
+        try:
+            L = np.linalg.cholesky(H.astype(np.float32))
+            Li = np.linalg.inv(L).astype(np.float32)
+            Hi_full = (Li.T @ Li).astype(np.float32)  # (L L^T)^-1, what cholesky_inverse(L) returns
+            U = np.linalg.cholesky(Hi_full).T.astype(np.float32)  # upper=True: Hi_full = U^T U
+            if not np.all(np.isfinite(U)):
+                raise np.linalg.LinAlgError("non-finite factor")
+            return np.ascontiguousarray(U), dead
+        except np.linalg.LinAlgError:
+            add = np.float32(damp) * np.float32(np.mean(np.diag(H), dtype=np.float32))
+            H[np.diag_indices_from(H)] += add
+    return None, dead
+
+
+def gptq_sweep(W1: np.ndarray, Hi: np.ndarray, bits: int, group_size: int, method: str = "mse"):
+    """quant.py:172-186, one block of columns: left to right, a group's scale is chosen (on the
+    weights as corrected so far) at its first column; q = rint(col / s) clamped; err = (col -
+    q s) / Hi[i, i]; the columns from i on lose err * Hi[i, i:] (each product and difference
+    rounded to float32). W1 (out, nb) float32 is updated in place. Returns (q int16 (out, nb),
+    scales fp16 (out, nb / gs), E1 float32 (out, nb))."""
+    qmin, qmax = QMIN[bits], QMAX[bits]
+    out_f, nb = W1.shape
+    Q = np.zeros((out_f, nb), np.int16)
+    S = np.zeros((out_f, nb // group_size), np.float16)
+    E1 = np.zeros((out_f, nb), np.float32)
+    sf = None
+    for i in range(nb):
+        if i % group_size == 0:
+            sc = choose_scales(W1[:, None, i:i + group_size], bits, method).reshape(-1)
+            S[:, i // group_size] = sc
+            sf = sc.astype(np.float32)
+        col = W1[:, i].copy()
+        q = np.clip(np.rint(col / sf), qmin, qmax).astype(np.float32)
+        Q[:, i] = q.astype(np.int16)
+        err = ((col - q * sf) / Hi[i, i]).astype(np.float32)
+        W1[:, i:] -= (err[:, None] * Hi[i, i:][None, :]).astype(np.float32)
+        E1[:, i] = err
+    return Q, S, E1
+
+
+def gptq_quantize(w: np.ndarray, hessian: np.ndarray, bits: int, group_size: int, method: str = "mse",
+                  damp: float = 0.01, block: int = 128):
+    """quant.py:130-188 (GPTQ, Frantar et al. 2023, in the store's format) -> (packed q, fp16
+    scales (out, in/gs)). The lazy update of the columns right of a block is one float32 matrix
+    product (BLAS order)."""
+    W = np.array(w, dtype=np.float32, copy=True)
+    out_f, in_f = W.shape
+    if in_f % group_size or block % group_size:
+        raise ValueError("in_features and block must be multiples of group_size")
+    Hinv, dead = gptq_hinv(hessian, damp)
+    if Hinv is None:
+        return quantize(w, bits, group_size, method)
+    W[:, dead] = 0.0
+    Q = np.zeros((out_f, in_f), np.int16)
+    S = np.zeros((out_f, in_f // group_size), np.float16)
+    for i1 in range(0, in_f, block):
+        i2 = min(i1 + block, in_f)
+        W1 = W[:, i1:i2].copy()
+        q, sc, E1 = gptq_sweep(W1, Hinv[i1:i2, i1:i2], bits, group_size, method)
+        Q[:, i1:i2] = q
+        S[:, i1 // group_size:i2 // group_size] = sc
+        W[:, i2:] -= (E1 @ Hinv[i1:i2, i2:]).astype(np.float32)
+    return pack(Q, bits), S
 
 
 def unpack_int4(q: np.ndarray) -> np.ndarray:

@@ -84,6 +84,61 @@ def test_quantize_bit_exact(dev, bits, O_, I_, gs):
     assert np.array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
 
 
+def _mse_groups(O_, I_, gs, seed):
+    """N(0, 0.02) weights with planted groups: all zero (fp16(1e-7) scale), exact halves (ties to
+    even), tiny (the clamp), the largest magnitude on a negative weight (max / -8 > 0), two
+    weights of equal magnitude and opposite signs (the first index wins the argmax), one positive
+    outlier 30x the rest (a negative int4 scale, max / -8), and a row of duplicated groups (the
+    same choice in every group)."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(O_, I_, generator=g) * 0.02
+    w[0, :gs] = 0.0
+    w[1, :gs] = torch.arange(gs) - gs / 2
+    w[2, :gs] = torch.linspace(-1e-9, 1e-9, gs)
+    w[3, :gs] = torch.linspace(-0.9, 0.5, gs)
+    w[4, :gs] = torch.randn(gs, generator=g) * 0.01
+    w[4, 1], w[4, gs - 1] = 0.3, -0.3
+    w[5, :gs] = torch.randn(gs, generator=g) * 0.01
+    w[5, gs // 2] = 0.3
+    w[6, :] = w[6, :gs].repeat(I_ // gs)
+    return w
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("O_,I_,gs", [(64, 128, 64), (2048, 768, 64), (40, 96, 48), (16, 96, 32), (12, 60, 10),
+                                      (12, 36, 6)])
+def test_quantize_mse_bit_exact(dev, bits, O_, I_, gs):
+    """moehip_quantize_mse against the oracle's mse restatement (quant.py:64-93): scales and
+    packed values bit for bit, planted groups included, group sizes with and without a
+    remainder below 8 (numpy's pairwise order for the error sums)."""
+    print(f"quantize mse bits={bits} O={O_} I={I_} gs={gs}", flush=True)
+    w = _mse_groups(O_, I_, gs, O_ + I_ + gs + bits)
+    q_ref, s_ref = O.quantize(w.numpy(), bits, gs, "mse")
+    if bits == 4:
+        assert (s_ref.astype(np.float32) < 0).any()  # the negative scales are exercised
+    wd = w.to(dev)
+    q = torch.empty(q_ref.shape, dtype=torch.uint8 if bits == 4 else torch.int8, device=dev)
+    s = torch.empty(s_ref.shape, dtype=torch.float16, device=dev)
+    _lib.call("moehip_quantize_mse", wd.data_ptr(), O_, I_, bits, gs, q.data_ptr(), s.data_ptr(), _lib.stream_of(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
+    assert np.array_equal(q.cpu().numpy().view(np.uint8), q_ref.view(np.uint8))
+
+
+@pytest.mark.parametrize("prec", ["int4", "int8"])
+def test_encode_record_mse_bit_exact(dev, prec):
+    """A record of an mse layout (the int4 store default) encoded on the GPU: the same bytes as
+    the oracle's encoder (store.py:122-150 with scale="mse")."""
+    H, I = 512, 256
+    g = torch.Generator().manual_seed(8)
+    gu, dn = torch.randn(2 * I, H, generator=g) * 0.05, torch.randn(H, I, generator=g) * 0.05
+    lay = record_layout(prec, H, I, 64, scale="mse")
+    blob = torch.empty(lay["record_bytes"], dtype=torch.uint8, device=dev)
+    encode_record_(lay, blob, gu.to(dev), dn.to(dev))
+    ref = O.encode_record(O.record_layout(prec, H, I, 64, scale="mse"), gu.numpy(), dn.numpy(), method="mse")
+    assert np.array_equal(blob.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("prec", ["int4", "int8", "fp16", "bf16", "fp32", "fp8"])
 def test_encode_record_bit_exact(dev, prec):
     H, I = 256, 128

@@ -103,6 +103,62 @@ def test_mse_never_worse_than_absmax():
     assert bool((em <= ea + 1e-6).all())
 
 
+def _gptq_case(seed=1, O_=64, I_=256):
+    """The reference's GPTQ test set-up (tests/test_requant.py:45-51), numpy-seeded: N(0, 0.05)
+    weights, correlated inputs X = N(0, 1) (1 + 0.4 N / sqrt(I)) with 8 columns scaled by 6."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((O_, I_)) * 0.05).astype(np.float32)
+    X = (rng.standard_normal((2048, I_)) @ (np.eye(I_) + 0.4 * rng.standard_normal((I_, I_)) / I_ ** 0.5))
+    X = X.astype(np.float32)
+    X[:, :8] *= 6
+    return w, X, (X.T @ X).astype(np.float32)
+
+
+def test_gptq_reduces_output_error():
+    """tests/test_requant.py:45-60: GPTQ's output error on the calibration inputs is at least 15 %
+    below mse quantisation's; shapes and dtypes of the store's format."""
+    w, X, H = _gptq_case()
+
+    def out_err(q, s):
+        return float(((X @ (O.dequantize(q, s, 4, "float32") - w).T) ** 2).mean())
+
+    e_mse = out_err(*O.quantize(w, 4, 64, "mse"))
+    q, s = O.gptq_quantize(w, H, 4, 64)
+    assert out_err(q, s) < 0.85 * e_mse
+    assert q.shape == (64, 128) and q.dtype == np.uint8 and s.shape == (64, 4) and s.dtype == np.float16
+
+
+@pytest.mark.parametrize("bits,method", [(4, "mse"), (8, "mse"), (4, "absmax")])
+def test_gptq_diagonal_hessian_is_plain_quantisation(bits, method):
+    """Uncorrelated inputs (a diagonal Hessian): Hinv is diagonal, no error is carried to other
+    columns, and GPTQ gives exactly the plain quantisation of the same method."""
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((48, 384)) * 0.05).astype(np.float32)
+    H = np.diag(rng.uniform(0.5, 3.0, 384)).astype(np.float32)
+    q, s = O.gptq_quantize(w, H, bits, 64, method)
+    q2, s2 = O.quantize(w, bits, 64, method)
+    assert np.array_equal(q, q2) and np.array_equal(s.view(np.uint16), s2.view(np.uint16))
+
+
+def test_gptq_dead_columns_and_hinv():
+    """Columns the calibration never excited (zero Hessian row and column: quant.py:153-155) are
+    quantised as zeros; Hinv is upper triangular with Hinv^T Hinv = (H + damp)^-1."""
+    w, X, H = _gptq_case(3, 32, 128)
+    dead = [5, 70, 71]
+    H[dead, :] = 0.0
+    H[:, dead] = 0.0
+    U, d = O.gptq_hinv(H)
+    assert d.sum() == 3 and np.allclose(U, np.triu(U))
+    Hd = H.astype(np.float64).copy()
+    Hd[dead, dead] = 1.0
+    Hd[np.diag_indices_from(Hd)] += 0.01 * np.mean(np.diag(Hd))
+    ref = np.linalg.inv(Hd)
+    assert np.abs(U.astype(np.float64).T @ U - ref).max() < 1e-4 * np.abs(ref).max()
+    q, s = O.gptq_quantize(w, H, 4, 64)
+    vals = O.unpack_int4(q)
+    assert (vals[:, dead] == 0).all()
+
+
 def test_dequantize_fp16_rounds_product():
     """quant.py:199-204 in float16: (q-8) and the scale are fp16, their product rounds to fp16."""
     q = np.array([[0x0F | (0x0 << 4)]], np.uint8)  # values +7, -8
