@@ -34,6 +34,7 @@ extern "C" {
 #define MOEHIP_EINVAL 1       /* bad argument (null pointer, size, unsupported combination) */
 #define MOEHIP_ELAUNCH 2      /* the HIP runtime refused the launch */
 #define MOEHIP_ENODEV 3       /* no usable gfx950 device */
+#define MOEHIP_EIO 4          /* a disk read failed or came back short */
 
 /* record precisions: the `precision` of moelab/store.py:39-45, plus block-scaled fp8 */
 #define MOEHIP_PREC_INT4 0
@@ -186,6 +187,20 @@ int moehip_dispatch(const int64_t *idx, const uint8_t *skip, int T, int k, int E
  * written in the store's packing (quant.py:96-101): bits = 4 -> q (O, I/2) u8, value + 8,
  * low nibble = even column; bits = 8 -> q (O, I) i8. s (O, I/gs) f16. gs even, gs <= 64.
  */
+/*
+ * The disk tier's record read (moelab/store.py:423-445 ExpertStore.read, 378-401 _read_range,
+ * 403-421 _split_reads, 229-255 the direct file): `bytes` bytes at `offset` of the open file into
+ * dst (host memory), as `parts` ranges of ceil(bytes / parts) rounded up to 4096 bytes read at
+ * once on the library's reader threads. fd is an ordinary descriptor; fd_direct an O_DIRECT one on
+ * the same file or -1: a range whose address, offset and length are multiples of 4096 goes through
+ * it (no page-cache copy), and falls back to fd if refused (EINVAL, EFAULT). On return
+ * *direct_ranges and *fallbacks (either may be NULL) count those ranges. Returns MOEHIP_EIO with
+ * the reason on a failed or short read (the reference's "truncated read"). Host only: no HIP
+ * call, no device needed.
+ */
+int moehip_disk_read(int fd, int fd_direct, int64_t offset, void *dst, size_t bytes, int parts, int *direct_ranges,
+                     int *fallbacks);
+
 int moehip_quantize(const float *w, int O, int I, int bits, int gs, void *q, void *s, void *stream);
 
 /*

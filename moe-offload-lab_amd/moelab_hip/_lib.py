@@ -65,6 +65,7 @@ _SIGS = {
     "moehip_dispatch": ([_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _i),
     "moehip_quantize": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
     "moehip_quantize_mse": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
+    "moehip_disk_read": ([_i, _i, ctypes.c_int64, _vp, ctypes.c_size_t, _i, _vp, _vp], _i),
     "moehip_gptq_block": ([_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _i, _vp, _i, _vp, _i, _vp], _i),
     "moehip_quantize_fp8_block": ([_vp, _i, _i, _vp, _vp, _vp], _i),
     "moehip_decode_layer": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp,

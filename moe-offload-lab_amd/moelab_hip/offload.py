@@ -227,7 +227,9 @@ class OffloadDecoder:
     stream wait for every needed record, run the fused experts kernel on the resident table,
     then stage the next layer's predicted experts in the background (runtime.py:899-951).
 
-    host_record(layer, expert, prec) -> pinned uint8 tensor of the record (the host tier).
+    host_record(layer, expert, prec) -> pinned uint8 tensor of the record (the host tier): a
+    callable over records in host memory, or a `diskstore.DiskTier` (RAM cache over a store on
+    disk, which also offers `many` for a batch and `copied` for the copies' completion).
     fast_budget_bytes bounds the resident records (the TierCache budget); the device pool holds
     that plus `margin_records` slots of headroom for copies in flight."""
 
@@ -312,7 +314,12 @@ class OffloadDecoder:
             self.stats["misses"] += len(todo)
         else:
             self.stats["prefetch_issued"] += len(todo)
-        dsts, ev = self.stager.stage([(self.host_record(layer, e, p), p) for e, p in todo])
+        many = getattr(self.host_record, "many", None)  # a host tier that reads a batch at once
+        srcs = many([(layer, e, p) for e, p in todo]) if many else [self.host_record(layer, e, p) for e, p in todo]
+        dsts, ev = self.stager.stage([(src, p) for src, (_, p) in zip(srcs, todo)])
+        copied = getattr(self.host_record, "copied", None)  # its buffers are reusable after `ev`
+        if copied:
+            copied(srcs, ev)
         added = []
         for (e, p), dst in zip(todo, dsts):
             self._blob_prec[dst.data_ptr()] = p

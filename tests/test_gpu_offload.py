@@ -167,3 +167,41 @@ def test_offload_gate_predictor(dev, mode):
     assert st["pred_total"] == T * (L - 1) * k
     assert st["pred_hits"] == st["pred_total"]  # the same state: the gate predicts exactly
     assert st["prefetch_issued"] > 0 and st["prefetch_hits"] > 0
+
+
+@pytest.mark.parametrize("direct,parts", [(True, 4), (False, 1)])
+def test_offload_decoder_from_disk_matches_resident(dev, tmp_path, direct, parts):
+    """The disk tier under the offloaded decoder: records written to a store directory, read back
+    (O_DIRECT + split reads, or plain reads) into pinned pool buffers through a RAM cache smaller
+    than the working set, staged to the device: the outputs are exactly the resident decode's, and
+    RAM and VRAM both evict and re-read."""
+    from moelab_hip.diskstore import DiskTier, ExpertStore, write_store
+
+    H, I, E, L, k, T = 512, 256, 32, 3, 4, 8
+    lay, store, Wr, host_record = _setup(dev, H, I, E, L, k, 7)
+    rb = lay["record_bytes"]
+    write_store(tmp_path / "store", [lay], [f"model.layers.{i}.mlp" for i in range(L)], E, H, I,
+                lambda l, e, p: host_record(l, e, p))
+    tier = DiskTier(ExpertStore(tmp_path / "store"), 20 * rb, pin=True, parts=parts, direct=direct)
+    ref_dec = MoEDecoder(store, k, PrecisionPolicy("lo"), torch.float16, router_weights=Wr)
+    off = OffloadDecoder({"int4": lay}, L, E, k, tier, 13 * rb, dev, PrecisionPolicy("lo"), torch.float16,
+                         router_weights=Wr, mode="kernel")
+    g = torch.Generator().manual_seed(8)
+    xs = (torch.randn(T, L, 1, H, generator=g).half()).to(dev)
+    got = torch.zeros(T, L, 1, H, dtype=torch.float16, device=dev)
+    ref = torch.zeros_like(got)
+    print(f"offload decode from disk direct={direct} parts={parts}: {T} tokens x {L} layers", flush=True)
+    for t in range(T):
+        for l in range(L):
+            ref_dec.route(l, xs[t, l])
+            ref_dec.layer(l, xs[t, l], ref[t, l], idx=ref_dec.idx, w32=ref_dec.w32)
+            off.layer(l, xs[t, l], got[t, l])
+        off.tick()
+    torch.cuda.synchronize()
+    assert off.dec.miss.item() == 0
+    assert torch.equal(got, ref)
+    assert tier.stats["disk_reads"] > 0 and tier.cache.stats.evictions > 0 and tier.stats["host_hits"] > 0
+    assert off.cache.stats.evictions > 0
+    if direct:
+        assert tier.store.direct_reads + tier.store.direct_fallbacks == tier.stats["disk_reads"]
+    tier.close()
