@@ -31,6 +31,7 @@ F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workl
                                                    # layer on a 512-token bf16 chunk (own JSON line)
     python bench.py --workload qwen3-next-offload  # offloaded decode, records in pinned host memory
     python bench.py --workload dense-int8          # one-token int8 GEMVs of the dense part (LM head)
+    python bench.py --workload disk-tier           # offloaded decode served from an expert store on disk
 """
 
 from __future__ import annotations
@@ -781,6 +782,146 @@ def offload_line(args):
     }
 
 
+def _drop_cache(paths) -> None:
+    """Evict the files' pages from the page cache (fsync + POSIX_FADV_DONTNEED: the next reads
+    come from the disk)."""
+    for f in paths:
+        fd = os.open(f, os.O_RDONLY)
+        try:
+            os.fsync(fd)
+            os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+        finally:
+            os.close(fd)
+
+
+def disk_bench(args):
+    """The disk tier at the Qwen3-Next shape: args.disk_layers layers of int4 records (512 per
+    layer) written as a store on the box's disk, then (1) record reads straight from the disk
+    (page cache dropped before each mode): O_DIRECT into page-aligned pageable buffers with 1, 4
+    and 8 ranges in flight, and ordinary reads into pinned buffers with 4; (2) the offloaded
+    decode served from that store through DiskTier (RAM tier a quarter of the store, VRAM budget a
+    tenth), gate predictor on."""
+    import numpy as np
+    import torch
+
+    from moelab_hip import _lib
+    from moelab_hip.diskstore import DiskTier, ExpertStore, write_store
+    from moelab_hip.layer import ResidentStore
+    from moelab_hip.offload import OffloadDecoder
+    from moelab_hip.policy import PrecisionPolicy
+    from moelab_hip.store import record_layout
+
+    dev = torch.device("cuda:0")
+    _lib.check_device(dev)
+    L = args.disk_layers
+    lay = record_layout("int4", NH, NI, 64, scale="absmax")
+    rb = lay["record_bytes"]
+    root = Path(args.store_dir or os.environ.get("TMPDIR", "/tmp")) / f"moehip_store_{os.getpid()}"
+    tmp = ResidentStore({"int4": lay}, 1, NE, dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    cur = {}
+
+    def record(li, e, prec):
+        if cur.get("l") != li:
+            tmp.fill_synthetic(g, std=0.02)
+            cur["l"], cur["host"] = li, tmp.arena["int4"].cpu().numpy()
+        return cur["host"][e * rb:(e + 1) * rb]
+
+    t0 = time.time()
+    write_store(root, [lay], [f"model.layers.{i}.mlp" for i in range(L)], NE, NH, NI, record, model_type="qwen3_next")
+    files = sorted(root.glob("layer*.bin"))
+    _drop_cache(files)
+    log(f"[bench] store of {L * NE} int4 records ({L * NE * rb / 1e9:.2f} GB) written to {root} in {time.time() - t0:.1f} s")
+    del tmp
+    try:
+        st = ExpertStore(root)
+        rng = np.random.default_rng(0)
+        n = min(args.disk_reads, L * NE)
+        picks = [divmod(int(i), NE) for i in rng.choice(L * NE, n, replace=False)]
+        raw = torch.empty(rb + 4096, dtype=torch.uint8)
+        off = (-raw.data_ptr()) % 4096
+        pageable = raw[off:off + rb]
+        pinned = torch.empty(rb, dtype=torch.uint8).pin_memory()
+        reads = {}
+        for name, direct, parts, buf in (("direct_p1", True, 1, pageable), ("direct_p4", True, 4, pageable),
+                                         ("direct_p8", True, 8, pageable), ("pinned_p4", False, 4, pinned)):
+            _drop_cache(files)
+            st.direct = direct
+            st.direct_reads = st.direct_fallbacks = 0
+            ta = time.perf_counter()
+            for li, e in picks:
+                st.read(li, e, "int4", out=buf, parts=parts)
+            dt = time.perf_counter() - ta
+            reads[name] = {"gbs": n * rb / dt / 1e9, "ms_per_record": dt * 1000 / n,
+                           "direct_share": st.direct_reads / n if direct else 0.0}
+            log(f"[bench] disk read {name}: {reads[name]}")
+        st.close()
+        # the offloaded decode from disk
+        steps, warm = args.disk_steps, max(4, args.disk_steps // 8)
+        Wr, xs = residual_stream(dev, warm + steps, L, NE, NH, seed=1)
+        _drop_cache(files)
+        tier = DiskTier(ExpertStore(root), L * NE * rb // 4, pin=True, parts=4, direct=False)
+        off = OffloadDecoder({"int4": lay}, L, NE, NK, tier, L * NE * rb // 10, dev, PrecisionPolicy("lo"),
+                             torch.bfloat16, router_weights=Wr, renorm=True, mode="kernel", predictor="gate")
+        out = torch.zeros(1, NH, dtype=torch.bfloat16, device=dev)
+        for t in range(warm):
+            for li in range(L):
+                off.layer(li, xs[t, li], out)
+            off.tick()
+        torch.cuda.synchronize()
+        s0, d0, b0 = dict(off.stats), dict(tier.stats), tier.store.bytes_read
+        ta = time.perf_counter()
+        for t in range(warm, warm + steps):
+            for li in range(L):
+                off.layer(li, xs[t, li], out)
+            off.tick()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - ta
+        off.dec.check_error()
+        if off.dec.miss.item() != 0:
+            raise RuntimeError("offloaded decode ran an expert that was not resident")
+        ds = {k: off.stats[k] - s0[k] for k in s0}
+        dd = {k: tier.stats[k] - d0[k] for k in d0}
+        dec = {"tok_s": steps / dt, "ms_per_token": dt * 1000 / steps,
+               "vram_hit_rate": ds["hits"] / max(1, ds["hits"] + ds["misses"]),
+               "ram_hit_rate": dd["host_hits"] / max(1, dd["host_hits"] + dd["disk_reads"]),
+               "disk_reads_per_token": dd["disk_reads"] / steps,
+               "disk_gbs": (tier.store.bytes_read - b0) / dt / 1e9}
+        log(f"[bench] offload from disk: {dec}")
+        tier.close()
+    finally:
+        for f in root.glob("*"):
+            f.unlink()
+        root.rmdir()
+    return {"reads": reads, "dec": dec, "L": L, "steps": steps, "warm": warm, "store_gb": L * NE * rb / 1e9,
+            "n_reads": n, "rb": rb}
+
+
+def disk_line(args):
+    r = disk_bench(args)
+    d = r["dec"]
+    peak = max(v["gbs"] for v in r["reads"].values())
+    side = lambda d_: {k: round(v, 4) if isinstance(v, float) else v for k, v in d_.items()}  # noqa: E731
+    return {
+        "metric": "offloaded int4 MoE decode tok/s from an expert store on disk, Qwen3-Next shape, bs=1, 1 GPU",
+        "value": round(d["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": r["steps"], "warmup": r["warm"],
+        "ms_per_step": round(d["ms_per_token"], 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int4", "data": "synthetic",
+        "config": {"workload": f"Qwen3-Next-shaped offloaded decode over {r['L']} layers whose int4 gs64 records "
+                               f"({r['store_gb']:.2f} GB) are a store on the box's disk: RAM tier 1/4 of it (pinned "
+                               "pool, LRFU), VRAM budget 1/10, gate predictor, bs=1",
+                   "d_model": NH, "experts": NE, "top_k": NK, "d_ff": NI, "layers": r["L"],
+                   "record_bytes": r["rb"]},
+        "vram_hit_rate": round(d["vram_hit_rate"], 4), "ram_hit_rate": round(d["ram_hit_rate"], 4),
+        "disk_reads_per_token": round(d["disk_reads_per_token"], 2),
+        "roofline": {"bound": "disk", "achieved": round(d["disk_gbs"], 3), "peak": round(peak, 3), "unit": "GB/s",
+                     "frac": round(d["disk_gbs"] / peak, 4), "traffic": None,
+                     "peak_is": f"best record-read rate measured on this disk ({r['n_reads']} random records)"},
+        "disk_reads": {k: side(v) for k, v in r["reads"].items()},
+        "cpu_baseline": None,
+    }
+
+
 def cpu_baseline(seconds: float):
     """moelab's CPU expert branch (runtime.py:646-702: fp32 dequantize, F.linear, silu, add_ with
     alpha = w) restated in torch (oracle/cpu_path.py), on one OLMoE layer of 8 int4 records, all
@@ -809,12 +950,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload", "dense-int8",
+                                           "disk-tier",
                                            *DECODE_SPECS, *BATCH_SPECS],
                     default="olmoe-decode-bs1")
     ap.add_argument("--offload-layers", type=int, default=48)
     ap.add_argument("--offload-steps", type=int, default=256)
     ap.add_argument("--offload-warmup", type=int, default=32)
     ap.add_argument("--stage-mode", choices=["auto", "kernel", "sdma"], default="auto")
+    ap.add_argument("--disk-layers", type=int, default=4)
+    ap.add_argument("--disk-reads", type=int, default=512)
+    ap.add_argument("--disk-steps", type=int, default=64)
+    ap.add_argument("--store-dir", default=None, help="where the disk-tier workload writes its store")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
@@ -833,6 +979,9 @@ def main():
         return
     if args.workload == "dense-int8":
         print(json.dumps(dense_line(args)), flush=True)
+        return
+    if args.workload == "disk-tier":
+        print(json.dumps(disk_line(args)), flush=True)
         return
     if args.workload in DECODE_SPECS:
         print(json.dumps(decode_line(args, args.workload)), flush=True)
