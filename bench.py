@@ -287,8 +287,25 @@ def prefill_line(args):
                      "bytes_per_launch": int(r["alg"])},
         "mfma": {"achieved": round(tfs, 1), "peak": MFMA_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_PEAK_TFS, 4),
                  "flops_per_launch": r["flops"]},
-        "cpu_baseline": None,
+        "cpu_baseline": None if args.no_cpu else prefill_cpu_baseline(args.cpu_seconds),
     }
+
+
+def prefill_cpu_baseline(seconds: float):
+    """moelab's prefill expert path on the host (runtime.py:418-436, 352-353: per expert materialize,
+    F.linear, index_add_) restated in torch fp32 (oracle/cpu_path.py), on a bounded sample of
+    experts of the chunk's average token count."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_path
+
+    r = cpu_path.time_prefill_layer(seconds, QH, QI, QE, QK, QT)
+    log(f"[bench] prefill cpu baseline: {r['n']} experts in {r['seconds']:.1f} s on {r['threads']} threads "
+        f"({r['cpu_model']}): {r['layer_s'] * 1000:.1f} ms per layer")
+    return {"value": round(QT / r["layer_s"], 1), "unit": "tok/s", "cores": r["threads"], "kind": "port",
+            "host_cpus": r["host_cpus"], "cpu_model": r["cpu_model"],
+            "sample": f"{r['n']} experts of {r['tokens_per_expert']} tokens (int4 gs64 records, torch fp32 "
+                      f"dequantize + F.linear + index_add_) in {r['seconds']:.1f} s on {r['threads']} threads; "
+                      f"layer = {QE} experts x {r['expert_s'] * 1000:.2f} ms"}
 
 
 # The dense part in int8 (moelab/denseq.py), one token: the LM heads and an attention projection
@@ -506,8 +523,24 @@ def decode_line(args, name):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "fused decode layer (one launch per layer, HIP graph per token)",
                      "bytes_per_launch": int(alg)},
-        "cpu_baseline": None,
+        "cpu_baseline": (decode_cpu_baseline(args.cpu_seconds, H_, I_, k_ + (1 if sp["shared"] else 0), L_)
+                         if not args.no_cpu and sp["precs"] == ["int4"] else None),
     }
+
+
+def decode_cpu_baseline(seconds: float, H_: int, I_: int, n_exp: int, L_: int):
+    """moelab's CPU expert branch (runtime.py:646-702) restated in torch (oracle/cpu_path.py) on one
+    layer of this workload's shape: n_exp int4 gs64 records (the routed experts, plus the shared
+    one where the model has it), one token, the host's cores."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_path
+
+    r = cpu_path.time_olmoe_layer(seconds, H_, I_, n_exp)
+    log(f"[bench] cpu baseline: {r['n']} layers in {r['seconds']:.1f} s on {r['threads']} threads")
+    return {"value": round(1.0 / r["layer_s"] / L_, 3), "unit": "tok/s", "cores": r["threads"], "kind": "port",
+            "host_cpus": r["host_cpus"], "cpu_model": r["cpu_model"],
+            "sample": f"{r['n']} token-layers ({n_exp} int4 gs64 records of H={H_}, I={I_}, torch fp32 dequantize + "
+                      f"F.linear on {r['threads']} threads) in {r['seconds']:.1f} s; tok/s over the {L_}-layer stack"}
 
 
 def batch_line(args, name):

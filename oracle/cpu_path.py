@@ -111,3 +111,41 @@ def time_olmoe_layer(seconds: float, H: int = 2048, I: int = 1024, k: int = 8, s
             break
     return {"layer_s": el / n, "n": n, "seconds": el, "threads": threads, "host_cpus": os.cpu_count(),
             "cpu_model": cpu_model(), "record_bytes": lay["record_bytes"], "k": k}
+
+
+def time_prefill_layer(seconds: float, H: int = 2048, I: int = 768, E: int = 128, k: int = 8, T: int = 512,
+                       seed: int = 0) -> dict:
+    """A prefill chunk on the CPU path (runtime.py:418-436 `_run_grouped_tokens` with the experts on
+    the host: per expert the rows of its tokens, `materialize`, `expert_ffn`, then
+    out.index_add_(0, rows, y * w) as runtime.py:352-353), fp32, on a bounded sample: experts of
+    T * k / E tokens each (the chunk's average), as many as fit in about `seconds`; the layer time is
+    the per-expert time times E."""
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(seed)
+    lay = O.record_layout("int4", H, I, 64, scale="absmax")
+    n_rec = 4
+    blobs = [torch.from_numpy(O.encode_record(lay, (rng.standard_normal((2 * I, H)) * 0.02).astype(np.float32),
+                                              (rng.standard_normal((H, I)) * 0.02).astype(np.float32), "absmax"))
+             for _ in range(n_rec)]
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32))
+    per = max(1, T * k // E)
+    out = torch.zeros(T, H)
+
+    def one(i):
+        rows = torch.from_numpy(rng.choice(T, per, replace=False))
+        w = torch.from_numpy(rng.random(per).astype(np.float32))
+        gu, dn = materialize(lay, blobs[i % n_rec], torch.float32)
+        y = expert_ffn(x.index_select(0, rows), gu, dn)
+        out.index_add_(0, rows, y * w[:, None])
+
+    one(0)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        one(n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"expert_s": el / n, "layer_s": el / n * E, "n": n, "seconds": el, "threads": threads,
+            "tokens_per_expert": per, "host_cpus": os.cpu_count(), "cpu_model": cpu_model()}
