@@ -9,8 +9,9 @@
 //
 //   1. routing, replicated per XCD: the workgroups of an XCD compute the E router logits (and the
 //      Qwen3-Next shared gate) between them, each into its XCD's copy, and every workgroup reads
-//      all of them back and ranks them itself (top-k and the record of each table row; the
-//      weights, renorm and HOBBIT decision follow while the expert weights load);
+//      all of them back and ranks them itself (top-k and the record of each table row, the keys
+//      in registers; the weights, renorm and HOBBIT decision follow while the other waves'
+//      expert weights load);
 //   2. the table rows' h values (k routed + shared, I each, flattened row after row) are cut into
 //      8 contiguous segments, one per XCD; workgroup q of an XCD holds up part q (hpi h values
 //      of its segment: h = w * silu(gate x) * (up x), w = the row's routed weight, into the XCD's
@@ -235,6 +236,29 @@ __device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int fi
 // follow while they are in flight. A row with no resident copy (or an unplanned layer) has
 // base 0 and never runs; a row that part 2 skips runs with weight 0.
 // ---------------------------------------------------------------------------------------
+// top-k of E > 64 keys by one wave: EPL keys per lane (lane + 64 i), held in registers for the k
+// rounds of a wave maximum (no LDS traffic per round; EPL fixed so that a round costs 3 EPL VALU
+// operations plus the maximum); keys are distinct (the index is part of the key)
+template <int EPL>
+__device__ __forceinline__ void xc_topk(const uint32_t *s_key, int E, int k, int lane, int &myc) {
+    uint32_t key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int c = lane + 64 * i;
+        key[i] = c < E ? s_key[c] : 0u;
+    }
+    for (int r = 0; r < k; ++r) {
+        uint32_t lb = key[0];
+#pragma unroll
+        for (int i = 1; i < EPL; ++i) lb = max(lb, key[i]);
+        const uint32_t M = wave_max_u32(lb);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i)
+            if (key[i] == M) key[i] = 0u;
+        if (lane == r) myc = min(1023 - (int)(M & 1023u), E - 1);
+    }
+}
+
 template <int XDT>
 __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag, int spin,
                                         int64_t idx_pre, int &myc, float &myv, bool &poisoned) {
@@ -311,20 +335,10 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
             }
         } else {
             const int epl = (E + 63) >> 6;
-            for (int r = 0; r < k; ++r) {
-                uint32_t lb = 0u;
-                for (int i = 0; i < epl; ++i) {
-                    const int c = lane + 64 * i;
-                    const uint32_t kk = c < E ? s_key[c] : 0u;
-                    lb = kk > lb ? kk : lb;
-                }
-                const uint32_t M = wave_max_u32(lb);
-                const int c = min(1023 - (int)(M & 1023u), E - 1);
-                __builtin_amdgcn_wave_barrier();
-                if (lane == (c & 63)) s_key[c] = 0u;
-                __builtin_amdgcn_wave_barrier();
-                if (lane == r) myc = c;
-            }
+            if (epl <= 2) xc_topk<2>(s_key, E, k, lane, myc);
+            else if (epl <= 4) xc_topk<4>(s_key, E, k, lane, myc);
+            else if (epl <= 8) xc_topk<8>(s_key, E, k, lane, myc);
+            else xc_topk<XC_MAXE / 64>(s_key, E, k, lane, myc);
         }
         if (lane < k) myv = s_lv[myc];
     } else if (lane < k) {
@@ -342,7 +356,8 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
 }
 
 // ---------------------------------------------------------------------------------------
-// routing, part 2, by wave 0 of the up items while their weights load: softmax over the E logits
+// routing, part 2, by the routing wave of the up items before it requests its own weights (the
+// other waves' weights load meanwhile): softmax over the E logits
 // (fp32), the top-k weights (renormalised when asked), the HOBBIT levels and skips (the shared
 // row: level 0, never skipped, weight sigmoid(shared gate logit)); sh.rw[j] = the weight of table
 // row j, 0 for a row that does not run; the report's indices, weights, levels and choices.
@@ -695,9 +710,12 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     if (is_up) {
         // 2. h of this item's rows: the loads, routing part 2 meanwhile, then the products
         XcUp<PREC> u;
+        // the routing wave weighs the rows before requesting its own weights: behind them, its
+        // softmax would wait for the CU's queue of weight requests to drain, and every product
+        // waits for the weights it decides
+        if (wave == rwave) xc_weigh<XDT>(a, sh, myc, myv, poisoned, w_pre);
         const bool run = up_work && xc_up_issue<PREC, XDT>(a, sh, f0, seg0, hx, tag, u);
         xc_stamp(a, sh, 7);
-        if (wave == rwave) xc_weigh<XDT>(a, sh, myc, myv, poisoned, w_pre);
         __syncthreads();
         if (run) xc_up_finish<PREC, XDT>(a, sh, f0, seg0, hx, tag, u, xr);
         if (tag != 0u) xc_gen_read(a.ws);  // (counted once this item's loads are all used)
