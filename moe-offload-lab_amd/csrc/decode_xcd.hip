@@ -646,7 +646,149 @@ __device__ __forceinline__ void xc_down_rows(const XcArgs &a, const XcDown<PREC>
 // ---------------------------------------------------------------------------------------
 // the kernel
 // ---------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------
+// down item `item` of XCD x: output rows [d * dr, ...) (d = item - nu) over the XCD's segment
+// [seg0, seg0 + seg_len) of h: the down weights (after the gate/up weights' head start, for a
+// first item), the segment's h from the XCD's L2 into LDS, the products, then the partial rows:
+// the combiner of the row block (d % 8 == x) sums the 8 XCDs' partials and writes the output
+// ---------------------------------------------------------------------------------------
 template <int XDT, int PREC>
+__device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, const int item, const bool first, const int x,
+                                             const int seg0, const int seg_len, uint64_t *hx, uint64_t *part,
+                                             const uint32_t tag, const int spin) {
+    constexpr int VPC = DlFmt<PREC>::VPC, NPD = XcFmt<PREC>::NPD;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // 3. the down rows over the segment: their weights (after the gate/up weights' head start),
+    //    the segment's h -> LDS (piece-major: piece m of chunk c at (m * C + c) * 4), the products
+    const int d = item - a.nu;
+    const int lgd = a.lg_dn, G = 1 << lgd, RPW = 64 >> lgd;
+    const int row0 = d * a.dr + wave * NPD * RPW;
+    const int nch = seg_len / VPC;
+    if (first && a.defer != 0u) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        const uint32_t defer = (uint32_t)uni((int)a.defer);
+        while (__builtin_amdgcn_s_memrealtime() - t0 < defer) __builtin_amdgcn_s_sleep(8);
+    }
+    XcDown<PREC> dd;
+    xc_down_load<PREC>(a, sh, row0, seg0, nch, true, dd);
+    if (first && tag != 0u) xc_gen_read(a.ws);
+    xc_stamp(a, sh, 8);
+    float *s_h = sh.u.h;
+    const int C = nch > 0 ? nch : 1;
+    bool h_ok = true;
+    for (int w0 = 0; w0 < seg_len; w0 += 256 * 8) {
+        // two rounds of 8 words in flight (every round loads all 8, at clamped indices, so the
+        // wait for the older round is exact)
+        uint32_t need = 0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            if (w0 + tid + 256 * m < seg_len) need |= 1u << m;
+        const uint64_t *hs = hx + w0 + tid;
+        const int lim = seg_len - 1 - w0 - tid;  // (index of the last word, relative)
+        auto take = [&](const uint64_t (&v)[8]) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) {
+                if ((need & (1u << m)) && tag_ok(v[m], tag)) {
+                    const int i = w0 + tid + 256 * m;
+                    const int c = i / VPC, qq = i - c * VPC;
+                    s_h[((qq >> 2) * C + c) * 4 + (qq & 3)] = __uint_as_float((uint32_t)v[m]);
+                    need &= ~(1u << m);
+                }
+            }
+        };
+        uint64_t va[8], vb[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+        int it = 0;
+        for (; it < spin; it += 2) {
+#pragma unroll
+            for (int m = 0; m < 8; ++m) vb[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+            take(va);
+            if (!__syncthreads_or(need != 0)) break;
+#pragma unroll
+            for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
+            take(vb);
+            if (!__syncthreads_or(need != 0)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (it >= spin) {
+            h_ok = false;
+            if (tid == 0) flag_error(a.ws + XC_ERR);
+        }
+    }
+    xc_stamp(a, sh, 10);
+    LaneVec<PREC, XDT> lh;
+    load_h<PREC, XDT>(s_h, lane & (G - 1), G, C, lh);
+    float v[NPD];
+    xc_down_rows<PREC, XDT>(a, dd, lh, v);
+    if (!h_ok)
+#pragma unroll
+        for (int p = 0; p < NPD; ++p) v[p] = __uint_as_float(0x7fc00000u);
+    xc_stamp(a, sh, 11);
+    // 4. the partial rows: the combiner of this row block keeps its own, the others send theirs
+    const bool combiner = (d % XC_N) == x;
+    const int cl = lane & (G - 1), slot = lane >> lgd;
+    if (cl == G - 1) {
+#pragma unroll
+        for (int p = 0; p < NPD; ++p) {
+            const int r = row0 + p * RPW + slot;
+            if (r < a.H) {
+                if (combiner) sh.part[r - d * a.dr] = v[p];
+                else st_tag(part + (size_t)x * a.H + r, __float_as_uint(v[p]), tag);
+            }
+        }
+    }
+    if (combiner) {
+        __syncthreads();
+        const int r0 = d * a.dr, nrow = min(a.dr, a.H - r0);
+        for (int rr = tid; rr < nrow; rr += 256) {
+            // two rounds of the 8 words in flight at once (each round loads all 8, so the
+            // compiler's wait for the older round is exact): a new round every poll, not every
+            // round trip
+            const uint64_t *src = part + r0 + rr;
+            float val[XC_N];
+            uint32_t need = 0xFFu & ~(1u << x);
+            val[x] = sh.part[rr];
+            uint64_t wa[XC_N], wb[XC_N];
+#pragma unroll
+            for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
+            for (int it = 0; it < spin; it += 2) {
+#pragma unroll
+                for (int xx = 0; xx < XC_N; ++xx) wb[xx] = ld_tag(src + (size_t)xx * a.H);
+#pragma unroll
+                for (int xx = 0; xx < XC_N; ++xx)
+                    if ((need & (1u << xx)) && tag_ok(wa[xx], tag)) {
+                        val[xx] = __uint_as_float((uint32_t)wa[xx]);
+                        need &= ~(1u << xx);
+                    }
+                if (need == 0) break;
+                __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
+#pragma unroll
+                for (int xx = 0; xx < XC_N; ++xx)
+                    if ((need & (1u << xx)) && tag_ok(wb[xx], tag)) {
+                        val[xx] = __uint_as_float((uint32_t)wb[xx]);
+                        need &= ~(1u << xx);
+                    }
+                if (need == 0) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
+            float acc = 0.f;
+#pragma unroll
+            for (int xx = 0; xx < XC_N; ++xx) acc += (need & (1u << xx)) ? __uint_as_float(0x7fc00000u) : val[xx];
+            if (need != 0) flag_error(a.ws + XC_ERR);
+            if (a.accumulate) acc += ld_act<XDT>(a.out, r0 + rr);
+            if (a.add != nullptr) acc += ld_act<XDT>(a.add, r0 + rr);
+            st_act<XDT>(a.out, r0 + rr, acc);
+        }
+    }
+    xc_stamp(a, sh, 12);
+}
+
+// TWO: a second pass of down items (its own instantiation: the single-pass kernel's registers and
+// schedule stay those of a kernel without it)
+template <int XDT, int PREC, bool TWO>
 __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     __shared__ XcShared sh;
     constexpr int VPC = DlFmt<PREC>::VPC, NPD = XcFmt<PREC>::NPD;
@@ -721,137 +863,27 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
         if (tag != 0u) xc_gen_read(a.ws);  // (counted once this item's loads are all used)
         xc_stamp(a, sh, 9);
     } else {
-        // 3. the down rows over the segment: their weights (after the gate/up weights' head start),
-        //    the segment's h -> LDS (piece-major: piece m of chunk c at (m * C + c) * 4), the products
-        const int d = q - a.nu;
-        const int lgd = a.lg_dn, G = 1 << lgd, RPW = 64 >> lgd;
-        const int row0 = d * a.dr + wave * NPD * RPW;
-        const int nch = seg_len / VPC;
-        if (a.defer != 0u) {
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            const uint32_t defer = (uint32_t)uni((int)a.defer);
-            while (__builtin_amdgcn_s_memrealtime() - t0 < defer) __builtin_amdgcn_s_sleep(8);
-        }
-        XcDown<PREC> dd;
-        xc_down_load<PREC>(a, sh, row0, seg0, nch, true, dd);
-        if (tag != 0u) xc_gen_read(a.ws);
-        xc_stamp(a, sh, 8);
-        float *s_h = sh.u.h;
-        const int C = nch > 0 ? nch : 1;
-        bool h_ok = true;
-        for (int w0 = 0; w0 < seg_len; w0 += 256 * 8) {
-            // two rounds of 8 words in flight (every round loads all 8, at clamped indices, so the
-            // wait for the older round is exact)
-            uint32_t need = 0;
-#pragma unroll
-            for (int m = 0; m < 8; ++m)
-                if (w0 + tid + 256 * m < seg_len) need |= 1u << m;
-            const uint64_t *hs = hx + w0 + tid;
-            const int lim = seg_len - 1 - w0 - tid;  // (index of the last word, relative)
-            auto take = [&](const uint64_t (&v)[8]) {
-#pragma unroll
-                for (int m = 0; m < 8; ++m) {
-                    if ((need & (1u << m)) && tag_ok(v[m], tag)) {
-                        const int i = w0 + tid + 256 * m;
-                        const int c = i / VPC, qq = i - c * VPC;
-                        s_h[((qq >> 2) * C + c) * 4 + (qq & 3)] = __uint_as_float((uint32_t)v[m]);
-                        need &= ~(1u << m);
-                    }
-                }
-            };
-            uint64_t va[8], vb[8];
-#pragma unroll
-            for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
-            int it = 0;
-            for (; it < spin; it += 2) {
-#pragma unroll
-                for (int m = 0; m < 8; ++m) vb[m] = ld_local(hs + min(256 * m, max(lim, 0)));
-                take(va);
-                if (!__syncthreads_or(need != 0)) break;
-#pragma unroll
-                for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
-                take(vb);
-                if (!__syncthreads_or(need != 0)) break;
-                __builtin_amdgcn_s_sleep(1);
-            }
-            if (it >= spin) {
-                h_ok = false;
-                if (tid == 0) flag_error(a.ws + XC_ERR);
-            }
-        }
-        xc_stamp(a, sh, 10);
-        LaneVec<PREC, XDT> lh;
-        load_h<PREC, XDT>(s_h, lane & (G - 1), G, C, lh);
-        float v[NPD];
-        xc_down_rows<PREC, XDT>(a, dd, lh, v);
-        if (!h_ok)
-#pragma unroll
-            for (int p = 0; p < NPD; ++p) v[p] = __uint_as_float(0x7fc00000u);
-        xc_stamp(a, sh, 11);
-        // 4. the partial rows: the combiner of this row block keeps its own, the others send theirs
-        const bool combiner = (d % XC_N) == x;
-        const int cl = lane & (G - 1), slot = lane >> lgd;
-        if (cl == G - 1) {
-#pragma unroll
-            for (int p = 0; p < NPD; ++p) {
-                const int r = row0 + p * RPW + slot;
-                if (r < a.H) {
-                    if (combiner) sh.part[r - d * a.dr] = v[p];
-                    else st_tag(part + (size_t)x * a.H + r, __float_as_uint(v[p]), tag);
-                }
-            }
-        }
-        if (combiner) {
-            __syncthreads();
-            const int r0 = d * a.dr, nrow = min(a.dr, a.H - r0);
-            for (int rr = tid; rr < nrow; rr += 256) {
-                // two rounds of the 8 words in flight at once (each round loads all 8, so the
-                // compiler's wait for the older round is exact): a new round every poll, not every
-                // round trip
-                const uint64_t *src = part + r0 + rr;
-                float val[XC_N];
-                uint32_t need = 0xFFu & ~(1u << x);
-                val[x] = sh.part[rr];
-                uint64_t wa[XC_N], wb[XC_N];
-#pragma unroll
-                for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
-                for (int it = 0; it < spin; it += 2) {
-#pragma unroll
-                    for (int xx = 0; xx < XC_N; ++xx) wb[xx] = ld_tag(src + (size_t)xx * a.H);
-#pragma unroll
-                    for (int xx = 0; xx < XC_N; ++xx)
-                        if ((need & (1u << xx)) && tag_ok(wa[xx], tag)) {
-                            val[xx] = __uint_as_float((uint32_t)wa[xx]);
-                            need &= ~(1u << xx);
-                        }
-                    if (need == 0) break;
-                    __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-                    for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
-#pragma unroll
-                    for (int xx = 0; xx < XC_N; ++xx)
-                        if ((need & (1u << xx)) && tag_ok(wb[xx], tag)) {
-                            val[xx] = __uint_as_float((uint32_t)wb[xx]);
-                            need &= ~(1u << xx);
-                        }
-                    if (need == 0) break;
-                    __builtin_amdgcn_s_sleep(2);
-                }
-                float acc = 0.f;
-#pragma unroll
-                for (int xx = 0; xx < XC_N; ++xx) acc += (need & (1u << xx)) ? __uint_as_float(0x7fc00000u) : val[xx];
-                if (need != 0) flag_error(a.ws + XC_ERR);
-                if (a.accumulate) acc += ld_act<XDT>(a.out, r0 + rr);
-                if (a.add != nullptr) acc += ld_act<XDT>(a.add, r0 + rr);
-                st_act<XDT>(a.out, r0 + rr, acc);
-            }
-        }
-        xc_stamp(a, sh, 12);
+        xc_down_item<XDT, PREC>(a, sh, q, true, x, seg0, seg_len, hx, part, tag, spin);
     }
-    xc_stamp(a, sh, 13);
-    if (b == 0) {
-        __syncthreads();
-        xc_report<XDT>(a, sh);
+    if constexpr (TWO) {
+        if (b == 0) {  // (the report reads the routing's LDS, which a second item reuses for h)
+            __syncthreads();
+            xc_report<XDT>(a, sh);
+        }
+        // a second pass only where the layer has more items than the GPU holds workgroups: every
+        // up item is a first item and every second item is a down item of a workgroup whose first
+        // item was an up item, so no wait depends on an item that has not started
+        if (q + NQ < a.nu + a.nd) {
+            __syncthreads();
+            xc_down_item<XDT, PREC>(a, sh, q + NQ, false, x, seg0, seg_len, hx, part, tag, spin);
+        }
+        xc_stamp(a, sh, 13);
+    } else {
+        xc_stamp(a, sh, 13);
+        if (b == 0) {
+            __syncthreads();
+            xc_report<XDT>(a, sh);
+        }
     }
     xc_gen_manage(a.ws, tag);
     if (a.trace != nullptr) {
@@ -868,20 +900,20 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
 // ---------------------------------------------------------------------------------------
 typedef void (*XcKernel)(XcArgs);
 
-template <int XDT>
+template <int XDT, bool TWO>
 static XcKernel xc_kernel_x(int prec) {
     switch (prec) {
-        case MOEHIP_PREC_INT4: return k_decode_xcd<XDT, MOEHIP_PREC_INT4>;
-        case MOEHIP_PREC_INT8: return k_decode_xcd<XDT, MOEHIP_PREC_INT8>;
-        case MOEHIP_PREC_F16: return k_decode_xcd<XDT, MOEHIP_PREC_F16>;
-        case MOEHIP_PREC_BF16: return k_decode_xcd<XDT, MOEHIP_PREC_BF16>;
-        case MOEHIP_PREC_FP8: return k_decode_xcd<XDT, MOEHIP_PREC_FP8>;
+        case MOEHIP_PREC_INT4: return k_decode_xcd<XDT, MOEHIP_PREC_INT4, TWO>;
+        case MOEHIP_PREC_INT8: return k_decode_xcd<XDT, MOEHIP_PREC_INT8, TWO>;
+        case MOEHIP_PREC_F16: return k_decode_xcd<XDT, MOEHIP_PREC_F16, TWO>;
+        case MOEHIP_PREC_BF16: return k_decode_xcd<XDT, MOEHIP_PREC_BF16, TWO>;
+        case MOEHIP_PREC_FP8: return k_decode_xcd<XDT, MOEHIP_PREC_FP8, TWO>;
         default: return nullptr;
     }
 }
-static XcKernel xc_kernel(int dtype, int prec) {
-    if (dtype == MOEHIP_DT_F16) return xc_kernel_x<MOEHIP_DT_F16>(prec);
-    if (dtype == MOEHIP_DT_BF16) return xc_kernel_x<MOEHIP_DT_BF16>(prec);
+static XcKernel xc_kernel(int dtype, int prec, bool two) {
+    if (dtype == MOEHIP_DT_F16) return two ? xc_kernel_x<MOEHIP_DT_F16, true>(prec) : xc_kernel_x<MOEHIP_DT_F16, false>(prec);
+    if (dtype == MOEHIP_DT_BF16) return two ? xc_kernel_x<MOEHIP_DT_BF16, true>(prec) : xc_kernel_x<MOEHIP_DT_BF16, false>(prec);
     return nullptr;
 }
 
@@ -997,13 +1029,24 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     const int ks = d->k + (d->shared_gate != nullptr ? 1 : 0);
     const XcPlan p = xc_plan(d->prec[0], ks, d->E, d->H, d->I);
     if (!p.ok || ws_bytes < p.total) return MOEHIP_OK;
-    XcKernel kern = xc_kernel(d->dtype, d->prec[0]);
-    if (kern == nullptr) return MOEHIP_OK;
-    int cus = 0, per_cu = 0;
+    XcKernel kern = xc_kernel(d->dtype, d->prec[0], false);
+    XcKernel kern2 = xc_kernel(d->dtype, d->prec[0], true);
+    if (kern == nullptr || kern2 == nullptr) return MOEHIP_OK;
+    int cus = 0, per_cu = 0, per_cu2 = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(kern), 256, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, reinterpret_cast<const void *>(kern2), 256, 0) != hipSuccess)
         return MOEHIP_OK;
-    if (p.grid > per_cu * cus) return MOEHIP_OK;  // every workgroup must be resident at once
+    // every workgroup must be resident at once; a layer with more items than that (fp8 rows at the
+    // Qwen3-Next shape: 152 items per XCD) runs the two-pass kernel, when every up item can be a
+    // first item and no workgroup whose first item is a down item needs a second
+    int grid = p.grid;
+    if (grid > per_cu * cus) {
+        const int nq = per_cu2 * cus / XC_N;
+        if (nq < p.nu || nq < p.nd || p.nu + p.nd > 2 * nq) return MOEHIP_OK;
+        grid = nq * XC_N;
+        kern = kern2;
+    }
     XcArgs a{};
     a.x = x;
     a.Wr = Wr;
@@ -1057,7 +1100,7 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     // with it, 15.1 without, 15.0 with half of it)
     const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
     a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8);
-    hipLaunchKernelGGL(kern, dim3(p.grid), dim3(256), 0, as_stream(stream), a);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream), a);
     *used = 1;
     return check_launch("decode_layer (xcd)");
 }
