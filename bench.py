@@ -50,14 +50,17 @@ H, I, E, K_TOP, L = 2048, 1024, 64, 8, 16
 HBM_PEAK_GBS = 8000.0
 PROFILE = ROOT / "profiles" / "k_decode_xcd_olmoe_int4_bs1.md"
 PREFILL_PROFILE = ROOT / "profiles" / "k_gemm_qwen3_30b_prefill_t512.md"
+BATCH_PROFILE = ROOT / "profiles" / "k_gemv_batched_decode.md"
 
 
-def measured_traffic(profile: Path = PROFILE):
+def measured_traffic(profile: Path = PROFILE, workload: str | None = None):
     """HBM bytes per launch from a committed counter summary (its `traffic_bytes_per_launch:`
-    line), or None."""
+    line, or `traffic_bytes_per_layer[workload]:` for a summary that covers several workloads),
+    or None."""
+    key = "traffic_bytes_per_launch:" if workload is None else f"traffic_bytes_per_layer[{workload}]:"
     try:
         for line in profile.read_text().splitlines():
-            if line.strip().startswith("traffic_bytes_per_launch:"):
+            if line.strip().startswith(key):
                 return int(float(line.split(":", 1)[1].split()[0]))
     except (OSError, ValueError):
         pass
@@ -543,6 +546,25 @@ def decode_cpu_baseline(seconds: float, H_: int, I_: int, n_exp: int, L_: int):
                       f"F.linear on {r['threads']} threads) in {r['seconds']:.1f} s; tok/s over the {L_}-layer stack"}
 
 
+def batch_cpu_baseline(seconds: float, H_: int, I_: int, n_exp: float, B: int, L_: int):
+    """moelab's CPU expert branch (runtime.py:646-702, oracle/cpu_path.py) for a batch: each distinct
+    expert of the layer is dequantised once and run on its tokens. Timed on 8 int4 gs64 records
+    with one token each; the layer time is the per-record time times the layer's distinct experts
+    (a record's dequantisation dominates: its 1-2 tokens' products are left out, which favours the
+    CPU)."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import cpu_path
+
+    r = cpu_path.time_olmoe_layer(seconds, H_, I_, 8)
+    layer_s = r["layer_s"] / 8 * n_exp
+    log(f"[bench] cpu baseline: {r['n']} 8-record layers in {r['seconds']:.1f} s on {r['threads']} threads")
+    return {"value": round(B / (layer_s * L_), 3), "unit": "tok/s", "cores": r["threads"], "kind": "port",
+            "host_cpus": r["host_cpus"], "cpu_model": r["cpu_model"],
+            "sample": f"{r['n']} x 8 int4 gs64 records of H={H_}, I={I_} (torch fp32 dequantize + F.linear, one "
+                      f"token each, {r['threads']} threads) in {r['seconds']:.1f} s; scaled to {n_exp:.1f} "
+                      f"distinct experts per layer, {B} tokens, {L_} layers"}
+
+
 def batch_line(args, name):
     """Batched decode: B tokens per step through L layers on the grouped path (GroupedLayer: router,
     levels, dispatch, per-expert vote, grouped GEMMs per precision, ordered combine), a HIP graph
@@ -611,11 +633,14 @@ def batch_line(args, name):
                    "distinct_experts_per_layer": round(distinct / (S * L_), 2)},
         "layer_us": round(layer_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(PREFILL_PROFILE),
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(BATCH_PROFILE, name),
+                     "traffic_scope": "k_gemv_up + k_gemv_down per layer (FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "whole layer: router logits + top-k / shared slot + levels, dispatch, vote and "
                                "work list + k_gemv_up/down per precision + combine (HIP graph per step)",
                      "bytes_per_launch": int(alg)},
-        "cpu_baseline": None,
+        "cpu_baseline": (None if args.no_cpu else
+                         batch_cpu_baseline(args.cpu_seconds, H_, I_, distinct / (S * L_) + (1 if sp["shared"] else 0),
+                                            B, L_)),
     }
 
 
