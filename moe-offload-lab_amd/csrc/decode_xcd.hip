@@ -324,15 +324,28 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
     __builtin_amdgcn_wave_barrier();
     if (routed) {
         if (E <= 64) {
-            // one key per lane: k rounds of a wave maximum, the winner's key cleared after each
-            // (keys are distinct: the expert index is part of the key)
-            uint32_t key = lane < E ? s_key[lane] : 0u;
-            for (int r = 0; r < k; ++r) {
-                const uint32_t M = wave_max_u32(key);
-                const int c = min(1023 - (int)(M & 1023u), E - 1);
-                if (lane == c) key = 0u;
-                if (lane == r) myc = c;
+            // one key per lane, ranked by counting the larger keys (keys are distinct: the
+            // expert index is part of the key): 64 independent compares against the keys read
+            // back from LDS, not a chain of k wave maxima. The experts ranked below k write
+            // their index into their slot; a slot that no key reaches (expired waits left fewer
+            // than k logits) keeps E - 1, as the rounds of a maximum over zero keys give it.
+            wave_sync();  // (every lane's keys, written while polling)
+            const uint32_t key = lane < E ? s_key[lane] : 0u;
+            int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+#pragma unroll
+            for (int j = 0; j < 64; j += 4) {
+                const uint4 kk = *reinterpret_cast<const uint4 *>(s_key + j);
+                r0 += kk.x > key ? 1 : 0;
+                r1 += kk.y > key ? 1 : 0;
+                r2 += kk.z > key ? 1 : 0;
+                r3 += kk.w > key ? 1 : 0;
             }
+            const int rank = (r0 + r1) + (r2 + r3);
+            if (lane < k) sh.idx[lane] = E - 1;
+            wave_sync();
+            if (key != 0u && rank < k) sh.idx[rank] = lane;
+            wave_sync();
+            if (lane < k) myc = sh.idx[lane];
         } else {
             const int epl = (E + 63) >> 6;
             if (epl <= 2) xc_topk<2>(s_key, E, k, lane, myc);
