@@ -105,6 +105,13 @@ def build_workload(dev, n_tokens: int, seed: int = 0):
     return store, dec, xs, Wr, lay
 
 
+# stamps of the XCD decode kernel's traced launches (index: stage reached)
+XC_STAGES = {1: "router rows done", 2: "logits polled", 3: "experts ranked", 4: "softmax (routing wave)",
+             5: "levels decided (routing wave)", 6: "routing known (workgroup)", 7: "up weights requested",
+             8: "up data in / down weights requested", 9: "h stored", 10: "segment's h in (down items)",
+             11: "down products", 12: "combined (combiners)", 13: "item(s) done", 14: "end"}
+
+
 def gpu_bench(args):
     import torch
 
@@ -176,7 +183,7 @@ def gpu_bench(args):
 
     # the expert phase of the launch (first weight request to the last down product, per-workgroup
     # real-time stamps of a traced launch), over a few (token, layer) launches
-    phases = []
+    phases, stages = [], []
     tr = torch.zeros(16 * 4096, dtype=torch.int64, device=dev)
     for j in range(min(nA, 12)):
         dec.grid, dec.trace = -1, tr
@@ -189,7 +196,20 @@ def gpu_bench(args):
         done = t[:, 11][t[:, 11] > 0]
         if len(t) and len(done):
             phases.append(float(done.max() - t[:, 6].min()) * 10 / 1000)
+            stages.append(t)
     dec.check_error()
+    if getattr(args, "stage_stamps", False) and stages:
+        # every stage's time over all workgroups of these launches: median / max in us from the
+        # launch's first workgroup start (a stage a workgroup does not pass reads 0 and is left out)
+        for i, name in XC_STAGES.items():
+            vals = []
+            for t in stages:
+                s0 = int(t[:, 0].min())
+                col = t[:, i]
+                vals += [(int(v) - s0) * 10 / 1000 for v in col[col > 0]]
+            if vals:
+                vals.sort()
+                log(f"[bench] stage {i:2d} {name:<34s} median {vals[len(vals) // 2]:6.2f} us  max {vals[-1]:6.2f} us")
     phases.sort()
     expert_phase_us = phases[len(phases) // 2] if phases else None
 
@@ -1004,6 +1024,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--tokens", type=int, default=16, help="distinct decode tokens (one graph each)")
     ap.add_argument("--kernel-launches", type=int, default=4096)
+    ap.add_argument("--stage-stamps", action="store_true",
+                    help="log each stage of the headline kernel's traced launches (median / max us)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
