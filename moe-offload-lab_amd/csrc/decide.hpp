@@ -175,16 +175,17 @@ __device__ __forceinline__ uint32_t topk_key16(uint32_t bits16, int c) {
 // k rounds of a DPP wave maximum over the keys, optional renorm (the serial sum in slot order);
 // lane j < k gets its expert and its final fp32 weight. s_p: 32 floats of the wave's LDS.
 // transformers OlmoeTopKRouter.forward (modeling_olmoe.py:337-346) and Qwen3MoeTopKRouter.
-template <int DT>
-__device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E, int k, int renorm, float *s_p,
-                                          int &myc, float &myp) {
+// EPL keys per lane (E <= 64 EPL): the rounds only touch the slots that can hold a key.
+template <int DT, int EPL>
+__device__ __forceinline__ void topk_wave_n(const void *logits, size_t row, int E, int k, int renorm, float *s_p,
+                                            int &myc, float &myp) {
     const int lane = threadIdx.x & 63;
     const uint16_t *lr = reinterpret_cast<const uint16_t *>(logits) + row * E;
-    float lv[16];
-    uint32_t key[16];
+    float lv[EPL];
+    uint32_t key[EPL];
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < EPL; ++i) {
         const int c = lane + 64 * i;
         key[i] = 0u;
         lv[i] = -INFINITY;
@@ -198,7 +199,7 @@ __device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E,
     m = wave_max(m);
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+    for (int i = 0; i < EPL; ++i)
         if (lane + 64 * i < E) sum += expf(lv[i] - m);
     sum = wave_sum(sum);
     uint32_t myk = 0u;
@@ -206,10 +207,10 @@ __device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E,
     for (int j = 0; j < k; ++j) {
         uint32_t lb = 0u;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) lb = max(lb, key[i]);
+        for (int i = 0; i < EPL; ++i) lb = max(lb, key[i]);
         const uint32_t M = wave_max_u32(lb);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < EPL; ++i)
             if (key[i] == M) key[i] = 0u;  // keys are distinct: exactly one lane clears one
         if (lane == j) {
             myc = 1023 - (int)(M & 1023u);
@@ -230,6 +231,15 @@ __device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E,
         for (int j = 0; j < k; ++j) tot += s_p[j];
     myp = renorm ? p / tot : p;
     wave_sync();  // s_p is free for the wave's next token
+}
+template <int DT>
+__device__ __forceinline__ void topk_wave(const void *logits, size_t row, int E, int k, int renorm, float *s_p,
+                                          int &myc, float &myp) {
+    if (E <= 64) topk_wave_n<DT, 1>(logits, row, E, k, renorm, s_p, myc, myp);
+    else if (E <= 128) topk_wave_n<DT, 2>(logits, row, E, k, renorm, s_p, myc, myp);
+    else if (E <= 256) topk_wave_n<DT, 4>(logits, row, E, k, renorm, s_p, myc, myp);
+    else if (E <= 512) topk_wave_n<DT, 8>(logits, row, E, k, renorm, s_p, myc, myp);
+    else topk_wave_n<DT, 16>(logits, row, E, k, renorm, s_p, myc, myp);
 }
 
 // x[t] . g over H values (16-bit DT: 8 per 16-byte load; x and g 16-byte aligned, H % 8 == 0), by
