@@ -86,6 +86,27 @@ struct SharedRecs {
     int64_t r[4];
 };
 
+// what the vote of expert e reads besides its tallies: its copy per precision (rtab, or the shared
+// expert's records for e == E), the precisions the layer planned and the per-precision offsets of
+// the table fields. None of it depends on the routing, so the decision kernels load it at their
+// start and the vote, at the end of their chain, waits for no global load.
+struct VoteRecs {
+    int64_t base[4];
+    int64_t offs[16];
+    uint32_t planned;  // bit p: precision p planned
+};
+__device__ __forceinline__ void vote_recs(VoteRecs &vr, int e, int E, int EA, const int64_t *rtab,
+                                          const SharedRecs &srec, int P, const int64_t *offs, const int *planned) {
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi)
+        vr.base[pi] = pi < P && e < EA ? (e < E ? rtab[(size_t)pi * E + e] : srec.r[pi]) : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) vr.offs[i] = i < 4 * P ? offs[i] : 0;
+    vr.planned = 0u;
+    for (int pi = 0; pi < P; ++pi)
+        if (planned[pi]) vr.planned |= 1u << pi;
+}
+
 // expert e (of E routed, plus the shared one, id E, when has_shared): the most precise level
 // requested by at least hi_vote of its pairs (policy.py:148-154), its precision (lv2p) and
 // resident copy (as k_decide_table), the table row of that precision (all other precisions' rows
@@ -93,8 +114,7 @@ struct SharedRecs {
 // them in miss. info[e] = chosen precision, -1 = missing, -2 = no pairs.
 __device__ __forceinline__ int vote_apply(int e, int n, int c0, int c1, const int32_t *offsets, int E, int has_shared,
                                            const int32_t *sorted_pos, double hi_vote, int upgrade, int lv0, int lv1,
-                                           int lv2, const int64_t *rtab, const SharedRecs &srec, int P,
-                                           const int64_t *offs, const int *planned, int64_t *tabs, int32_t *rank,
+                                           int lv2, const VoteRecs &vr, int P, int64_t *tabs, int32_t *rank,
                                            float *info, float *miss) {
     const int EA = E + (has_shared ? 1 : 0);
     int chosen = -1;
@@ -105,16 +125,17 @@ __device__ __forceinline__ int vote_apply(int e, int n, int c0, int c1, const in
         const bool shared_row = e >= E;
         const int req = shared_row ? P - 1 : (level == 0 ? lv0 : (level == 1 ? lv1 : lv2));
         const bool up = shared_row || upgrade;
-        for (int pi = P - 1; pi >= 0; --pi) {
-            const int64_t base = e < E ? rtab[(size_t)pi * E + e] : srec.r[pi];
-            if (base != 0 && (up ? req >= pi : req == pi)) chosen = pi;
-        }
-        if (chosen >= 0 && !planned[chosen]) chosen = -1;
+#pragma unroll
+        for (int pi = 3; pi >= 0; --pi)
+            if (pi < P && vr.base[pi] != 0 && (up ? req >= pi : req == pi)) chosen = pi;
+        if (chosen >= 0 && !((vr.planned >> chosen) & 1u)) chosen = -1;
     }
-    for (int pi = 0; pi < P; ++pi) {
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+        if (pi >= P) break;
         const bool sel = chosen == pi;
-        const int64_t base = !sel ? 0 : (e < E ? rtab[(size_t)pi * E + e] : srec.r[pi]);
-        for (int f = 0; f < 4; ++f) tabs[((size_t)pi * EA + e) * 4 + f] = sel ? base + offs[pi * 4 + f] : 0;
+        const int64_t base = sel ? vr.base[pi] : 0;
+        for (int f = 0; f < 4; ++f) tabs[((size_t)pi * EA + e) * 4 + f] = sel ? base + vr.offs[pi * 4 + f] : 0;
     }
     if (n > 0 && chosen < 0) {
         const int p0 = offsets[e];
@@ -138,8 +159,10 @@ __device__ __forceinline__ void vote_expert(int e, const int32_t *levels, int E,
         c0 += l <= 0;
         c1 += l <= 1;
     }
-    (void)vote_apply(e, n, c0, c1, offsets, E, has_shared, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, rtab, srec, P, offs,
-               planned, tabs, rank, info, miss);
+    VoteRecs vr;
+    vote_recs(vr, e, E, E + (has_shared ? 1 : 0), rtab, srec, P, offs, planned);
+    (void)vote_apply(e, n, c0, c1, offsets, E, has_shared, sorted_pos, hi_vote, upgrade, lv0, lv1, lv2, vr, P, tabs, rank,
+                     info, miss);
 }
 
 // per-expert tallies of the kept pairs for the vote, gathered while the levels are made (LDS

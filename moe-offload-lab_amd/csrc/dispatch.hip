@@ -248,6 +248,8 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     __shared__ VoteTally s_vt;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int EA = E + (has_shared ? 1 : 0);
+    VoteRecs vr;  // (thread e votes for expert e: EA <= 1024)
+    vote_recs(vr, tid, E, EA, rtab, srec, P, offs, planned);
     tally_clear(s_vt, EA);
     __syncthreads();
     for (int t = wave; t < T; t += DP_WAVES)
@@ -256,9 +258,9 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
-    for (int e = tid; e < EA; e += 1024)
-        s_ch[e] = vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, has_shared, sorted_pos, hi_vote,
-                             pol.upgrade, lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
+    if (tid < EA)
+        s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, has_shared, sorted_pos, hi_vote,
+                               pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
     write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
@@ -312,6 +314,8 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     int64_t *pidx = shared ? idx_ext : idx;
     float *pw = shared ? w_ext : w32;
     __shared__ VoteTally s_vt;
+    VoteRecs vr;  // (thread e votes for expert e: EA <= 1024)
+    vote_recs(vr, tid, E, EA, rtab, srec, P, offs, planned);
     tally_clear(s_vt, EA);  // ordered before the levels by the barrier after the routing
     // routing of every token
     for (int t = wave; t < T; t += DP_WAVES)
@@ -324,9 +328,9 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
-    for (int e = tid; e < EA; e += 1024)
-        s_ch[e] = vote_apply(e, s_vt.n[e], s_vt.c0[e], s_vt.c1[e], offsets, E, shared ? 1 : 0, sorted_pos, hi_vote,
-                             pol.upgrade, lv0, lv1, lv2, rtab, srec, P, offs, planned, tabs, rank, info, miss);
+    if (tid < EA)
+        s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, shared ? 1 : 0, sorted_pos,
+                               hi_vote, pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
     __syncthreads();  // the offsets are this workgroup's own writes
     write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
