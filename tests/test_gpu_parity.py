@@ -285,8 +285,10 @@ def test_grouped_graph_replays(dev):
 # ---------------------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("T,E,k,renorm", [(1, 64, 8, False), (33, 64, 8, False), (8, 128, 8, True),
-                                          (32, 512, 10, True), (5, 16, 4, True)])
+                                          (32, 512, 10, True), (5, 16, 4, True), (7, 200, 6, False),
+                                          (6, 256, 8, True), (9, 1024, 8, False)])
 def test_router_topk(dev, dtype, T, E, k, renorm):
+    # (E picks the top-k's key slots per lane: 1 up to 64 experts, then 2, 4, 8, 16 up to 1024)
     H = 2048
     g = torch.Generator().manual_seed(T * E + k)
     x = torch.randn(T, H, generator=g).to(dtype)
