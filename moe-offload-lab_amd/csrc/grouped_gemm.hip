@@ -1501,27 +1501,33 @@ __global__ __launch_bounds__(256) void k_combine_pairs(const float *__restrict__
                                                        int T, int k, int H, const void *__restrict__ add,
                                                        void *__restrict__ out, int accumulate, int *__restrict__ clear,
                                                        int nclear, int cstride) {
-    const int t = blockIdx.x;
+    // token t, columns [blockIdx.y * 1024, + 1024): 4 per thread
+    const int t = blockIdx.x, c0 = blockIdx.y * 1024 + threadIdx.x * 4;
     // words left zero for the next launch (a prefill layer's routing counters, read before this one)
-    if (clear != nullptr && t == 0)
+    if (clear != nullptr && t == 0 && blockIdx.y == 0)
         for (int i = threadIdx.x; i < nclear; i += 256) clear[(size_t)i * cstride] = 0;
-    for (int c0 = threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
-        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int jj = 0; jj < k; ++jj) {
-            const int p = rank[(size_t)t * k + jj];
-            if (p < 0) continue;
-            const float4 *src = reinterpret_cast<const float4 *>(y + (size_t)p * H + c0);
-            const float4 a = src[0], b = src[1];
-            s[0] += a.x, s[1] += a.y, s[2] += a.z, s[3] += a.w;
-            s[4] += b.x, s[5] += b.y, s[6] += b.z, s[7] += b.w;
-        }
+    if (c0 >= H) return;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    const int32_t *rk = rank + (size_t)t * k;
+    // 8 slots at a time: their ranks, then their rows, all requested before any is added (a slot
+    // past k or without a pair loads row 0 and is not added); the sums stay in slot order
+    for (int j0 = 0; j0 < k; j0 += 8) {
+        int p[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            float v = s[q];
-            if (accumulate) v += ld_act<DT>(out, (size_t)t * H + c0 + q);
-            if (add != nullptr) v += ld_act<DT>(add, (size_t)t * H + c0 + q);
-            st_act<DT>(out, (size_t)t * H + c0 + q, v);
-        }
+        for (int u = 0; u < 8; ++u) p[u] = rk[min(j0 + u, k - 1)];
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4 *>(y + (size_t)max(p[u], 0) * H + c0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (j0 + u < k && p[u] >= 0) s[0] += v[u].x, s[1] += v[u].y, s[2] += v[u].z, s[3] += v[u].w;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float o = s[q];
+        if (accumulate) o += ld_act<DT>(out, (size_t)t * H + c0 + q);
+        if (add != nullptr) o += ld_act<DT>(add, (size_t)t * H + c0 + q);
+        st_act<DT>(out, (size_t)t * H + c0 + q, o);
     }
 }
 
@@ -1956,10 +1962,10 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
         }
     }
     if (xdtype == MOEHIP_DT_F16)
-        hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_F16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
+        hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_F16>), dim3(T, (H + 1023) / 1024), dim3(256), 0, st, y, rank, T, k, H, add, out,
                            accumulate, clear, nclear, cstride);
     else
-        hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_BF16>), dim3(T), dim3(256), 0, st, y, rank, T, k, H, add, out,
+        hipLaunchKernelGGL((k_combine_pairs<MOEHIP_DT_BF16>), dim3(T, (H + 1023) / 1024), dim3(256), 0, st, y, rank, T, k, H, add, out,
                            accumulate, clear, nclear, cstride);
     return check_launch("grouped_gemm");
 }
