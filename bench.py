@@ -170,6 +170,7 @@ def gpu_bench(args):
     reps = max(1, args.kernel_launches // nA)
     for j in range(nA):
         dec.layer(j % L, xs[j // L, j % L], outs[j // L, j % L])
+    kernel_name = _lib.last_decode_kernel()  # the kernel these launches ran (the library's readout)
     torch.cuda.synchronize()
     ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ea.record(st)
@@ -226,7 +227,7 @@ def gpu_bench(args):
         "layer_alg_gbs": layer_alg / (layer_us * 1e-6) / 1e9,
         "kernel_us": kern_us, "kernel_bytes": layer_alg,
         "kernel_gbs": layer_alg / (kern_us * 1e-6) / 1e9,
-        "record_bytes": rec_bytes, "fused": dec.fused,
+        "record_bytes": rec_bytes, "fused": dec.fused, "kernel": kernel_name,
         "expert_phase_us": expert_phase_us,
         "expert_phase_gbs": (K_TOP * rec_bytes / (expert_phase_us * 1e-6) / 1e9) if expert_phase_us else None,
     }
@@ -483,6 +484,7 @@ def decode_line(args, name):
     + router + shared gate + x/out."""
     import torch
 
+    from moelab_hip import _lib
     from moelab_hip.layer import MoEDecoder
 
     sp = DECODE_SPECS[name]
@@ -498,6 +500,7 @@ def decode_line(args, name):
     for s_ in range(S):
         for l in range(L_):
             dec.layer(l, xs[s_, l], outs[s_, l])
+            kernel_name = _lib.last_decode_kernel()
             info = dec.info[l].cpu()
             for j in range(k_):
                 c = int(info[1, j])
@@ -544,7 +547,7 @@ def decode_line(args, name):
         "layer_us": round(layer_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "fused decode layer (one launch per layer, HIP graph per token)",
+                     "kernel": f"{kernel_name} (one launch per layer, HIP graph per token)",
                      "bytes_per_launch": int(alg)},
         "cpu_baseline": (decode_cpu_baseline(args.cpu_seconds, H_, I_, k_ + (1 if sp["shared"] else 0), L_)
                          if not args.no_cpu and sp["precs"] == ["int4"] else None),
@@ -1101,7 +1104,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-            "kernel": "k_decode_xcd<f16, int4> (router + routing + 8 int4 experts + combine, one launch)",
+            "kernel": f"{r['kernel']} (router + routing + 8 int4 experts + combine, one launch per layer)",
             "bytes_per_launch": r["kernel_bytes"],
         },
         "cpu_baseline": cpu,

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define MOEHIP_ABI_VERSION 3
+#define MOEHIP_ABI_VERSION 4
 
 /* error codes */
 #define MOEHIP_OK 0
@@ -148,10 +148,14 @@ typedef struct moehip_policy {
      * the whole-token graph use. The two differ only when s lies within float32 rounding of a
      * threshold. Batched (T > 1) entry points ignore f64: moelab's T > 1 path is the tensor rule. */
     int f64;
-    int reserved;
+    /* e3 = 1: moelab's cache-miss rule (E3, runtime.py:600-615; policy.py:36-38, `miss_t1`) in the
+     * one-token rule (f64 = 1 only): a level-0 slot that no resident copy serves at its level-0
+     * precision, with s > miss_t1_64 (= miss_t1 + 1e-6 in float64), is served at level 1. */
+    int e3;
     double t1_64;
     double t_mid_64;
     double t2_64;
+    double miss_t1_64;
 } moehip_policy;
 
 /*
@@ -311,6 +315,17 @@ size_t moehip_decode_rows_workspace_bytes(int P, int k, int H, int I);
 int moehip_decode_layer_work_items(const moehip_layer_desc *desc, int with_router);
 /* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device). */
 int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
+
+/* Which decode kernel the calling thread's last moehip_decode_layer, moehip_decode_layer_noalloc
+ * or moehip_decode_rows call launched (0 before any call). No counterpart in the reference (its
+ * Triton kernels have one form each): a host-side readout for tests and benchmarks that must know
+ * which of the kernels below produced a result. */
+#define MOEHIP_KERNEL_XCD 1        /* k_decode_xcd: one layer per launch, organised by XCD */
+#define MOEHIP_KERNEL_XCD_TWO 2    /* k_decode_xcd in two passes (more items than resident workgroups) */
+#define MOEHIP_KERNEL_ONE_ITEM 3   /* k_decode_tok: one work item per workgroup */
+#define MOEHIP_KERNEL_ITEM_LOOP 4  /* k_decode_layer: a loop over work items */
+int moehip_decode_last_kernel(void);
+const char *moehip_decode_kernel_name(int kernel);
 
 /*
  * T > 1 tokens (prefill chunks, batched decode) through the experts of one layer, int4 gs64

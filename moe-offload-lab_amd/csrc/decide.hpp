@@ -20,8 +20,11 @@ __device__ __forceinline__ void wave_sync() {
 // s_total[1]). policy.py:77-123 (unimportance over the normalised weights, stable descending
 // rank), the fixed modes (hi / lo / protected layer) and the weight threshold. With one64 and
 // pol.f64 set, the one-token float64 rule of levels_one (policy.py:89-98, 125-137) instead.
+// s_out (optional) receives the slot's unimportance s (0 in the fixed and weight modes, as
+// levels_one returns it), which the cache-miss rule below reads.
 __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_policy &pol, float *s_w, float *s_sorted,
-                                           float *s_total, int &lvl, bool &skip, bool one64 = false) {
+                                           float *s_total, int &lvl, bool &skip, bool one64 = false,
+                                           double *s_out = nullptr) {
     const bool act = j < k;
     s_w[j] = wj;
     wave_sync();
@@ -33,6 +36,7 @@ __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_
     }
     wave_sync();
     skip = false;
+    if (s_out) *s_out = 0.0;
     if (pol.mode == 1 || pol.protect) {
         lvl = 0;
     } else if (pol.mode == 2) {
@@ -59,6 +63,7 @@ __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_
         if (pol.t_mid_64 >= 0.0 && s <= pol.t_mid_64) lvl = 1;
         if (s <= pol.t1_64) lvl = 0;
         skip = pol.t2_64 >= 0.0 && s > pol.t2_64 && lvl != 0;
+        if (s_out) *s_out = s;
     } else {
         // unimportance (policy.py:77-87): stable descending rank, s = cumsum(sorted) - own weight
         const float wn = wj / s_total[0];
@@ -79,7 +84,16 @@ __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_
         if (pol.t_mid >= 0.f && s <= pol.t_mid) lvl = 1;
         if (s <= pol.t1) lvl = 0;
         skip = pol.t2 >= 0.f && s > pol.t2 && lvl != 0;
+        if (s_out) *s_out = (double)s;
     }
+}
+
+// The cache-miss rule of moelab's one-token decode (runtime.py:600-615, policy.py:36-38): a slot
+// at level 0 whose level-0 request no resident copy serves, and whose unimportance s exceeds
+// miss_t1 + 1e-6 (float64), is served at level 1 instead. Only the one-token rule (pol.f64)
+// applies it, as moelab applies it only in its T == 1 path.
+__device__ __forceinline__ bool miss_downgrade(const moehip_policy &pol, int lvl, double s) {
+    return pol.f64 != 0 && pol.e3 != 0 && lvl == 0 && s > pol.miss_t1_64;
 }
 
 struct SharedRecs {

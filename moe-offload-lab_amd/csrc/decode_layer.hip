@@ -62,7 +62,15 @@ constexpr int WAIT_SPINS = 1 << 22;   // x ~0.3 us per poll: a wait gives up aft
 // generation 1 KB apart (read by every workgroup at start)
 constexpr int NGEN = 16;
 constexpr int NSUB = 16;
-enum { W_READ = 0, W_ERR = NSUB * 32, W_TOP = NSUB * 32 + 32, W_GEN = 1024, W_HDR = W_GEN + 256 * NGEN };
+enum { W_READ = 0, W_ERR = NSUB * 32, W_TOP = NSUB * 32 + 32, W_TEST = NSUB * 32 + 64, W_GEN = 1024,
+       W_HDR = W_GEN + 256 * NGEN };
+// W_TEST: a word the library never writes (zero from the workspace's first zero-fill; the XCD
+// kernel reads the same word). When a test sets it, every later launch on that workspace polls
+// the logits for a tag that is never written and gives up after TEST_SPINS polls: an expired wait
+// forced from the host, in a launch whose every workgroup still exits normally (the routing is
+// then poisoned, so every other wait is still satisfied, and the generation's counting keeps its
+// full bound).
+constexpr int TEST_SPINS = 8;
 constexpr int NLC = 1;         // copies of the logits
 constexpr int RT_LDS = 1024;   // record-table entries (P * E) prefetched into LDS
 constexpr int REC_SHARED = 0xFFF;  // expert field of the shared row in a routing record
@@ -304,6 +312,7 @@ struct DlShared {
     uint32_t tag;
     int routed;
     int poison;
+    int forced;                    // the workspace's test word was set (see W_TEST)
     int idx[64];
     float w[64];
     float sorted[64];
@@ -357,7 +366,10 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                     if (lane + 64 * i < E) need |= 1u << i;
             if (has_sh && lane == 0) need |= 1u << 31;
             int nap = 1;
-            for (int it = 0; it < WAIT_SPINS && __ballot(need != 0) != 0ull; ++it) {
+            const bool forced = sh.forced != 0;
+            const uint32_t ptag = forced ? tag + 0x40000000u : tag;  // (forced: never written)
+            const int spin = forced ? TEST_SPINS : WAIT_SPINS;
+            for (int it = 0; it < spin && __ballot(need != 0) != 0ull; ++it) {
                 uint64_t v[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
@@ -365,7 +377,7 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                 const uint64_t vg = (need >> 31) ? ld_tag(logits + E) : 0ull;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    if (i < epl && (need & (1u << i)) && tag_ok(v[i], tag)) {
+                    if (i < epl && (need & (1u << i)) && tag_ok(v[i], ptag)) {
                         const int c = lane + 64 * i;
                         const float l = __uint_as_float((uint32_t)v[i]);
                         s_lv[c] = l;
@@ -373,12 +385,12 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                         need &= ~(1u << i);
                     }
                 }
-                if ((need >> 31) && tag_ok(vg, tag)) {
+                if ((need >> 31) && tag_ok(vg, ptag)) {
                     sh.gl = __uint_as_float((uint32_t)vg);
                     need &= ~(1u << 31);
                 }
                 if (__ballot(need != 0) != 0ull) backoff(nap, 2);
-                if (it == WAIT_SPINS - 1 && lane == 0) flag_error(err);
+                if (it == spin - 1 && lane == 0) flag_error(err);
             }
             if (a.Wr != nullptr)
                 for (int i = 0; i < epl; ++i) {  // logits still missing after the wait: never chosen
@@ -443,7 +455,15 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
                         }
                     }
                 }
-                if (lane < E && rank < k) {
+                // a slot that no key reaches (an expired wait left fewer than k logits, whose keys
+                // are 0) keeps E - 1, as the rounds of a maximum over zero keys give it: every
+                // workgroup routes the same way, so every other wait of the launch is still met
+                if (lane < k) {
+                    s_key[512 + lane] = (uint32_t)(E - 1);
+                    s_lv[512 + lane] = -INFINITY;
+                }
+                __builtin_amdgcn_wave_barrier();
+                if (lane < E && rank < k && key != 0u) {
                     s_key[512 + rank] = (uint32_t)lane;
                     s_lv[512 + rank] = lvv;
                 }
@@ -527,21 +547,27 @@ __device__ __forceinline__ void route_local(const LayerArgs &a, uint32_t tag, Dl
         const float wj = act ? myw : 0.f;
         int lvl;
         bool skip;
-        slot_level(j, k, wj, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true);
+        double s;
+        slot_level(j, k, wj, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true, &s);
         if (shr) {
             lvl = 0;
             skip = false;
         }
         TS(4);
         const int l2p0 = uni(a.lv2p[0]), l2p1 = uni(a.lv2p[1]), l2p2 = uni(a.lv2p[2]);
-        // the shared row takes its most precise present copy
-        const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
         const bool upg = shr || a.pol.upgrade;
         int chosen = -1;
+        for (int pass = 0; pass < 2; ++pass) {
+            // the shared row takes its most precise present copy
+            const int req = shr ? DL_MAXP - 1 : (lvl == 0 ? l2p0 : (lvl == 1 ? l2p1 : l2p2));
 #pragma unroll
-        for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
-            const bool avail = pi < P && rt[pi] != 0;
-            if (avail && (upg ? req >= pi : req == pi)) chosen = pi;
+            for (int pi = DL_MAXP - 1; pi >= 0; --pi) {
+                const bool avail = pi < P && rt[pi] != 0;
+                if (avail && (upg ? req >= pi : req == pi)) chosen = pi;
+            }
+            // a routed level-0 miss below the cache-miss threshold is looked up again at level 1
+            if (chosen >= 0 || shr || !miss_downgrade(a.pol, lvl, s)) break;
+            lvl = 1;
         }
         const bool usable = chosen >= 0 && pick4(a.planned, chosen) != 0;
         const bool is_miss = row && !skip && !usable;
@@ -971,6 +997,7 @@ __global__ __launch_bounds__(256) void k_decode_layer(LayerArgs a) {
         sh.tag = ld_co32(ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
         sh.routed = 0;
         sh.poison = 0;
+        sh.forced = ld_co32(ws + W_TEST) != 0u ? 1 : 0;
     }
     __syncthreads();
     const uint32_t tag = uni((int)sh.tag);
@@ -1069,6 +1096,7 @@ __global__ __launch_bounds__(256) void k_decode_tok(LayerArgs) {
             sh.tag = ld_co32(a.ws + W_GEN + 256 * (blockIdx.x % NGEN)) + 1u;  // launch tag (never 0)
             sh.routed = 0;
             sh.poison = 0;
+            sh.forced = ld_co32(a.ws + W_TEST) != 0u ? 1 : 0;
         }
     }
     __syncthreads();
@@ -1226,6 +1254,10 @@ extern "C" size_t moehip_decode_layer_workspace_bytes(int P, int k, int E, int H
     return n;
 }
 
+// the decode kernel the calling thread's last moehip_decode_layer / moehip_decode_rows call
+// launched (MOEHIP_KERNEL_*; 0 before any)
+static thread_local int t_last_kernel = 0;
+
 extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in,
                                    const float *w32_in, const int64_t *rtab, void *out, const void *add,
                                    int accumulate, void *logits_out, int64_t *idx_out, void *w_out, float *w32_out,
@@ -1270,7 +1302,11 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
         const int rc = xcd_launch(d, x, Wr, idx_in, w32_in, nullptr, nullptr, rtab, out, add, accumulate, logits_out,
                                   idx_out, w_out, w32_out, info, miss, ws, ws_bytes, grid < 0 ? trace : nullptr,
                                   stream, &used);
-        if (rc != MOEHIP_OK || used) return rc;
+        if (rc != MOEHIP_OK) return rc;
+        if (used) {
+            t_last_kernel = used;
+            return rc;
+        }
     }
     if (grid < 0) grid = 0;
     LayerArgs a{};
@@ -1340,9 +1376,24 @@ extern "C" int moehip_decode_layer(const moehip_layer_desc *d, const void *x, co
         }
         g = grid > 0 ? (grid < total ? grid : total) : total;
         if (g > cap) g = cap;  // every workgroup must fit on the GPU at once (see the kernel's header)
+        t_last_kernel = MOEHIP_KERNEL_ITEM_LOOP;
+    } else {
+        t_last_kernel = MOEHIP_KERNEL_ONE_ITEM;
     }
     hipLaunchKernelGGL(kern, dim3(g), dim3(256), 0, as_stream(stream), a);
     return check_launch("decode_layer");
+}
+
+extern "C" int moehip_decode_last_kernel(void) { return t_last_kernel; }
+
+extern "C" const char *moehip_decode_kernel_name(int kernel) {
+    switch (kernel) {
+        case MOEHIP_KERNEL_XCD: return "k_decode_xcd";
+        case MOEHIP_KERNEL_XCD_TWO: return "k_decode_xcd (two passes)";
+        case MOEHIP_KERNEL_ONE_ITEM: return "k_decode_tok";
+        case MOEHIP_KERNEL_ITEM_LOOP: return "k_decode_layer";
+        default: return "none";
+    }
 }
 
 extern "C" int moehip_decode_rows(const moehip_layer_desc *d, const void *x, const int64_t *rows_b, const float *rows_w,
@@ -1407,6 +1458,7 @@ extern "C" int moehip_decode_rows(const moehip_layer_desc *d, const void *x, con
         return MOEHIP_ELAUNCH;
     }
     hipLaunchKernelGGL(kern, dim3(total < cap ? total : cap), dim3(256), 0, as_stream(stream), a);
+    t_last_kernel = MOEHIP_KERNEL_ITEM_LOOP;
     return check_launch("decode_rows");
 }
 

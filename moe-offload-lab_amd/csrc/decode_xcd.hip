@@ -401,7 +401,8 @@ __device__ __forceinline__ void xc_weigh(const XcArgs &a, XcShared &sh, int myc,
     const bool act = lane < k, shr = has_sh && lane == k;
     int lvl;
     bool skip;
-    slot_level(lane, k, act ? myw : 0.f, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true);
+    double s;
+    slot_level(lane, k, act ? myw : 0.f, a.pol, sh.w, sh.sorted, &sh.tot, lvl, skip, true, &s);
     if (shr) lvl = 0, skip = false;
     xc_stamp_r(a, sh, 5);
     float wt = myw;
@@ -411,6 +412,9 @@ __device__ __forceinline__ void xc_weigh(const XcArgs &a, XcShared &sh, int myc,
     }
     if (lane < ks) {
         const bool usable = sh.rb[lane] != 0;
+        // one record precision: a level-0 miss below the cache-miss threshold is looked up again
+        // at level 1, i.e. the same precision, and stays a miss at level 1
+        if (act && !usable && miss_downgrade(a.pol, lvl, s)) lvl = 1;
         sh.rw[lane] = (act || shr) && !skip && usable ? wt : 0.f;
         sh.w[lane] = myp;  // (slot_level is done with sh.w)
         sh.lvl[lane] = lvl;
@@ -1028,8 +1032,9 @@ size_t xcd_workspace_bytes(int prec, int ks, int E, int H, int I) {
     return p.ok ? p.total : 0;
 }
 
-// the XCD kernel for one launch when it applies: returns MOEHIP_OK after launching, 1 when the
-// layer does not fit this kernel (the caller then runs the item-loop kernel), or an error code
+// the XCD kernel for one launch when it applies: returns MOEHIP_OK, with *used = the kernel
+// launched (MOEHIP_KERNEL_XCD or MOEHIP_KERNEL_XCD_TWO) or 0 when the layer or the device does
+// not fit this kernel (the caller then runs the item kernels), or an error code
 int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in,
                       const float *w32_in, const int64_t *rows_b, const float *rows_w, const int64_t *rtab,
                       void *out, const void *add, int accumulate, void *logits_out, int64_t *idx_out, void *w_out,
@@ -1054,11 +1059,13 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     // Qwen3-Next shape: 152 items per XCD) runs the two-pass kernel, when every up item can be a
     // first item and no workgroup whose first item is a down item needs a second
     int grid = p.grid;
+    int which = MOEHIP_KERNEL_XCD;
     if (grid > per_cu * cus) {
         const int nq = per_cu2 * cus / XC_N;
         if (nq < p.nu || nq < p.nd || p.nu + p.nd > 2 * nq) return MOEHIP_OK;
         grid = nq * XC_N;
         kern = kern2;
+        which = MOEHIP_KERNEL_XCD_TWO;
     }
     XcArgs a{};
     a.x = x;
@@ -1115,7 +1122,7 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
     a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8 * 0.9);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream), a);
-    *used = 1;
+    *used = which;
     return check_launch("decode_layer (xcd)");
 }
 

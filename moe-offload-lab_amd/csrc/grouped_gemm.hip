@@ -2022,6 +2022,10 @@ extern "C" int moehip_prefill_layer(int prec, const int64_t *tab, const void *x,
                    "prefill_layer: T=%d E=%d k=%d H=%d I=%d (E <= 1024, k <= 32, H a multiple of 512, I of 128)", T, E,
                    k, H, I);
     MOEHIP_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)Wr % 16) == 0, "prefill_layer: x and Wr must be 16-byte aligned");
+    // everything the grouped GEMM checks is checked here, before the routing launches bump the
+    // per-expert counters (only this call's combine clears them again)
+    MOEHIP_REQUIRE(gg_prec_ok(prec), "prefill_layer: record precision %d", prec);
+    MOEHIP_REQUIRE(gs == GG_KG, "prefill_layer: group size %d (64)", gs);
     const RpLayout R = rp_layout(T, k, H, I, E);
     const GgLayout G = gg_layout(T, k, H, I);
     MOEHIP_REQUIRE(ws_bytes >= R.total && ((uintptr_t)ws % 256) == 0, "prefill_layer: workspace %zu < %zu bytes (or unaligned)",

@@ -234,13 +234,19 @@ __global__ __launch_bounds__(64) void k_decide_table(const int64_t *__restrict__
     __shared__ float s_w[64], s_sorted[64], s_total[1];
     int lvl;
     bool skip;
-    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, skip, true);
-    const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
+    double s;
+    slot_level(j, k, wj, pol, s_w, s_sorted, s_total, lvl, skip, true, &s);
     int chosen = -1;
-    for (int pi = P - 1; pi >= 0; --pi) {
-        const bool avail = act && e >= 0 && e < E && rtab[(size_t)pi * E + e] != 0;
-        const bool ok = avail && (pol.upgrade ? req >= pi : req == pi);
-        if (ok) chosen = pi;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int req = lvl == 0 ? lv0 : (lvl == 1 ? lv1 : lv2);
+        for (int pi = P - 1; pi >= 0; --pi) {
+            const bool avail = act && e >= 0 && e < E && rtab[(size_t)pi * E + e] != 0;
+            const bool ok = avail && (pol.upgrade ? req >= pi : req == pi);
+            if (ok) chosen = pi;
+        }
+        // a level-0 miss below the cache-miss threshold is looked up again at level 1
+        if (chosen >= 0 || !miss_downgrade(pol, lvl, s)) break;
+        lvl = 1;
     }
     const bool usable = chosen >= 0 && planned[chosen];
     const bool is_miss = act && !skip && !usable;

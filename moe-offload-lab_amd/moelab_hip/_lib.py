@@ -15,7 +15,7 @@ import torch
 
 LIB_PATH = Path(os.environ.get("MOEHIP_LIB", Path(__file__).resolve().parent / "libmoehip.so"))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 PREC_CODES = {"int4": 0, "int8": 1, "fp16": 2, "bf16": 3, "fp32": 4, "fp8": 5}
 DT_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -28,8 +28,8 @@ class Policy(ctypes.Structure):
     """moehip_policy: HOBBIT parameters for one layer (thresholds include the +1e-6 of policy.py:120-122)."""
 
     _fields_ = [("mode", _i), ("t1", _f), ("t_mid", _f), ("t2", _f), ("protect", _i), ("upgrade", _i),
-                ("f64", _i), ("reserved", _i), ("t1_64", ctypes.c_double), ("t_mid_64", ctypes.c_double),
-                ("t2_64", ctypes.c_double)]
+                ("f64", _i), ("e3", _i), ("t1_64", ctypes.c_double), ("t_mid_64", ctypes.c_double),
+                ("t2_64", ctypes.c_double), ("miss_t1_64", ctypes.c_double)]
 
 
 class LayerDesc(ctypes.Structure):
@@ -77,6 +77,8 @@ _SIGS = {
     "moehip_decode_rows": ([ctypes.POINTER(LayerDesc), _vp, _vp, _vp, _vp, _vp, _i, _vp, ctypes.c_size_t, _vp], _i),
     "moehip_decode_rows_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
     "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
+    "moehip_decode_last_kernel": ([], _i),
+    "moehip_decode_kernel_name": ([_i], ctypes.c_char_p),
     "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                              ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemm_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
@@ -158,6 +160,14 @@ def call(name: str, *args) -> None:
     rc = getattr(lib, name)(*args)
     if rc != 0:
         raise RuntimeError(f"{name} failed ({rc}): {lib.moehip_last_error().decode()}")
+
+
+def last_decode_kernel() -> str:
+    """Name of the decode kernel the calling thread's last moehip_decode_layer(_noalloc) or
+    moehip_decode_rows call launched: "k_decode_xcd", "k_decode_xcd (two passes)", "k_decode_tok",
+    "k_decode_layer", or "none"."""
+    lib = load()
+    return lib.moehip_decode_kernel_name(lib.moehip_decode_last_kernel()).decode()
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

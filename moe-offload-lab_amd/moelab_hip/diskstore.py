@@ -244,8 +244,14 @@ class DiskTier:
         self.pool.release(blob, self._last_copy.pop(blob.data_ptr(), None))
 
     def _read(self, key: tuple) -> torch.Tensor:
+        """One record into a pool buffer; the buffer goes back to the pool if the read fails."""
         layer, e, prec = key
-        return self.store.read(layer, e, prec, out=self.pool.acquire(prec))
+        buf = self.pool.acquire(prec)
+        try:
+            return self.store.read(layer, e, prec, out=buf)
+        except BaseException:
+            self.pool.release(buf)
+            raise
 
     def many(self, items: list) -> list:
         """Pinned record buffers for [(layer, expert, prec), ...]: RAM hits as they are, the
@@ -263,15 +269,27 @@ class DiskTier:
                 out[k] = ent.blob
             elif k not in todo:
                 todo.append(k)
-        for k, blob in zip(todo, self._io.map(self._read, todo)):
+        # every read of the batch runs to its end before anything is raised: a failed read has
+        # released its own buffer, the others' buffers are cached (or released) as usual
+        futures = [self._io.submit(self._read, k) for k in todo]
+        first_error = None
+        for k, fut in zip(todo, futures):
+            try:
+                blob = fut.result()
+            except Exception as exc:  # noqa: BLE001  (re-raised below, after the batch is settled)
+                first_error = first_error or exc
+                continue
             self.stats["disk_reads"] += 1
             self.stats["bytes_disk"] += blob.numel()
             ent = self.cache.insert(k, blob, protect=protect)
             if ent is None or ent.blob is not blob:
                 self.pool.release(blob)
-                raise RuntimeError(f"the host cache cannot hold the batch ({self.cache.describe()}): "
-                                   "raise host_budget_bytes")
+                first_error = first_error or RuntimeError(
+                    f"the host cache cannot hold the batch ({self.cache.describe()}): raise host_budget_bytes")
+                continue
             out[k] = blob
+        if first_error is not None:
+            raise first_error
         return [out[k] for k in keys]
 
     def __call__(self, layer: int, expert: int, prec: str) -> torch.Tensor:

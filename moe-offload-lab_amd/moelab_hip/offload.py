@@ -274,30 +274,43 @@ class OffloadDecoder:
         self.rb = torch.empty(4, k, dtype=torch.float32, pin_memory=True)
         self._predicted: tuple[int, frozenset] | None = None
         self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0,
-                      "pred_hits": 0, "pred_total": 0}
+                      "pred_hits": 0, "pred_total": 0, "miss_downgrades": 0}
 
     def _evicted(self, blob: torch.Tensor) -> None:
         prec = self._blob_prec.pop(blob.data_ptr())
         self.pool.release(blob, prec, self.table.removal_event)
 
     def _wants(self, layer: int, idx: list, w: list) -> dict:
-        levels, skip, _ = self.policy.levels_one(layer, w)
-        want = {}
-        for j, e in enumerate(idx):
-            if not skip[j]:
-                p = level_to_precision(levels[j], self.precisions)
-                if e not in want or self.precisions.index(p) < self.precisions.index(want[e]):
-                    want[e] = p
-        return want
+        """{expert: (precision, level, s)} of one token's non-skipped slots: the one-token rule
+        (levels_one, policy.py:125-137; the kernel uses the same float64 rule) and level ->
+        precision (policy.py:188-192)."""
+        levels, skip, s = self.policy.levels_one(layer, w)
+        return {e: (level_to_precision(levels[j], self.precisions), levels[j], s[j])
+                for j, e in enumerate(idx) if not skip[j]}
 
-    def _stage_missing(self, layer: int, want: dict, protect: frozenset, prefetch: bool) -> list:
-        """Stage the wanted records of `layer` that no resident entry serves; returns the events
-        the compute stream must wait on for the wanted records (in flight or just staged)."""
-        exact = not self.policy.upgrade
-        waits, todo = [], []
-        for e, prec in want.items():
-            ent = self.cache.lookup(layer, e, prec, exact=exact, count=not prefetch)
+    def _stage_missing(self, layer: int, want: dict, protect: frozenset, prefetch: bool):
+        """Look the wanted records of `layer` up in the device cache as moelab's decode does
+        (runtime.py:587-615) and stage the misses; returns (events the compute stream must wait
+        on, the keys this layer uses: its hits and its staged records).
+
+        The lookup takes a more precise resident copy only when the policy allows upgrades
+        (`allow_upgrade`: never in mode "lo"), as the kernel's copy choice does. With `miss_t1`
+        set, a level-0 request that misses and whose unimportance s exceeds miss_t1 + 1e-6 is
+        looked up again at level 1 and, if still absent, staged at level 1 (E3; the kernel
+        applies the same rule to the table it finds). Prefetches take neither step (moelab's
+        background prefetch stages what it is given)."""
+        exact = not self.policy.allow_upgrade
+        e3 = not prefetch and self.policy.miss_t1 is not None
+        count = not prefetch
+        waits, todo, used = [], [], set()
+        for e, (prec, level, s) in want.items():
+            ent = self.cache.lookup(layer, e, prec, exact=exact, count=count)
+            if ent is None and e3 and level == 0 and s > self.policy.miss_t1 + 1e-6:
+                prec = level_to_precision(1, self.precisions)
+                self.stats["miss_downgrades"] += 1
+                ent = self.cache.lookup(layer, e, prec, exact=exact, count=count)
             if ent is not None:
+                used.add(ent.key)
                 if not prefetch:
                     self.cache.touch(ent)
                     self.stats["hits"] += 1
@@ -308,8 +321,10 @@ class OffloadDecoder:
                         waits.append(ent.event)
                 continue
             todo.append((e, prec))
+            used.add((layer, e, prec))
+        used = frozenset(used) | protect
         if not todo:
-            return waits
+            return waits, used
         if not prefetch:
             self.stats["misses"] += len(todo)
         else:
@@ -323,7 +338,7 @@ class OffloadDecoder:
         added = []
         for (e, p), dst in zip(todo, dsts):
             self._blob_prec[dst.data_ptr()] = p
-            ent = self.cache.insert((layer, e, p), dst, protect=protect, event=ev)
+            ent = self.cache.insert((layer, e, p), dst, protect=used, event=ev)
             if ent is None or ent.blob is not dst:
                 self._blob_prec.pop(dst.data_ptr(), None)
                 self.pool.release(dst, p, ev)
@@ -338,7 +353,7 @@ class OffloadDecoder:
             ent.event = tab_ev
         if not prefetch:
             waits.append(tab_ev)
-        return waits
+        return waits, used
 
     def _gate_predict(self, layer: int, x: torch.Tensor) -> None:
         """Layer `layer`'s router on x into the prediction buffers (the next layer's gate applied
@@ -378,15 +393,17 @@ class OffloadDecoder:
         if gate:
             pids = [int(v) for v in self.rb[2].tolist()]
             predict = self._wants(layer + 1, pids, self.rb[3].tolist())
+        elif predict:
+            predict = {e: (p, 0, 0.0) for e, p in predict.items()}
         if predict and layer + 1 < self.L:
             self._predicted = (layer + 1, frozenset(predict))
         want = self._wants(layer, ids, ws)
-        protect = frozenset((layer, e, p) for e, p in want.items())
-        for wev in self._stage_missing(layer, want, protect, prefetch=False):
+        waits, used = self._stage_missing(layer, want, frozenset(), prefetch=False)
+        for wev in waits:
             cur.wait_event(wev)
         self.dec.layer(layer, x, out, idx=idx, w32=w32)
         if predict and layer + 1 < self.L:
-            self._stage_missing(layer + 1, predict, protect, prefetch=True)
+            self._stage_missing(layer + 1, predict, used, prefetch=True)
         return out
 
     def tick(self) -> None:

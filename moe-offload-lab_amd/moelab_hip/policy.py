@@ -132,15 +132,18 @@ class PrecisionPolicy:
         f32 = lambda v: float(torch.tensor(v, dtype=torch.float32))  # noqa: E731
         prot = 1 if layer in self.protect_layers else 0
         upg = 1 if self.allow_upgrade else 0
+        # the cache-miss rule (runtime.py:600-615) belongs to the one-token path only
+        e3 = 1 if one_token and self.miss_t1 is not None else 0
+        mt = self.miss_t1 + 1e-6 if e3 else 0.0
         if self.mode == "weight":
             return Policy(mode=mode, t1=f32(self.t1), t_mid=-1.0, t2=-1.0, protect=prot, upgrade=upg,
-                          f64=0, t1_64=-1.0, t_mid_64=-1.0, t2_64=-1.0)
+                          f64=1 if e3 else 0, e3=e3, t1_64=-1.0, t_mid_64=-1.0, t2_64=-1.0, miss_t1_64=mt)
         t1 = self.t1_for(layer) + 1e-6
         tm = None if self.t_mid is None else self.t_mid + 1e-6
         t2 = None if self.t2 is None else self.t2 + 1e-6
         return Policy(mode=mode, t1=f32(t1), t_mid=-1.0 if tm is None else f32(tm), t2=-1.0 if t2 is None else f32(t2),
-                      protect=prot, upgrade=upg, f64=1 if one_token else 0, t1_64=t1,
-                      t_mid_64=-1.0 if tm is None else tm, t2_64=-1.0 if t2 is None else t2)
+                      protect=prot, upgrade=upg, f64=1 if one_token else 0, e3=e3, t1_64=t1,
+                      t_mid_64=-1.0 if tm is None else tm, t2_64=-1.0 if t2 is None else t2, miss_t1_64=mt)
 
 
 def level_to_precision(level: int, precisions: list) -> str:

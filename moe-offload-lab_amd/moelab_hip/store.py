@@ -168,3 +168,41 @@ def encode_record_(layout: dict, blob: torch.Tensor, gate_up: torch.Tensor, down
         _lib.call(entry, wf.data_ptr(), O, I, bits, gs, v[f"{name}.q"].data_ptr(),
                   v[f"{name}.s"].data_ptr(), _lib.stream_of(blob.device))
     return blob
+
+
+def unpacked_layout(layout: dict) -> dict | None:
+    """The "unpacked" form of an int4 record (moelab/store.py:177-189, `fast_int4_unpacked`): the
+    int8 layout of the same shapes and groups, one int4 value per byte. None for other records,
+    or when the int8 layout cannot keep the int4 groups."""
+    if layout["precision"] != "int4":
+        return None
+    H, I = dims(layout)
+    l8 = record_layout("int8", H, I, max(layout["group_sizes"].values()))
+    return l8 if l8["group_sizes"] == layout["group_sizes"] else None
+
+
+_NIBBLE_TABLES: dict = {}
+
+
+def _nibble_table(device) -> torch.Tensor:
+    """(256, 2) int8 on `device`: byte b -> (low nibble - 8, high nibble - 8), the even and the odd
+    value of moelab's packing (quant.py:96-101)."""
+    key = str(device)
+    if key not in _NIBBLE_TABLES:
+        b = torch.arange(256, dtype=torch.int16)
+        _NIBBLE_TABLES[key] = torch.stack([(b & 15) - 8, (b >> 4) - 8], dim=1).to(torch.int8).to(device)
+    return _NIBBLE_TABLES[key]
+
+
+def unpack_int4_record(blob: torch.Tensor, layout4: dict, layout8: dict) -> torch.Tensor:
+    """An int4 record rewritten in its unpacked int8 layout (moelab/store.py:192-203): the same
+    values one per byte and the same scales, on the device of `blob` (padding bytes zero).
+    moelab's int8 kernels then run it (grouped_ffn_int8, runtime.py:230-240, 405)."""
+    table = _nibble_table(blob.device)
+    out = torch.zeros(layout8["record_bytes"], dtype=torch.uint8, device=blob.device)
+    src, dst = views(layout4, blob), views(layout8, out)
+    for name in ("gate_up", "down"):
+        packed = src[f"{name}.q"]
+        dst[f"{name}.q"].copy_(table[packed.long()].reshape(packed.shape[0], -1))
+        dst[f"{name}.s"].copy_(src[f"{name}.s"])
+    return out

@@ -14,7 +14,7 @@ import oracle as O
 from conftest import ROOT
 from moelab_hip import _lib
 from moelab_hip.policy import PrecisionPolicy, level_to_precision
-from moelab_hip.store import dims, field_offsets, group_size_of, record_layout
+from moelab_hip.store import dims, field_offsets, group_size_of, record_layout, unpack_int4_record, unpacked_layout
 
 HEADER = ROOT / "include" / "moehip.h"
 
@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.moehip_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.moehip_abi_version() == _lib.ABI_VERSION == 4
     assert lib.moehip_layer_desc_bytes() == ctypes.sizeof(_lib.LayerDesc)
 
 
@@ -51,7 +51,20 @@ def test_argument_validation_without_gpu():
 
 
 def test_policy_struct_layout():
-    assert ctypes.sizeof(_lib.Policy) == 56
+    assert ctypes.sizeof(_lib.Policy) == 64
+    assert _lib.Policy.miss_t1_64.offset == 56
+
+
+def test_device_policy_cache_miss_rule():
+    """miss_t1 (E3, runtime.py:600-615) reaches the kernels only through the one-token rule, with
+    the +1e-6 slack in float64; mode "lo" never allows upgrades (policy.py:176-185)."""
+    p = PrecisionPolicy("hobbit", t1=0.6, miss_t1=0.2)
+    one, many = p.device_policy(0, one_token=True), p.device_policy(0)
+    assert one.e3 == 1 and one.f64 == 1 and one.miss_t1_64 == 0.2 + 1e-6
+    assert many.e3 == 0
+    assert PrecisionPolicy("hobbit").device_policy(0, one_token=True).e3 == 0
+    assert PrecisionPolicy("lo", upgrade=True).device_policy(0, one_token=True).upgrade == 0
+    assert PrecisionPolicy("hobbit", upgrade=False).device_policy(0).upgrade == 0
 
 
 @pytest.mark.parametrize("prec", ["fp32", "fp16", "bf16", "int8", "int4", "fp8"])
@@ -94,3 +107,21 @@ def test_device_policy_thresholds():
     assert d.f64 == 0 and d.t1_64 == 0.2 + 1e-6 and d.t2_64 == 0.9 + 1e-6 and d.t_mid_64 == -1.0
     assert p.device_policy(3, one_token=True).f64 == 1
     assert [level_to_precision(v, ["fp16", "int4"]) for v in (0, 1, 2)] == ["fp16", "int4", "int4"]
+
+
+@pytest.mark.parametrize("H,I", [(2048, 1024), (2048, 512), (256, 128)])
+def test_unpacked_int4_record_dequantizes_identically(H, I):
+    """The reference's check (test_optim.py:86-98): an int4 record rewritten in its unpacked int8
+    layout materialises to exactly the same weights; the layout is moelab's int8 one, larger."""
+    l4 = record_layout("int4", H, I, 64, scale="absmax")
+    l8 = unpacked_layout(l4)
+    assert l8 == O.record_layout("int8", H, I, 64) and l8["record_bytes"] > l4["record_bytes"]
+    assert unpacked_layout(record_layout("fp16", H, I)) is None
+    g = torch.Generator().manual_seed(H + I)
+    gu, dn = (torch.randn(2 * I, H, generator=g) * 0.05).numpy(), (torch.randn(H, I, generator=g) * 0.05).numpy()
+    blob = O.encode_record(l4, gu, dn, "absmax")
+    off = O.field(l4, "gate_up.q")[2]
+    blob[off:off + 256] = np.arange(256, dtype=np.uint8)  # every byte value once
+    b8 = unpack_int4_record(torch.from_numpy(blob), l4, l8).numpy()
+    a, b = O.materialize(l4, blob), O.materialize(l8, b8)
+    assert all(np.array_equal(x, y) for x, y in zip(a, b))

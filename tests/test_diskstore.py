@@ -144,3 +144,24 @@ def test_disk_tier_ram_cache(store_dir):
     with pytest.raises(RuntimeError, match="host cache"):
         tier.many([(2, e, "int4") for e in range(5)])  # one batch larger than the budget
     tier.close()
+
+
+def test_disk_tier_failed_reads_return_their_buffers(store_dir):
+    """A batch with a truncated record raises, and no pool buffer is lost: the failed read gives
+    its buffer back, the batch's good reads are cached, and every buffer the pool has lent out is
+    held by a cache entry."""
+    f = store_dir / "layer002.int4.bin"
+    f.write_bytes(f.read_bytes()[:-100])  # the last expert of layer 2 is cut short
+    st = ExpertStore(store_dir)
+    rb4 = st.record_bytes("int4")
+    tier = DiskTier(st, host_budget_bytes=8 * rb4, pin=False, parts=2)
+    batch = [(2, e, "int4") for e in range(E)]
+    for _ in range(2):
+        with pytest.raises(RuntimeError, match="truncated"):
+            tier.many(batch)
+        held = {ent.blob.data_ptr() for ent in tier.cache.entries.values()}
+        assert set(tier.pool._lent) == held
+        assert len(held) == E - 1  # the intact records of the batch stay cached
+    for e in range(E - 1):
+        assert np.array_equal(tier(2, e, "int4").numpy(), _record(2, e, "int4", rb4))
+    tier.close()

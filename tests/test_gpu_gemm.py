@@ -9,6 +9,7 @@ import pytest
 import torch
 
 import oracle as O
+from moelab_hip import _lib
 from moelab_hip.layer import ResidentStore
 from moelab_hip.prefill import GroupedTokens
 from moelab_hip.store import record_layout
@@ -190,3 +191,35 @@ def test_prefill_layer_one_call_matches_route_then_run(dev, dtype, renorm):
     assert torch.equal(o1.view(torch.int16), ref_out.view(torch.int16))
     ref = O.moe_layer_grouped(x.float().cpu().numpy(), idx.cpu().numpy(), w32.cpu().numpy().astype(np.float64), ex.mats)
     assert_layer_close(o1.float().cpu().numpy(), ref, dtype)
+
+
+def test_prefill_layer_refused_call_leaves_the_workspace_clean(dev):
+    """A call refused for its record precision or group size launches nothing (the routing
+    counters in the workspace stay zero): the next valid call on the same workspace equals a
+    call on a fresh one, bit for bit."""
+    H, I, E, k, T = 2048, 768, 64, 8, 64
+    dtype = torch.bfloat16
+    ex = _Experts(dev, H, I, E, 23)
+    g = torch.Generator().manual_seed(24)
+    Wr = (torch.randn(E, H, generator=g) * 0.05).to(dtype).to(dev)
+    x = torch.randn(T, H, generator=g).to(dtype).to(dev)
+    outs = []
+    for refuse in (False, True):
+        gt = GroupedTokens(ex.store.layouts["int4"], E, k, T, dev)
+        tab = gt.table(ex.bases())
+        out = torch.zeros(T, H, dtype=dtype, device=dev)
+        if refuse:
+            lib = _lib.load()
+            logits, idx, w, w32 = gt.route(x, Wr, True)
+            for prec, gs in ((_lib.prec_code("fp32"), 64), (_lib.prec_code("int4"), 32)):
+                rc = lib.moehip_prefill_layer(prec, tab.data_ptr(), x.data_ptr(), Wr.data_ptr(), _lib.dt_code(dtype), T,
+                                              H, I, k, E, gs, 1, logits.data_ptr(), idx.data_ptr(), w.data_ptr(),
+                                              w32.data_ptr(), out.data_ptr(), None, 0, gt.ws_layer.data_ptr(),
+                                              gt.ws_layer.numel(), _lib.stream_of(dev))
+                assert rc == 1, lib.moehip_last_error()
+            torch.cuda.synchronize()
+            assert int(gt.ws_layer.count_nonzero()) == 0
+        gt.layer(x, Wr, True, tab, out)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))

@@ -98,6 +98,7 @@ def test_fused_qwen3_30b_decode(dev):
         out = torch.zeros(1, H, dtype=dtype, device=dev)
         print(f"qwen3-30b decode token {t}", flush=True)
         dec.layer(0, x.to(dev), out)
+        assert _lib.last_decode_kernel() == "k_decode_xcd"
         torch.cuda.synchronize()
         lo, idx, w, ref = S.reference(0, x, k, True, O.Policy("lo"))
         assert dec.idx.cpu().numpy().tolist() == idx.tolist()
@@ -470,27 +471,38 @@ def test_grouped_graph_fp32_records(dev):
 # ---------------------------------------------------------------------------------------
 XC_TEST_WORD, ERR_WORD = 576, 512  # header words of the decode-layer workspace (uint32 index)
 
+# (record precisions, grid, the kernel that runs): the XCD kernel, the one-item kernel (a grid at
+# least the layer's item count), the item loop (a smaller grid), and the item loop on two record
+# precisions (mixed launches never run the XCD kernel)
+FORCED = {"xcd": (["int4"], 0, "k_decode_xcd"), "one_item": (["int4"], 1 << 20, "k_decode_tok"),
+          "item_loop": (["int4"], 64, "k_decode_layer"), "two_precisions": (["fp16", "int4"], 0, "k_decode_layer")}
 
-def test_forced_expired_wait_poisons_output_and_sets_the_flag(dev):
+
+@pytest.mark.parametrize("kernel", list(FORCED))
+def test_forced_expired_wait_poisons_output_and_sets_the_flag(dev, kernel):
+    precs, grid, name = FORCED[kernel]
     H, I, E, k = 2048, 1024, 64, 8
-    S = _Stack(dev, H, I, E, 1, ["int4"], 31)
-    dec = MoEDecoder(S.store, k, PrecisionPolicy("lo"), torch.float16, router_weights=[S.Wr[0].to(dev)])
+    S = _Stack(dev, H, I, E, 1, precs, 31)
+    pol = PrecisionPolicy("hobbit", t1=0.5, upgrade=False) if len(precs) > 1 else PrecisionPolicy("lo")
+    dec = MoEDecoder(S.store, k, pol, torch.float16, router_weights=[S.Wr[0].to(dev)], grid=grid)
     assert dec.fused
     x = torch.randn(1, H, generator=torch.Generator().manual_seed(5)).half().to(dev)
     ref = torch.zeros(1, H, dtype=torch.float16, device=dev)
     dec.layer(0, x, ref)
+    assert _lib.last_decode_kernel() == name
     torch.cuda.synchronize()
     dec.check_error()
     words = dec.ws.view(torch.int32)
-    print("forced expiry: test word set", flush=True)
+    print(f"forced expiry ({name}): test word set", flush=True)
     words[XC_TEST_WORD] = 1
     out = torch.zeros(1, H, dtype=torch.float16, device=dev)
     dec.layer(0, x, out)
+    assert _lib.last_decode_kernel() == name
     torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
     with pytest.raises(RuntimeError, match="bounded wait expired"):
         dec.check_error()
-    print("forced expiry: cleared, normal launch", flush=True)
+    print(f"forced expiry ({name}): cleared, normal launch", flush=True)
     words[XC_TEST_WORD] = 0
     words[ERR_WORD] = 0
     out2 = torch.zeros(1, H, dtype=torch.float16, device=dev)

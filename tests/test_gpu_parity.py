@@ -20,6 +20,7 @@ import oracle as O
 from moelab_hip import _lib
 from moelab_hip import kernels as K
 from moelab_hip.layer import MoEDecoder, ResidentStore
+from moelab_hip.store import unpack_int4_record, unpacked_layout
 from moelab_hip.policy import PrecisionPolicy
 from moelab_hip.store import encode_record_, record_layout, views
 
@@ -280,6 +281,49 @@ def test_grouped_graph_replays(dev):
     assert gg.graph is not None and gg.replays == 4
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_unpacked_int4_records_through_the_int8_kernels(dev, dtype):
+    """moelab's unpacked int4 form (store.py:177-203; runtime.py:230-240 runs it with
+    grouped_ffn_int8): int4 records rewritten in the int8 layout on the GPU hold exactly the
+    oracle's weights, and grouped_ffn_int8 and a GroupedGraph of that layout (first run and
+    replays) give the packed records' result: the same weights, so equal up to the fp32 sums'
+    order, and the oracle's layer within the north-star tolerance."""
+    H, I, n = 2048, 1024, 8
+    lay4, blobs, mats = make_records("int4", H, I, n, 41, std=0.02)
+    lay8 = unpacked_layout(lay4)
+    r4 = to_dev(blobs, dev)
+    r8 = [unpack_int4_record(b, lay4, lay8) for b in r4]
+    olay8 = O.record_layout("int8", H, I, 64)
+    for e in range(2):
+        m8 = O.materialize(olay8, r8[e].cpu().numpy())
+        assert all(np.array_equal(a, b) for a, b in zip(m8, mats[e]))
+    rng = np.random.default_rng(7)
+    for step in range(3):
+        x = torch.randn(1, H, generator=torch.Generator().manual_seed(40 + step)).to(dtype).to(dev)
+        w = rng.random(n).astype(np.float32)
+        ref = O.moe_layer(x.float().cpu().numpy(), np.arange(n)[None], w[None], lambda e: mats[e])
+        out4 = torch.zeros(1, H, dtype=dtype, device=dev)
+        out8 = torch.zeros(1, H, dtype=dtype, device=dev)
+        K.grouped_ffn_int4(x, [(views(lay4, b), float(v)) for b, v in zip(r4, w)], lay4["group_sizes"], out4)
+        K.grouped_ffn_int8(x, [(views(lay8, b), float(v)) for b, v in zip(r8, w)], lay8, out8)
+        if step == 0:
+            g4 = torch.zeros(1, H, dtype=dtype, device=dev)
+            g8 = torch.zeros(1, H, dtype=dtype, device=dev)
+            gg4 = K.GroupedGraph({"int4": lay4}, x, g4, n)
+            gg8 = K.GroupedGraph({"int4": lay8}, x, g8, n)  # the fast tier keeps the store's name
+            xg = x
+        xg.copy_(x)
+        gg4.run({"int4": [(b, float(v)) for b, v in zip(r4, w)]})
+        gg8.run({"int4": [(b, float(v)) for b, v in zip(r8, w)]})
+        torch.cuda.synchronize()
+        scale = np.abs(ref).max()
+        for got in (out4, out8, g4, g8):
+            assert_layer_close(got.float().cpu().numpy(), ref, dtype)
+        for a, b in ((out8, out4), (g8, g4)):
+            assert np.abs(a.float().cpu().numpy() - b.float().cpu().numpy()).max() / scale < 2.0 ** -8
+    assert gg8.replays == 2 and gg4.replays == 2
+
+
 # ---------------------------------------------------------------------------------------
 # router
 # ---------------------------------------------------------------------------------------
@@ -490,6 +534,8 @@ def test_decoder_layer_olmoe(dev, mode, fused):
         x = xs[l]
         out = torch.zeros(1, H, dtype=dtype, device=dev)
         dec.layer(l, x.to(dev), out)
+        if fused:  # the kernel that produced this output: one record kind -> the XCD kernel
+            assert _lib.last_decode_kernel() == ("k_decode_xcd" if len(precs) == 1 else "k_decode_layer")
         torch.cuda.synchronize()
         lo, idx, w, ref = S.reference(l, x, k, False, O.Policy(mode, t1=t1))
         assert dec.idx.cpu().numpy().tolist() == idx.tolist()
@@ -594,6 +640,8 @@ def test_fused_qwen3next_shape(dev, prec):
         x = torch.randn(1, H, generator=S.g).to(dtype)
         out = torch.zeros(1, H, dtype=dtype, device=dev)
         dec.layer(0, x.to(dev), out)
+        # fp8 rows make more items than resident workgroups: the two-pass instantiation
+        assert _lib.last_decode_kernel() == ("k_decode_xcd" if prec == "int4" else "k_decode_xcd (two passes)")
         torch.cuda.synchronize()
         lo, idx, w, ref = S.reference(0, x, k, True, O.Policy("lo"))
         assert dec.idx.cpu().numpy().tolist() == idx.tolist()
@@ -659,6 +707,7 @@ def test_fused_qwen3next_shared_expert(dev, prec, routed):
             dec.layer(0, x.to(dev), out, idx=torch.from_numpy(idx).to(dev),
                       w32=torch.from_numpy(w.astype(np.float32)).to(dev))
             ref = O.moe_layer(x.float().numpy(), idx, w.astype(np.float64), lambda e: S.mats(0, e, prec))
+        assert _lib.last_decode_kernel() == ("k_decode_xcd" if prec == "int4" else "k_decode_xcd (two passes)")
         torch.cuda.synchronize()
         xf = x.float().numpy().astype(np.float64)
         logit = O.round_to((xf @ gate.float().numpy().astype(np.float64)).astype(np.float32), "bfloat16")
