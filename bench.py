@@ -32,6 +32,7 @@ F.linear-equivalent matvecs, weighted sum) on a bounded sample of the same workl
     python bench.py --workload qwen3-next-offload  # offloaded decode, records in pinned host memory
     python bench.py --workload dense-int8          # one-token int8 GEMVs of the dense part (LM head)
     python bench.py --workload disk-tier           # offloaded decode served from an expert store on disk
+    python bench.py --workload stream-floor        # the dependency-free read of one decode layer's bytes
 """
 
 from __future__ import annotations
@@ -1003,6 +1004,108 @@ def disk_line(args):
     }
 
 
+def stream_floor(dev, arena: "torch.Tensor", routers: list, rec_bytes: int, n_rec: int, grids: list,
+                 launches: int = 2048, seed: int = 0, stamp_grid: int | None = None) -> dict:
+    """The dependency-free floor of one launch that reads one decode layer's bytes (n_rec records
+    chosen at random per launch among the arena's, plus one layer's router matrix) with
+    moehip_stream_read, per grid: us per launch from HIP events over back-to-back launches on
+    the stream they run on, rotating over 256 (layer, token) choices so that the records come
+    from HBM. With stamp_grid, also the per-workgroup stamps of 12 launches at that grid."""
+    import ctypes
+
+    import torch
+
+    from moelab_hip import _lib
+
+    lib = _lib.load()
+    n_all = arena.numel() // rec_bytes
+    g = torch.Generator().manual_seed(seed)
+    choices = []
+    for j in range(256):
+        recs = torch.randperm(n_all, generator=g)[:n_rec].tolist()
+        bases = (ctypes.c_int64 * n_rec)(*[arena.data_ptr() + r * rec_bytes for r in recs])
+        choices.append((bases, routers[j % len(routers)]))
+    sink = torch.zeros(max(grids + [stamp_grid or 0]), dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    rb = routers[0].numel() * routers[0].element_size()
+    out = {}
+    for grid in grids:
+        def launch(j, stamps=None):
+            bases, wr = choices[j % len(choices)]
+            _lib.call("moehip_stream_read", bases, n_rec, rec_bytes, wr.data_ptr(), rb, grid, sink.data_ptr(),
+                      _lib.ptr(stamps), st.cuda_stream)
+        for j in range(256):
+            launch(j)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for j in range(launches):
+            launch(j)
+        b.record(st)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1000 / launches
+        out[grid] = us
+        if grid == stamp_grid:
+            ends, durs = [], []
+            stamps = torch.zeros(2 * grid, dtype=torch.int64, device=dev)
+            for j in range(12):
+                launch(j)  # an untraced launch first: the traced one starts behind a busy GPU
+                stamps.zero_()
+                launch(j + 1, stamps)
+                torch.cuda.synchronize()
+                t = stamps.view(-1, 2).cpu()
+                t0 = int(t[:, 0].min())
+                ends += [(int(v) - t0) * 10 / 1000 for v in t[:, 1]]
+                durs += [(int(e) - int(s_)) * 10 / 1000 for s_, e in t.tolist()]
+            ends.sort()
+            durs.sort()
+            out["stamps"] = {"grid": grid, "data_in_median_us": ends[len(ends) // 2], "data_in_max_us": ends[-1],
+                             "per_workgroup_median_us": durs[len(durs) // 2]}
+    return out
+
+
+def stream_line(args):
+    """The read floor behind the headline: one launch reading what one OLMoE decode layer reads
+    (8 int4 records of 3,342,336 B drawn from 16 x 64 of them, 3.42 GB, and the layer's 262,144 B
+    router), without the dependencies of the decode (no routing before the record reads, no h
+    exchange): us per launch at several grids, the decode kernel's own grid (768) among them."""
+    import torch
+
+    from moelab_hip import _lib
+
+    dev = torch.device("cuda:0")
+    _lib.check_device(dev)
+    rec = 3_342_336
+    arena = torch.ones(L * E * rec, dtype=torch.uint8, device=dev)
+    routers = [torch.ones(E, H, dtype=torch.float16, device=dev) for _ in range(L)]
+    grids = [256, 512, 768, 1024, 1536, 2048, 3072]
+    r = stream_floor(dev, arena, routers, rec, K_TOP, grids, stamp_grid=768)
+    nbytes = K_TOP * rec + E * H * 2
+    per = {str(gd): {"us": round(r[gd], 3), "gbs": round(nbytes / (r[gd] * 1e-6) / 1e9, 1)} for gd in grids}
+    best = min(grids, key=lambda gd: r[gd])
+    # more bytes per launch: the launch's fixed costs against the transfer
+    more = {}
+    for n in (16, 32):
+        rr = stream_floor(dev, arena, routers, rec, n, [1536, 3072])
+        nb = n * rec + E * H * 2
+        gd = min(rr, key=rr.get)
+        more[f"{n}_records"] = {"bytes": nb, "grid": gd, "us": round(rr[gd], 3), "gbs": round(nb / (rr[gd] * 1e-6) / 1e9, 1)}
+    log(f"[bench] stream floor, {nbytes} B per launch: " + ", ".join(f"grid {gd}: {r[gd]:.2f} us" for gd in grids))
+    return {
+        "metric": "dependency-free read floor of one OLMoE decode layer's bytes in one launch, 1 GPU",
+        "value": round(nbytes / (r[768] * 1e-6) / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": 2048, "warmup": 256,
+        "ms_per_step": round(r[768] / 1000, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "8 int4 records (3,342,336 B) drawn at random per launch from 16 x 64 (3.42 GB) + "
+                               "one 64 x 2048 fp16 router, read once by moehip_stream_read", "bytes_per_launch": nbytes},
+        "per_grid": per, "best_grid": best, "stamps_grid_768": r.get("stamps"), "more_bytes": more,
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / (r[768] * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(nbytes / (r[768] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_stream_read (moehip_stream_read), grid 768"},
+        "cpu_baseline": None,
+    }
+
+
 def cpu_baseline(seconds: float):
     """moelab's CPU expert branch (runtime.py:646-702: fp32 dequantize, F.linear, silu, add_ with
     alpha = w) restated in torch (oracle/cpu_path.py), on one OLMoE layer of 8 int4 records, all
@@ -1033,7 +1136,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     ap.add_argument("--workload", choices=["olmoe-decode-bs1", "qwen3-30b-prefill", "qwen3-next-offload", "dense-int8",
-                                           "disk-tier",
+                                           "disk-tier", "stream-floor",
                                            *DECODE_SPECS, *BATCH_SPECS],
                     default="olmoe-decode-bs1")
     ap.add_argument("--offload-layers", type=int, default=48)
@@ -1065,6 +1168,9 @@ def main():
         return
     if args.workload == "disk-tier":
         print(json.dumps(disk_line(args)), flush=True)
+        return
+    if args.workload == "stream-floor":
+        print(json.dumps(stream_line(args)), flush=True)
         return
     if args.workload in DECODE_SPECS:
         print(json.dumps(decode_line(args, args.workload)), flush=True)

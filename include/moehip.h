@@ -328,6 +328,20 @@ int moehip_decode_last_kernel(void);
 const char *moehip_decode_kernel_name(int kernel);
 
 /*
+ * A dependency-free streaming read of a decode layer's bytes in ONE launch: the floor the decode
+ * kernels are measured against. Replaces the role of moelab's read floor (profiling.py:81-120,
+ * `microbenchmarks`: the expert bytes at the bandwidth a plain streaming product reaches), here at
+ * the decode kernel's own grid and bytes. seg_base: HOST array of nseg (<= 32) device addresses of
+ * equal segments of seg_bytes (records), then an optional extra segment (the router matrix, NULL
+ * with extra_bytes = 0); sizes multiples of 16, segments 16-byte aligned. grid workgroups of 256
+ * threads split the bytes evenly (each at most one segment's worth, at most 32 x 4 KB). sink: grid
+ * uint32 (device; in practice never written); stamps: NULL or 2 * grid uint64 (device): per
+ * workgroup its start and the moment all its words arrived (s_memrealtime, 100 MHz).
+ */
+int moehip_stream_read(const int64_t *seg_base, int nseg, int64_t seg_bytes, const void *extra, int64_t extra_bytes,
+                       int grid, uint32_t *sink, uint64_t *stamps, void *stream);
+
+/*
  * T > 1 tokens (prefill chunks, batched decode) through the experts of one layer, int4 gs64
  * records: the pairs (token, slot) sorted by expert (offsets (E+1), sorted_pos (T*k) = t*k+j,
  * rank (T*k) = position of pair t*k+j in sorted_pos or -1, as written by moehip_dispatch), for

@@ -79,6 +79,8 @@ _SIGS = {
     "moehip_decode_layer_error": ([_vp, _vp, _vp], _i),
     "moehip_decode_last_kernel": ([], _i),
     "moehip_decode_kernel_name": ([_i], ctypes.c_char_p),
+    "moehip_stream_read": ([ctypes.POINTER(ctypes.c_int64), _i, ctypes.c_int64, _vp, ctypes.c_int64, _i, _vp, _vp,
+                            _vp], _i),
     "moehip_grouped_gemm": ([_i, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                              ctypes.c_size_t, _vp], _i),
     "moehip_grouped_gemm_workspace_bytes": ([_i, _i, _i, _i], ctypes.c_size_t),
