@@ -44,40 +44,91 @@ STAGE_MODES = {"kernel": 0, "sdma": 1}
 # Device tier
 # ---------------------------------------------------------------------------------------------
 class DevicePool:
-    """Fixed device memory for resident records: slabs (<= 256 MiB) allocated once and cut into
-    4096-B aligned record slots per precision, never returned to the allocator. A released
-    slot carries the event after which it may be overwritten (the copy stream waits on it)."""
+    """Fixed device memory for resident records, shared by every record precision: slabs
+    (<= 256 MiB, allocated once, up to the cap, never returned to the allocator) cut into 4096-B
+    pages; a record slot is a run of pages taken first-fit from a slab's free extents, and a
+    released slot's pages rejoin their neighbours. Each free extent carries the events after
+    which its pages may be overwritten (the copy stream waits on them), so records of any
+    precision can reuse any freed space: a two-precision cache never strands one precision's
+    slots while the other runs out."""
+
+    PAGE = 4096
 
     def __init__(self, record_bytes: dict, cap_bytes: int, device):
         self.record_bytes = dict(record_bytes)
         self.cap = int(cap_bytes)
         self.device = torch.device(device)
         self.slabs: list[torch.Tensor] = []
+        self.free_ext: list[list] = []   # per slab: sorted [first page, pages, [events]]
         self.allocated = 0
-        self.free: dict[str, list] = {p: [] for p in self.record_bytes}  # (slot, event or None)
+        self.lent: dict[int, tuple] = {}  # slot address -> (slab, first page, pages)
 
-    def _grow(self, prec: str) -> bool:
-        rb = self.record_bytes[prec]
-        stride = (rb + 4095) // 4096 * 4096
-        n = max(1, min(SLAB_BYTES // stride, (self.cap - self.allocated) // stride))
-        if self.allocated + stride > self.cap:
+    def _pages(self, prec: str) -> int:
+        return (self.record_bytes[prec] + self.PAGE - 1) // self.PAGE
+
+    def _new_slab(self, pages: int) -> bool:
+        room = (self.cap - self.allocated) // self.PAGE
+        if room < pages:
             return False
-        slab = torch.empty(n * stride + 4096, dtype=torch.uint8, device=self.device)
-        off = (-slab.data_ptr()) % 4096
-        self.slabs.append(slab)
-        self.allocated += n * stride
-        self.free[prec].extend((slab[off + i * stride: off + i * stride + rb], None) for i in range(n))
+        n = min(max(pages, SLAB_BYTES // self.PAGE), room)
+        slab = torch.empty(n * self.PAGE + self.PAGE, dtype=torch.uint8, device=self.device)
+        off = (-slab.data_ptr()) % self.PAGE
+        self.slabs.append(slab[off:off + n * self.PAGE])
+        self.free_ext.append([[0, n, []]])
+        self.allocated += n * self.PAGE
         return True
 
+    def _carve(self, pages: int):
+        for si, exts in enumerate(self.free_ext):
+            for ei, ext in enumerate(exts):
+                if ext[1] >= pages:
+                    first, events = ext[0], ext[2]
+                    if ext[1] == pages:
+                        exts.pop(ei)
+                    else:
+                        ext[0] += pages
+                        ext[1] -= pages
+                        ext[2] = list(events)
+                    return si, first, [e for e in events if not e.query()]
+        return None
+
     def acquire(self, prec: str):
-        """(slot, event to wait on before writing it, or None); raises when the cap is reached."""
-        if not self.free[prec] and not self._grow(prec):
+        """(slot, events to wait on before writing it); raises when the cap is reached."""
+        pages = self._pages(prec)
+        got = self._carve(pages)
+        if got is None and self._new_slab(pages):
+            got = self._carve(pages)
+        if got is None:
             raise RuntimeError(f"device record pool full ({self.allocated / 2**30:.2f} GiB, cap "
                                f"{self.cap / 2**30:.2f} GiB): raise the budget margin")
-        return self.free[prec].pop()
+        si, first, events = got
+        slot = self.slabs[si][first * self.PAGE:first * self.PAGE + self.record_bytes[prec]]
+        self.lent[slot.data_ptr()] = (si, first, pages)
+        return slot, events
 
     def release(self, slot: torch.Tensor, prec: str, event=None) -> None:
-        self.free[prec].append((slot, event))
+        """Return a slot; its pages are reusable once `event` (if any) has passed on the device."""
+        si, first, pages = self.lent.pop(slot.data_ptr())
+        exts = self.free_ext[si]
+        ev = [event] if event is not None else []
+        i = 0
+        while i < len(exts) and exts[i][0] < first:
+            i += 1
+        exts.insert(i, [first, pages, ev])
+        # merge with the extent after, then with the one before
+        if i + 1 < len(exts) and exts[i][0] + exts[i][1] == exts[i + 1][0]:
+            nxt = exts.pop(i + 1)
+            exts[i][1] += nxt[1]
+            exts[i][2] = exts[i][2] + nxt[2]
+        if i > 0 and exts[i - 1][0] + exts[i - 1][1] == exts[i][0]:
+            cur = exts.pop(i)
+            exts[i - 1][1] += cur[1]
+            exts[i - 1][2] = exts[i - 1][2] + cur[2]
+            i -= 1
+        exts[i][2] = [e for e in exts[i][2] if not e.query()]
+
+    def free_pages(self) -> int:
+        return sum(e[1] for exts in self.free_ext for e in exts)
 
 
 class DeviceTable:
@@ -173,10 +224,9 @@ class Stager:
                                    f"({self.pool.record_bytes[prec]} B expected)")
             if self.mode == "kernel" and not blob.is_pinned():
                 raise RuntimeError("stage: kernel staging reads pinned host memory; this record is pageable")
-            slot, ev = self.pool.acquire(prec)
+            slot, evs = self.pool.acquire(prec)
             dsts.append(slot)
-            if ev is not None:
-                waits.append(ev)
+            waits.extend(evs)
         cs = self.copy_stream
         for ev in waits:
             cs.wait_event(ev)

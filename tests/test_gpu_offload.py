@@ -133,8 +133,9 @@ def test_offload_decoder_matches_resident(dev, mode, routed):
     if not routed:
         assert off.stats["prefetch_hits"] > 0
     # every slot handed out is either resident or free again
-    n_slots = off.pool.allocated // ((rb + 4095) // 4096 * 4096)
-    assert len(off.cache.entries) + len(off.pool.free["int4"]) == n_slots
+    pages = (rb + 4095) // 4096
+    assert len(off.pool.lent) == len(off.cache.entries)
+    assert off.pool.free_pages() + pages * len(off.pool.lent) == off.pool.allocated // 4096
 
 
 @pytest.mark.parametrize("mode", ["kernel", "sdma"])

@@ -253,3 +253,45 @@ def test_host_pool_arena_rule():
     small = HostPool({"int4": rb}, cap_bytes=5 * rb + 100, pin=False, log=lambda *a: None)
     ys = [small.acquire("int4") for _ in range(6)]
     assert small.allocated == 5 * rb and small.fallbacks == 1 and sum(small.is_pooled(y) for y in ys) == 5
+
+
+class _Ev:
+    """Stands in for a device event: done or not."""
+
+    def __init__(self, done=False):
+        self.done = done
+
+    def query(self):
+        return self.done
+
+
+def test_device_pool_pages():
+    """The device record pool (on host memory here: the bookkeeping is what is tested) carves
+    slots of every precision from the same pages: the pages of a freed slot serve the other
+    precision, neighbours coalesce, pending events travel with the pages, and the cap holds."""
+    from moelab_hip.offload import DevicePool
+
+    rb = {"fp16": 3 * 4096 + 100, "int4": 4096}
+    pool = DevicePool(rb, 9 * 4096, "cpu")
+    a, ea = pool.acquire("fp16")            # pages 0-3
+    b, _ = pool.acquire("int4")             # page 4
+    c, _ = pool.acquire("fp16")             # pages 5-8
+    assert ea == [] and a.numel() == rb["fp16"] and a.data_ptr() % 4096 == 0
+    assert pool.allocated == 9 * 4096 and pool.free_pages() == 0
+    with pytest.raises(RuntimeError, match="pool full"):
+        pool.acquire("int4")
+    pending = _Ev()
+    pool.release(a, "fp16", pending)        # pages 0-3 free once `pending` has passed
+    ints = [pool.acquire("int4") for _ in range(4)]  # the fp16 slot's pages serve four int4 records
+    assert all(evs == [pending] for _, evs in ints)
+    assert {t.data_ptr() for t, _ in ints} == {a.data_ptr() + i * 4096 for i in range(4)}
+    for t, _ in ints:
+        pool.release(t, "int4")
+    pool.release(b, "int4")
+    assert pool.free_pages() == 5 and len(pool.free_ext[0]) == 1  # pages 0-4 coalesced
+    pending.done = True
+    d, evs = pool.acquire("fp16")           # done events are dropped
+    assert evs == [] and d.data_ptr() == a.data_ptr()
+    pool.release(c, "fp16")
+    pool.release(d, "fp16")
+    assert pool.free_pages() == 9 and pool.free_ext[0] == [[0, 9, []]] and not pool.lent
