@@ -56,6 +56,7 @@ constexpr int XC_MAXKS = 33;
 constexpr int XC_LDS_H = 8192;     // h values of one XCD's segment staged in LDS (fp32)
 constexpr int XC_MAXDR = 512;      // output rows of one down item
 constexpr int XC_NST = 16;         // trace stamps per workgroup
+constexpr int XC_SPLIT_E = 256;    // from this many experts on, the router rows are split over the XCDs
 
 struct XcArgs {
     const void *x;            // (H) activation dtype, 16-byte aligned
@@ -80,6 +81,7 @@ struct XcArgs {
     uint32_t *ws;
     uint64_t *trace;          // XC_NST stamps per workgroup or null
     uint32_t off_lg, off_h, off_part;  // byte offsets of the tagged areas in ws
+    uint32_t off_glg;                  // the agent-scope logit area (router rows split over the XCDs)
     uint32_t lg_stride, h_stride;      // 64-bit words between two XCDs' copies
     int E, k, ks, H, I, gs_up, gs_dn, renorm, accumulate, planned;
     int unit, units;          // h values per segment unit, units over all table rows
@@ -88,6 +90,7 @@ struct XcArgs {
     int lg_up, lg_dn;         // log2 lanes per gate/up row and per down row
     int dr;                   // output rows per down item
     uint32_t defer;           // real-time ticks (10 ns) the down items wait before loading
+    int split;                // router rows split over the XCDs (E / 8 each), logits relayed between them
 };
 
 struct XcShared {
@@ -106,6 +109,8 @@ struct XcShared {
             int64_t rt[XC_MAXE];
             float lv[XC_MAXE + 64];
             uint32_t key[XC_MAXE + 64];
+            uint32_t lmax[64];            // top-k of E > 64 keys: the lanes' largest keys
+            uint32_t cand[XC_MAXE + 4];   //                       the candidates
         } r;
         __align__(16) float h[XC_LDS_H];
     } u;
@@ -172,18 +177,20 @@ __device__ __forceinline__ void xc_gen_manage(uint32_t *ws, uint32_t tag) {
 }
 
 // ---------------------------------------------------------------------------------------
-// router rows of this workgroup (every wave): rows id = q + NQ * (4 m + wave) < nrows, logit index
-// first + id: Wr's row when < E, the shared gate at E. Each lane holds 32 values (H <= 2048). The logit is
-// rounded to the activation dtype (the gate's F.linear output) and stored in the XCD's copy.
+// router rows of this workgroup (every wave): rows id = q + NQ * (4 m + wave) < nrows; row id < nr is
+// logit r0 + id (Wr's row), row nr the shared gate (logit index E). Each lane holds 32 values
+// (H <= 2048). The logit is rounded to the activation dtype (the gate's F.linear output) and stored
+// in the XCD's copy, and, when the rows are split over the XCDs (glg), at agent scope for the others.
 // ---------------------------------------------------------------------------------------
 template <int XDT>
-__device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int first, int nrows, uint64_t *lg, uint32_t gen) {
+__device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int r0, int nr, int nrows, uint64_t *lg,
+                                          uint64_t *glg, uint32_t gen) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c0 = lane * 32;
     const bool on = c0 < a.H;
     // the first row's weights are requested before x is used (both loads in flight together)
     auto row_ptr = [&](int id) {
-        const int r = first + id;  // logit index: Wr row r < E, the shared gate at E
+        const int r = id < nr ? r0 + id : a.E;  // logit index: Wr row r < E, the shared gate at E
         return r < a.E ? reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.Wr) + ((size_t)r * a.H + c0) * 2)
                        : reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(a.sgate) + (size_t)c0 * 2);
     };
@@ -218,7 +225,12 @@ __device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int fi
             }
         }
         acc = wave_sum(acc);
-        if (lane == 0) st_local(lg + first + id, __float_as_uint(rnd_act<XDT>(acc)), xc_tag_of(gen));
+        if (lane == 0) {
+            const int r = id < nr ? r0 + id : a.E;
+            const uint32_t v = __float_as_uint(rnd_act<XDT>(acc));
+            st_local(lg + r, v, xc_tag_of(gen));
+            if (glg != nullptr && r < a.E) st_tag(glg + r, v, xc_tag_of(gen));
+        }
         id += 4 * NQ;
         if (id >= nrows) break;
         if (on) {
@@ -230,33 +242,144 @@ __device__ __forceinline__ void xc_router(const XcArgs &a, int q, int NQ, int fi
 }
 
 // ---------------------------------------------------------------------------------------
+// relay (router rows split over the XCDs): one wave copies the E / 8 logits of XCD y from the
+// agent-scope area into this XCD's copy, each as soon as it is there (bounded; on expiry the error
+// flag is set and the word is not copied, so this XCD's pollers expire too and route on NaN)
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void xc_relay(const XcArgs &a, int y, const uint64_t *glg, uint64_t *lg, uint32_t tag) {
+    const int lane = threadIdx.x & 63;
+    const int nr = a.E / XC_N, r0 = y * nr;
+    for (int i0 = 0; i0 < nr; i0 += 64) {
+        const int r = r0 + i0 + lane;
+        bool need = i0 + lane < nr;
+        int nap = 1;
+        for (int it = 0; it < XC_SPIN && __ballot(need) != 0ull; ++it) {
+            if (need) {
+                const uint64_t v = ld_tag(glg + r);
+                if (tag_ok(v, tag)) {
+                    st_local(lg + r, (uint32_t)v, tag);
+                    need = false;
+                }
+            }
+            if (__ballot(need) != 0ull) backoff(nap, 2);
+        }
+        if (__ballot(need) != 0ull && lane == 0) flag_error(a.ws + XC_ERR);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // routing, part 1, by wave 0 of every workgroup: the k routed experts in rank order (lanes < k:
 // expert myc, logit myv) and the record base of every table row (k routed + the shared row) in
 // sh.rb. The rows' weight loads start from these; the weights and the HOBBIT decision (part 2)
 // follow while they are in flight. A row with no resident copy (or an unplanned layer) has
 // base 0 and never runs; a row that part 2 skips runs with weight 0.
 // ---------------------------------------------------------------------------------------
-// top-k of E > 64 keys by one wave: EPL keys per lane (lane + 64 i), held in registers for the k
-// rounds of a wave maximum (no LDS traffic per round; EPL fixed so that a round costs 3 EPL VALU
-// operations plus the maximum); keys are distinct (the index is part of the key)
+// r[i] += (k.i > b) for unsigned values: each compare's lane mask added straight into a count as the
+// carry (two VALU operations per key, no select), four independent chains so that no compare waits
+// for the count before it; every mask is read three instructions after it is written
+__device__ __forceinline__ void count_gt4(const uint4 kk, uint32_t b, int (&r)[4]) {
+    uint64_t m0, m1, m2, m3;
+    asm(
+        "v_cmp_gt_u32_e64 %4, %8, %12\n\t"
+        "v_cmp_gt_u32_e64 %5, %9, %12\n\t"
+        "v_cmp_gt_u32_e64 %6, %10, %12\n\t"
+        "v_cmp_gt_u32_e64 %7, %11, %12\n\t"
+        "v_addc_co_u32_e64 %0, %4, 0, %0, %4\n\t"
+        "v_addc_co_u32_e64 %1, %5, 0, %1, %5\n\t"
+        "v_addc_co_u32_e64 %2, %6, 0, %2, %6\n\t"
+        "v_addc_co_u32_e64 %3, %7, 0, %3, %7"
+        : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "=&s"(m0), "=&s"(m1), "=&s"(m2), "=&s"(m3)
+        : "v"(kk.x), "v"(kk.y), "v"(kk.z), "v"(kk.w), "v"(b));
+}
+// the number of the n (a multiple of 4) words of LDS array s greater than b
+__device__ __forceinline__ int count_greater(const uint32_t *s, int n, uint32_t b) {
+    int r[4] = {0, 0, 0, 0};
+    for (int j = 0; j < n; j += 4) count_gt4(*reinterpret_cast<const uint4 *>(s + j), b, r);
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+template <int N>
+__device__ __forceinline__ int count_greater_n(const uint32_t *s, uint32_t b) {
+    uint4 kv[N / 4];  // (every read issued before the first compare)
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) kv[j] = *reinterpret_cast<const uint4 *>(s + 4 * j);
+    int r[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) count_gt4(kv[j], b, r);
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
+// top-k of E > 64 keys by one wave, EPL keys per lane (key c at lane c % 64, slot c / 64): T = the
+// k-th largest of the 64 lanes' largest keys, ranked by counting; only the k lanes whose largest key
+// is >= T hold keys >= T, so there are at most k * EPL candidates (about k + a few for routing
+// logits), compacted into LDS and ranked by counting among themselves. Keys are distinct (the expert
+// index is part of the key); zero keys (padding, expired polls) are never candidates, and a rank that
+// no key reaches keeps E - 1, as k rounds of a maximum over zero keys would give it.
 template <int EPL>
-__device__ __forceinline__ void xc_topk(const uint32_t *s_key, int E, int k, int lane, int &myc) {
+__device__ __forceinline__ void xc_topk(XcShared &sh, const uint32_t *s_key, int E, int k, int lane, int &myc) {
     uint32_t key[EPL];
+    uint32_t lm = 0u;
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
         const int c = lane + 64 * i;
         key[i] = c < E ? s_key[c] : 0u;
+        lm = max(lm, key[i]);
     }
-    for (int r = 0; r < k; ++r) {
-        uint32_t lb = key[0];
+    uint32_t *s_lm = sh.u.r.lmax, *s_c = sh.u.r.cand;
+    s_lm[lane] = lm;
+    if (lane < k) sh.idx[lane] = E - 1;
+    wave_sync();
+    const int r = count_greater_n<64>(s_lm, lm);
+    const unsigned long long bt = __ballot(r == k - 1 && lm != 0u);
+    const uint32_t T = bt != 0ull ? (uint32_t)__builtin_amdgcn_readlane((int)lm, __builtin_ffsll((long long)bt) - 1) : 1u;
+    int base = 0;
 #pragma unroll
-        for (int i = 1; i < EPL; ++i) lb = max(lb, key[i]);
-        const uint32_t M = wave_max_u32(lb);
-#pragma unroll
-        for (int i = 0; i < EPL; ++i)
-            if (key[i] == M) key[i] = 0u;
-        if (lane == r) myc = min(1023 - (int)(M & 1023u), E - 1);
+    for (int i = 0; i < EPL; ++i) {
+        const bool sel = key[i] >= T && key[i] != 0u;
+        const unsigned long long b = __ballot(sel);
+        const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if (sel) s_c[pos] = key[i];
+        base += __popcll(b);
     }
+    if (lane < 4) s_c[base + lane] = 0u;  // (the last uint4 read past the candidates sees zeros)
+    wave_sync();
+    const int C = uni(base);
+    for (int j0 = 0; j0 < C; j0 += 64) {
+        const uint32_t mine = j0 + lane < C ? s_c[j0 + lane] : 0u;
+        const int rr = count_greater(s_c, (C + 3) & ~3, mine);
+        if (mine != 0u && rr < k) sh.idx[rr] = min(1023 - (int)(mine & 1023u), E - 1);
+    }
+    wave_sync();
+    if (lane < k) myc = sh.idx[lane];
+}
+
+// the logits of this XCD's copy, polled by one wave (word first + lane + 64 i for the bits i of need):
+// every word a lane still needs is requested before any is looked at (one round trip per poll; NB
+// words per lane at a time); returns the words that never arrived (bounded by spin)
+template <int XDT, int NB>
+__device__ __forceinline__ uint32_t xc_poll_logits(const uint64_t *lg, int first, int E, int epl, int lane, uint32_t tag,
+                                                   int spin, uint32_t need, float *s_lv, uint32_t *s_key) {
+    int nap = 1;
+    for (int it = 0; it < spin && __ballot(need != 0) != 0ull; ++it) {
+        for (int i0 = 0; i0 < epl; i0 += NB) {
+            uint64_t v[NB];
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+                if (i0 + i < epl && (need & (1u << (i0 + i)))) v[i] = ld_local(lg + first + lane + 64 * (i0 + i));
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int ii = i0 + i;
+                if (ii < epl && (need & (1u << ii)) && tag_ok(v[i], tag)) {
+                    const int c = first + lane + 64 * ii;
+                    const float l = __uint_as_float((uint32_t)v[i]);
+                    s_lv[c] = l;
+                    if (c < E) s_key[c] = logit_key<XDT>(l, c);
+                    need &= ~(1u << ii);
+                }
+            }
+        }
+        if (__ballot(need != 0) != 0ull) backoff(nap, 2);
+    }
+    return need;
 }
 
 template <int XDT>
@@ -286,27 +409,9 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
         uint32_t need = 0;
         for (int i = 0; i < epl; ++i)
             if (lane + 64 * i < nlog) need |= 1u << i;
-        int nap = 1;
-        for (int it = 0; it < spin && __ballot(need != 0) != 0ull; ++it) {
-            for (int i0 = 0; i0 < epl; i0 += 4) {  // up to 4 words per lane in flight at a time
-                uint64_t v[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (i0 + i < epl && (need & (1u << (i0 + i)))) v[i] = ld_local(lg + first + lane + 64 * (i0 + i));
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int ii = i0 + i;
-                    if (ii < epl && (need & (1u << ii)) && tag_ok(v[i], tag)) {
-                        const int c = first + lane + 64 * ii;
-                        const float l = __uint_as_float((uint32_t)v[i]);
-                        s_lv[c] = l;
-                        if (c < E) s_key[c] = logit_key<XDT>(l, c);
-                        need &= ~(1u << ii);
-                    }
-                }
-            }
-            if (__ballot(need != 0) != 0ull) backoff(nap, 2);
-        }
+        if (epl == 1) need = xc_poll_logits<XDT, 1>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
+        else if (epl <= 4) need = xc_poll_logits<XDT, 4>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
+        else need = xc_poll_logits<XDT, 16>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
         if (__ballot(need != 0) != 0ull) {  // expired: NaN weights, the rest routes on what arrived
             poisoned = true;
             if (lane == 0) flag_error(a.ws + XC_ERR);
@@ -331,16 +436,7 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
             // than k logits) keeps E - 1, as the rounds of a maximum over zero keys give it.
             wave_sync();  // (every lane's keys, written while polling)
             const uint32_t key = lane < E ? s_key[lane] : 0u;
-            int r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-#pragma unroll
-            for (int j = 0; j < 64; j += 4) {
-                const uint4 kk = *reinterpret_cast<const uint4 *>(s_key + j);
-                r0 += kk.x > key ? 1 : 0;
-                r1 += kk.y > key ? 1 : 0;
-                r2 += kk.z > key ? 1 : 0;
-                r3 += kk.w > key ? 1 : 0;
-            }
-            const int rank = (r0 + r1) + (r2 + r3);
+            const int rank = count_greater_n<64>(s_key, key);
             if (lane < k) sh.idx[lane] = E - 1;
             wave_sync();
             if (key != 0u && rank < k) sh.idx[rank] = lane;
@@ -348,10 +444,11 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
             if (lane < k) myc = sh.idx[lane];
         } else {
             const int epl = (E + 63) >> 6;
-            if (epl <= 2) xc_topk<2>(s_key, E, k, lane, myc);
-            else if (epl <= 4) xc_topk<4>(s_key, E, k, lane, myc);
-            else if (epl <= 8) xc_topk<8>(s_key, E, k, lane, myc);
-            else xc_topk<XC_MAXE / 64>(s_key, E, k, lane, myc);
+            wave_sync();  // (every lane's keys, written while polling)
+            if (epl <= 2) xc_topk<2>(sh, s_key, E, k, lane, myc);
+            else if (epl <= 4) xc_topk<4>(sh, s_key, E, k, lane, myc);
+            else if (epl <= 8) xc_topk<8>(sh, s_key, E, k, lane, myc);
+            else xc_topk<XC_MAXE / 64>(sh, s_key, E, k, lane, myc);
         }
         if (lane < k) myv = s_lv[myc];
     } else if (lane < k) {
@@ -808,7 +905,6 @@ __device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, cons
 template <int XDT, int PREC, bool TWO>
 __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     __shared__ XcShared sh;
-    constexpr int VPC = DlFmt<PREC>::VPC, NPD = XcFmt<PREC>::NPD;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int b = blockIdx.x, x = b % XC_N, q = b / XC_N, NQ = gridDim.x / XC_N;
     uint8_t *wsb = reinterpret_cast<uint8_t *>(a.ws);
@@ -842,13 +938,20 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     // 1. router rows of this XCD (logits, shared gate), then the routing, by one wave chosen by
     //    workgroup: the workgroups q, q + 32, q + 64 of an XCD usually share a CU, and route on
     //    different SIMDs
-    const int nrows = tab ? (routed ? a.E : 0) + (a.sgate != nullptr ? 1 : 0) : 0;
-    if (nrows > 0) xc_router<XDT>(a, q, NQ, routed ? 0 : a.E, nrows, lg, gen);
+    //    With the rows split over the XCDs (E / 8 each), every logit also goes out at agent scope and
+    //    one wave of workgroups 0..6 of every XCD relays another XCD's block into this XCD's copy.
+    const bool split = tab && routed && a.split != 0;
+    const int nr = tab && routed ? (split ? a.E / XC_N : a.E) : 0;
+    const int nrows = tab ? nr + (a.sgate != nullptr ? 1 : 0) : 0;
+    uint64_t *glg = split ? reinterpret_cast<uint64_t *>(wsb + a.off_glg) : nullptr;
+    if (nrows > 0) xc_router<XDT>(a, q, NQ, split ? x * (a.E / XC_N) : 0, nr, nrows, lg, glg, gen);
 #pragma unroll
     for (int i = 0; i < XC_MAXE / 256; ++i) {
         const int e = tid + 256 * i;
         if (tab && e < a.E) sh.u.r.rt[e] = rtv[i];
     }
+    // (the relay wave is never the routing wave below, nor wave 0, which holds a router row)
+    if (split && q < XC_N - 1 && wave == 3 - (q & 1)) xc_relay(a, (x + 1 + q) % XC_N, glg, lg, xc_tag_of(gen));
     const uint32_t tag = (uint32_t)uni((int)xc_tag_of(gen));
     xc_stamp(a, sh, 1);
     const int seg0u = xc_seg_begin(x, a.units), seg1u = xc_seg_begin(x + 1, a.units);
@@ -946,7 +1049,8 @@ static inline int xc_lg(int chunks, int prec) {  // log2 lanes for `chunks` chun
 struct XcPlan {
     int ok;
     int unit, units, nu, nd, hpi, lg_up, lg_dn, dr, grid;
-    uint32_t lg_stride, h_stride, off_lg, off_h, off_part, total;
+    uint32_t lg_stride, h_stride, off_lg, off_h, off_part, off_glg, total;
+    int split;
 };
 
 static inline uint32_t xc_al256(size_t v) { return (uint32_t)((v + 255) / 256 * 256); }
@@ -980,6 +1084,10 @@ static XcPlan xc_plan(int prec, int ks, int E, int H, int I) {
     off = xc_al256(off + (size_t)XC_N * p.h_stride * 8);
     p.off_part = (uint32_t)off;
     off = xc_al256(off + (size_t)XC_N * H * 8);
+    // router rows split over the XCDs from E = XC_SPLIT_E on (E / 8 rows each instead of E per XCD)
+    p.split = E >= XC_SPLIT_E && E % XC_N == 0 ? 1 : 0;
+    p.off_glg = (uint32_t)off;
+    if (p.split) off = xc_al256(off + (size_t)E * 8);
     p.total = (uint32_t)off;
     p.ok = 1;
     return p;
@@ -1095,6 +1203,8 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     a.off_lg = p.off_lg;
     a.off_h = p.off_h;
     a.off_part = p.off_part;
+    a.off_glg = p.off_glg;
+    a.split = p.split && Wr != nullptr && rows_b == nullptr && grid / XC_N >= XC_N ? 1 : 0;
     a.lg_stride = p.lg_stride;
     a.h_stride = p.h_stride;
     a.E = d->E;

@@ -650,12 +650,14 @@ def test_fused_qwen3next_shape(dev, prec):
     dec.check_error()
 
 
-@pytest.mark.parametrize("E", [16, 128])
+@pytest.mark.parametrize("E", [16, 128, 256, 1024])
 @pytest.mark.parametrize("k", [2, 3, 6, 13])
 def test_fused_router_planted_ties(dev, k, E):
     """Fused router on tied logits (including -0 against +0): equal logits go to the lowest
-    expert index, in the oracle's order (E = 16: ranked by counting; E = 128: by rounds of a
-    maximum, the pattern repeated so that ties span far-apart indices)."""
+    expert index, in the oracle's order. E = 16: one key per lane, ranked by counting; E = 128:
+    the candidate filter (keys at or above the k-th largest of the lanes' largest keys, ranked
+    among themselves); E = 256 and 1024: the same with the router rows split over the XCDs and
+    the logits relayed between them. The pattern repeats so that ties span far-apart indices."""
     H, I = 512, 256
     S = _Stack(dev, H, I, E, 1, ["int4"], 5)
     col = torch.tensor([0.1, 0.9, 0.5, -0.0, 0.3, 0.5, 0.4, 0.4, 0.0, 0.5, 0.1, -0.2, 0.3, 0.4, 0.9, 0.0]).repeat(E // 16)
