@@ -52,6 +52,8 @@ HBM_PEAK_GBS = 8000.0
 PROFILE = ROOT / "profiles" / "k_decode_xcd_olmoe_int4_bs1.md"
 PREFILL_PROFILE = ROOT / "profiles" / "k_gemm_qwen3_30b_prefill_t512.md"
 BATCH_PROFILE = ROOT / "profiles" / "k_gemv_batched_decode.md"
+SHAPES_PROFILE = ROOT / "profiles" / "k_decode_xcd_bs1_other_shapes.md"
+STREAM_PROFILE = ROOT / "profiles" / "k_stream_read_olmoe_layer.md"
 
 
 def measured_traffic(profile: Path = PROFILE, workload: str | None = None):
@@ -392,7 +394,8 @@ def dense_line(args):
         "config": {"workload": "one-token int8 gs64 GEMVs of the dense part (QLinear), bf16 activations",
                    "shapes": {k: [v["O"], v["K"]] for k, v in res.items()}},
         "roofline": {"bound": "hbm", "achieved": h["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(h["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(ROOT / "profiles" / "k_gemv8_dense_int8.md", "olmoe-lm-head"),
                      "kernel": "k_gemv8<bf16> (moehip_dense_gemv_int8)", "bytes_per_launch": h["bytes"]},
         "shapes": res,
         "cpu_baseline": None,
@@ -547,7 +550,7 @@ def decode_line(args, name):
                    "batch": 1, "activations": sp["dtype"], "shared_expert": sp["shared"]},
         "layer_us": round(layer_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(SHAPES_PROFILE, name),
                      "kernel": f"{kernel_name} (one launch per layer, HIP graph per token)",
                      "bytes_per_launch": int(alg)},
         "cpu_baseline": (decode_cpu_baseline(args.cpu_seconds, H_, I_, k_ + (1 if sp["shared"] else 0), L_)
@@ -1100,7 +1103,8 @@ def stream_line(args):
                                "one 64 x 2048 fp16 router, read once by moehip_stream_read", "bytes_per_launch": nbytes},
         "per_grid": per, "best_grid": best, "stamps_grid_768": r.get("stamps"), "more_bytes": more,
         "roofline": {"bound": "hbm", "achieved": round(nbytes / (r[768] * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(nbytes / (r[768] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(nbytes / (r[768] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(STREAM_PROFILE),
                      "kernel": "k_stream_read (moehip_stream_read), grid 768"},
         "cpu_baseline": None,
     }
