@@ -64,8 +64,10 @@ template <> struct GgPrec<MOEHIP_PREC_BF16> { static constexpr int CK = 32, BITS
 // weights -> fp16 B operands in operand order c0 c4 c1 c5 c2 c6 c3 c7 (the order the activation
 // chunks are stored in). int4: dword d of a row (K elements c0..c7 as nibbles) and the group
 // scale s (fp16, both halves): (d & mask) | magic = fp16 1024 + n in one v_and_or_b32 (common.hpp
-// and_or; its result feeds the compiler's packed fp16 add, never an MFMA operand directly),
-// - 1032 (exact), * s (one rounding).
+// and_or; its result feeds the compiler's packed fp16 add, never an MFMA operand directly) for the
+// nibbles at bits 0-3 of each half; for those at bits 4-7 the magic is fp16 64, whose unit in the
+// last place is 1/16, so the same mask-and-or gives 64 + n with no shift; - 1032 or - 72 (exact),
+// * s (one rounding). 13 VALU operations per 8 weights.
 // ---------------------------------------------------------------------------------------
 struct DeqK {
     uint32_t mask, magic;  // 0x000F000F, 0x64006400
@@ -74,14 +76,16 @@ struct DeqK {
 __device__ __forceinline__ f16x8 wdeq8(uint32_t d, half2_t s2, DeqK k) {
 #pragma clang fp contract(off)
     const half2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const uint32_t u0 = and_or(d, k.mask, k.magic);  // 1024 + n
-    const uint32_t u1 = and_or(d >> 4, k.mask, k.magic);
-    const uint32_t u2 = and_or(d >> 8, k.mask, k.magic);
-    const uint32_t u3 = and_or(d >> 12, k.mask, k.magic);
+    const half2_t off_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
+    const uint32_t t = d >> 8;
+    const uint32_t u0 = and_or(d, k.mask, k.magic);           // 1024 + n (c0, c4)
+    const uint32_t u1 = and_or(d, 0x00F000F0u, 0x54005400u);  // 64 + n   (c1, c5)
+    const uint32_t u2 = and_or(t, k.mask, k.magic);           // 1024 + n (c2, c6)
+    const uint32_t u3 = and_or(t, 0x00F000F0u, 0x54005400u);  // 64 + n   (c3, c7)
     const half2_t h0 = (__builtin_bit_cast(half2_t, u0) + off) * s2;
-    const half2_t h1 = (__builtin_bit_cast(half2_t, u1) + off) * s2;
+    const half2_t h1 = (__builtin_bit_cast(half2_t, u1) + off_hi) * s2;
     const half2_t h2 = (__builtin_bit_cast(half2_t, u2) + off) * s2;
-    const half2_t h3 = (__builtin_bit_cast(half2_t, u3) + off) * s2;
+    const half2_t h3 = (__builtin_bit_cast(half2_t, u3) + off_hi) * s2;
     const uint4 u = make_uint4(__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
                                __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3));
     return __builtin_bit_cast(f16x8, u);
