@@ -823,6 +823,68 @@ __global__ __launch_bounds__(256) void k_gemv_down(const float *__restrict__ hb,
                                  w, y, H, dk);
 }
 
+// Both record precisions of a two-precision store in ONE launch (a mixed store's per-precision
+// launches mostly find few or no experts at one of the precisions, and an empty launch still
+// costs its dispatch and every workgroup's read of the count): items i < n0 of the grid's y run
+// precision 0's list, the next n1 precision 1's, each side with its own row geometry (grid.x is
+// the larger of the two sides' row-block counts; a side's surplus blocks exit).
+struct GvSide {
+    const int32_t *items;  // the precision's work list ([NP] = its length)
+    const int64_t *tab;    // its record table
+    int lg, NG, gx;        // lanes per row (log2), row groups per workgroup, row blocks
+};
+template <int PA, int CA, int QA, int PB, int CB, int QB, bool XBF>
+__global__ __launch_bounds__(256) void k_gemv_up2(const uint16_t *__restrict__ x, const int *__restrict__ xe, int H,
+                                                  int I, int k, int NP, const int32_t *__restrict__ offsets,
+                                                  const int32_t *__restrict__ sorted_pos, float *__restrict__ hb,
+                                                  DeqK dk, GvSide sa, GvSide sb) {
+    const int n0 = sa.items[NP], n1 = sb.items[NP];
+    int i = blockIdx.y;
+    const bool first = i < n0;
+    if (!first) i -= n0;
+    if (!first && i >= n1) return;
+    const GvSide &sd = first ? sa : sb;
+    if ((int)blockIdx.x >= sd.gx) return;
+    const int it = sd.items[i], e = it >> 8;
+    const int p0 = offsets[e] + (it & 255) * GV_TG, ne = min(GV_TG, offsets[e + 1] - p0);
+    gu8 *qb = record_ptr(sd.tab[4 * e + 0]);
+    if (ne <= 0 || qb == nullptr) return;
+    gu8 *sc = record_ptr(sd.tab[4 * e + 1]);
+    if (first) {
+        const int r0 = blockIdx.x * sa.NG * 4 * QA * (64 >> sa.lg);
+        if (r0 < I) gv_rows<PA, CA, QA, true, XBF>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, sc, sa.lg, r0, sa.NG, nullptr, hb, I, dk);
+    } else {
+        const int r0 = blockIdx.x * sb.NG * 4 * QB * (64 >> sb.lg);
+        if (r0 < I) gv_rows<PB, CB, QB, true, XBF>(x, xe, H, I, I, k, p0, ne, sorted_pos, qb, sc, sb.lg, r0, sb.NG, nullptr, hb, I, dk);
+    }
+}
+
+template <int PA, int CA, int QA, int PB, int CB, int QB>
+__global__ __launch_bounds__(256) void k_gemv_down2(const float *__restrict__ hb, int H, int I, int NP,
+                                                    const int32_t *__restrict__ offsets,
+                                                    const int32_t *__restrict__ sorted_pos, const float *__restrict__ w,
+                                                    float *__restrict__ y, DeqK dk, GvSide sa, GvSide sb) {
+    const int n0 = sa.items[NP], n1 = sb.items[NP];
+    int i = blockIdx.y;
+    const bool first = i < n0;
+    if (!first) i -= n0;
+    if (!first && i >= n1) return;
+    const GvSide &sd = first ? sa : sb;
+    if ((int)blockIdx.x >= sd.gx) return;
+    const int it = sd.items[i], e = it >> 8;
+    const int p0 = offsets[e] + (it & 255) * GV_TG, ne = min(GV_TG, offsets[e + 1] - p0);
+    gu8 *qb = record_ptr(sd.tab[4 * e + 2]);
+    if (ne <= 0 || qb == nullptr) return;
+    gu8 *sc = record_ptr(sd.tab[4 * e + 3]);
+    if (first) {
+        const int r0 = blockIdx.x * sa.NG * 4 * QA * (64 >> sa.lg);
+        if (r0 < H) gv_rows<PA, CA, QA, false>(hb, nullptr, I, H, 0, 1, p0, ne, sorted_pos, qb, sc, sa.lg, r0, sa.NG, w, y, H, dk);
+    } else {
+        const int r0 = blockIdx.x * sb.NG * 4 * QB * (64 >> sb.lg);
+        if (r0 < H) gv_rows<PB, CB, QB, false>(hb, nullptr, I, H, 0, 1, p0, ne, sorted_pos, qb, sc, sb.lg, r0, sb.NG, w, y, H, dk);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // down: tiles (expert, 256 output rows); wave w: rows nb*256 + 64 w + 32 t + (lane % 32).
 // y[pair, row] = w[pair] * (down_row . h_pair); h is read as the up tiles left it (fp16 times
@@ -1790,27 +1852,33 @@ static GvGeo gv_geo(int prec, int K) {
 
 constexpr int GV_WG_BYTES = 128 << 10;  // weight bytes per workgroup at most
 constexpr int GV_MIN_WGS = 2048;        // workgroups per launch at least (about two per CU slot)
-template <int PREC, int CPL>
-static void launch_gv_cpl(int mode, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
-                          int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
-                          float *out, const float *w, DeqK dk) {
-    constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
-    const bool up = mode != 0;
+// row groups per workgroup (ng) and row blocks per item (gx) of one precision's GEMV launch
+static void gv_grid(int prec, bool up, int rows, int NP, const GvGeo &g, int H, int I, int &ng, int &gx) {
     // row groups per workgroup: up to 128 KiB of weights and GV_MAXROWS rows, while the pairs
     // (an upper bound of the work items) still give about two workgroups per CU slot
     const int groups = (rows + g.rows_per_block - 1) / g.rows_per_block;
-    const int row_bytes = (up ? 2 : 1) * (up ? H : I) * (PREC == MOEHIP_PREC_INT4 ? 1 : (PREC == MOEHIP_PREC_INT8 || PREC == MOEHIP_PREC_FP8 ? 2 : 4)) / 2;
-    int ng = max(1, min(groups, GV_WG_BYTES / max(1, g.rows_per_block * row_bytes)));
+    const int row_bytes = (up ? 2 : 1) * (up ? H : I) *
+                          (prec == MOEHIP_PREC_INT4 ? 1 : (prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8 ? 2 : 4)) / 2;
+    ng = max(1, min(groups, GV_WG_BYTES / max(1, g.rows_per_block * row_bytes)));
     ng = max(1, min(ng, GV_MAXROWS / g.rows_per_block));
     ng = max(1, min(ng, groups * NP / GV_MIN_WGS));
     // row blocks per item a multiple of the 8 XCDs: workgroups are dealt to the XCDs round robin,
     // so row block b of every item (the items of one expert, one per token, are adjacent) then
     // runs on XCD b % 8 and the re-reads of its rows hit that XCD's L2
-    int gx = (groups + ng - 1) / ng;
+    gx = (groups + ng - 1) / ng;
     gx = (gx + 7) & ~7;
     ng = (groups + gx - 1) / gx;
     gx = (groups + ng - 1) / ng;
     gx = (gx + 7) & ~7;
+}
+
+template <int PREC, int CPL>
+static void launch_gv_cpl(int mode, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
+                          int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
+                          float *out, const float *w, DeqK dk) {
+    constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
+    int ng = 1, gx = 8;
+    gv_grid(PREC, mode != 0, rows, NP, g, H, I, ng, gx);
     const dim3 grid(gx, NP);
     if (mode == 2)  // bf16 activations, scaled into fp16 per chunk by the kernel
         hipLaunchKernelGGL((k_gemv_up<PREC, CPL, P, true>), grid, dim3(256), 0, st, reinterpret_cast<const uint16_t *>(act),
@@ -1851,6 +1919,52 @@ static void launch_gv_prec(int prec, int mode, const int32_t *items, int NP, hip
         case MOEHIP_PREC_F16: launch_gv<MOEHIP_PREC_F16>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
         default: launch_gv<MOEHIP_PREC_BF16>(mode, items, NP, st, act, ae, H, I, k, offsets, sorted_pos, tab, out, w, dk); break;
     }
+}
+
+// one launch for both precisions of a two-precision store, when the pair is one this library
+// instantiates (a 16-bit record with int4 or int8, each with the chunks per lane its K gives);
+// false: the caller launches per precision
+template <int PA, int CA, int PB, int CB>
+static void launch_gv2_t(int mode, const GvSide &a, const GvSide &b, int NP, hipStream_t st, const void *act, const int *ae,
+                         int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, float *out,
+                         const float *w, DeqK dk) {
+    constexpr int QA = CA >= 4 ? 1 : 4 / CA, QB = CB >= 4 ? 1 : 4 / CB;
+    const dim3 grid(max(a.gx, b.gx), NP);
+    if (mode == 2)
+        hipLaunchKernelGGL((k_gemv_up2<PA, CA, QA, PB, CB, QB, true>), grid, dim3(256), 0, st,
+                           reinterpret_cast<const uint16_t *>(act), nullptr, H, I, k, NP, offsets, sorted_pos, out, dk, a, b);
+    else if (mode == 1)
+        hipLaunchKernelGGL((k_gemv_up2<PA, CA, QA, PB, CB, QB, false>), grid, dim3(256), 0, st,
+                           reinterpret_cast<const uint16_t *>(act), ae, H, I, k, NP, offsets, sorted_pos, out, dk, a, b);
+    else
+        hipLaunchKernelGGL((k_gemv_down2<PA, CA, QA, PB, CB, QB>), grid, dim3(256), 0, st,
+                           reinterpret_cast<const float *>(act), H, I, NP, offsets, sorted_pos, w, out, dk, a, b);
+}
+static bool launch_gv2(const int *precs, int mode, const int32_t *items, int NP, hipStream_t st, const void *act,
+                       const int *ae, int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos,
+                       const int64_t *tabs, int E, float *out, const float *w, DeqK dk) {
+    const int K = mode != 0 ? H : I, rows = mode != 0 ? I : H;
+    const GvGeo g0 = gv_geo(precs[0], K), g1 = gv_geo(precs[1], K);
+    if (g0.rows_per_block > GV_MAXROWS || g1.rows_per_block > GV_MAXROWS) return false;
+    GvSide a{items, tabs, g0.lg, 1, 8}, b{items + (NP + 1), tabs + (size_t)E * 4, g1.lg, 1, 8};
+    gv_grid(precs[0], mode != 0, rows, NP, g0, H, I, a.NG, a.gx);
+    gv_grid(precs[1], mode != 0, rows, NP, g1, H, I, b.NG, b.gx);
+    const bool p16 = precs[0] == MOEHIP_PREC_F16 || precs[0] == MOEHIP_PREC_BF16;
+    if (!p16 || (precs[1] != MOEHIP_PREC_INT4 && precs[1] != MOEHIP_PREC_INT8)) return false;
+    // (16-bit records: K = 2048 gives 4 chunks per lane, 1024 gives 2; int4 / int8: 1)
+    if (g1.cpl != 1 || (g0.cpl != 2 && g0.cpl != 4)) return false;
+#define GV2(P0, C0, P1) launch_gv2_t<P0, C0, P1, 1>(mode, a, b, NP, st, act, ae, H, I, k, offsets, sorted_pos, out, w, dk)
+    if (precs[0] == MOEHIP_PREC_F16 && precs[1] == MOEHIP_PREC_INT4) {
+        if (g0.cpl == 4) GV2(MOEHIP_PREC_F16, 4, MOEHIP_PREC_INT4); else GV2(MOEHIP_PREC_F16, 2, MOEHIP_PREC_INT4);
+    } else if (precs[0] == MOEHIP_PREC_BF16 && precs[1] == MOEHIP_PREC_INT4) {
+        if (g0.cpl == 4) GV2(MOEHIP_PREC_BF16, 4, MOEHIP_PREC_INT4); else GV2(MOEHIP_PREC_BF16, 2, MOEHIP_PREC_INT4);
+    } else if (precs[0] == MOEHIP_PREC_F16 && precs[1] == MOEHIP_PREC_INT8) {
+        if (g0.cpl == 4) GV2(MOEHIP_PREC_F16, 4, MOEHIP_PREC_INT8); else GV2(MOEHIP_PREC_F16, 2, MOEHIP_PREC_INT8);
+    } else {
+        if (g0.cpl == 4) GV2(MOEHIP_PREC_BF16, 4, MOEHIP_PREC_INT8); else GV2(MOEHIP_PREC_BF16, 2, MOEHIP_PREC_INT8);
+    }
+#undef GV2
+    return true;
 }
 
 static bool gg_prec_ok(int prec) {
@@ -1935,7 +2049,11 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
     if (gemv && items_in == nullptr)
         hipLaunchKernelGGL(k_gv_items, dim3(1), dim3(1024), 0, st, offsets, E, NP, tabs, P, items);
     if (items_in != nullptr) items = const_cast<int32_t *>(items_in);
-    for (int p = 0; p < P && gemv; ++p)
+    // a two-precision store: both precisions in one up and one down launch where the pair is instantiated
+    const bool two = gemv && P == 2 &&
+                     launch_gv2(precs, bf ? 2 : 1, items, NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets,
+                                sorted_pos, tabs, E, hb, nullptr, dk);
+    for (int p = 0; p < P && gemv && !two; ++p)
         launch_gv_prec(precs[p], bf ? 2 : 1, items + (size_t)p * (NP + 1), NP, st, bf ? xs : xa, bf ? nullptr : xea, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4, hb, nullptr,
                        dk);
     // the MFMA up tiles write h as fp16 with a power of two per (pair, 32 columns); the GEMVs fp32
@@ -1951,7 +2069,8 @@ static int gg_run(int P, const int *precs, const int64_t *tabs, const void *x, i
             default: launch_up<MOEHIP_PREC_BF16>(gu, st, xa, xea, H, I, k, E, offsets, sorted_pos, tab, h16, hbe, dk); break;
         }
     }
-    for (int p = 0; p < P && gemv; ++p)
+    if (two) launch_gv2(precs, 0, items, NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs, E, y, w, dk);
+    for (int p = 0; p < P && gemv && !two; ++p)
         launch_gv_prec(precs[p], 0, items + (size_t)p * (NP + 1), NP, st, hb, nullptr, H, I, k, offsets, sorted_pos, tabs + (size_t)p * E * 4,
                        y, w, dk);
     for (int p = 0; p < P && !gemv && !fused; ++p) {
