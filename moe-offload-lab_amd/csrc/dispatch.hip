@@ -36,12 +36,22 @@ __device__ __forceinline__ void match_lanes(int e, bool valid, int ebits, int la
     r = __popcll(m & lt);
 }
 
-// the dispatch by one workgroup of 1024 threads; s_cnt: DP_WAVES * E ints of LDS
+// kept-pair experts of a decision kernel held in LDS (the levels write them, the dispatch reads
+// them: no read-back of this workgroup's own global writes), for batches of up to DP_LDS_PAIRS pairs
+constexpr int DP_LDS_PAIRS = 4096;
+
+// the dispatch by one workgroup of 1024 threads; s_cnt: DP_WAVES * E ints of LDS. With s_pe, the
+// expert of kept pair p (or -1) is s_pe[p] instead of idx / skip.
 __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip, int NP,
                                             int E, int ebits, int32_t *__restrict__ counts,
                                             int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
-                                            int32_t *__restrict__ rank, int *s_cnt, int *s_wtot) {
+                                            int32_t *__restrict__ rank, int *s_cnt, int *s_wtot,
+                                            const int16_t *s_pe = nullptr) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto pair_e = [&](int p, int p1) -> int {
+        if (s_pe == nullptr) return pair_expert(idx, skip, p, p1, E);
+        return p < p1 ? (int)s_pe[p] : -1;
+    };
     const int SEG = (NP + DP_WAVES - 1) / DP_WAVES;
     const int p0 = wave * SEG, p1 = min(NP, p0 + SEG);
     for (int i = tid; i < DP_WAVES * E; i += 1024) s_cnt[i] = 0;
@@ -50,7 +60,7 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
     // the expert of each of the first DP_PRE steps' pairs, loaded at once (-1 = not a kept pair)
     int pre[DP_PRE];
 #pragma unroll
-    for (int i = 0; i < DP_PRE; ++i) pre[i] = pair_expert(idx, skip, p0 + 64 * i + lane, p1, E);
+    for (int i = 0; i < DP_PRE; ++i) pre[i] = pair_e(p0 + 64 * i + lane, p1);
     // pass 1: per-wave counts (only the wave itself touches its row)
     for (int base = p0, step = 0; base < p1; base += 64, ++step) {
         const int p = base + lane;
@@ -58,7 +68,7 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
 #pragma unroll
         for (int i = 0; i < DP_PRE; ++i)
             if (step == i) ev = pre[i];
-        if (step >= DP_PRE) ev = pair_expert(idx, skip, p, p1, E);
+        if (step >= DP_PRE) ev = pair_e(p, p1);
         const bool valid = ev >= 0;
         const int e = valid ? ev : 0;
         uint64_t m;
@@ -104,7 +114,7 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
 #pragma unroll
         for (int i = 0; i < DP_PRE; ++i)
             if (step == i) ev = pre[i];
-        if (step >= DP_PRE) ev = pair_expert(idx, skip, p, p1, E);
+        if (step >= DP_PRE) ev = pair_e(p, p1);
         const bool valid = ev >= 0;
         const int e = valid ? ev : 0;
         uint64_t m;
@@ -123,6 +133,50 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
     for (int i = total + tid; i < NP; i += 1024) sorted_pos[i] = -1;
 }
 
+// The same dispatch for at most 64 pairs over at most 64 experts by ONE wave (lane = pair; the
+// batched decode's few tokens): the stable rank of a pair is its rank among the lower lanes with the
+// same expert (match_lanes), the group's last lane writes the expert's count, one prefix scan over
+// the experts gives the offsets. No workgroup barrier: the rest of the workgroup is not involved.
+// s_cnt: EA words of LDS.
+__device__ __forceinline__ void dispatch_wave64(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip, int NP,
+                                                int EA, int ebits, int32_t *__restrict__ counts,
+                                                int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
+                                                int32_t *__restrict__ rank, int *s_cnt, const int16_t *s_pe) {
+    const int lane = threadIdx.x & 63;
+    const int ev = lane < NP ? (s_pe != nullptr ? (int)s_pe[lane] : pair_expert(idx, skip, lane, NP, EA)) : -1;
+    const bool valid = ev >= 0;
+    const int e = valid ? ev : 0;
+    uint64_t m;
+    int r;
+    match_lanes(e, valid, ebits, lane, m, r);
+    if (lane < EA) s_cnt[lane] = 0;
+    wave_sync();
+    if (valid && r == __popcll(m) - 1) s_cnt[e] = __popcll(m);
+    wave_sync();
+    const int c = lane < EA ? s_cnt[lane] : 0;
+    int incl = c;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+    }
+    const int total = __shfl(incl, EA - 1, 64);
+    if (lane < EA) {
+        counts[lane] = c;
+        offsets[lane] = incl - c;
+        s_cnt[lane] = incl - c;
+    }
+    if (lane == EA - 1) offsets[EA] = incl;
+    wave_sync();
+    if (valid) {
+        const int pos = s_cnt[e] + r;
+        sorted_pos[pos] = lane;
+        rank[lane] = pos;
+    } else if (lane < NP) {
+        rank[lane] = -1;
+    }
+    if (lane >= total && lane < NP) sorted_pos[lane] = -1;
+}
+
 __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ idx, const uint8_t *__restrict__ skip,
                                                    int NP, int E, int ebits, int32_t *__restrict__ counts,
                                                    int32_t *__restrict__ offsets, int32_t *__restrict__ sorted_pos,
@@ -138,13 +192,14 @@ __global__ __launch_bounds__(1024) void k_dispatch(const int64_t *__restrict__ i
 template <int DT>
 __device__ __forceinline__ void route_topk_part(const void *logits, int E, int k, int renorm, bool shared, int t,
                                                 int64_t *idx, void *wout, float *w32, int64_t *idx_ext, float *w_ext,
-                                                float *s_p) {
+                                                float *s_p, int *myc_out = nullptr, float *r_out = nullptr) {
     const int lane = threadIdx.x & 63;
     const int ks = k + (shared ? 1 : 0);
     int myc;
     float p;
     topk_wave<DT>(logits, (size_t)t, E, k, renorm, s_p, myc, p);
     const float r = rnd_act<DT>(p);
+    if (myc_out != nullptr) *myc_out = myc, *r_out = r;
     if (lane < k) {
         idx[(size_t)t * k + lane] = myc;
         if (wout != nullptr) st_act<DT>(wout, (size_t)t * k + lane, p);
@@ -176,12 +231,12 @@ __device__ __forceinline__ void route_token(const void *logits, int E, int k, in
 // levels and skip of token t's ks slots (one wave; slot k, when ks > k, is the shared expert:
 // level 0, never skipped), and the vote tallies of its kept pairs (expert id in [0, EA), not
 // skipped: the pairs the dispatch keeps)
-__device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const float *w, const int64_t *idx,
-                                             const moehip_policy &pol, int32_t *levels, uint8_t *skip, float *s_w,
-                                             float *s_sorted, float *s_total, VoteTally &vt) {
+// (token_levels_r: the slot's weight wj (lanes < k) and expert e (lanes < ks) in registers; with s_pe,
+// the expert of each kept pair, or -1, also goes to s_pe[t * ks + lane])
+__device__ __forceinline__ void token_levels_r(int t, int k, int ks, int EA, float wj, int64_t e,
+                                               const moehip_policy &pol, int32_t *levels, uint8_t *skip, float *s_w,
+                                               float *s_sorted, float *s_total, VoteTally &vt, int16_t *s_pe) {
     const int lane = threadIdx.x & 63;
-    const float wj = lane < k ? w[(size_t)t * ks + lane] : 0.f;
-    const int64_t e = lane < ks ? idx[(size_t)t * ks + lane] : -1;
     int lvl;
     bool sk;
     slot_level(lane, k, wj, pol, s_w, s_sorted, s_total, lvl, sk);
@@ -189,16 +244,44 @@ __device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const
     if (lane < ks) {
         levels[(size_t)t * ks + lane] = lvl;
         skip[(size_t)t * ks + lane] = sk ? 1 : 0;
-        if (!sk && e >= 0 && e < EA) tally_add(vt, (int)e, lvl);
+        const bool kept = !sk && e >= 0 && e < EA;
+        if (kept) tally_add(vt, (int)e, lvl);
+        if (s_pe != nullptr) s_pe[(size_t)t * ks + lane] = kept ? (int16_t)e : (int16_t)-1;
     }
     wave_sync();  // the wave's LDS is reused for its next token
+}
+__device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const float *w, const int64_t *idx,
+                                             const moehip_policy &pol, int32_t *levels, uint8_t *skip, float *s_w,
+                                             float *s_sorted, float *s_total, VoteTally &vt, int16_t *s_pe = nullptr) {
+    const int lane = threadIdx.x & 63;
+    const float wj = lane < k ? w[(size_t)t * ks + lane] : 0.f;
+    const int64_t e = lane < ks ? idx[(size_t)t * ks + lane] : -1;
+    token_levels_r(t, k, ks, EA, wj, e, pol, levels, skip, s_w, s_sorted, s_total, vt, s_pe);
+}
+
+// the same work lists for at most 64 experts by one wave (lane = expert)
+__device__ __forceinline__ void write_items_wave64(const int *s_n, int EA, int np, int P, const int *s_ch,
+                                                   int32_t *items) {
+    const int lane = threadIdx.x & 63;
+    for (int p = 0; p < P; ++p) {
+        int32_t *it = items + (size_t)p * (np + 1);
+        const int n = (lane < EA && s_ch[lane] == p) ? s_n[lane] : 0;
+        const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
+        int incl = nz;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        for (int z = 0; z < nz; ++z) it[incl - nz + z] = (lane << 8) | z;
+        if (lane == 63) it[np] = incl;
+    }
 }
 
 // the work lists of the batched GEMVs (whole workgroup of 1024), one per record precision p < P
 // at items + p * (np + 1): one item (e << 8 | z) per GV_TOKENS pairs of every expert voted to p
 // (s_ch[e], LDS), in expert order (exclusive scan of ceil(n_e / GV_TOKENS)); [np] = their number.
-// offsets must be visible to the workgroup (its own writes + barrier).
-__device__ __forceinline__ void write_items(const int32_t *offsets, int EA, int np, int P, const int *s_ch,
+// s_n[e] = the kept pairs of expert e (the vote tallies, LDS).
+__device__ __forceinline__ void write_items(const int *s_n, int EA, int np, int P, const int *s_ch,
                                             int32_t *items, int *s_wtot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     for (int p = 0; p < P; ++p) {
@@ -206,7 +289,7 @@ __device__ __forceinline__ void write_items(const int32_t *offsets, int EA, int 
         int base = 0;
         for (int e0 = 0; e0 < EA; e0 += 1024) {
             const int e = e0 + tid;
-            const int n = (e < EA && s_ch[e] == p) ? offsets[e + 1] - offsets[e] : 0;
+            const int n = (e < EA && s_ch[e] == p) ? s_n[e] : 0;
             const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
             int incl = nz;
             for (int off = 1; off < 64; off <<= 1) {
@@ -246,24 +329,34 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     __shared__ int s_wtot[DP_WAVES];
     __shared__ float s_w[DP_WAVES][64], s_sorted[DP_WAVES][64], s_total[DP_WAVES];
     __shared__ VoteTally s_vt;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ int16_t s_pe[DP_LDS_PAIRS];
+    const int tid = threadIdx.x, wave = tid >> 6;
     const int EA = E + (has_shared ? 1 : 0);
+    int16_t *pe = T * ks <= DP_LDS_PAIRS ? s_pe : nullptr;
     VoteRecs vr;  // (thread e votes for expert e: EA <= 1024)
     vote_recs(vr, tid, E, EA, rtab, srec, P, offs, planned);
     tally_clear(s_vt, EA);
     __syncthreads();
     for (int t = wave; t < T; t += DP_WAVES)
-        token_levels(t, k, ks, EA, w, idx, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt);
+        token_levels(t, k, ks, EA, w, idx, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt, pe);
     __syncthreads();
-    dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
+    if (T * ks <= 64 && EA <= 64) {
+        if (wave == 0) dispatch_wave64(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, pe);
+    } else {
+        dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
+    }
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
     if (tid < EA)
         s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, has_shared, sorted_pos, hi_vote,
                                pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
-    __syncthreads();  // the offsets are this workgroup's own writes
-    write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
+    __syncthreads();  // (s_ch)
+    if (EA <= 64) {
+        if (wave == 0) write_items_wave64(s_vt.n, EA, T * ks, P, s_ch, items);
+    } else {
+        write_items(s_vt.n, EA, T * ks, P, s_ch, items, s_wtot);
+    }
 }
 
 }  // namespace moehip
@@ -312,33 +405,48 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     const bool shared = gate != nullptr;
     const int ks = k + (shared ? 1 : 0), EA = E + (shared ? 1 : 0);
     int64_t *pidx = shared ? idx_ext : idx;
-    float *pw = shared ? w_ext : w32;
     __shared__ VoteTally s_vt;
+    __shared__ int16_t s_pe[DP_LDS_PAIRS];
+    int16_t *pe = T * ks <= DP_LDS_PAIRS ? s_pe : nullptr;
     VoteRecs vr;  // (thread e votes for expert e: EA <= 1024)
     vote_recs(vr, tid, E, EA, rtab, srec, P, offs, planned);
-    tally_clear(s_vt, EA);  // ordered before the levels by the barrier after the routing
-    // routing of every token
-    for (int t = wave; t < T; t += DP_WAVES)
-        route_token<DT>(logits, E, k, renorm, x, gate, H, t, idx, wout, w32, idx_ext, w_ext, s_w[wave]);
+    tally_clear(s_vt, EA);
+    __syncthreads();  // (the tallies are clear before any token adds to them)
+    // routing and levels of every token on one wave, the slot's expert and weight passed on in
+    // registers (not read back from this workgroup's own global writes)
+    for (int t = wave; t < T; t += DP_WAVES) {
+        int myc = -1;
+        float r = 0.f;
+        route_topk_part<DT>(logits, E, k, renorm, shared, t, idx, wout, w32, idx_ext, w_ext, s_w[wave], &myc, &r);
+        if (shared) route_shared_part<DT>(x, gate, H, E, k, t, idx_ext, w_ext);
+        wave_sync();  // (s_w is the routing's scratch and then the levels')
+        const float wj = lane < k ? r : 0.f;
+        const int64_t e = lane < k ? (int64_t)myc : (shared && lane == k ? (int64_t)E : (int64_t)-1);
+        token_levels_r(t, k, ks, EA, wj, e, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt, pe);
+    }
     __syncthreads();
-    // levels
-    for (int t = wave; t < T; t += DP_WAVES)
-        token_levels(t, k, ks, EA, pw, pidx, pol, levels, skip, s_w[wave], s_sorted[wave], &s_total[wave], s_vt);
-    __syncthreads();
-    dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot);
+    if (T * ks <= 64 && EA <= 64) {
+        if (wave == 0) dispatch_wave64(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, pe);
+    } else {
+        dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
+    }
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
     if (tid < EA)
         s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, shared ? 1 : 0, sorted_pos,
                                hi_vote, pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
-    __syncthreads();  // the offsets are this workgroup's own writes
-    write_items(offsets, EA, T * ks, P, s_ch, items, s_wtot);
+    __syncthreads();  // (s_ch)
+    if (EA <= 64) {
+        if (wave == 0) write_items_wave64(s_vt.n, EA, T * ks, P, s_ch, items);
+    } else {
+        write_items(s_vt.n, EA, T * ks, P, s_ch, items, s_wtot);
+    }
 }
 
-// more than 64 KiB of LDS per workgroup (dynamic + the kernels' static ~25 KiB) must be enabled
+// more than 64 KiB of LDS per workgroup (dynamic + the kernels' static ~33 KiB) must be enabled
 static bool enable_big_lds(const void *fn, size_t lds) {
-    if (lds + 28 * 1024 <= 64 * 1024) return true;
+    if (lds + 36 * 1024 <= 64 * 1024) return true;
     return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024) == hipSuccess;
 }
 

@@ -245,17 +245,18 @@ def test_grouped_layer_routed_graph_replays(dev, T):
         assert torch.equal(out2, eager), r
 
 
-@pytest.mark.parametrize("E,shared", [(64, False), (512, True), (800, False), (1023, True)])
+@pytest.mark.parametrize("E,shared,T", [(64, False, 40), (512, True, 40), (800, False, 40), (1023, True, 40),
+                                         (64, False, 8), (16, False, 4), (63, True, 6)])
 @pytest.mark.parametrize("mode", ["hobbit", "weight"])
-def test_batch_decide_matches_steps(dev, E, shared, mode):
+def test_batch_decide_matches_steps(dev, E, shared, T, mode):
     """moehip_batch_decide (one launch: levels, dispatch, vote from per-expert tallies, work list)
     against moehip_batch_levels + moehip_dispatch + moehip_batch_vote: every output bit-exact, up to
     1023 experts + the shared one (the largest LDS), with skipped pairs (HOBBIT t2) and experts
     without a resident copy (their pairs ranked -1 and counted in miss); the work list against the
-    offsets."""
+    offsets. T * ks <= 64 pairs over at most 64 experts take the one-wave dispatch and work list."""
     import ctypes
     from moelab_hip import _lib
-    T, k, P = 40, 8, 2
+    k, P = 8, 2
     ks, EA = (k + 1, E + 1) if shared else (k, E)
     g = np.random.default_rng(E + (7 if shared else 0))
     idx = np.stack([g.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
@@ -304,12 +305,15 @@ def test_batch_decide_matches_steps(dev, E, shared, mode):
     for name in a:
         assert torch.equal(a[name], b[name]), name
     sk = a["skip"].cpu().numpy()
-    assert (sk == 1).any() == (mode == "hobbit")
-    assert a["miss"].item() > 0  # some chosen experts have no copy
+    big = T == 40
+    if big:
+        assert (sk == 1).any() == (mode == "hobbit")
+        assert a["miss"].item() > 0  # some chosen experts have no copy
     off = a["offsets"].cpu().numpy()
     ch = a["info"].cpu().numpy()
     it = items.cpu().numpy().reshape(P, T * ks + 1)
     for p in range(P):  # one work list per record precision: the experts voted to it
         exp = [(e << 8) | z for e in range(EA) if ch[e] == p for z in range(off[e + 1] - off[e])]
         assert it[p, T * ks] == len(exp) and it[p, :len(exp)].tolist() == exp, p
-    assert (ch == 0).any() and (ch == 1).any()
+    if big:
+        assert (ch == 0).any() and (ch == 1).any()
