@@ -52,9 +52,12 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
         if (s_pe == nullptr) return pair_expert(idx, skip, p, p1, E);
         return p < p1 ? (int)s_pe[p] : -1;
     };
-    const int SEG = (NP + DP_WAVES - 1) / DP_WAVES;
+    // up to 1024 pairs: 64 per wave (one step each), so the per-expert columns span only the
+    // NW waves that hold pairs; beyond, the pairs spread over all 16 waves
+    const int SEG = NP <= 64 * DP_WAVES ? 64 : (NP + DP_WAVES - 1) / DP_WAVES;
+    const int NW = (NP + SEG - 1) / SEG;
     const int p0 = wave * SEG, p1 = min(NP, p0 + SEG);
-    for (int i = tid; i < DP_WAVES * E; i += 1024) s_cnt[i] = 0;
+    for (int i = tid; i < NW * E; i += 1024) s_cnt[i] = 0;
     __syncthreads();
     int *mine = s_cnt + wave * E;
     // the expert of each of the first DP_PRE steps' pairs, loaded at once (-1 = not a kept pair)
@@ -81,7 +84,7 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
     // per expert: column prefix over the waves (wave starts relative to the expert's offset)
     int tot = 0;  // E <= 1024: thread e owns expert e
     if (tid < E) {
-        for (int w = 0; w < DP_WAVES; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const int c = s_cnt[w * E + tid];
             s_cnt[w * E + tid] = tot;
             tot += c;
@@ -101,7 +104,7 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
     const int excl = wbase + incl - tot;
     if (tid < E) {
         offsets[tid] = excl;
-        for (int w = 0; w < DP_WAVES; ++w) s_cnt[w * E + tid] += excl;
+        for (int w = 0; w < NW; ++w) s_cnt[w * E + tid] += excl;
         if (tid == E - 1) offsets[E] = excl + tot;
     }
     int total = 0;
