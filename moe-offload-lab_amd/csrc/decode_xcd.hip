@@ -823,7 +823,6 @@ __device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, cons
             for (int m = 0; m < 8; ++m) va[m] = ld_local(hs + min(256 * m, max(lim, 0)));
             take(vb);
             if (!__syncthreads_or(need != 0)) break;
-            __builtin_amdgcn_s_sleep(1);
         }
         if (it >= spin) {
             h_ok = false;
@@ -876,7 +875,6 @@ __device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, cons
                         need &= ~(1u << xx);
                     }
                 if (need == 0) break;
-                __builtin_amdgcn_s_sleep(2);
 #pragma unroll
                 for (int xx = 0; xx < XC_N; ++xx) wa[xx] = ld_tag(src + (size_t)xx * a.H);
 #pragma unroll
@@ -886,7 +884,6 @@ __device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, cons
                         need &= ~(1u << xx);
                     }
                 if (need == 0) break;
-                __builtin_amdgcn_s_sleep(2);
             }
             float acc = 0.f;
 #pragma unroll
