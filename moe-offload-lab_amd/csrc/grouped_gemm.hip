@@ -1833,10 +1833,15 @@ static void launch_ffn(hipStream_t st, FfnArgs a, const int64_t *tab, int E, int
 }
 
 // batched GEMV launch geometry for rows of K values: G = 2^lg lanes per row, CPL chunks per lane,
-// P passes per wave (P * CPL = 4 16-byte loads per lane and matrix in flight)
+// P passes per wave (gv_passes: P * CPL 16-byte loads per lane and matrix in flight)
 struct GvGeo {
     int lg, cpl, p, rows_per_block;
 };
+// passes per wave: 4 / CPL, but 2 at one chunk per lane (int4 rows of up to 2048 values): four
+// passes there held 140 registers (3 waves per SIMD), two hold 94 (5), and the extra waves hide
+// more of each item's dependent loads (table, offsets, token) than the deeper ring did (OLMoE mixed
+// bs=8 61.8 -> 59.2 us per layer, Qwen3-Next int4 bs=32 125.9 -> 120.0)
+constexpr int gv_passes(int cpl) { return cpl >= 4 ? 1 : (cpl == 1 ? 2 : 4 / cpl); }
 static GvGeo gv_geo(int prec, int K) {
     const int vpc = prec == MOEHIP_PREC_INT4 ? 32 : ((prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8) ? 16 : 8);
     const int C = K / vpc;
@@ -1845,7 +1850,7 @@ static GvGeo gv_geo(int prec, int K) {
     GvGeo g;
     g.lg = lg;
     g.cpl = (C + (1 << lg) - 1) >> lg;
-    g.p = g.cpl >= 4 ? 1 : 4 / g.cpl;
+    g.p = gv_passes(g.cpl);
     g.rows_per_block = 4 * g.p * (64 >> lg);
     return g;
 }
@@ -1876,7 +1881,7 @@ template <int PREC, int CPL>
 static void launch_gv_cpl(int mode, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
                           int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
                           float *out, const float *w, DeqK dk) {
-    constexpr int P = CPL >= 4 ? 1 : 4 / CPL;
+    constexpr int P = gv_passes(CPL);
     int ng = 1, gx = 8;
     gv_grid(PREC, mode != 0, rows, NP, g, H, I, ng, gx);
     const dim3 grid(gx, NP);
@@ -1928,7 +1933,7 @@ template <int PA, int CA, int PB, int CB>
 static void launch_gv2_t(int mode, const GvSide &a, const GvSide &b, int NP, hipStream_t st, const void *act, const int *ae,
                          int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, float *out,
                          const float *w, DeqK dk) {
-    constexpr int QA = CA >= 4 ? 1 : 4 / CA, QB = CB >= 4 ? 1 : 4 / CB;
+    constexpr int QA = gv_passes(CA), QB = gv_passes(CB);
     const dim3 grid(max(a.gx, b.gx), NP);
     if (mode == 2)
         hipLaunchKernelGGL((k_gemv_up2<PA, CA, QA, PB, CB, QB, true>), grid, dim3(256), 0, st,
