@@ -1840,17 +1840,24 @@ struct GvGeo {
 // passes per wave: 4 / CPL, but 2 at one chunk per lane (int4 rows of up to 2048 values): four
 // passes there held 140 registers (3 waves per SIMD), two hold 94 (5), and the extra waves hide
 // more of each item's dependent loads (table, offsets, token) than the deeper ring did (OLMoE mixed
-// bs=8 61.8 -> 59.2 us per layer, Qwen3-Next int4 bs=32 125.9 -> 120.0)
-constexpr int gv_passes(int cpl) { return cpl >= 4 ? 1 : (cpl == 1 ? 2 : 4 / cpl); }
-static GvGeo gv_geo(int prec, int K) {
+// bs=8 61.8 -> 59.2 us per layer, Qwen3-Next int4 bs=32 125.9 -> 120.0); and 1 for int4 rows of
+// two chunks per lane (the wide gate/up rows below)
+constexpr int gv_passes(int prec, int cpl) {
+    return cpl >= 4 ? 1 : (cpl == 1 ? 2 : (prec == MOEHIP_PREC_INT4 ? 1 : 4 / cpl));
+}
+// wide: int4 gate/up rows of 2048 values on 32 lanes, two chunks each (one pass), not 64 lanes
+// of one: Qwen3-Next int4 bs=32 119.8 -> 116.9 us per layer (single-precision launches; the
+// two-precision kernels are instantiated for int4 rows of one chunk per lane)
+static GvGeo gv_geo(int prec, int K, bool wide = false) {
     const int vpc = prec == MOEHIP_PREC_INT4 ? 32 : ((prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8) ? 16 : 8);
     const int C = K / vpc;
     int lg = 0;
     while ((1 << lg) < C && lg < 6) ++lg;
+    if (wide && prec == MOEHIP_PREC_INT4 && C == 64) --lg;
     GvGeo g;
     g.lg = lg;
     g.cpl = (C + (1 << lg) - 1) >> lg;
-    g.p = gv_passes(g.cpl);
+    g.p = gv_passes(prec, g.cpl);
     g.rows_per_block = 4 * g.p * (64 >> lg);
     return g;
 }
@@ -1881,7 +1888,7 @@ template <int PREC, int CPL>
 static void launch_gv_cpl(int mode, int rows, const int32_t *items, int NP, const GvGeo &g, hipStream_t st, const void *act, const int *ae,
                           int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab,
                           float *out, const float *w, DeqK dk) {
-    constexpr int P = gv_passes(CPL);
+    constexpr int P = gv_passes(PREC, CPL);
     int ng = 1, gx = 8;
     gv_grid(PREC, mode != 0, rows, NP, g, H, I, ng, gx);
     const dim3 grid(gx, NP);
@@ -1902,7 +1909,7 @@ template <int PREC>
 static void launch_gv(int mode, const int32_t *items, int NP, hipStream_t st, const void *act, const int *ae, int H, int I, int k,
                       const int32_t *offsets, const int32_t *sorted_pos, const int64_t *tab, float *out,
                       const float *w, DeqK dk) {
-    const GvGeo g = gv_geo(PREC, mode != 0 ? H : I);
+    const GvGeo g = gv_geo(PREC, mode != 0 ? H : I, mode != 0);
     const int rows = mode != 0 ? I : H;
     if (g.rows_per_block > GV_MAXROWS) return;  // unreachable for K >= 128 (checked by the caller)
     switch (g.cpl) {
@@ -1933,7 +1940,7 @@ template <int PA, int CA, int PB, int CB>
 static void launch_gv2_t(int mode, const GvSide &a, const GvSide &b, int NP, hipStream_t st, const void *act, const int *ae,
                          int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos, float *out,
                          const float *w, DeqK dk) {
-    constexpr int QA = gv_passes(CA), QB = gv_passes(CB);
+    constexpr int QA = gv_passes(PA, CA), QB = gv_passes(PB, CB);
     const dim3 grid(max(a.gx, b.gx), NP);
     if (mode == 2)
         hipLaunchKernelGGL((k_gemv_up2<PA, CA, QA, PB, CB, QB, true>), grid, dim3(256), 0, st,
