@@ -1846,8 +1846,8 @@ constexpr int gv_passes(int prec, int cpl) {
     return cpl >= 4 ? 1 : (cpl == 1 ? 2 : (prec == MOEHIP_PREC_INT4 ? 1 : 4 / cpl));
 }
 // wide: int4 gate/up rows of 2048 values on 32 lanes, two chunks each (one pass), not 64 lanes
-// of one: Qwen3-Next int4 bs=32 119.8 -> 116.9 us per layer (single-precision launches; the
-// two-precision kernels are instantiated for int4 rows of one chunk per lane)
+// of one: Qwen3-Next int4 bs=32 119.8 -> 116.9 us per layer, OLMoE mixed bs=8 59.3 -> 57.1 (the
+// int4 side of the two-precision up launch)
 static GvGeo gv_geo(int prec, int K, bool wide = false) {
     const int vpc = prec == MOEHIP_PREC_INT4 ? 32 : ((prec == MOEHIP_PREC_INT8 || prec == MOEHIP_PREC_FP8) ? 16 : 8);
     const int C = K / vpc;
@@ -1956,17 +1956,24 @@ static bool launch_gv2(const int *precs, int mode, const int32_t *items, int NP,
                        const int *ae, int H, int I, int k, const int32_t *offsets, const int32_t *sorted_pos,
                        const int64_t *tabs, int E, float *out, const float *w, DeqK dk) {
     const int K = mode != 0 ? H : I, rows = mode != 0 ? I : H;
-    const GvGeo g0 = gv_geo(precs[0], K), g1 = gv_geo(precs[1], K);
+    const GvGeo g0 = gv_geo(precs[0], K), g1 = gv_geo(precs[1], K, mode != 0);
     if (g0.rows_per_block > GV_MAXROWS || g1.rows_per_block > GV_MAXROWS) return false;
     GvSide a{items, tabs, g0.lg, 1, 8}, b{items + (NP + 1), tabs + (size_t)E * 4, g1.lg, 1, 8};
     gv_grid(precs[0], mode != 0, rows, NP, g0, H, I, a.NG, a.gx);
     gv_grid(precs[1], mode != 0, rows, NP, g1, H, I, b.NG, b.gx);
     const bool p16 = precs[0] == MOEHIP_PREC_F16 || precs[0] == MOEHIP_PREC_BF16;
     if (!p16 || (precs[1] != MOEHIP_PREC_INT4 && precs[1] != MOEHIP_PREC_INT8)) return false;
-    // (16-bit records: K = 2048 gives 4 chunks per lane, 1024 gives 2; int4 / int8: 1)
-    if (g1.cpl != 1 || (g0.cpl != 2 && g0.cpl != 4)) return false;
+    // (16-bit records: K = 2048 gives 4 chunks per lane, 1024 gives 2; int4 / int8: 1, and 2 for
+    // the wide int4 gate/up rows)
+    const bool w4 = g1.cpl == 2 && precs[1] == MOEHIP_PREC_INT4 && mode != 0;
+    if ((g1.cpl != 1 && !w4) || (g0.cpl != 2 && g0.cpl != 4)) return false;
 #define GV2(P0, C0, P1) launch_gv2_t<P0, C0, P1, 1>(mode, a, b, NP, st, act, ae, H, I, k, offsets, sorted_pos, out, w, dk)
-    if (precs[0] == MOEHIP_PREC_F16 && precs[1] == MOEHIP_PREC_INT4) {
+#define GV2W(P0, C0, P1) launch_gv2_t<P0, C0, P1, 2>(mode, a, b, NP, st, act, ae, H, I, k, offsets, sorted_pos, out, w, dk)
+    if (w4 && precs[0] == MOEHIP_PREC_F16) {
+        if (g0.cpl == 4) GV2W(MOEHIP_PREC_F16, 4, MOEHIP_PREC_INT4); else GV2W(MOEHIP_PREC_F16, 2, MOEHIP_PREC_INT4);
+    } else if (w4) {
+        if (g0.cpl == 4) GV2W(MOEHIP_PREC_BF16, 4, MOEHIP_PREC_INT4); else GV2W(MOEHIP_PREC_BF16, 2, MOEHIP_PREC_INT4);
+    } else if (precs[0] == MOEHIP_PREC_F16 && precs[1] == MOEHIP_PREC_INT4) {
         if (g0.cpl == 4) GV2(MOEHIP_PREC_F16, 4, MOEHIP_PREC_INT4); else GV2(MOEHIP_PREC_F16, 2, MOEHIP_PREC_INT4);
     } else if (precs[0] == MOEHIP_PREC_BF16 && precs[1] == MOEHIP_PREC_INT4) {
         if (g0.cpl == 4) GV2(MOEHIP_PREC_BF16, 4, MOEHIP_PREC_INT4); else GV2(MOEHIP_PREC_BF16, 2, MOEHIP_PREC_INT4);
@@ -1976,6 +1983,7 @@ static bool launch_gv2(const int *precs, int mode, const int32_t *items, int NP,
         if (g0.cpl == 4) GV2(MOEHIP_PREC_BF16, 4, MOEHIP_PREC_INT8); else GV2(MOEHIP_PREC_BF16, 2, MOEHIP_PREC_INT8);
     }
 #undef GV2
+#undef GV2W
     return true;
 }
 
