@@ -136,6 +136,58 @@ __device__ __forceinline__ void dispatch_wg(const int64_t *__restrict__ idx, con
     for (int i = total + tid; i < NP; i += 1024) sorted_pos[i] = -1;
 }
 
+// The same dispatch for up to 1024 pairs whose experts are in LDS (s_pe), one pair per thread: the
+// experts' counts by LDS atomics and their scan, each pair put at an arbitrary slot of its
+// expert's segment, then ranked within the segment by pair index (segments are short: the order
+// the atomics gave is undone by one pass over the pair's own segment), so the placement is the
+// stable one of dispatch_wg. s_cnt: 2 E + NP ints.
+__device__ __forceinline__ void dispatch_lds(int NP, int E, int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                             int32_t *__restrict__ sorted_pos, int32_t *__restrict__ rank, int *s_cnt,
+                                             int *s_wtot, const int16_t *s_pe) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int *c_n = s_cnt, *c_b = s_cnt + E, *c_t = s_cnt + 2 * E;
+    if (tid < E) c_n[tid] = 0;
+    __syncthreads();
+    const int e = tid < NP ? (int)s_pe[tid] : -1;
+    int slot = 0;
+    if (e >= 0) slot = atomicAdd(&c_n[e], 1);
+    __syncthreads();
+    // exclusive scan of the counts (thread e owns expert e: E <= 1024)
+    const int n = tid < E ? c_n[tid] : 0;
+    int incl = n;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += v;
+    }
+    if (lane == 63) s_wtot[wave] = incl;
+    __syncthreads();
+    int wb = 0, total = 0;
+    for (int w = 0; w < DP_WAVES; ++w) {
+        if (w < wave) wb += s_wtot[w];
+        total += s_wtot[w];
+    }
+    const int excl = wb + incl - n;
+    if (tid < E) {
+        counts[tid] = n;
+        offsets[tid] = excl;
+        c_b[tid] = excl;
+    }
+    if (tid == 0) offsets[E] = total;
+    __syncthreads();
+    if (e >= 0) c_t[c_b[e] + slot] = tid;
+    __syncthreads();
+    if (e >= 0) {
+        const int b = c_b[e], m = c_n[e];
+        int r = 0;
+        for (int i = 0; i < m; ++i) r += c_t[b + i] < tid ? 1 : 0;
+        sorted_pos[b + r] = tid;
+        rank[tid] = b + r;
+    } else if (tid < NP) {
+        rank[tid] = -1;
+    }
+    for (int i = total + tid; i < NP; i += 1024) sorted_pos[i] = -1;
+}
+
 // The same dispatch for at most 64 pairs over at most 64 experts by ONE wave (lane = pair; the
 // batched decode's few tokens): the stable rank of a pair is its rank among the lower lanes with the
 // same expert (match_lanes), the group's last lane writes the expert's count, one prefix scan over
@@ -345,6 +397,8 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     __syncthreads();
     if (T * ks <= 64 && EA <= 64) {
         if (wave == 0) dispatch_wave64(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, pe);
+    } else if (pe != nullptr && T * ks <= 1024 && 2 * EA + T * ks <= DP_WAVES * EA) {
+        dispatch_lds(T * ks, EA, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
     } else {
         dispatch_wg(idx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
     }
@@ -430,6 +484,8 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     __syncthreads();
     if (T * ks <= 64 && EA <= 64) {
         if (wave == 0) dispatch_wave64(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, pe);
+    } else if (pe != nullptr && T * ks <= 1024 && 2 * EA + T * ks <= DP_WAVES * EA) {
+        dispatch_lds(T * ks, EA, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
     } else {
         dispatch_wg(pidx, skip, T * ks, EA, ebits, counts, offsets, sorted_pos, rank, s_cnt, s_wtot, pe);
     }
