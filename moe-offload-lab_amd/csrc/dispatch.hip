@@ -314,7 +314,10 @@ __device__ __forceinline__ void token_levels(int t, int k, int ks, int EA, const
     token_levels_r(t, k, ks, EA, wj, e, pol, levels, skip, s_w, s_sorted, s_total, vt, s_pe);
 }
 
-// the same work lists for at most 64 experts by one wave (lane = expert)
+// the work lists of the batched GEMVs, one per record precision p < P at items + p * (np + 1): one
+// item (e << 8 | z) per GV_TOKENS pairs of every expert voted to p (s_ch[e]), in expert order
+// (exclusive scan of ceil(n_e / GV_TOKENS)); [np] = their number. For at most 64 experts by one
+// wave (lane = expert)
 __device__ __forceinline__ void write_items_wave64(const int *s_n, int EA, int np, int P, const int *s_ch,
                                                    int32_t *items) {
     const int lane = threadIdx.x & 63;
@@ -332,37 +335,39 @@ __device__ __forceinline__ void write_items_wave64(const int *s_n, int EA, int n
     }
 }
 
-// the work lists of the batched GEMVs (whole workgroup of 1024), one per record precision p < P
-// at items + p * (np + 1): one item (e << 8 | z) per GV_TOKENS pairs of every expert voted to p
-// (s_ch[e], LDS), in expert order (exclusive scan of ceil(n_e / GV_TOKENS)); [np] = their number.
-// s_n[e] = the kept pairs of expert e (the vote tallies, LDS).
-__device__ __forceinline__ void write_items(const int *s_n, int EA, int np, int P, const int *s_ch,
-                                            int32_t *items, int *s_wtot) {
+// The same work lists for up to 1024 experts by the workgroup, from the vote's own registers
+// (thread e: its chosen precision ch and kept pairs n): one scan per precision, one barrier
+__device__ __forceinline__ void write_items_1k(int ch, int n, int EA, int np, int P, int32_t *items,
+                                               int (*s_wt)[DP_WAVES]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int p = 0; p < P; ++p) {
-        int32_t *it = items + (size_t)p * (np + 1);
-        int base = 0;
-        for (int e0 = 0; e0 < EA; e0 += 1024) {
-            const int e = e0 + tid;
-            const int n = (e < EA && s_ch[e] == p) ? s_n[e] : 0;
-            const int nz = (n + GV_TOKENS - 1) / GV_TOKENS;
-            int incl = nz;
-            for (int off = 1; off < 64; off <<= 1) {
-                const int v = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += v;
-            }
-            if (lane == 63) s_wtot[wave] = incl;
-            __syncthreads();
-            int wb = base, tot = base;
-            for (int w = 0; w < DP_WAVES; ++w) {
-                if (w < wave) wb += s_wtot[w];
-                tot += s_wtot[w];
-            }
-            for (int z = 0; z < nz; ++z) it[wb + incl - nz + z] = (e << 8) | z;
-            base = tot;
-            __syncthreads();
+    const int nz = tid < EA && ch >= 0 ? (n + GV_TOKENS - 1) / GV_TOKENS : 0;
+    int incl[GV_MAXP];
+#pragma unroll
+    for (int p = 0; p < GV_MAXP; ++p) {
+        incl[p] = 0;
+        if (p >= P) continue;
+        int v = ch == p ? nz : 0;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int u = __shfl_up(v, off, 64);
+            if (lane >= off) v += u;
         }
-        if (tid == 0) it[np] = base;
+        incl[p] = v;
+        if (lane == 63) s_wt[p][wave] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < GV_MAXP; ++p) {
+        if (p >= P) break;
+        int wb = 0, tot = 0;
+        for (int w = 0; w < DP_WAVES; ++w) {
+            const int c = s_wt[p][w];
+            if (w < wave) wb += c;
+            tot += c;
+        }
+        int32_t *it = items + (size_t)p * (np + 1);
+        if (ch == p)
+            for (int z = 0; z < nz; ++z) it[wb + incl[p] - nz + z] = (tid << 8) | z;
+        if (tid == 0) it[np] = tot;
     }
 }
 
@@ -404,15 +409,17 @@ __global__ __launch_bounds__(1024) void k_batch_decide(const float *__restrict__
     }
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
+    __shared__ int s_wt[GV_MAXP][DP_WAVES];
+    int ch = -1;
     if (tid < EA)
-        s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, has_shared, sorted_pos, hi_vote,
-                               pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
+        s_ch[tid] = ch = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, has_shared, sorted_pos,
+                                    hi_vote, pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
-    __syncthreads();  // (s_ch)
     if (EA <= 64) {
+        __syncthreads();  // (s_ch)
         if (wave == 0) write_items_wave64(s_vt.n, EA, T * ks, P, s_ch, items);
     } else {
-        write_items(s_vt.n, EA, T * ks, P, s_ch, items, s_wtot);
+        write_items_1k(ch, tid < EA ? s_vt.n[tid] : 0, EA, T * ks, P, items, s_wt);
     }
 }
 
@@ -491,15 +498,17 @@ __global__ __launch_bounds__(1024) void k_batch_route_decide(
     }
     __syncthreads();
     __shared__ int s_ch[VT_MAX];
+    __shared__ int s_wt[GV_MAXP][DP_WAVES];
+    int ch = -1;
     if (tid < EA)
-        s_ch[tid] = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, shared ? 1 : 0, sorted_pos,
-                               hi_vote, pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
+        s_ch[tid] = ch = vote_apply(tid, s_vt.n[tid], s_vt.c0[tid], s_vt.c1[tid], offsets, E, shared ? 1 : 0, sorted_pos,
+                                    hi_vote, pol.upgrade, lv0, lv1, lv2, vr, P, tabs, rank, info, miss);
     if (items == nullptr) return;
-    __syncthreads();  // (s_ch)
     if (EA <= 64) {
+        __syncthreads();  // (s_ch)
         if (wave == 0) write_items_wave64(s_vt.n, EA, T * ks, P, s_ch, items);
     } else {
-        write_items(s_vt.n, EA, T * ks, P, s_ch, items, s_wtot);
+        write_items_1k(ch, tid < EA ? s_vt.n[tid] : 0, EA, T * ks, P, items, s_wt);
     }
 }
 
