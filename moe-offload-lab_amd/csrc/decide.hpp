@@ -221,13 +221,18 @@ __device__ __forceinline__ void topk_wave_n(const void *logits, size_t row, int 
     float lv[EPL];
     uint32_t key[EPL];
     float m = -INFINITY;
+    // every load unconditional (index clamped): a load under a lane-dependent branch is waited for
+    // before the next one is issued, EPL round trips in a row
+    uint32_t braw[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) braw[i] = lr[min(lane + 64 * i, E - 1)];
 #pragma unroll
     for (int i = 0; i < EPL; ++i) {
         const int c = lane + 64 * i;
         key[i] = 0u;
         lv[i] = -INFINITY;
         if (c < E) {
-            const uint32_t b = lr[c];
+            const uint32_t b = braw[i];
             lv[i] = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)b) : __uint_as_float(b << 16);
             key[i] = topk_key16(b, c);
         }
@@ -287,17 +292,31 @@ __device__ __forceinline__ float gate_dot_wave(const void *x, const void *g, int
     float acc = 0.f;
     const uint4 *xr = reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(x) + (size_t)t * H);
     const uint4 *gr = reinterpret_cast<const uint4 *>(g);
-    for (int c = lane; c < H / 8; c += 64) {
-        const uint4 xv = xr[c], gv = gr[c];
-        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w}, ga[4] = {gv.x, gv.y, gv.z, gv.w};
+    // 4 chunks per lane requested before any is used (a loop of one chunk per trip waits for each
+    // chunk's round trip in turn); the products are added in the same order as one chunk at a time
+    constexpr int U = 4;
+    const int nc = H / 8;
+    for (int c0 = lane; c0 < nc; c0 += 64 * U) {
+        uint4 xv[U], gv[U];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float x0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)xa[i]) : __uint_as_float(xa[i] << 16);
-            const float x1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(xa[i] >> 16)) : __uint_as_float(xa[i] & 0xffff0000u);
-            const float g0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)ga[i]) : __uint_as_float(ga[i] << 16);
-            const float g1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(ga[i] >> 16)) : __uint_as_float(ga[i] & 0xffff0000u);
-            acc = fmaf(x0, g0, acc);
-            acc = fmaf(x1, g1, acc);
+        for (int u = 0; u < U; ++u) {
+            const int c = min(c0 + 64 * u, nc - 1);
+            xv[u] = xr[c];
+            gv[u] = gr[c];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + 64 * u >= nc) break;
+            const uint32_t xa[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w}, ga[4] = {gv[u].x, gv[u].y, gv[u].z, gv[u].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)xa[i]) : __uint_as_float(xa[i] << 16);
+                const float x1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(xa[i] >> 16)) : __uint_as_float(xa[i] & 0xffff0000u);
+                const float g0 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)ga[i]) : __uint_as_float(ga[i] << 16);
+                const float g1 = DT == MOEHIP_DT_F16 ? f16_to_f32((uint16_t)(ga[i] >> 16)) : __uint_as_float(ga[i] & 0xffff0000u);
+                acc = fmaf(x0, g0, acc);
+                acc = fmaf(x1, g1, acc);
+            }
         }
     }
     return wave_sum(acc);
