@@ -57,6 +57,7 @@ constexpr int XC_LDS_H = 8192;     // h values of one XCD's segment staged in LD
 constexpr int XC_MAXDR = 512;      // output rows of one down item
 constexpr int XC_NST = 16;         // trace stamps per workgroup
 constexpr int XC_SPLIT_E = 256;    // from this many experts on, the router rows are split over the XCDs
+constexpr uint64_t XC_RELAY_TICKS = 260;  // the split router's first logit poll: 2.6 us of the 100 MHz real-time counter
 
 struct XcArgs {
     const void *x;            // (H) activation dtype, 16-byte aligned
@@ -384,7 +385,7 @@ __device__ __forceinline__ uint32_t xc_poll_logits(const uint64_t *lg, int first
 
 template <int XDT>
 __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uint64_t *lg, uint32_t tag, int spin,
-                                        int64_t idx_pre, int &myc, float &myv, bool &poisoned) {
+                                        int64_t idx_pre, int &myc, float &myv, bool &poisoned, uint64_t t_in) {
     const int lane = threadIdx.x & 63;
     const int k = a.k, E = a.E, ks = a.ks;
     const bool has_sh = a.sgate != nullptr;
@@ -409,6 +410,12 @@ __device__ __forceinline__ void xc_rank(const XcArgs &a, XcShared &sh, const uin
         uint32_t need = 0;
         for (int i = 0; i < epl; ++i)
             if (lane + 64 * i < nlog) need |= 1u << i;
+        // with the rows split over the XCDs, the first poll waits until XC_RELAY_TICKS after the
+        // workgroup started: the relayed blocks land at ~2.6-3.0 us, and a poll round of words
+        // written moments before takes 1.4-1.7 us, so polling earlier costs a round (Qwen3-Next
+        // E = 512: int4 18.9 -> 18.7, fp8 21.0 -> 20.6-20.8 us per layer with 2.4-2.8 us)
+        if (a.split != 0 && routed)
+            while (__builtin_amdgcn_s_memrealtime() - t_in < XC_RELAY_TICKS) __builtin_amdgcn_s_sleep(2);
         if (epl == 1) need = xc_poll_logits<XDT, 1>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
         else if (epl <= 4) need = xc_poll_logits<XDT, 4>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
         else need = xc_poll_logits<XDT, 16>(lg, first, E, epl, lane, tag, spin, need, s_lv, s_key);
@@ -902,6 +909,7 @@ __device__ __forceinline__ void xc_down_item(const XcArgs &a, XcShared &sh, cons
 template <int XDT, int PREC, bool TWO>
 __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     __shared__ XcShared sh;
+    const uint64_t t_in = __builtin_amdgcn_s_memrealtime();
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int b = blockIdx.x, x = b % XC_N, q = b / XC_N, NQ = gridDim.x / XC_N;
     uint8_t *wsb = reinterpret_cast<uint8_t *>(a.ws);
@@ -963,7 +971,7 @@ __global__ __launch_bounds__(256) void k_decode_xcd(XcArgs a) {
     asm volatile("" : "+v"(test));  // (read here, long after its load was issued)
     const bool forced = uni((int)test) != 0;
     const int spin = forced ? XC_TEST_SPIN : XC_SPIN;
-    if (wave == rwave) xc_rank<XDT>(a, sh, lg, forced ? tag + 0x40000000u : tag, spin, idx_pre, myc, myv, poisoned);
+    if (wave == rwave) xc_rank<XDT>(a, sh, lg, forced ? tag + 0x40000000u : tag, spin, idx_pre, myc, myv, poisoned, t_in);
     __syncthreads();
     xc_stamp(a, sh, 6);
     if (is_up) {
