@@ -246,14 +246,17 @@ def test_grouped_layer_routed_graph_replays(dev, T):
 
 
 @pytest.mark.parametrize("E,shared,T", [(64, False, 40), (512, True, 40), (800, False, 40), (1023, True, 40),
-                                         (64, False, 8), (16, False, 4), (63, True, 6)])
+                                         (64, False, 8), (16, False, 4), (63, True, 6), (200, False, 128),
+                                         (1023, True, 113), (1023, True, 120)])
 @pytest.mark.parametrize("mode", ["hobbit", "weight"])
 def test_batch_decide_matches_steps(dev, E, shared, T, mode):
     """moehip_batch_decide (one launch: levels, dispatch, vote from per-expert tallies, work list)
     against moehip_batch_levels + moehip_dispatch + moehip_batch_vote: every output bit-exact, up to
     1023 experts + the shared one (the largest LDS), with skipped pairs (HOBBIT t2) and experts
     without a resident copy (their pairs ranked -1 and counted in miss); the work list against the
-    offsets. T * ks <= 64 pairs over at most 64 experts take the one-wave dispatch and work list."""
+    offsets. T * ks <= 64 pairs over at most 64 experts take the one-wave dispatch and work list; up
+    to 1024 pairs the LDS counting sort (1024 and 1017 pairs here), beyond it the per-wave column
+    dispatch (1080 pairs)."""
     import ctypes
     from moelab_hip import _lib
     k, P = 8, 2
