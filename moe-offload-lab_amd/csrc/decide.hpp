@@ -27,6 +27,14 @@ __device__ __forceinline__ void slot_level(int j, int k, float wj, const moehip_
                                            double *s_out = nullptr) {
     const bool act = j < k;
     s_w[j] = wj;
+    // the fixed modes and the weight threshold read nothing of the other slots: no LDS round trip
+    // (the weights' total below is a serial sum by one lane between two wave barriers)
+    if (pol.mode != 0 || pol.protect) {
+        skip = false;
+        if (s_out) *s_out = 0.0;
+        lvl = (pol.mode == 1 || pol.protect) ? 0 : (pol.mode == 2 ? 2 : (wj >= pol.t1 ? 0 : 2));
+        return;
+    }
     wave_sync();
     const bool f64 = one64 && pol.f64 != 0 && pol.mode == 0 && !pol.protect;
     if (j == 0 && !f64) {
