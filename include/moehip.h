@@ -313,7 +313,9 @@ size_t moehip_decode_rows_workspace_bytes(int P, int k, int H, int I);
  * (with_router = 1) or without the router rows; -1 for a bad description. A grid larger than
  * this is clamped to it; the per-item trace needs 3 * (items + 3) + 8 * items uint64. */
 int moehip_decode_layer_work_items(const moehip_layer_desc *desc, int with_router);
-/* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device). */
+/* Copies the workspace's sticky error word (non-zero after a bounded wait expired) to flag_out (device).
+ * ws = NULL: the current device's scratch array of moehip_decode_layer_noalloc (MOEHIP_EINVAL before
+ * moehip_device_check has set it up); copies only, allocates nothing. */
 int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream);
 
 /* Which decode kernel the calling thread's last moehip_decode_layer, moehip_decode_layer_noalloc

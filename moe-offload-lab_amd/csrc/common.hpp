@@ -34,6 +34,7 @@ int xcd_dispatch_ok();
 // logits (T, E) = x Wr^T in dtype (router.hip): MFMA tiles for 16-bit rows when the shape allows
 void launch_router_logits(const void *x, const void *Wr, int T, int H, int E, int dtype, void *logits, hipStream_t st);
 int noalloc_init(int dev);
+void *noalloc_scratch(int dev);
 size_t xcd_workspace_bytes(int prec, int ks, int E, int H, int I);
 int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const int64_t *idx_in, const float *w32_in,
                const int64_t *rows_b, const float *rows_w, const int64_t *rtab, void *out, const void *add,

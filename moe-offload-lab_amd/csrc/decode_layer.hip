@@ -1474,7 +1474,14 @@ extern "C" int moehip_decode_layer_work_items(const moehip_layer_desc *d, int wi
 }
 
 extern "C" int moehip_decode_layer_error(const void *ws, void *flag_out, void *stream) {
-    MOEHIP_REQUIRE(ws && flag_out, "decode_layer_error: null pointer");
+    MOEHIP_REQUIRE(flag_out, "decode_layer_error: null flag_out");
+    if (ws == nullptr) {  // the current device's scratch array of moehip_decode_layer_noalloc
+        int dev = -1;
+        MOEHIP_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0, "decode_layer_error: no current device");
+        ws = noalloc_scratch(dev);
+        MOEHIP_REQUIRE(ws != nullptr, "decode_layer_error: no workspace given and device %d's scratch array is not "
+                       "set up (moehip_device_check(%d) sets it up)", dev, dev);
+    }
     const hipError_t e = hipMemcpyAsync(flag_out, reinterpret_cast<const uint32_t *>(ws) + W_ERR, 4,
                                         hipMemcpyDeviceToDevice, as_stream(stream));
     if (e != hipSuccess) {

@@ -58,6 +58,10 @@ int noalloc_init(int dev) {
     return rc;
 }
 
+// device dev's copy of `scratch` (null before noalloc_init(dev)): the workspace whose error word
+// moehip_decode_layer_error reads when it is given no workspace
+void *noalloc_scratch(int dev) { return dev >= 0 && dev < 64 ? g_scratch[dev] : nullptr; }
+
 }  // namespace moehip
 
 using namespace moehip;

@@ -63,6 +63,11 @@ def test_noalloc_matches_workspace_entry(dev, shapes):
                     assert torch.equal(r_na[key], r_ws[key]), key
             assert r_na["miss"].item() == r_ws["miss"].item() == 0
         dec.check_error()
+        # the scratch array's own error word (no workspace pointer): clear after these calls
+        flag = torch.full((1,), 7, dtype=torch.int32, device=dev)
+        _lib.call("moehip_decode_layer_error", None, flag.data_ptr(), _lib.stream_of(dev))
+        torch.cuda.synchronize()
+        assert flag.item() == 0
 
 
 def test_noalloc_refuses_an_oversized_layer(dev):
