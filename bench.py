@@ -780,7 +780,8 @@ def offload_bench(args):
     Wr, xs = residual_stream(dev, warm + steps, L, NE, NH, seed=1)
     budget = 16 * 10**9 * L // 48  # 16 GB for the 48-layer model: the same resident fraction (39 %)
     off = OffloadDecoder({"int4": lay}, L, NE, NK, lambda l, e, p: host[(l, e)], budget, dev, PrecisionPolicy("lo"),
-                         torch.bfloat16, router_weights=Wr, renorm=True, mode=mode, predictor="gate")
+                         torch.bfloat16, router_weights=Wr, renorm=True, mode=mode, predictor="gate",
+                         prefetch_mode=args.prefetch_mode)
     out = torch.zeros(1, NH, dtype=torch.bfloat16, device=dev)
     # the routing every layer will get (the same router kernel on the same states), for the
     # ground-truth predictor run only
@@ -831,7 +832,8 @@ def offload_bench(args):
         if off.dec.miss.item() != 0:
             raise RuntimeError("offloaded decode ran an expert that was not resident")
         log(f"[bench] offload predictor={how}: {res[how]}")
-    return {"res": res, "peaks": peaks, "copy_peak": copy_peak, "mode": mode, "L": L, "steps": steps, "warm": warm,
+    return {"res": res, "peaks": peaks, "copy_peak": copy_peak, "mode": mode, "prefetch_mode": args.prefetch_mode,
+            "L": L, "steps": steps, "warm": warm,
             "records_host_gb": L * NE * rb / 1e9, "budget_gb": budget / 1e9, "distinct": distinct, "reuse": reuse}
 
 
@@ -850,7 +852,7 @@ def offload_line(args):
                                "residual stream (Zipf-like expert popularity, token-to-token correlation), bs=1",
                    "d_model": NH, "experts": NE, "top_k": NK, "d_ff": NI, "layers": r["L"],
                    "records_host_gb": round(r["records_host_gb"], 1), "device_budget_gb": r["budget_gb"],
-                   "staging": r["mode"],
+                   "staging": r["mode"], "prefetch_staging": r["prefetch_mode"],
                    "prefetch": "the next layer's gate on the current hidden state, on the GPU (read back with "
                                "the current routing)",
                    "distinct_experts_per_layer": round(r["distinct"], 1), "token_reuse": round(r["reuse"], 3),
@@ -1147,6 +1149,8 @@ def main():
     ap.add_argument("--offload-steps", type=int, default=256)
     ap.add_argument("--offload-warmup", type=int, default=32)
     ap.add_argument("--stage-mode", choices=["auto", "kernel", "sdma"], default="auto")
+    ap.add_argument("--prefetch-mode", choices=["kernel", "sdma"], default="sdma",
+                    help="offload: how predicted experts are staged while the decode kernel runs")
     ap.add_argument("--disk-layers", type=int, default=4)
     ap.add_argument("--disk-reads", type=int, default=512)
     ap.add_argument("--disk-steps", type=int, default=64)

@@ -70,7 +70,10 @@ class DevicePool:
         room = (self.cap - self.allocated) // self.PAGE
         if room < pages:
             return False
-        n = min(max(pages, SLAB_BYTES // self.PAGE), room)
+        # a whole number of the largest records per slab: a slab's tail shorter than a record
+        # would be capacity the cap counts but no record of that size can use
+        unit = max(self._pages(p) for p in self.record_bytes)
+        n = min(max(pages, SLAB_BYTES // self.PAGE // unit * unit), room)
         slab = torch.empty(n * self.PAGE + self.PAGE, dtype=torch.uint8, device=self.device)
         off = (-slab.data_ptr()) % self.PAGE
         self.slabs.append(slab[off:off + n * self.PAGE])
@@ -212,17 +215,21 @@ class Stager:
     def _prune(self) -> None:
         self._inflight = [(ev, b) for ev, b in self._inflight if not ev.query()]
 
-    def stage(self, items: list) -> tuple[list, object]:
-        """[(host_blob, prec)] -> ([device slot], event after the copies and table entries)."""
+    def stage(self, items: list, mode: str | None = None) -> tuple[list, object]:
+        """[(host_blob, prec)] -> ([device slot], event after the copies and table entries);
+        mode overrides the stager's own ("kernel" or "sdma") for this batch."""
         if not items:
             return [], None
+        mode = self.mode if mode is None else mode
+        if mode not in STAGE_MODES:
+            raise ValueError(f"staging mode {mode} (kernel or sdma)")
         self._prune()
         dsts, waits = [], []
         for blob, prec in items:
             if blob.dtype != torch.uint8 or not blob.is_contiguous() or blob.numel() != self.pool.record_bytes[prec]:
                 raise RuntimeError(f"stage: host record of {blob.numel()} B for {prec} "
                                    f"({self.pool.record_bytes[prec]} B expected)")
-            if self.mode == "kernel" and not blob.is_pinned():
+            if mode == "kernel" and not blob.is_pinned():
                 raise RuntimeError("stage: kernel staging reads pinned host memory; this record is pageable")
             slot, evs = self.pool.acquire(prec)
             dsts.append(slot)
@@ -230,13 +237,13 @@ class Stager:
         cs = self.copy_stream
         for ev in waits:
             cs.wait_event(ev)
-        mode = STAGE_MODES[self.mode]
+        code = STAGE_MODES[mode]
         for i in range(0, len(items), STAGE_MAX):
             part = list(zip(items[i:i + STAGE_MAX], dsts[i:i + STAGE_MAX]))
             arr = (_lib.Copy * len(part))()
             for j, ((blob, _), dst) in enumerate(part):
                 arr[j].src, arr[j].dst, arr[j].bytes = blob.data_ptr(), dst.data_ptr(), blob.numel()
-            _lib.call("moehip_stage_records", arr, len(part), mode, cs.cuda_stream)
+            _lib.call("moehip_stage_records", arr, len(part), code, cs.cuda_stream)
         self.bytes_h2d += sum(b.numel() for b, _ in items)
         self.batches += 1
         done = torch.cuda.Event()
@@ -281,12 +288,18 @@ class OffloadDecoder:
     callable over records in host memory, or a `diskstore.DiskTier` (RAM cache over a store on
     disk, which also offers `many` for a batch and `copied` for the copies' completion).
     fast_budget_bytes bounds the resident records (the TierCache budget); the device pool holds
-    that plus `margin_records` slots of headroom for copies in flight."""
+    that plus `margin_records` slots of headroom for copies in flight. `mode` stages the misses
+    (the compute stream waits for them); `prefetch_mode` ("sdma" by default) stages the
+    predicted experts, which copy while the decode kernel runs: a gather kernel there would hold
+    CU slots that the decode kernel's grid (every workgroup resident at once) waits for."""
 
     def __init__(self, layouts: dict, num_layers: int, num_experts: int, k: int, host_record, fast_budget_bytes: int,
                  device, policy: PrecisionPolicy | None = None, dtype=torch.float16, router_weights: list | None = None,
                  renorm: bool = False, mode: str = "kernel", half_life: float = 32.0, eviction: str = "lrfu",
-                 margin_records: int | None = None, predictor: str = "none"):
+                 margin_records: int | None = None, predictor: str = "none", prefetch_mode: str = "sdma"):
+        if prefetch_mode not in STAGE_MODES:
+            raise ValueError(f"prefetch staging mode {prefetch_mode} (kernel or sdma)")
+        self.prefetch_mode = prefetch_mode
         self.device = torch.device(device)
         _lib.check_device(self.device)
         self.precisions = list(layouts)
@@ -381,7 +394,10 @@ class OffloadDecoder:
             self.stats["prefetch_issued"] += len(todo)
         many = getattr(self.host_record, "many", None)  # a host tier that reads a batch at once
         srcs = many([(layer, e, p) for e, p in todo]) if many else [self.host_record(layer, e, p) for e, p in todo]
-        dsts, ev = self.stager.stage([(src, p) for src, (_, p) in zip(srcs, todo)])
+        # a prefetch batch runs beside the next kernels: it goes by SDMA, since the gather kernel's
+        # workgroups would take CU slots the decode kernel's co-resident grid needs
+        dsts, ev = self.stager.stage([(src, p) for src, (_, p) in zip(srcs, todo)],
+                                     mode=self.prefetch_mode if prefetch else None)
         copied = getattr(self.host_record, "copied", None)  # its buffers are reusable after `ev`
         if copied:
             copied(srcs, ev)

@@ -295,3 +295,18 @@ def test_device_pool_pages():
     pool.release(c, "fp16")
     pool.release(d, "fp16")
     assert pool.free_pages() == 9 and pool.free_ext[0] == [[0, 9, []]] and not pool.lent
+
+
+def test_device_pool_holds_cap_over_record_size_records(monkeypatch):
+    """Slabs are cut to a whole number of the largest records, so a pool whose slab size is not a
+    multiple of the record size still holds cap // record_bytes records (a Qwen3-Next int4
+    record is 408 pages: 160 of them leave 256 pages of a 65,536-page slab, which no record fits)."""
+    import moelab_hip.offload as off
+
+    monkeypatch.setattr(off, "SLAB_BYTES", 64 * 4096)  # 64 pages: 6 records of 10 pages + 4 left
+    rb = {"int4": 10 * 4096}
+    pool = off.DevicePool(rb, 60 * 10 * 4096, "cpu")
+    got = [pool.acquire("int4") for _ in range(60)]
+    assert len({t.data_ptr() for t, _ in got}) == 60 and pool.allocated == 60 * 10 * 4096
+    with pytest.raises(RuntimeError, match="pool full"):
+        pool.acquire("int4")
