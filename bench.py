@@ -778,7 +778,8 @@ def offload_bench(args):
     mode = max(peaks, key=peaks.get) if args.stage_mode == "auto" else args.stage_mode
     steps, warm = args.offload_steps, args.offload_warmup
     Wr, xs = residual_stream(dev, warm + steps, L, NE, NH, seed=1)
-    budget = 16 * 10**9 * L // 48  # 16 GB for the 48-layer model: the same resident fraction (39 %)
+    # 16 GB for the 48-layer model by default: the same resident fraction (39 %)
+    budget = int(args.offload_budget_gb * 10**9) * L // 48
     off = OffloadDecoder({"int4": lay}, L, NE, NK, lambda l, e, p: host[(l, e)], budget, dev, PrecisionPolicy("lo"),
                          torch.bfloat16, router_weights=Wr, renorm=True, mode=mode, predictor="gate",
                          prefetch_mode=args.prefetch_mode)
@@ -1148,6 +1149,8 @@ def main():
     ap.add_argument("--offload-layers", type=int, default=48)
     ap.add_argument("--offload-steps", type=int, default=256)
     ap.add_argument("--offload-warmup", type=int, default=32)
+    ap.add_argument("--offload-budget-gb", type=float, default=16.0,
+                    help="offload: device budget of the 48-layer model (scaled to --offload-layers)")
     ap.add_argument("--stage-mode", choices=["auto", "kernel", "sdma"], default="auto")
     ap.add_argument("--prefetch-mode", choices=["kernel", "sdma"], default="sdma",
                     help="offload: how predicted experts are staged while the decode kernel runs")

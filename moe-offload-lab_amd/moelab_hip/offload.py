@@ -334,7 +334,8 @@ class OffloadDecoder:
         self.p_w = torch.zeros(1, k, dtype=dtype, device=self.device)
         self.p_w32 = torch.zeros(1, k, dtype=torch.float32, device=self.device)
         # one pinned readback per layer: the current routing and the prediction for the next layer
-        self.rb = torch.empty(4, k, dtype=torch.float32, pin_memory=True)
+        self.rb = torch.empty(2, k, dtype=torch.float32, pin_memory=True)      # weights: current, predicted
+        self.rb_idx = torch.empty(2, k, dtype=torch.int64, pin_memory=True)    # experts: current, predicted
         self._predicted: tuple[int, frozenset] | None = None
         self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0,
                       "pred_hits": 0, "pred_total": 0, "miss_downgrades": 0}
@@ -351,10 +352,12 @@ class OffloadDecoder:
         return {e: (level_to_precision(levels[j], self.precisions), levels[j], s[j])
                 for j, e in enumerate(idx) if not skip[j]}
 
-    def _stage_missing(self, layer: int, want: dict, protect: frozenset, prefetch: bool):
+    def _stage_missing(self, layer: int, want: dict, protect: frozenset, prefetch: bool, stream=None):
         """Look the wanted records of `layer` up in the device cache as moelab's decode does
         (runtime.py:587-615) and stage the misses; returns (events the compute stream must wait
-        on, the keys this layer uses: its hits and its staged records).
+        on, the keys this layer uses: its hits and its staged records). `stream` (the compute
+        stream's handle) has already waited for an entry's copy event once it is the entry's
+        `waited`: such a hit adds no wait (the stream's later work is ordered after that wait).
 
         The lookup takes a more precise resident copy only when the policy allows upgrades
         (`allow_upgrade`: never in mode "lo"), as the kernel's copy choice does. With `miss_t1`
@@ -380,8 +383,9 @@ class OffloadDecoder:
                     if ent.prefetched:
                         self.stats["prefetch_hits"] += 1
                         ent.prefetched = False
-                    if ent.event is not None:
+                    if ent.event is not None and ent.waited != stream:
                         waits.append(ent.event)
+                        ent.waited = stream
                 continue
             todo.append((e, prec))
             used.add((layer, e, prec))
@@ -417,9 +421,10 @@ class OffloadDecoder:
         tab_ev = self.stager.flush_table()
         for ent in added:  # usable once bytes AND table entry are in place
             ent.event = tab_ev
+            ent.waited = None if prefetch else stream
         if not prefetch:
             waits.append(tab_ev)
-        return waits, used
+        return list({id(ev): ev for ev in waits}.values()), used
 
     def _gate_predict(self, layer: int, x: torch.Tensor) -> None:
         """Layer `layer`'s router on x into the prediction buffers (the next layer's gate applied
@@ -442,29 +447,29 @@ class OffloadDecoder:
         gate = predict is None and self.predictor == "gate" and layer + 1 < self.L
         if gate:
             self._gate_predict(layer + 1, x)
-        self.rb[0].copy_(idx.view(-1).float(), non_blocking=True)
-        self.rb[1].copy_(w32.view(-1), non_blocking=True)
+        self.rb_idx[0].copy_(idx.view(-1), non_blocking=True)
+        self.rb[0].copy_(w32.view(-1), non_blocking=True)
         if gate:
-            self.rb[2].copy_(self.p_idx.view(-1).float(), non_blocking=True)
-            self.rb[3].copy_(self.p_w32.view(-1), non_blocking=True)
+            self.rb_idx[1].copy_(self.p_idx.view(-1), non_blocking=True)
+            self.rb[1].copy_(self.p_w32.view(-1), non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(cur)
         ev.synchronize()
-        ids = [int(v) for v in self.rb[0].tolist()]
-        ws = self.rb[1].tolist()
+        ids = self.rb_idx[0].tolist()
+        ws = self.rb[0].tolist()
         if self._predicted is not None and self._predicted[0] == layer:
             self.stats["pred_total"] += len(ids)
             self.stats["pred_hits"] += sum(1 for e in ids if e in self._predicted[1])
         self._predicted = None
         if gate:
-            pids = [int(v) for v in self.rb[2].tolist()]
-            predict = self._wants(layer + 1, pids, self.rb[3].tolist())
+            pids = self.rb_idx[1].tolist()
+            predict = self._wants(layer + 1, pids, self.rb[1].tolist())
         elif predict:
             predict = {e: (p, 0, 0.0) for e, p in predict.items()}
         if predict and layer + 1 < self.L:
             self._predicted = (layer + 1, frozenset(predict))
         want = self._wants(layer, ids, ws)
-        waits, used = self._stage_missing(layer, want, frozenset(), prefetch=False)
+        waits, used = self._stage_missing(layer, want, frozenset(), prefetch=False, stream=cur.cuda_stream)
         for wev in waits:
             cur.wait_event(wev)
         self.dec.layer(layer, x, out, idx=idx, w32=w32)

@@ -186,9 +186,10 @@ class Entry:
     t: int = 0
     pinned: bool = False
     event: object = None       # copy to this tier still in flight
+    waited: object = None      # the stream (handle) that has already waited for `event`
     prefetched: bool = False   # staged ahead and not used yet
     rank: tuple = (0.0, 0)     # (log f - t log gamma, sequence): the eviction order
-    slot: int = field(default=-1, repr=False)  # position in the victim heap, -1 = not in it
+    slot: int = field(default=-1, repr=False)  # 0 while in the victim heap, -1 = not in it
 
 
 @dataclass
@@ -202,70 +203,59 @@ class TierStats:
 
 
 class _VictimHeap:
-    """Indexed binary min-heap of entries by Entry.rank; every entry stores its own index."""
+    """Min-heap of entries by Entry.rank with lazy removal (heapq on (rank, entry) pairs; ranks
+    are unique, so entries are never compared). A re-ranked entry gets a new pair and its old one
+    stays behind, stale: its rank is no longer the entry's, or the entry has left (slot -1). The
+    candidate walk pops pairs in rank order, dropping stale ones for good and handing live ones
+    back afterwards (restore); the array is also rebuilt from the live pairs once stale ones
+    outnumber them. Entry.slot is 0 while the entry is in the heap."""
 
     def __init__(self):
-        self.a: list[Entry] = []
+        self.a: list[tuple] = []
+        self.live = 0
+        self._held: list[tuple] = []
 
     def __len__(self):
-        return len(self.a)
+        return self.live
 
-    def _put(self, i: int, e: Entry) -> None:
-        self.a[i] = e
-        e.slot = i
+    @staticmethod
+    def _current(item) -> bool:
+        r, e = item
+        return e.slot >= 0 and e.rank is r
 
-    def _up(self, i: int) -> None:
-        e = self.a[i]
-        while i > 0:
-            p = (i - 1) >> 1
-            if self.a[p].rank <= e.rank:
-                break
-            self._put(i, self.a[p])
-            i = p
-        self._put(i, e)
-
-    def _down(self, i: int) -> None:
-        n = len(self.a)
-        e = self.a[i]
-        while True:
-            c = 2 * i + 1
-            if c >= n:
-                break
-            if c + 1 < n and self.a[c + 1].rank < self.a[c].rank:
-                c += 1
-            if e.rank <= self.a[c].rank:
-                break
-            self._put(i, self.a[c])
-            i = c
-        self._put(i, e)
+    def _compact(self) -> None:
+        if len(self.a) > 2 * self.live + 64:
+            self.a = [it for it in self.a if self._current(it)]
+            heapq.heapify(self.a)
 
     def add(self, e: Entry) -> None:
-        self.a.append(e)
-        e.slot = len(self.a) - 1
-        self._up(e.slot)
+        e.slot = 0
+        self.live += 1
+        heapq.heappush(self.a, (e.rank, e))
+        self._compact()
 
     def rekey(self, e: Entry) -> None:
-        self._up(e.slot)
-        self._down(e.slot)
+        heapq.heappush(self.a, (e.rank, e))
+        self._compact()
 
     def drop(self, e: Entry) -> None:
-        i, last = e.slot, self.a.pop()
         e.slot = -1
-        if last is not e:
-            self._put(i, last)
-            self.rekey(last)
+        self.live -= 1
 
     def ascending(self):
-        """Entries in increasing rank: best-first walk of the tree (the heap is not modified)."""
-        if not self.a:
-            return
-        front = [(self.a[0].rank, 0)]
-        while front:
-            _, i = heapq.heappop(front)
-            yield self.a[i]
-            for c in (2 * i + 1, 2 * i + 2):
-                if c < len(self.a):
-                    heapq.heappush(front, (self.a[c].rank, c))
+        """Entries in increasing rank, popped: stale pairs are dropped, live ones held until
+        restore() puts them back (call it once the walk is over, however far it went)."""
+        a = self.a
+        while a:
+            it = heapq.heappop(a)
+            if self._current(it):
+                self._held.append(it)
+                yield it[1]
+
+    def restore(self) -> None:
+        for it in self._held:
+            heapq.heappush(self.a, it)
+        self._held.clear()
 
 
 class TierCache:
@@ -356,12 +346,16 @@ class TierCache:
         else:
             order = (e for e in self._heap.ascending() if e.key not in protect)
         out, freed = [], 0
-        for e in order:
-            out.append(e)
-            freed += e.nbytes
-            if freed >= over:
-                return out
-        return None
+        try:
+            for e in order:
+                out.append(e)
+                freed += e.nbytes
+                if freed >= over:
+                    return out
+            return None
+        finally:
+            if self.eviction != "stale":
+                self._heap.restore()
 
     def insert(self, key: tuple, blob: torch.Tensor, pinned: bool = False, protect: frozenset = frozenset(),
                event=None) -> Entry | None:

@@ -135,6 +135,11 @@ def test_heap_victims_match_sorted_scores():
             c.unpin(rnd.choice(list(c.entries)))
         elif c.entries:
             c.pin(rnd.choice(list(c.entries)))
+        if step % 97 == 0:  # the whole candidate order, and the stale pairs kept bounded
+            order = [e.key for e in c._heap.ascending()]
+            c._heap.restore()
+            assert order == [e.key for e in sorted((e for e in c.entries.values() if not e.pinned), key=lambda e: e.rank)]
+            assert len(c._heap) == len(order) and len(c._heap.a) <= 2 * len(order) + 64
     assert checked > 500 and c.used <= c.budget
 
 
