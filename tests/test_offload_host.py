@@ -128,6 +128,9 @@ def test_heap_victims_match_sorted_scores():
             if expect is not None:
                 assert sorted(round(before[k], 9) for k in gone) == expect, step
                 assert not set(gone) & protect
+                # the victim walk dropped the stale pairs it passed: the top pair was current or held
+                top = c._heap.a[0] if c._heap.a else None
+                assert top is None or c._heap._current(top) or top[1].key in gone
                 checked += 1
         elif r < 0.8:
             c.tick()
