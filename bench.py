@@ -115,6 +115,57 @@ XC_STAGES = {1: "router rows done", 2: "logits polled", 3: "experts ranked", 4: 
              11: "down products", 12: "combined (combiners)", 13: "item(s) done", 14: "end"}
 
 
+def layer_reference_check(store, lay, dec, xs, Wr, outs, token=0):
+    """Before timing: token `token`'s layers against a torch fp32 reference of the MoE layer on
+    the same int4 records (nibbles - 8 times the fp16 group scales), with the kernel's routing
+    (its experts must be a top-k of the fp32 router logits, its weights their softmax within
+    2^-9 relative). Raises unless each layer's output is within max-abs 2e-2 and mean-rel 1e-3."""
+    import torch
+
+    from moelab_hip.store import _nibble_table, views
+
+    table = _nibble_table(outs.device)
+
+    def deq(v, name, rows, cols):
+        q = table[v[f"{name}.q"].long()].reshape(rows, cols).float()
+        sc = v[f"{name}.s"].float()
+        return q * sc.repeat_interleave(cols // sc.shape[1], dim=1)
+
+    worst_abs, worst_rel = 0.0, 0.0
+    for l in range(L):
+        x = xs[token, l]
+        dec.layer(l, x, outs[token, l])
+        torch.cuda.synchronize()
+        idx = dec.idx.view(-1).tolist()
+        w = dec.w32.view(-1).float()
+        xf = x.view(-1).float()
+        logits = (Wr[l].float() @ xf).to(x.dtype).float()  # the router's logits are rounded to the dtype
+        prob = torch.softmax(logits, dim=0)
+        kth = torch.topk(logits, K_TOP + 1).values
+        chosen = logits[idx]
+        if chosen.min() < kth[K_TOP - 1] - 1e-3 or len(set(idx)) != K_TOP:
+            raise RuntimeError(f"layer {l}: routed experts {idx} are not a top-{K_TOP} of the fp32 router logits")
+        if not torch.allclose(w, prob[idx], rtol=2.0 ** -9, atol=1e-6):
+            raise RuntimeError(f"layer {l}: routed weights differ from the softmax of the fp32 logits")
+        y = torch.zeros(H, device=x.device)
+        for j, e in enumerate(idx):
+            v = views(lay, store.blob("int4", l, e))
+            gu = deq(v, "gate_up", 2 * I, H)
+            dn = deq(v, "down", H, I)
+            gate, up = gu[:I] @ xf, gu[I:] @ xf
+            y += w[j] * (dn @ (torch.nn.functional.silu(gate) * up))
+        got = outs[token, l].view(-1).float()
+        ref = y.half().float()
+        d = (got - ref).abs()
+        mabs, mrel = float(d.max()), float(d.mean() / ref.abs().mean())
+        if mabs > 2e-2 or mrel > 1e-3:
+            raise RuntimeError(f"layer {l}: output off the fp32 reference (max-abs {mabs:.3g}, mean-rel {mrel:.3g})")
+        worst_abs, worst_rel = max(worst_abs, mabs), max(worst_rel, mrel)
+    log(f"[bench] parity: token {token}, {L} layers against a torch fp32 reference: max-abs {worst_abs:.2e}, "
+        f"mean-rel {worst_rel:.2e} (bars 2e-2, 1e-3)")
+    return {"layers": L, "max_abs": worst_abs, "mean_rel": worst_rel}
+
+
 def gpu_bench(args):
     import torch
 
@@ -149,6 +200,9 @@ def gpu_bench(args):
         raise RuntimeError("graph replay differs from the eager run")
     if dec.miss.item() != 0:
         raise RuntimeError("experts missing from the resident store")
+    parity = layer_reference_check(store, lay, dec, xs, Wr, outs)
+    if not torch.equal(outs, ref_out):
+        raise RuntimeError("the checked eager layers differ from the graph replay")
 
     for i in range(args.warmup):
         graphs[i % S].replay()
@@ -224,6 +278,7 @@ def gpu_bench(args):
     tok_s = 1000.0 / ms_step
     layer_us = ms_step * 1000 / L
     return {
+        "parity": parity,
         "tok_s": tok_s, "ms_step": ms_step, "layer_us": layer_us,
         "layer_tok_s": tok_s * L,
         "expert_gbs": K_TOP * rec_bytes / (layer_us * 1e-6) / 1e9,
@@ -1227,6 +1282,9 @@ def main():
         "cpu_baseline": cpu,
         "torch": torch.__version__,
     }
+    line["parity"] = {"checked": f"token 0, {r['parity']['layers']} layers, torch fp32 reference before timing",
+                      "max_abs": float(f"{r['parity']['max_abs']:.3g}"),
+                      "mean_rel": float(f"{r['parity']['mean_rel']:.3g}")}
     print(json.dumps(line), flush=True)
 
 
