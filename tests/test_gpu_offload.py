@@ -139,22 +139,24 @@ def test_offload_decoder_matches_resident(dev, mode, routed):
 
 
 @pytest.mark.parametrize("mode", ["kernel", "sdma"])
-def test_offload_gate_predictor(dev, mode):
+@pytest.mark.parametrize("prefetch_mode", ["sdma", "kernel"])
+def test_offload_gate_predictor(dev, mode, prefetch_mode):
     """The gate predictor (the next layer's router on the current state, on the GPU, read back with
     the current routing) stages layer l + 1's predicted experts while layer l runs: outputs stay
     identical to the resident decoder's, predictions are counted, and the states that repeat
-    (a layer's state fed to the next layer unchanged) are predicted exactly."""
+    (a layer's state fed to the next layer unchanged) are predicted exactly. Misses and
+    prefetches are staged by either mode (prefetches by SDMA unless told otherwise)."""
     H, I, E, L, k, T = 512, 256, 32, 4, 4, 8
     lay, store, Wr, host_record = _setup(dev, H, I, E, L, k, 7)
     rb = lay["record_bytes"]
     ref_dec = MoEDecoder(store, k, PrecisionPolicy("lo"), torch.float16, router_weights=Wr)
     off = OffloadDecoder({"int4": lay}, L, E, k, host_record, 3 * k * rb, dev, PrecisionPolicy("lo"), torch.float16,
-                         router_weights=Wr, mode=mode, predictor="gate")
+                         router_weights=Wr, mode=mode, predictor="gate", prefetch_mode=prefetch_mode)
     g = torch.Generator().manual_seed(11)
     xs = torch.randn(T, 1, 1, H, generator=g).half().repeat(1, L, 1, 1).to(dev)  # one state through every layer
     got = torch.zeros(T, L, 1, H, dtype=torch.float16, device=dev)
     ref = torch.zeros_like(got)
-    print(f"offload gate predictor mode {mode}", flush=True)
+    print(f"offload gate predictor mode {mode} prefetch {prefetch_mode}", flush=True)
     for t in range(T):
         for l in range(L):
             ref_dec.route(l, xs[t, l])
