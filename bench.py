@@ -837,7 +837,7 @@ def offload_bench(args):
     budget = int(args.offload_budget_gb * 10**9) * L // 48
     off = OffloadDecoder({"int4": lay}, L, NE, NK, lambda l, e, p: host[(l, e)], budget, dev, PrecisionPolicy("lo"),
                          torch.bfloat16, router_weights=Wr, renorm=True, mode=mode, predictor="gate",
-                         prefetch_mode=args.prefetch_mode)
+                         prefetch_mode=args.prefetch_mode, prefetch_mass=args.prefetch_mass)
     out = torch.zeros(1, NH, dtype=torch.bfloat16, device=dev)
     # the routing every layer will get (the same router kernel on the same states), for the
     # ground-truth predictor run only
@@ -889,6 +889,7 @@ def offload_bench(args):
             raise RuntimeError("offloaded decode ran an expert that was not resident")
         log(f"[bench] offload predictor={how}: {res[how]}")
     return {"res": res, "peaks": peaks, "copy_peak": copy_peak, "mode": mode, "prefetch_mode": args.prefetch_mode,
+            "prefetch_mass": args.prefetch_mass,
             "L": L, "steps": steps, "warm": warm,
             "records_host_gb": L * NE * rb / 1e9, "budget_gb": budget / 1e9, "distinct": distinct, "reuse": reuse}
 
@@ -908,7 +909,7 @@ def offload_line(args):
                                "residual stream (Zipf-like expert popularity, token-to-token correlation), bs=1",
                    "d_model": NH, "experts": NE, "top_k": NK, "d_ff": NI, "layers": r["L"],
                    "records_host_gb": round(r["records_host_gb"], 1), "device_budget_gb": r["budget_gb"],
-                   "staging": r["mode"], "prefetch_staging": r["prefetch_mode"],
+                   "staging": r["mode"], "prefetch_staging": r["prefetch_mode"], "prefetch_mass": r["prefetch_mass"],
                    "prefetch": "the next layer's gate on the current hidden state, on the GPU (read back with "
                                "the current routing)",
                    "distinct_experts_per_layer": round(r["distinct"], 1), "token_reuse": round(r["reuse"], 3),
@@ -1207,6 +1208,8 @@ def main():
     ap.add_argument("--offload-budget-gb", type=float, default=16.0,
                     help="offload: device budget of the 48-layer model (scaled to --offload-layers)")
     ap.add_argument("--stage-mode", choices=["auto", "kernel", "sdma"], default="auto")
+    ap.add_argument("--prefetch-mass", type=float, default=None,
+                    help="offload: stage the predicted experts up to this probability mass (at most 2k)")
     ap.add_argument("--prefetch-mode", choices=["kernel", "sdma"], default="sdma",
                     help="offload: how predicted experts are staged while the decode kernel runs")
     ap.add_argument("--disk-layers", type=int, default=4)

@@ -274,6 +274,25 @@ class Stager:
             torch.cuda.current_stream(blob.device).wait_event(ev)
 
 
+def mass_prediction(logits, weights: list, mass: float) -> list[tuple[int, int]]:
+    """moelab's score-mass prefetch (runtime.py:851-870, 872-890, prefetch_mass = m): the router's
+    most probable experts, in decreasing probability of the softmax over all E logits, while the
+    probability before each is below m, at most 2k of them (kp = min(E, 2k)). Returns
+    [(expert, j)]: j < k pairs the j-th most probable expert with the router's j-th top-k weight
+    (`weights`, decreasing), j >= k marks an expert beyond the router's top-k."""
+    import numpy as np
+
+    lg = np.asarray(logits, dtype=np.float32).reshape(-1)
+    k = len(weights)
+    kp = min(lg.size, 2 * k)
+    e = np.exp(lg - lg.max())
+    probs = (e / e.sum()).astype(np.float32)
+    order = np.argsort(-probs, kind="stable")[:kp]
+    pv = probs[order]
+    chosen = (np.cumsum(pv) - pv) < mass
+    return [(int(order[j]), j) for j in range(kp) if chosen[j]]
+
+
 # ---------------------------------------------------------------------------------------------
 # Offloaded decode
 # ---------------------------------------------------------------------------------------------
@@ -291,15 +310,22 @@ class OffloadDecoder:
     that plus `margin_records` slots of headroom for copies in flight. `mode` stages the misses
     (the compute stream waits for them); `prefetch_mode` ("sdma" by default) stages the
     predicted experts, which copy while the decode kernel runs: a gather kernel there would hold
-    CU slots that the decode kernel's grid (every workgroup resident at once) waits for."""
+    CU slots that the decode kernel's grid (every workgroup resident at once) waits for.
+    `prefetch_mass` m (moelab's S3, runtime.py:79, 851-890): the gate predictor stages the next
+    layer's most probable experts up to probability mass m (at most 2k; those within the router's
+    top k at their policy precision, the others at the lowest one) instead of its top k."""
 
     def __init__(self, layouts: dict, num_layers: int, num_experts: int, k: int, host_record, fast_budget_bytes: int,
                  device, policy: PrecisionPolicy | None = None, dtype=torch.float16, router_weights: list | None = None,
                  renorm: bool = False, mode: str = "kernel", half_life: float = 32.0, eviction: str = "lrfu",
-                 margin_records: int | None = None, predictor: str = "none", prefetch_mode: str = "sdma"):
+                 margin_records: int | None = None, predictor: str = "none", prefetch_mode: str = "sdma",
+                 prefetch_mass: float | None = None):
         if prefetch_mode not in STAGE_MODES:
             raise ValueError(f"prefetch staging mode {prefetch_mode} (kernel or sdma)")
+        if prefetch_mass is not None and not 0.0 < prefetch_mass <= 1.0:
+            raise ValueError(f"prefetch_mass {prefetch_mass}: in (0, 1] or None")
         self.prefetch_mode = prefetch_mode
+        self.prefetch_mass = prefetch_mass
         self.device = torch.device(device)
         _lib.check_device(self.device)
         self.precisions = list(layouts)
@@ -336,6 +362,7 @@ class OffloadDecoder:
         # one pinned readback per layer: the current routing and the prediction for the next layer
         self.rb = torch.empty(2, k, dtype=torch.float32, pin_memory=True)      # weights: current, predicted
         self.rb_idx = torch.empty(2, k, dtype=torch.int64, pin_memory=True)    # experts: current, predicted
+        self.rb_logits = torch.empty(num_experts, dtype=dtype, pin_memory=True)  # predicted logits (mass)
         self._predicted: tuple[int, frozenset] | None = None
         self.stats = {"hits": 0, "misses": 0, "prefetch_issued": 0, "prefetch_hits": 0, "skipped": 0,
                       "pred_hits": 0, "pred_total": 0, "miss_downgrades": 0}
@@ -351,6 +378,21 @@ class OffloadDecoder:
         levels, skip, s = self.policy.levels_one(layer, w)
         return {e: (level_to_precision(levels[j], self.precisions), levels[j], s[j])
                 for j, e in enumerate(idx) if not skip[j]}
+
+    def _mass_wants(self, layer: int, weights: list) -> dict:
+        """{expert: (precision, level, s)} of a score-mass prediction (runtime.py:872-890): the
+        experts paired with the router's top-k weights take the one-token rule's precision unless
+        skipped, the further ones the lowest precision."""
+        levels, skip, s = self.policy.levels_one(layer, weights)
+        low = self.precisions[-1]
+        want = {}
+        for e, j in mass_prediction(self.rb_logits.float().numpy(), weights, self.prefetch_mass):
+            if j < len(weights):
+                if not skip[j]:
+                    want[e] = (level_to_precision(levels[j], self.precisions), levels[j], s[j])
+            else:
+                want.setdefault(e, (low, 2, 0.0))
+        return want
 
     def _stage_missing(self, layer: int, want: dict, protect: frozenset, prefetch: bool, stream=None):
         """Look the wanted records of `layer` up in the device cache as moelab's decode does
@@ -452,6 +494,8 @@ class OffloadDecoder:
         if gate:
             self.rb_idx[1].copy_(self.p_idx.view(-1), non_blocking=True)
             self.rb[1].copy_(self.p_w32.view(-1), non_blocking=True)
+            if self.prefetch_mass is not None:
+                self.rb_logits.copy_(self.p_logits.view(-1), non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(cur)
         ev.synchronize()
@@ -463,7 +507,10 @@ class OffloadDecoder:
         self._predicted = None
         if gate:
             pids = self.rb_idx[1].tolist()
-            predict = self._wants(layer + 1, pids, self.rb[1].tolist())
+            if self.prefetch_mass is None:
+                predict = self._wants(layer + 1, pids, self.rb[1].tolist())
+            else:
+                predict = self._mass_wants(layer + 1, self.rb[1].tolist())
         elif predict:
             predict = {e: (p, 0, 0.0) for e, p in predict.items()}
         if predict and layer + 1 < self.L:

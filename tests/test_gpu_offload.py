@@ -208,3 +208,32 @@ def test_offload_decoder_from_disk_matches_resident(dev, tmp_path, direct, parts
     if direct:
         assert tier.store.direct_reads + tier.store.direct_fallbacks == tier.stats["disk_reads"]
     tier.close()
+
+
+@pytest.mark.parametrize("mass", [0.5, 0.95])
+def test_offload_gate_predictor_mass(dev, mass):
+    """Score-mass prefetch (moelab prefetch_mass): the predicted experts up to mass m, at most 2k,
+    are staged ahead; the outputs stay identical to the resident decoder's."""
+    H, I, E, L, k, T = 512, 256, 32, 4, 4, 6
+    lay, store, Wr, host_record = _setup(dev, H, I, E, L, k, 9)
+    rb = lay["record_bytes"]
+    ref_dec = MoEDecoder(store, k, PrecisionPolicy("lo"), torch.float16, router_weights=Wr)
+    off = OffloadDecoder({"int4": lay}, L, E, k, host_record, 4 * k * rb, dev, PrecisionPolicy("lo"), torch.float16,
+                         router_weights=Wr, predictor="gate", prefetch_mass=mass)
+    g = torch.Generator().manual_seed(13)
+    xs = torch.randn(T, 1, 1, H, generator=g).half().repeat(1, L, 1, 1).to(dev)
+    got = torch.zeros(T, L, 1, H, dtype=torch.float16, device=dev)
+    ref = torch.zeros_like(got)
+    print(f"offload gate predictor mass {mass}", flush=True)
+    for t in range(T):
+        for l in range(L):
+            ref_dec.route(l, xs[t, l])
+            ref_dec.layer(l, xs[t, l], ref[t, l], idx=ref_dec.idx, w32=ref_dec.w32)
+            off.layer(l, xs[t, l], got[t, l])
+        off.tick()
+    torch.cuda.synchronize()
+    assert off.dec.miss.item() == 0
+    assert torch.equal(got, ref)
+    assert off.stats["prefetch_issued"] > 0 and off.stats["prefetch_hits"] > 0
+    with pytest.raises(ValueError):
+        OffloadDecoder({"int4": lay}, L, E, k, host_record, 4 * k * rb, dev, router_weights=Wr, prefetch_mass=0.0)

@@ -318,3 +318,24 @@ def test_device_pool_holds_cap_over_record_size_records(monkeypatch):
     assert len({t.data_ptr() for t, _ in got}) == 60 and pool.allocated == 60 * 10 * 4096
     with pytest.raises(RuntimeError, match="pool full"):
         pool.acquire("int4")
+
+
+def test_mass_prediction():
+    """moelab's score-mass prefetch (runtime.py:851-870): the most probable experts while the mass
+    before each is below m, at most 2k; j < k pairs with the router's j-th weight."""
+    from moelab_hip.offload import mass_prediction
+
+    confident = [10.0] + [0.0] * 15
+    assert mass_prediction(confident, [0.9, 0.05], 0.8) == [(0, 0)]  # one expert holds the mass
+    flat = [0.0] * 8
+    assert mass_prediction(flat, [0.5, 0.5], 0.8) == [(0, 0), (1, 1), (2, 2), (3, 3)]  # capped at 2k
+    assert mass_prediction(flat, [0.5, 0.5], 0.3) == [(0, 0), (1, 1), (2, 2)]  # 0, 1/8, 2/8 < 0.3
+    assert mass_prediction([0.0, 3.0, 1.0], [0.8, 0.2], 1.0) == [(1, 0), (2, 1), (0, 2)]  # kp = E = 3
+    rnd = torch.Generator().manual_seed(3)
+    for _ in range(20):  # against the softmax / topk / cumsum of the reference's tensor form
+        lg = torch.randn(64, generator=rnd) * 2
+        m = float(torch.rand(1, generator=rnd)) * 0.9 + 0.05
+        pv, pi = torch.softmax(lg, 0).topk(16)
+        keep = ((pv.cumsum(0) - pv) < m).tolist()
+        want = [(int(pi[j]), j) for j in range(16) if keep[j]]
+        assert mass_prediction(lg.tolist(), [0.0] * 8, m) == want
