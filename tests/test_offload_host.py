@@ -339,3 +339,25 @@ def test_mass_prediction():
         keep = ((pv.cumsum(0) - pv) < m).tolist()
         want = [(int(pi[j]), j) for j in range(16) if keep[j]]
         assert mass_prediction(lg.tolist(), [0.0] * 8, m) == want
+
+
+def test_mass_wants_precisions():
+    """The score-mass prediction's precisions (moelab runtime.py:872-890): experts within the
+    router's top k take the one-token rule's precision (skipped ones are dropped), the experts
+    beyond it the lowest precision."""
+    from types import SimpleNamespace
+
+    from moelab_hip.offload import OffloadDecoder
+    from moelab_hip.policy import PrecisionPolicy
+
+    lg = torch.tensor([0.0, 4.0, 3.0, 2.0, 1.0, -5.0], dtype=torch.float16)
+    fake = SimpleNamespace(policy=PrecisionPolicy("weight", t1=0.5, upgrade=False), precisions=["fp16", "int4"],
+                           rb_logits=lg, prefetch_mass=0.999)
+    want = OffloadDecoder._mass_wants(fake, 0, [0.7, 0.3])  # k = 2: kp = 4 most probable experts
+    assert list(want) == [1, 2, 3, 4]
+    assert want[1][0] == "fp16" and want[2][0] == "int4"     # weight rule: 0.7 >= 0.5, 0.3 < 0.5
+    assert want[3] == ("int4", 2, 0.0) and want[4] == ("int4", 2, 0.0)  # beyond the top k: lowest
+    fake.prefetch_mass = 0.8  # p = 0.636, 0.234, 0.086, ...: the mass before expert 3 is 0.870
+    assert list(OffloadDecoder._mass_wants(fake, 0, [0.7, 0.3])) == [1, 2]
+    fake.prefetch_mass = 0.5
+    assert list(OffloadDecoder._mass_wants(fake, 0, [0.7, 0.3])) == [1]
