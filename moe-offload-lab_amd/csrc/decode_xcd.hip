@@ -1230,12 +1230,13 @@ int xcd_launch(const moehip_layer_desc *d, const void *x, const void *Wr, const 
     a.lg_up = p.lg_up;
     a.lg_dn = p.lg_dn;
     a.dr = p.dr;
-    // 0.9 of the time the HBM needs for the ks gate/up blocks (q + scales) at 8 TB/s, in 10 ns
+    // 0.85 of the time the HBM needs for the ks gate/up blocks (q + scales) at 8 TB/s, in 10 ns
     // ticks: the down items request theirs after it (measured at the OLMoE int4 bs=1 shape, ms per
-    // 16-layer token: 0.2323 with 0.8-0.9 of it, 0.2339 with all of it, 0.2344 with 0.7, 0.2404
-    // with 1.25; 15.1 us per layer without a head start)
+    // 16-layer token, one box: 0.2323 with 0.8-0.9 of it, 0.2339 with all of it, 0.2344 with 0.7,
+    // 0.2404 with 1.25, 15.1 us per layer without a head start; another box: 0.2314 with 0.8 and
+    // 0.85, 0.2319 with 0.9, 0.2332 with 0.99)
     const double gu = (double)(d->offs[0][2] - d->offs[0][0]);
-    a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8 * 0.9);
+    a.defer = (uint32_t)(ks * gu / 8.0e12 * 1.0e8 * 0.85);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, as_stream(stream), a);
     *used = which;
     return check_launch("decode_layer (xcd)");
