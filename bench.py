@@ -115,16 +115,17 @@ XC_STAGES = {1: "router rows done", 2: "logits polled", 3: "experts ranked", 4: 
              11: "down products", 12: "combined (combiners)", 13: "item(s) done", 14: "end"}
 
 
-def layer_reference_check(store, lay, dec, xs, Wr, outs, token=0):
+def layer_reference_check(store, lay, dec, xs, Wr, outs, token=0, dims=None, renorm=False, shared=None):
     """Before timing: token `token`'s layers against a torch fp32 reference of the MoE layer on
     the same int4 records (nibbles - 8 times the fp16 group scales), with the kernel's routing
     (its experts must be a top-k of the fp32 router logits, its weights their softmax within
-    2^-9 relative). Raises unless each layer's output is within max-abs 2e-2 and mean-rel 1e-3."""
+    2^-9 relative for fp16 logits, 2^-6 for bf16). Raises unless each layer's output is within max-abs 2e-2 and mean-rel 1e-3."""
     import torch
 
     from moelab_hip.store import _nibble_table, views
 
     table = _nibble_table(outs.device)
+    H, I, K_TOP, L = dims or (globals()["H"], globals()["I"], globals()["K_TOP"], globals()["L"])
 
     def deq(v, name, rows, cols):
         q = table[v[f"{name}.q"].long()].reshape(rows, cols).float()
@@ -145,17 +146,27 @@ def layer_reference_check(store, lay, dec, xs, Wr, outs, token=0):
         chosen = logits[idx]
         if chosen.min() < kth[K_TOP - 1] - 1e-3 or len(set(idx)) != K_TOP:
             raise RuntimeError(f"layer {l}: routed experts {idx} are not a top-{K_TOP} of the fp32 router logits")
-        if not torch.allclose(w, prob[idx], rtol=2.0 ** -9, atol=1e-6):
+        pw = prob[idx] / prob[idx].sum() if renorm else prob[idx]
+        # one unit in the last place of a 16-bit logit moves its weight by about that much: the
+        # kernel's and torch's fp32 sums may round to neighbouring logits
+        wtol = 2.0 ** -9 if x.dtype == torch.float16 else 2.0 ** -6
+        if not torch.allclose(w, pw, rtol=wtol, atol=1e-6):
             raise RuntimeError(f"layer {l}: routed weights differ from the softmax of the fp32 logits")
         y = torch.zeros(H, device=x.device)
-        for j, e in enumerate(idx):
-            v = views(lay, store.blob("int4", l, e))
+        # the weights in the activation dtype, as the model's routing hands them over
+        wd = w.to(x.dtype).float()
+        rows = [(wd[j], store.blob("int4", l, e)) for j, e in enumerate(idx)]
+        if shared is not None:  # the shared expert, weighted by the sigmoid of its gate's logit
+            sg = (shared[l]["gate"].float() @ xf).to(x.dtype).float()
+            rows.append((torch.sigmoid(sg).to(x.dtype).float(), shared[l]["rec"]["int4"]))
+        for wj, blob in rows:
+            v = views(lay, blob)
             gu = deq(v, "gate_up", 2 * I, H)
             dn = deq(v, "down", H, I)
             gate, up = gu[:I] @ xf, gu[I:] @ xf
-            y += w[j] * (dn @ (torch.nn.functional.silu(gate) * up))
+            y += wj * (dn @ (torch.nn.functional.silu(gate) * up))
         got = outs[token, l].view(-1).float()
-        ref = y.half().float()
+        ref = y.to(outs.dtype).float()
         d = (got - ref).abs()
         mabs, mrel = float(d.max()), float(d.mean() / ref.abs().mean())
         if mabs > 2e-2 or mrel > 1e-3:
@@ -570,6 +581,10 @@ def decode_line(args, name):
     alg = run_bytes / (S * L_) + E_ * H_ * 2 + (H_ * 2 if sp["shared"] else 0) + 2 * H_ * 2
     if dec.miss.item() != 0:
         raise RuntimeError("experts missing from the resident store")
+    parity = None
+    if precs == ["int4"]:
+        parity = layer_reference_check(store, lays["int4"], dec, xs, Wr, outs, dims=(H_, I_, k_, L_),
+                                       renorm=sp["renorm"], shared=shared)
 
     def token(s_):
         for l in range(L_):
@@ -610,6 +625,9 @@ def decode_line(args, name):
                      "bytes_per_launch": int(alg)},
         "cpu_baseline": (decode_cpu_baseline(args.cpu_seconds, H_, I_, k_ + (1 if sp["shared"] else 0), L_)
                          if not args.no_cpu and sp["precs"] == ["int4"] else None),
+        "parity": None if parity is None else {
+            "checked": f"token 0, {parity['layers']} layers, torch fp32 reference before timing",
+            "max_abs": float(f"{parity['max_abs']:.3g}"), "mean_rel": float(f"{parity['mean_rel']:.3g}")},
     }
 
 
